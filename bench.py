@@ -1,0 +1,198 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput on one MI355X.
+
+A step is one forward of the LLaDA2 block-routed MoE layer (the segment of
+src/diffuse-moe-graph.cpp:188-289) over one batch of synthetic tokens, with
+weights and activations already resident in HBM.  Default workload: the
+LLaDA2-flash-shaped layer with Q4_K experts over one 32-token block.
+
+Prints one JSON line with tokens/s, the roofline of the dominant kernel
+(timed live with HIP events on the launch stream) and the CPU baseline
+(the oracle, timed on this host over a bounded sample).
+
+    python bench.py [--steps K] [--warmup W] [--config flash_q4k]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "diffuse-cpp_amd"))
+
+METRIC = "MoE-layer tokens/s + % HBM-BW roofline (32-tok block, Q4_K); prefill % MFMA"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="flash_q4k")
+    ap.add_argument("--copies", type=int, default=3,
+                    help="weight copies rotated per step so the 256 MB MALL cannot serve repeats")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1234)
+    return ap.parse_args()
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import dmoe
+    from dmoe import synth
+
+    cfg = synth.CONFIGS[a.config]
+    if cfg.n_layers != 1:
+        raise SystemExit(f"{a.config} is a multi-layer parity case, not a bench line")
+    N, H, FF, E, K = cfg.n_tokens, cfg.n_embd, cfg.moe_ff, cfg.n_experts, cfg.top_k
+    ctx = dmoe.Context(0)
+    dev = torch.device("cuda:0")
+
+    t0 = time.time()
+    weights = [synth.device_layer(cfg, a.seed, ctx, weight_seed=a.seed + 17 * i)
+               for i in range(a.copies)]
+    layers = [ctx.wrap_device(w) for w in weights]
+    print(f"# built {a.copies} weight copies in {time.time() - t0:.1f}s", file=sys.stderr,
+          flush=True)
+    x_host = synth.make_x(cfg, a.seed)
+    x = torch.from_numpy(x_host).to(dev)
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    # routing of this input (identical for every copy: same router and bias)
+    _, dbg = ctx.forward(layers[0], x_host, debug=True)
+    counts = dbg["counts"]
+    touched = int((counts > 0).sum())
+    eb = weights[0].expert_bytes()
+    sb = weights[0].shared_bytes()
+
+    def step(i):
+        ctx.forward_device(layers[i % a.copies], x, N, y, sp)
+
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(a.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    ms_step = ev0.elapsed_time(ev1) / a.steps
+
+    # per-stage durations, HIP events around each launch on the same stream
+    ctx.profile(True)
+    for i in range(a.steps):
+        step(i)
+    torch.cuda.synchronize(dev)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    stages = {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.items()}   # us per launch
+
+    # algorithmic bytes of the dominant kernel (routed gate/up): the touched
+    # experts' gate and up matrices, the quantised activations, h written
+    rs_h = dmoe.row_size(cfg.wtype, H)
+    act_bytes = N * (H + 4 * (H // 256) + 2 * (H // 16)) if cfg.wtype == dmoe.TYPE_Q4_K else N * H * 2
+    gu_bytes = touched * 2 * FF * rs_h + act_bytes + N * K * FF * 4
+    gu_us = stages.get("gateup_routed")
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9 if gu_us else None
+
+    # layer-level: every weight byte the layer must read
+    layer_bytes = touched * eb + sb + E * H * 4 + E * 4 + 2 * N * H * 4
+    flops = 2.0 * N * (K * 3 * H * FF + 3 * H * cfg.shared_ff + H * E)
+
+    tokens_s = N / (ms_step * 1e-3)
+    out = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {dmoe.TYPE_Q4_K: "i8", dmoe.TYPE_Q8_0: "i8", dmoe.TYPE_F16: "f16",
+                  dmoe.TYPE_F32: "f32"}[cfg.wtype],
+        "data": "synthetic: random-init weights N(0,0.02) quantised on the GPU, x ~ N(0,1)",
+        "config": {
+            "workload": (f"{cfg.name}: LLaDA2 MoE layer, hidden {H}, {E} experts, moe_ff {FF}, "
+                         f"top-{K} within capacity {cfg.capacity} per {cfg.block_size}-token block, "
+                         f"shared ff {cfg.shared_ff}, {dmoe.TYPE_NAMES[cfg.wtype]} experts, "
+                         f"{N} tokens"),
+            "n_tokens": N,
+            "expert_type": dmoe.TYPE_NAMES[cfg.wtype],
+            "touched_experts": touched,
+            "max_tokens_per_expert": int(counts.max()),
+            "weight_copies_rotated": a.copies,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gateup_routed",
+            "achieved": round(achieved, 1) if achieved else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            "traffic": None,
+            "algorithmic_bytes": gu_bytes,
+            "us_per_launch": gu_us,
+        },
+        "layer": {
+            "bytes": layer_bytes,
+            "touched_expert_bytes": touched * eb,
+            "GB_s": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
+            "hbm_frac": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "touched_expert_frac": round(touched * eb / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
+            "stage_us": stages,
+        },
+    }
+
+    if not a.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+        wh = synth.to_host(weights[0])
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        yr = O.layer_forward(wh, x_host, n_threads=threads)     # warm-up
+        reps, t_start = 0, time.time()
+        while True:
+            O.layer_forward(wh, x_host, n_threads=threads)
+            reps += 1
+            el = time.time() - t_start
+            if el >= a.cpu_seconds or reps >= 1000:
+                break
+        out["cpu_baseline"] = {
+            "value": round(N * reps / el, 2),
+            "unit": "tokens/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"{reps} forwards of the same {N}-token layer ({el:.1f} s), oracle with "
+                      f"{threads} OpenMP threads",
+        }
+        ctx.forward_device(layers[0], x, N, y, sp)
+        torch.cuda.synchronize(dev)
+        err = float(np.abs(y.cpu().numpy() - yr).max() / np.abs(yr).max())
+        out["check_max_rel_err_vs_oracle"] = err
+
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

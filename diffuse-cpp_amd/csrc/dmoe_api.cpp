@@ -1,0 +1,709 @@
+// dmoe_api.cpp — host side of the C ABI declared in include/dmoe.h.
+//
+// Owns the device copies of one layer's MoE tensors and a per-context
+// workspace, validates shapes and types at the boundary, and queues the
+// kernel pipeline that replaces src/diffuse-moe-graph.cpp:188-289:
+//
+//   router_logits -> route -> dispatch -> act_quant(x) -> gate/up (+SwiGLU)
+//   -> act_quant(h) -> down -> [shared gate/up, shared down] -> combine
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "dmoe_internal.h"
+
+using namespace dmoe;
+
+struct dmoe_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // workspace, grown on demand
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    // per-stage timing
+    bool prof = false;
+    struct Mark { int stage; hipEvent_t a, b; };
+    std::vector<Mark> marks;        // recorded since the last read
+    std::vector<hipEvent_t> pool;   // free events
+};
+
+struct dmoe_layer {
+    dmoe_ctx *ctx = nullptr;
+    dmoe_hparams hp{};
+    float *gate_w = nullptr;       // [E][H] f32
+    float *gate_bias = nullptr;    // [E] or null
+    WTensor eg{}, eu{}, ed{};
+    WTensor sg{}, su{}, sd{};
+    bool has_shared = false;
+    std::vector<void *> owned;
+};
+
+namespace {
+
+int set_err(dmoe_ctx *ctx, int code, const char *fmt, ...)
+{
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return code;
+}
+
+#define HIP_TRY(ctx, expr)                                                                         \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess)                                                                      \
+            return set_err((ctx), e_ == hipErrorOutOfMemory ? DMOE_ERR_OOM : DMOE_ERR_HIP,         \
+                           "%s failed: %s", #expr, hipGetErrorString(e_));                         \
+    } while (0)
+
+bool type_supported(int32_t t)
+{
+    return t == DMOE_TYPE_F32 || t == DMOE_TYPE_F16 || t == DMOE_TYPE_Q8_0 || t == DMOE_TYPE_Q4_K;
+}
+
+// elements per block of the weight type (ggml_blck_size)
+int64_t block_elems(int32_t t)
+{
+    switch (t) {
+    case DMOE_TYPE_Q4_K: return 256;
+    case DMOE_TYPE_Q8_0: return 32;
+    case DMOE_TYPE_F16: return 8;      // the kernels read 16-byte units
+    case DMOE_TYPE_F32: return 4;
+    default: return 0;
+    }
+}
+
+size_t row_bytes(int32_t t, int64_t n)
+{
+    switch (t) {
+    case DMOE_TYPE_F32: return (size_t)n * 4;
+    case DMOE_TYPE_F16: return (size_t)n * 2;
+    case DMOE_TYPE_Q8_0: return (n % 32) ? 0 : (size_t)(n / 32) * Q8_0_BYTES;
+    case DMOE_TYPE_Q4_K: return (n % 256) ? 0 : (size_t)(n / 256) * Q4K_BYTES;
+    default: return 0;
+    }
+}
+
+// activation type of the routed products (ggml vec_dot_type)
+int32_t act_type_of(int32_t wt)
+{
+    return wt == DMOE_TYPE_Q4_K ? DMOE_ACT_Q8_K : wt;
+}
+
+size_t act_row_vals_bytes(int32_t at, int64_t n)
+{
+    switch (at) {
+    case DMOE_TYPE_F32: return (size_t)n * 4;
+    case DMOE_TYPE_F16: return (size_t)n * 2;
+    default: return (size_t)n;       // int8 values
+    }
+}
+
+// Check one weight tensor view against the expected ne; rows contiguous.
+int check_tensor(dmoe_ctx *ctx, const char *name, const dmoe_tensor &t, int64_t ne0, int64_t ne1,
+                 int64_t ne2, bool device_mode)
+{
+    if (!t.data) return set_err(ctx, DMOE_ERR_INVALID_ARG, "%s: data is NULL", name);
+    if (!type_supported(t.type))
+        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "%s: unsupported ggml type %d", name, t.type);
+    if (t.ne[0] != ne0 || t.ne[1] != ne1 || (ne2 > 0 && t.ne[2] != ne2) ||
+        (ne2 <= 0 && t.ne[2] > 1) || t.ne[3] > 1)
+        return set_err(ctx, DMOE_ERR_SHAPE,
+                       "%s: ne = [%lld,%lld,%lld,%lld], expected [%lld,%lld,%lld]", name,
+                       (long long)t.ne[0], (long long)t.ne[1], (long long)t.ne[2],
+                       (long long)t.ne[3], (long long)ne0, (long long)ne1, (long long)ne2);
+    if (ne0 % block_elems(t.type))
+        return set_err(ctx, DMOE_ERR_SHAPE, "%s: ne0 = %lld is not a multiple of %lld", name,
+                       (long long)ne0, (long long)block_elems(t.type));
+    const size_t rb = row_bytes(t.type, ne0);
+    if (t.nb[1] < rb) return set_err(ctx, DMOE_ERR_SHAPE, "%s: nb[1] below the row size", name);
+    if (ne2 > 0 && t.nb[2] < t.nb[1] * (size_t)ne1)
+        return set_err(ctx, DMOE_ERR_SHAPE, "%s: nb[2] below nb[1]*ne[1]", name);
+    if (device_mode) {
+        // the kernels load 16-byte units (2-byte for Q8_0 blocks)
+        const size_t al = t.type == DMOE_TYPE_Q8_0 ? 2 : 16;
+        if ((uintptr_t)t.data % al || t.nb[1] % al || (ne2 > 0 && t.nb[2] % al))
+            return set_err(ctx, DMOE_ERR_SHAPE, "%s: device data/strides not %zu-byte aligned",
+                           name, al);
+    }
+    return DMOE_OK;
+}
+
+int validate(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_layer_desc *d, bool device_mode)
+{
+    if (!hp || !d) return set_err(ctx, DMOE_ERR_INVALID_ARG, "hparams / desc is NULL");
+    const int H = hp->n_embd, E = hp->n_experts, K = hp->top_k, FF = hp->moe_ff;
+    if (H <= 0 || H % 256)
+        return set_err(ctx, DMOE_ERR_SHAPE, "n_embd = %d must be a positive multiple of 256", H);
+    if (E <= 0 || E > 1024) return set_err(ctx, DMOE_ERR_SHAPE, "n_experts = %d outside 1..1024", E);
+    if (K <= 0 || K > 32 || K > E)
+        return set_err(ctx, DMOE_ERR_SHAPE, "top_k = %d outside 1..min(32, n_experts)", K);
+    if (FF <= 0) return set_err(ctx, DMOE_ERR_SHAPE, "moe_ff = %d", FF);
+    if (hp->block_size < 0 || hp->capacity < 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "negative block_size / capacity");
+    if (hp->block_size > 1 && hp->capacity > 0 && hp->capacity < E && hp->block_size > 4096)
+        return set_err(ctx, DMOE_ERR_SHAPE, "block_size = %d above 4096", hp->block_size);
+
+    const dmoe_tensor &gw = d->gate_w;
+    if (!gw.data) return set_err(ctx, DMOE_ERR_INVALID_ARG, "gate_w: data is NULL");
+    if (gw.type != DMOE_TYPE_F32 && !(gw.type == DMOE_TYPE_F16 && !device_mode))
+        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "gate_w: type %d (F32%s expected)", gw.type,
+                       device_mode ? "" : " or F16");
+    if (gw.ne[0] != H || gw.ne[1] != E)
+        return set_err(ctx, DMOE_ERR_SHAPE, "gate_w: ne = [%lld,%lld], expected [%d,%d]",
+                       (long long)gw.ne[0], (long long)gw.ne[1], H, E);
+    if (gw.nb[1] < row_bytes(gw.type, H))
+        return set_err(ctx, DMOE_ERR_SHAPE, "gate_w: nb[1] below the row size");
+    if (device_mode && ((uintptr_t)gw.data % 16 || gw.nb[1] != (size_t)H * 4))
+        return set_err(ctx, DMOE_ERR_SHAPE, "gate_w: device router must be contiguous, 16-byte aligned");
+    if (d->gate_bias.data) {
+        if (d->gate_bias.type != DMOE_TYPE_F32)
+            return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "gate_bias: type %d (F32 expected)",
+                           d->gate_bias.type);
+        if (d->gate_bias.ne[0] != E)
+            return set_err(ctx, DMOE_ERR_SHAPE, "gate_bias: ne0 = %lld, expected %d",
+                           (long long)d->gate_bias.ne[0], E);
+    }
+    int rc;
+    if ((rc = check_tensor(ctx, "exp_gate", d->exp_gate, H, FF, E, device_mode))) return rc;
+    if ((rc = check_tensor(ctx, "exp_up", d->exp_up, H, FF, E, device_mode))) return rc;
+    if ((rc = check_tensor(ctx, "exp_down", d->exp_down, FF, H, E, device_mode))) return rc;
+    if (d->exp_up.type != d->exp_gate.type || d->exp_down.type != d->exp_gate.type)
+        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "routed expert tensors differ in type");
+    if (hp->n_shared > 0 && d->sh_gate.data) {
+        const int SF = hp->shared_ff;
+        if (SF <= 0) return set_err(ctx, DMOE_ERR_SHAPE, "shared_ff = %d", SF);
+        if ((rc = check_tensor(ctx, "sh_gate", d->sh_gate, H, SF, 0, device_mode))) return rc;
+        if ((rc = check_tensor(ctx, "sh_up", d->sh_up, H, SF, 0, device_mode))) return rc;
+        if ((rc = check_tensor(ctx, "sh_down", d->sh_down, SF, H, 0, device_mode))) return rc;
+        if (d->sh_up.type != d->sh_gate.type || d->sh_down.type != d->sh_gate.type)
+            return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "shared expert tensors differ in type");
+    }
+    return DMOE_OK;
+}
+
+float f16_to_f32_host(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t u;
+    if (e == 0) {
+        float v = (float)m * 5.9604644775390625e-08f;
+        memcpy(&u, &v, 4);
+        u |= sign;
+    } else if (e == 31) {
+        u = sign | 0x7f800000u | (m << 13);
+    } else {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+// Copy one (possibly strided) host tensor into a compact device buffer.
+int upload_tensor(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_tensor &t, int64_t nrows,
+                  int64_t nmats, WTensor &out)
+{
+    const size_t rb = row_bytes(t.type, t.ne[0]);
+    const size_t bytes = rb * (size_t)nrows * (size_t)nmats;
+    void *dev = nullptr;
+    HIP_TRY(ctx, hipMalloc(&dev, bytes));
+    L->owned.push_back(dev);
+    const uint8_t *src = (const uint8_t *)t.data;
+    if (t.nb[1] == rb && (nmats == 1 || t.nb[2] == rb * (size_t)nrows)) {
+        HIP_TRY(ctx, hipMemcpy(dev, src, bytes, hipMemcpyHostToDevice));
+    } else {
+        HIP_TRY(ctx, hipMemcpy2D(dev, rb, src, t.nb[1], rb, (size_t)nrows, hipMemcpyHostToDevice));
+        for (int64_t m = 1; m < nmats; m++)
+            HIP_TRY(ctx, hipMemcpy2D((uint8_t *)dev + (size_t)m * rb * nrows, rb,
+                                     src + (size_t)m * t.nb[2], t.nb[1], rb, (size_t)nrows,
+                                     hipMemcpyHostToDevice));
+    }
+    out.type = t.type;
+    out.data = (const uint8_t *)dev;
+    out.nb1 = rb;
+    out.nb2 = rb * (size_t)nrows;
+    return DMOE_OK;
+}
+
+WTensor wrap_tensor(const dmoe_tensor &t)
+{
+    WTensor w;
+    w.type = t.type;
+    w.data = (const uint8_t *)t.data;
+    w.nb1 = t.nb[1];
+    w.nb2 = t.nb[2];
+    return w;
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Workspace carve-up for one forward of N tokens.
+struct Workspace {
+    float *x, *y;
+    RouteBufs rb;
+    ActBuf xq, hq;
+    float *h, *ye, *hs, *ys;
+    float *bias;
+};
+
+size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, bool shared, int N, uint8_t *base,
+                      Workspace *w)
+{
+    const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
+    const int SF = shared ? hp.shared_ff : 0;
+    const int P = N * K;
+    const int B = hp.block_size > 0 ? (N + hp.block_size - 1) / hp.block_size : 1;
+    const int32_t at = act_type_of(wtype);
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> uint8_t * {
+        uint8_t *p = base ? base + off : nullptr;
+        off += align_up(bytes > 0 ? bytes : 1);
+        return p;
+    };
+    Workspace t{};
+    t.x = (float *)take((size_t)N * H * 4);
+    t.y = (float *)take((size_t)N * H * 4);
+    t.bias = (float *)take((size_t)E * 4);
+    t.rb.logits = (float *)take((size_t)N * E * 4);
+    t.rb.probs = (float *)take((size_t)N * E * 4);
+    t.rb.bmax = (float *)take((size_t)B * E * 4);
+    t.rb.thr = (float *)take((size_t)B * 4);
+    t.rb.allowed = (uint8_t *)take((size_t)B * E);
+    t.rb.idx = (int32_t *)take((size_t)P * 4);
+    t.rb.weights = (float *)take((size_t)P * 4);
+    t.rb.counts = (int32_t *)take((size_t)E * 4);
+    t.rb.offsets = (int32_t *)take((size_t)(E + 1) * 4);
+    t.rb.perm = (int32_t *)take((size_t)P * 4);
+    t.xq.type = at;
+    t.xq.n = H;
+    t.xq.vals = take((size_t)N * act_row_vals_bytes(at, H));
+    t.xq.d = (float *)take((size_t)N * (H / 32) * 4);
+    t.xq.bsums = (int16_t *)take((size_t)N * (H / 16) * 2);
+    t.h = (float *)take((size_t)P * FF * 4);
+    t.hq.type = at;
+    t.hq.n = FF;
+    t.hq.vals = take((size_t)P * act_row_vals_bytes(at, FF));
+    t.hq.d = (float *)take((size_t)P * (FF / 32 + 1) * 4);
+    t.hq.bsums = (int16_t *)take((size_t)P * (FF / 16 + 1) * 2);
+    t.ye = (float *)take((size_t)P * H * 4);
+    t.hs = (float *)take((size_t)N * (SF > 0 ? SF : 1) * 4);
+    t.ys = (float *)take((size_t)N * H * 4);
+    if (w) *w = t;
+    return off;
+}
+
+int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, Workspace *w)
+{
+    const size_t need = plan_workspace(L->hp, L->eg.type, L->has_shared, N, nullptr, nullptr);
+    if (need > ctx->ws_bytes) {
+        if (ctx->ws) {
+            // work queued on any stream may still read the old workspace
+            HIP_TRY(ctx, hipDeviceSynchronize());
+            HIP_TRY(ctx, hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        if (getenv("DMOE_FAIL_ALLOC"))
+            return set_err(ctx, DMOE_ERR_OOM, "workspace allocation of %zu bytes refused (DMOE_FAIL_ALLOC)", need);
+        HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
+        ctx->ws_bytes = need;
+    }
+    plan_workspace(L->hp, L->eg.type, L->has_shared, N, (uint8_t *)ctx->ws, w);
+    return DMOE_OK;
+}
+
+RouteParams route_params(const dmoe_hparams &hp, int N)
+{
+    RouteParams rp;
+    rp.n_tokens = N;
+    rp.n_experts = hp.n_experts;
+    rp.top_k = hp.top_k;
+    rp.capacity = hp.capacity;
+    rp.block_size = hp.block_size;
+    // src/diffuse-moe-graph.cpp:215-216
+    rp.use_block = hp.block_size > 1 && hp.capacity > 0 && hp.capacity < hp.n_experts &&
+                   N % hp.block_size == 0;
+    rp.norm_topk_prob = hp.norm_topk_prob;
+    rp.routed_scaling = hp.routed_scaling;
+    return rp;
+}
+
+const char *const kStageNames[DMOE_N_STAGES] = {
+    "router_logits", "route", "dispatch", "act_quant_x", "gateup_routed",
+    "act_quant_h", "down_routed", "gateup_shared", "down_shared", "combine"};
+
+enum { ST_LOGITS, ST_ROUTE, ST_DISPATCH, ST_ACTQ_X, ST_GATEUP, ST_ACTQ_H, ST_DOWN, ST_SH_GATEUP,
+       ST_SH_DOWN, ST_COMBINE };
+
+hipEvent_t take_event(dmoe_ctx *ctx)
+{
+    if (!ctx->pool.empty()) {
+        hipEvent_t e = ctx->pool.back();
+        ctx->pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Runs one stage; with profiling on, brackets it with an event pair.
+template <class F>
+hipError_t stage(dmoe_ctx *ctx, int id, hipStream_t s, F &&launch)
+{
+    if (!ctx->prof) return launch();
+    hipEvent_t a = take_event(ctx), b = take_event(ctx);
+    if (!a || !b) return hipErrorOutOfMemory;
+    hipError_t e = hipEventRecord(a, s);
+    if (e == hipSuccess) e = launch();
+    if (e == hipSuccess) e = hipEventRecord(b, s);
+    ctx->marks.push_back({id, a, b});
+    return e;
+}
+
+#define LAUNCH_TRY(ctx, expr)                                                                      \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess)                                                                      \
+            return set_err((ctx), DMOE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));           \
+    } while (0)
+
+int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, const float *x,
+                    int N, float *y, hipStream_t s)
+{
+    const dmoe_hparams &hp = L->hp;
+    const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
+    const RouteParams rp = route_params(hp, N);
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, id, s, [&] { return call; }))
+    STAGE(ST_LOGITS, launch_router_logits(L->gate_w, x, N, H, E, w.rb.logits, s));
+    STAGE(ST_ROUTE, launch_route(rp, w.rb.logits, L->gate_bias, w.rb, s));
+    STAGE(ST_DISPATCH, launch_dispatch(rp, w.rb, s));
+    STAGE(ST_ACTQ_X, launch_act_quant(x, N, H, w.xq, s));
+    STAGE(ST_GATEUP, launch_gateup_routed(L->eg, L->eu, w.xq, rp, w.rb, FF, w.h, s));
+    STAGE(ST_ACTQ_H, launch_act_quant(w.h, N * K, FF, w.hq, s));
+    STAGE(ST_DOWN, launch_down_routed(L->ed, w.hq, rp, w.rb, H, w.ye, s));
+    if (L->has_shared) {
+        STAGE(ST_SH_GATEUP, launch_gateup_shared(L->sg, L->su, x, N, H, hp.shared_ff, w.hs, s));
+        STAGE(ST_SH_DOWN, launch_down_shared(L->sd, w.hs, N, hp.shared_ff, H, w.ys, s));
+    }
+    STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N, K,
+                                     H, y, s));
+#undef STAGE
+    return DMOE_OK;
+}
+
+int copy_debug(dmoe_ctx *ctx, const dmoe_hparams &hp, const Workspace &w, int N,
+               dmoe_debug *dbg, hipStream_t s)
+{
+    if (!dbg) return DMOE_OK;
+    const int E = hp.n_experts, K = hp.top_k, P = N * K;
+    const RouteParams rp = route_params(hp, N);
+    const int B = rp.use_block ? N / hp.block_size : 0;
+    auto cp = [&](void *dst, const void *src, size_t bytes) -> hipError_t {
+        if (!dst || bytes == 0) return hipSuccess;
+        return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
+    };
+    HIP_TRY(ctx, cp(dbg->logits, w.rb.logits, (size_t)N * E * 4));
+    HIP_TRY(ctx, cp(dbg->probs, w.rb.probs, (size_t)N * E * 4));
+    HIP_TRY(ctx, cp(dbg->bmax, w.rb.bmax, (size_t)B * E * 4));
+    HIP_TRY(ctx, cp(dbg->thr, w.rb.thr, (size_t)B * 4));
+    HIP_TRY(ctx, cp(dbg->allowed, w.rb.allowed, (size_t)B * E));
+    HIP_TRY(ctx, cp(dbg->idx, w.rb.idx, (size_t)P * 4));
+    HIP_TRY(ctx, cp(dbg->weights, w.rb.weights, (size_t)P * 4));
+    HIP_TRY(ctx, cp(dbg->counts, w.rb.counts, (size_t)E * 4));
+    HIP_TRY(ctx, cp(dbg->offsets, w.rb.offsets, (size_t)E * 4));
+    HIP_TRY(ctx, cp(dbg->perm, w.rb.perm, (size_t)P * 4));
+    if (dbg->use_block_routing) *dbg->use_block_routing = rp.use_block;
+    return DMOE_OK;
+}
+
+int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmoe_layer_desc *d)
+{
+    L->hp = *hp;
+    L->has_shared = hp->n_shared > 0 && d->sh_gate.data != nullptr;
+    if (!L->has_shared) L->hp.shared_ff = 0;
+    (void)ctx;
+    return DMOE_OK;
+}
+
+} // namespace
+
+// ===========================================================================
+extern "C" {
+
+int dmoe_create(int hip_device, dmoe_ctx **out)
+{
+    if (!out) return DMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || hip_device < 0 || hip_device >= n)
+        return DMOE_ERR_HIP;
+    dmoe_ctx *ctx = new (std::nothrow) dmoe_ctx();
+    if (!ctx) return DMOE_ERR_OOM;
+    ctx->device = hip_device;
+    if (hipSetDevice(hip_device) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return DMOE_ERR_HIP;
+    }
+    *out = ctx;
+    return DMOE_OK;
+}
+
+void dmoe_destroy(dmoe_ctx *ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    for (auto &m : ctx->marks) {
+        (void)hipEventDestroy(m.a);
+        (void)hipEventDestroy(m.b);
+    }
+    for (hipEvent_t e : ctx->pool) (void)hipEventDestroy(e);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char *dmoe_last_error(const dmoe_ctx *ctx)
+{
+    return ctx ? ctx->err.c_str() : "null context";
+}
+
+size_t dmoe_row_size(int32_t type, int64_t n)
+{
+    return n > 0 ? row_bytes(type, n) : 0;
+}
+
+int dmoe_layer_upload(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_layer_desc *d,
+                      dmoe_layer **out)
+{
+    if (!ctx || !out) return DMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = validate(ctx, hp, d, false);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    dmoe_layer *L = new (std::nothrow) dmoe_layer();
+    if (!L) return set_err(ctx, DMOE_ERR_OOM, "host allocation failed");
+    L->ctx = ctx;
+    const int H = hp->n_embd, E = hp->n_experts, FF = hp->moe_ff;
+    auto fail = [&](int code) {
+        dmoe_layer_free(L);
+        return code;
+    };
+    // router -> f32 [E][H]  (ensure_f32_moe, diffuse-moe-graph.cpp:8-12, :203)
+    {
+        std::vector<float> w((size_t)E * H);
+        const dmoe_tensor &gw = d->gate_w;
+        for (int e = 0; e < E; e++) {
+            const uint8_t *row = (const uint8_t *)gw.data + (size_t)e * gw.nb[1];
+            if (gw.type == DMOE_TYPE_F32)
+                memcpy(&w[(size_t)e * H], row, (size_t)H * 4);
+            else
+                for (int k = 0; k < H; k++)
+                    w[(size_t)e * H + k] = f16_to_f32_host(((const uint16_t *)row)[k]);
+        }
+        void *dev = nullptr;
+        hipError_t he = hipMalloc(&dev, w.size() * 4);
+        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_OOM, "hipMalloc router: %s", hipGetErrorString(he)));
+        L->owned.push_back(dev);
+        he = hipMemcpy(dev, w.data(), w.size() * 4, hipMemcpyHostToDevice);
+        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_HIP, "router copy: %s", hipGetErrorString(he)));
+        L->gate_w = (float *)dev;
+    }
+    if (d->gate_bias.data) {
+        void *dev = nullptr;
+        hipError_t he = hipMalloc(&dev, (size_t)E * 4);
+        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_OOM, "hipMalloc bias: %s", hipGetErrorString(he)));
+        L->owned.push_back(dev);
+        he = hipMemcpy(dev, d->gate_bias.data, (size_t)E * 4, hipMemcpyHostToDevice);
+        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_HIP, "bias copy: %s", hipGetErrorString(he)));
+        L->gate_bias = (float *)dev;
+    }
+    if ((rc = upload_tensor(ctx, L, d->exp_gate, FF, E, L->eg))) return fail(rc);
+    if ((rc = upload_tensor(ctx, L, d->exp_up, FF, E, L->eu))) return fail(rc);
+    if ((rc = upload_tensor(ctx, L, d->exp_down, H, E, L->ed))) return fail(rc);
+    if (hp->n_shared > 0 && d->sh_gate.data) {
+        if ((rc = upload_tensor(ctx, L, d->sh_gate, hp->shared_ff, 1, L->sg))) return fail(rc);
+        if ((rc = upload_tensor(ctx, L, d->sh_up, hp->shared_ff, 1, L->su))) return fail(rc);
+        if ((rc = upload_tensor(ctx, L, d->sh_down, H, 1, L->sd))) return fail(rc);
+    }
+    finish_layer(ctx, L, hp, d);
+    *out = L;
+    return DMOE_OK;
+}
+
+int dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_layer_desc *d,
+                           dmoe_layer **out)
+{
+    if (!ctx || !out) return DMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = validate(ctx, hp, d, true);
+    if (rc) return rc;
+    dmoe_layer *L = new (std::nothrow) dmoe_layer();
+    if (!L) return set_err(ctx, DMOE_ERR_OOM, "host allocation failed");
+    L->ctx = ctx;
+    L->gate_w = (float *)d->gate_w.data;
+    L->gate_bias = (float *)d->gate_bias.data;
+    L->eg = wrap_tensor(d->exp_gate);
+    L->eu = wrap_tensor(d->exp_up);
+    L->ed = wrap_tensor(d->exp_down);
+    if (hp->n_shared > 0 && d->sh_gate.data) {
+        L->sg = wrap_tensor(d->sh_gate);
+        L->su = wrap_tensor(d->sh_up);
+        L->sd = wrap_tensor(d->sh_down);
+    }
+    finish_layer(ctx, L, hp, d);
+    *out = L;
+    return DMOE_OK;
+}
+
+void dmoe_layer_free(dmoe_layer *L)
+{
+    if (!L) return;
+    if (L->ctx) (void)hipSetDevice(L->ctx->device);
+    for (void *p : L->owned) (void)hipFree(p);
+    delete L;
+}
+
+int dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *x, int32_t n_tokens,
+                       float *y, dmoe_debug *dbg)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!L || !x || !y || n_tokens <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
+    const int H = L->hp.n_embd;
+    for (size_t i = 0; i < (size_t)n_tokens * H; i++)
+        if (!std::isfinite(x[i]))
+            return set_err(ctx, DMOE_ERR_NONFINITE, "x[%zu] = %g is not finite", i, (double)x[i]);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    Workspace w;
+    int rc = ensure_workspace(ctx, L, n_tokens, &w);
+    if (rc) return rc;
+    hipStream_t s = ctx->stream;
+    HIP_TRY(ctx, hipMemcpyAsync(w.x, x, (size_t)n_tokens * H * 4, hipMemcpyHostToDevice, s));
+    if ((rc = enqueue_forward(ctx, L, w, w.x, n_tokens, w.y, s))) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(y, w.y, (size_t)n_tokens * H * 4, hipMemcpyDeviceToHost, s));
+    if ((rc = copy_debug(ctx, L->hp, w, n_tokens, dbg, s))) return rc;
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return DMOE_OK;
+}
+
+int dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *x_dev,
+                              int32_t n_tokens, float *y_dev, void *stream)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!L || !x_dev || !y_dev || n_tokens <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
+    if ((uintptr_t)x_dev % 16)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "x_dev must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    Workspace w;
+    int rc = ensure_workspace(ctx, L, n_tokens, &w);
+    if (rc) return rc;
+    return enqueue_forward(ctx, L, w, x_dev, n_tokens, y_dev, (hipStream_t)stream);
+}
+
+int dmoe_route_logits(dmoe_ctx *ctx, const dmoe_hparams *hp, const float *bias,
+                      const float *logits, int32_t n_tokens, dmoe_debug *dbg)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!hp || !logits || n_tokens <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "hparams/logits NULL or n_tokens = %d", n_tokens);
+    const int E = hp->n_experts, K = hp->top_k;
+    if (E <= 0 || E > 1024) return set_err(ctx, DMOE_ERR_SHAPE, "n_experts = %d outside 1..1024", E);
+    if (K <= 0 || K > 32 || K > E)
+        return set_err(ctx, DMOE_ERR_SHAPE, "top_k = %d outside 1..min(32, n_experts)", K);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    // a routing-only pseudo layer: smallest valid sizes for the expert buffers
+    dmoe_layer L;
+    L.hp = *hp;
+    L.hp.n_embd = 256;
+    L.hp.moe_ff = 32;
+    L.eg.type = DMOE_TYPE_F32;
+    Workspace w;
+    int rc = ensure_workspace(ctx, &L, n_tokens, &w);
+    if (rc) return rc;
+    hipStream_t s = ctx->stream;
+    HIP_TRY(ctx, hipMemcpyAsync(w.rb.logits, logits, (size_t)n_tokens * E * 4,
+                                hipMemcpyHostToDevice, s));
+    const float *dbias = nullptr;
+    if (bias) {
+        HIP_TRY(ctx, hipMemcpyAsync(w.bias, bias, (size_t)E * 4, hipMemcpyHostToDevice, s));
+        dbias = w.bias;
+    }
+    const RouteParams rp = route_params(*hp, n_tokens);
+    LAUNCH_TRY(ctx, launch_route(rp, w.rb.logits, dbias, w.rb, s));
+    LAUNCH_TRY(ctx, launch_dispatch(rp, w.rb, s));
+    dmoe_debug d2 = dbg ? *dbg : dmoe_debug{};
+    d2.logits = nullptr;
+    if ((rc = copy_debug(ctx, *hp, w, n_tokens, &d2, s))) return rc;
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return DMOE_OK;
+}
+
+int dmoe_quantize_device(dmoe_ctx *ctx, int32_t type, const float *src_dev, void *dst_dev,
+                         int64_t nrows, int64_t n_per_row, void *stream)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!src_dev || !dst_dev || nrows <= 0 || n_per_row <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "quantize: NULL pointer or empty shape");
+    if (!type_supported(type))
+        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "quantize: unsupported type %d", type);
+    if (row_bytes(type, n_per_row) == 0)
+        return set_err(ctx, DMOE_ERR_SHAPE, "quantize: n_per_row = %lld not a block multiple",
+                       (long long)n_per_row);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    LAUNCH_TRY(ctx, launch_quantize_weights(type, src_dev, dst_dev, nrows, n_per_row,
+                                            (hipStream_t)stream));
+    return DMOE_OK;
+}
+
+int dmoe_profile_enable(dmoe_ctx *ctx, int enable)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    ctx->prof = enable != 0;
+    return DMOE_OK;
+}
+
+int dmoe_profile_read(dmoe_ctx *ctx, float *total_ms, int32_t *calls)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (total_ms) for (int i = 0; i < DMOE_N_STAGES; i++) total_ms[i] = 0.0f;
+    if (calls) for (int i = 0; i < DMOE_N_STAGES; i++) calls[i] = 0;
+    int rc = DMOE_OK;
+    for (auto &m : ctx->marks) {
+        float ms = 0.0f;
+        hipError_t e = hipEventSynchronize(m.b);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, m.a, m.b);
+        if (e != hipSuccess && rc == DMOE_OK)
+            rc = set_err(ctx, DMOE_ERR_HIP, "profile event: %s", hipGetErrorString(e));
+        if (total_ms) total_ms[m.stage] += ms;
+        if (calls) calls[m.stage] += 1;
+        ctx->pool.push_back(m.a);
+        ctx->pool.push_back(m.b);
+    }
+    ctx->marks.clear();
+    return rc;
+}
+
+const char *dmoe_stage_name(int stage)
+{
+    return (stage >= 0 && stage < DMOE_N_STAGES) ? kStageNames[stage] : "";
+}
+
+} // extern "C"

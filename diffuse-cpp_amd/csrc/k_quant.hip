@@ -1,0 +1,279 @@
+// k_quant.hip — quantisation kernels.
+//
+//  * activation conversion to the weight's vec_dot_type before the expert
+//    products, as ggml_mul_mat_id does on the CPU (the reference's expert
+//    products, src/diffuse-moe-graph.cpp:266-269):
+//      Q4_K weights -> Q8_K activations, Q8_0 -> Q8_0, F16 -> F16, F32 -> F32
+//  * weight quantisation into GGUF blocks (counterpart of quantize_to_type,
+//    tools/quant_lib.c:16-27), used to build synthetic expert tensors in HBM.
+#include "dmoe_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace dmoe {
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)f);   // round to nearest even
+}
+
+// round half to even for |v| < 2^22
+__device__ __forceinline__ int nearest_int(float v)
+{
+    const float t = v + 12582912.0f;
+    return (int)(__float_as_uint(t) & 0x007fffffu) - 0x00400000;
+}
+
+// ---------------------------------------------------------------------------
+// Q8_K: one wavefront per 256-value super-block; lane l holds values l,
+// l+64, l+128, l+192.  The value of largest magnitude (lowest index on ties)
+// maps to -127: iscale = -127/max, q = min(127, nearest(iscale*x)),
+// d = 1/iscale, bsums = sums of 16 consecutive q.
+__global__ __launch_bounds__(256) void k_act_q8K(const float *__restrict__ src, int rows, int n,
+                                                 int8_t *__restrict__ qs, float *__restrict__ dq,
+                                                 int16_t *__restrict__ bsums)
+{
+    const int lane = threadIdx.x & 63;
+    const int nsb = n / 256;
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= rows * nsb) return;
+    const int row = wid / nsb, sb = wid % nsb;
+    const float *x = src + (size_t)row * n + sb * 256;
+
+    float v[4];
+    float amax = -1.0f;
+    int aidx = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        v[c] = x[lane + 64 * c];
+        const float a = fabsf(v[c]);
+        if (a > amax) { amax = a; aidx = lane + 64 * c; }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float oa = __shfl_xor(amax, m, 64);
+        const int oi = __shfl_xor(aidx, m, 64);
+        if (oa > amax || (oa == amax && oi < aidx)) { amax = oa; aidx = oi; }
+    }
+    int8_t *q = qs + (size_t)row * n + sb * 256;
+    int16_t *bs = bsums + (size_t)row * (n / 16) + sb * 16;
+    if (amax == 0.0f) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[lane + 64 * c] = 0;
+        if (lane < 16) bs[lane] = 0;
+        if (lane == 0) dq[(size_t)row * nsb + sb] = 0.0f;
+        return;
+    }
+    const float vmax = x[aidx];
+    const float iscale = -127.0f / vmax;
+    int qi[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int t = nearest_int(iscale * v[c]);
+        qi[c] = t < 127 ? t : 127;
+        q[lane + 64 * c] = (int8_t)qi[c];
+    }
+    // group g = 16 consecutive values = lanes 16*(g%4)..+15 of register g/4
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        int s = qi[c];
+        s += __shfl_xor(s, 8, 64);
+        s += __shfl_xor(s, 4, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 1, 64);
+        if ((lane & 15) == 0) bs[4 * c + (lane >> 4)] = (int16_t)s;
+    }
+    if (lane == 0) dq[(size_t)row * nsb + sb] = 1.0f / iscale;
+}
+
+// Q8_0: lane = value; 32-lane halves are independent blocks.
+// d = amax/127, q = roundf(x/d) (half away from zero), d kept as its fp16 value.
+__global__ __launch_bounds__(256) void k_act_q8_0(const float *__restrict__ src, int rows, int n,
+                                                  int8_t *__restrict__ qs, float *__restrict__ dq)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)rows * n) return;     // n % 32 == 0: whole blocks exit together
+    const float v = src[i];
+    float amax = fabsf(v);
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    qs[i] = (int8_t)roundf(v * id);
+    if ((threadIdx.x & 31) == 0) dq[i / 32] = f16_bits_to_f32(f32_to_f16_bits(d));
+}
+
+__global__ __launch_bounds__(256) void k_act_f16(const float *__restrict__ src, size_t total,
+                                                 uint16_t *__restrict__ dst)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < total) dst[i] = f32_to_f16_bits(src[i]);
+}
+
+__global__ __launch_bounds__(256) void k_copy_f32(const float *__restrict__ src, size_t total,
+                                                  float *__restrict__ dst)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < total) dst[i] = src[i];
+}
+
+hipError_t launch_act_quant(const float *src, int rows, int n, const ActBuf &dst, hipStream_t s)
+{
+    const size_t total = (size_t)rows * n;
+    switch (dst.type) {
+    case DMOE_ACT_Q8_K: {
+        const int waves = rows * (n / 256);
+        hipLaunchKernelGGL(k_act_q8K, dim3((waves + 3) / 4), dim3(256), 0, s, src, rows, n,
+                           (int8_t *)dst.vals, dst.d, dst.bsums);
+        break;
+    }
+    case DMOE_TYPE_Q8_0:
+        hipLaunchKernelGGL(k_act_q8_0, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           src, rows, n, (int8_t *)dst.vals, dst.d);
+        break;
+    case DMOE_TYPE_F16:
+        hipLaunchKernelGGL(k_act_f16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           src, total, (uint16_t *)dst.vals);
+        break;
+    case DMOE_TYPE_F32:
+        hipLaunchKernelGGL(k_copy_f32, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           src, total, (float *)dst.vals);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Weight quantisers: one thread per block.
+//   Q8_0: as the activation quantiser above.
+//   Q4_K: min/max per 32-value sub-block (a plain quantiser, not ggml's
+//         iterative one): scale_j = (max - min')/15, min' = min(min, 0),
+//         d = max scale / 63, dmin = max(-min') / 63 (both as fp16),
+//         6-bit sc_j, m_j by nearest rounding, q = nearest((x + dmin*m_j) /
+//         (d*sc_j)) clamped to 0..15, packed in the GGUF Q4_K layout.
+__global__ __launch_bounds__(256) void k_wq_q8_0(const float *__restrict__ src, int64_t nblk,
+                                                 uint8_t *__restrict__ dst)
+{
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblk) return;
+    const float *x = src + b * 32;
+    uint8_t *y = dst + b * 34;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = f32_to_f16_bits(d);
+    y[0] = (uint8_t)(dh & 0xff);
+    y[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < 32; j++) y[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
+}
+
+__global__ __launch_bounds__(256) void k_wq_q4K(const float *__restrict__ src, int64_t nblk,
+                                                uint8_t *__restrict__ dst)
+{
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblk) return;
+    const float *x = src + b * 256;
+    uint8_t *y = dst + b * 144;
+    float scale[8], mn[8];
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        float lo = x[32 * j], hi = x[32 * j];
+        for (int l = 1; l < 32; l++) {
+            const float v = x[32 * j + l];
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
+        }
+        if (lo > 0.0f) lo = 0.0f;
+        scale[j] = (hi - lo) / 15.0f;
+        mn[j] = -lo;
+        if (scale[j] > max_scale) max_scale = scale[j];
+        if (mn[j] > max_min) max_min = mn[j];
+    }
+    const uint16_t dh = f32_to_f16_bits(max_scale / 63.0f);
+    const uint16_t mh = f32_to_f16_bits(max_min / 63.0f);
+    const float d = f16_bits_to_f32(dh), dmin = f16_bits_to_f32(mh);
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    const float imin = dmin > 0.0f ? 1.0f / dmin : 0.0f;
+    uint8_t sc[8], m[8];
+    for (int j = 0; j < 8; j++) {
+        const int a = nearest_int(scale[j] * id);
+        const int c = nearest_int(mn[j] * imin);
+        sc[j] = (uint8_t)(a < 0 ? 0 : a > 63 ? 63 : a);
+        m[j] = (uint8_t)(c < 0 ? 0 : c > 63 ? 63 : c);
+    }
+    uint8_t scales[12];
+    for (int j = 0; j < 4; j++) {
+        scales[j] = sc[j];
+        scales[j + 4] = m[j];
+    }
+    for (int j = 4; j < 8; j++) {
+        scales[j + 4] = (uint8_t)((sc[j] & 0x0f) | ((m[j] & 0x0f) << 4));
+        scales[j - 4] |= (uint8_t)((sc[j] >> 4) << 6);
+        scales[j] |= (uint8_t)((m[j] >> 4) << 6);
+    }
+    y[0] = (uint8_t)(dh & 0xff);
+    y[1] = (uint8_t)(dh >> 8);
+    y[2] = (uint8_t)(mh & 0xff);
+    y[3] = (uint8_t)(mh >> 8);
+    for (int j = 0; j < 12; j++) y[4 + j] = scales[j];
+    for (int c = 0; c < 4; c++) {
+        const float ed0 = d * (float)sc[2 * c], em0 = dmin * (float)m[2 * c];
+        const float ed1 = d * (float)sc[2 * c + 1], em1 = dmin * (float)m[2 * c + 1];
+        for (int l = 0; l < 32; l++) {
+            int q0 = 0, q1 = 0;
+            if (ed0 > 0.0f) q0 = nearest_int((x[64 * c + l] + em0) / ed0);
+            if (ed1 > 0.0f) q1 = nearest_int((x[64 * c + 32 + l] + em1) / ed1);
+            q0 = q0 < 0 ? 0 : q0 > 15 ? 15 : q0;
+            q1 = q1 < 0 ? 0 : q1 > 15 ? 15 : q1;
+            y[16 + 32 * c + l] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_wq_f16(const float *__restrict__ src, int64_t total,
+                                                uint16_t *__restrict__ dst)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < total) dst[i] = f32_to_f16_bits(src[i]);
+}
+
+hipError_t launch_quantize_weights(int32_t type, const float *src, void *dst, int64_t nrows,
+                                   int64_t n_per_row, hipStream_t s)
+{
+    const int64_t total = nrows * n_per_row;
+    switch (type) {
+    case DMOE_TYPE_Q4_K: {
+        const int64_t nblk = total / 256;
+        hipLaunchKernelGGL(k_wq_q4K, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, src,
+                           nblk, (uint8_t *)dst);
+        break;
+    }
+    case DMOE_TYPE_Q8_0: {
+        const int64_t nblk = total / 32;
+        hipLaunchKernelGGL(k_wq_q8_0, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, src,
+                           nblk, (uint8_t *)dst);
+        break;
+    }
+    case DMOE_TYPE_F16:
+        hipLaunchKernelGGL(k_wq_f16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
+                           total, (uint16_t *)dst);
+        break;
+    case DMOE_TYPE_F32:
+        hipLaunchKernelGGL(k_copy_f32, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
+                           (size_t)total, (float *)dst);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+} // namespace dmoe

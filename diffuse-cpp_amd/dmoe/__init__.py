@@ -1,0 +1,341 @@
+"""Host-side Python mirror of the dmoe C ABI (include/dmoe.h).
+
+The MoE segment of src/diffuse-moe-graph.cpp:188-289 runs in libdmoe.so (HIP
+kernels for gfx950); this module only marshals pointers and shapes through
+ctypes.  There is no Python or CPU compute path: if the library is missing
+the import of the entry points fails loudly.
+
+    ctx = dmoe.Context(0)
+    layer = ctx.upload(weights)              # weights: LayerWeights (host)
+    y, dbg = ctx.forward(layer, x, debug=True)
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+from ._abi import (Debug, HParams, LayerDesc, Tensor, TYPE_F16, TYPE_F32, TYPE_Q4_K,
+                   TYPE_Q8_0, TYPE_Q8_K, TYPE_NAMES, TYPE_BY_NAME, row_size, block_elems,
+                   block_bytes)
+from . import _abi
+
+PKG_DIR = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG_DIR / "libdmoe.so"
+
+EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload",
+           "dmoe_layer_wrap_device", "dmoe_layer_free", "dmoe_layer_forward",
+           "dmoe_layer_forward_device", "dmoe_route_logits", "dmoe_row_size",
+           "dmoe_quantize_device", "dmoe_profile_enable", "dmoe_profile_read",
+           "dmoe_stage_name")
+N_STAGES = 10
+
+
+class DmoeError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"dmoe error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load libdmoe.so (built in-tree by diffuse-cpp_amd/build.py)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise FileNotFoundError(f"{LIB_PATH} is not built; run diffuse-cpp_amd/build.py")
+    # torch wheels ship their own HIP runtime (same soname libamdhip64.so.7 as
+    # /opt/rocm's).  Loading torch first lets libdmoe bind to that already
+    # loaded runtime; the other order would put two HIP/HSA runtimes in one
+    # process and the second cannot open the device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = C.CDLL(str(LIB_PATH))
+    P = C.c_void_p
+    lib.dmoe_create.argtypes = [C.c_int, C.POINTER(P)]
+    lib.dmoe_destroy.argtypes = [P]
+    lib.dmoe_destroy.restype = None
+    lib.dmoe_last_error.argtypes = [P]
+    lib.dmoe_last_error.restype = C.c_char_p
+    lib.dmoe_layer_upload.argtypes = [P, C.POINTER(HParams), C.POINTER(LayerDesc), C.POINTER(P)]
+    lib.dmoe_layer_wrap_device.argtypes = [P, C.POINTER(HParams), C.POINTER(LayerDesc),
+                                           C.POINTER(P)]
+    lib.dmoe_layer_free.argtypes = [P]
+    lib.dmoe_layer_free.restype = None
+    lib.dmoe_layer_forward.argtypes = [P, P, P, C.c_int32, P, C.POINTER(Debug)]
+    lib.dmoe_layer_forward_device.argtypes = [P, P, P, C.c_int32, P, P]
+    lib.dmoe_route_logits.argtypes = [P, C.POINTER(HParams), P, P, C.c_int32, C.POINTER(Debug)]
+    lib.dmoe_row_size.argtypes = [C.c_int32, C.c_int64]
+    lib.dmoe_row_size.restype = C.c_size_t
+    lib.dmoe_quantize_device.argtypes = [P, C.c_int32, P, P, C.c_int64, C.c_int64, P]
+    lib.dmoe_profile_enable.argtypes = [P, C.c_int]
+    lib.dmoe_profile_read.argtypes = [P, P, P]
+    lib.dmoe_stage_name.argtypes = [C.c_int]
+    lib.dmoe_stage_name.restype = C.c_char_p
+    _lib = lib
+    return lib
+
+
+def _ptr(a) -> int:
+    if a is None:
+        return 0
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return int(a.data_ptr())          # torch tensor
+
+
+def tensor_view(ttype: int, data, ne, nb=None) -> Tensor:
+    """dmoe_tensor for a contiguous tensor with ggml ne (ne[0] innermost)."""
+    ne = list(ne) + [1] * (4 - len(ne))
+    t = Tensor()
+    t.type = ttype
+    t.data = _ptr(data) or None
+    for i in range(4):
+        t.ne[i] = ne[i]
+    if nb is None:
+        shape = tuple(getattr(data, "shape", ()))
+        is_bytes = str(getattr(data, "dtype", "")).endswith("uint8")
+        # byte arrays carry their row size in the last dimension
+        rs = int(shape[-1]) if is_bytes and shape else row_size(ttype, ne[0])
+        b0 = block_bytes(ttype) if ttype in _abi.TYPE_NAMES else 1
+        nb = [b0, rs, rs * ne[1], rs * ne[1] * ne[2]]
+    for i in range(4):
+        t.nb[i] = nb[i]
+    return t
+
+
+@dataclass
+class LayerWeights:
+    """One layer's MoE tensors as GGUF block bytes.
+
+    Arrays are numpy (host) or torch (device) buffers:
+      gate_w    f32 [E, H]                    (ggml ne [H, E])
+      gate_bias f32 [E] or None
+      exp_gate, exp_up  u8 [E, FF, row_size(T, H)]   (ne [H, FF, E])
+      exp_down          u8 [E, H, row_size(T, FF)]   (ne [FF, H, E])
+      sh_gate, sh_up    u8 [SF, row_size(Ts, H)] or None
+      sh_down           u8 [H, row_size(Ts, SF)] or None
+    """
+    n_embd: int
+    n_experts: int
+    top_k: int
+    capacity: int
+    block_size: int
+    moe_ff: int
+    wtype: int
+    gate_w: object
+    exp_gate: object
+    exp_up: object
+    exp_down: object
+    gate_bias: object = None
+    n_shared: int = 0
+    shared_ff: int = 0
+    stype: int = TYPE_F32
+    sh_gate: object = None
+    sh_up: object = None
+    sh_down: object = None
+    norm_topk_prob: int = 1
+    routed_scaling: float = 2.5
+    extra: dict = field(default_factory=dict)
+
+    def hparams(self) -> HParams:
+        hp = HParams()
+        hp.n_embd, hp.n_experts, hp.top_k = self.n_embd, self.n_experts, self.top_k
+        hp.capacity, hp.block_size, hp.moe_ff = self.capacity, self.block_size, self.moe_ff
+        hp.n_shared = self.n_shared if self.sh_gate is not None else 0
+        hp.shared_ff = self.shared_ff
+        hp.norm_topk_prob, hp.routed_scaling = self.norm_topk_prob, self.routed_scaling
+        return hp
+
+    def desc(self) -> LayerDesc:
+        H, E, FF, SF = self.n_embd, self.n_experts, self.moe_ff, self.shared_ff
+        d = LayerDesc()
+        d.gate_w = tensor_view(TYPE_F32, self.gate_w, [H, E])
+        if self.gate_bias is not None:
+            d.gate_bias = tensor_view(TYPE_F32, self.gate_bias, [E])
+        d.exp_gate = tensor_view(self.wtype, self.exp_gate, [H, FF, E])
+        d.exp_up = tensor_view(self.wtype, self.exp_up, [H, FF, E])
+        d.exp_down = tensor_view(self.wtype, self.exp_down, [FF, H, E])
+        if self.sh_gate is not None:
+            d.sh_gate = tensor_view(self.stype, self.sh_gate, [H, SF])
+            d.sh_up = tensor_view(self.stype, self.sh_up, [H, SF])
+            d.sh_down = tensor_view(self.stype, self.sh_down, [SF, H])
+        return d
+
+    def expert_bytes(self) -> int:
+        """Bytes of gate+up+down of one routed expert."""
+        return (2 * self.moe_ff * row_size(self.wtype, self.n_embd)
+                + self.n_embd * row_size(self.wtype, self.moe_ff))
+
+    def shared_bytes(self) -> int:
+        if self.sh_gate is None:
+            return 0
+        return (2 * self.shared_ff * row_size(self.stype, self.n_embd)
+                + self.n_embd * row_size(self.stype, self.shared_ff))
+
+
+def hparams_of(n_embd, n_experts, top_k, capacity, block_size, moe_ff=1, n_shared=0,
+               shared_ff=0, norm_topk_prob=1, routed_scaling=2.5) -> HParams:
+    hp = HParams()
+    hp.n_embd, hp.n_experts, hp.top_k = n_embd, n_experts, top_k
+    hp.capacity, hp.block_size, hp.moe_ff = capacity, block_size, moe_ff
+    hp.n_shared, hp.shared_ff = n_shared, shared_ff
+    hp.norm_topk_prob, hp.routed_scaling = norm_topk_prob, routed_scaling
+    return hp
+
+
+def use_block_routing(hp: HParams, n_tokens: int) -> bool:
+    """src/diffuse-moe-graph.cpp:215-216"""
+    return (hp.block_size > 1 and hp.capacity > 0 and hp.capacity < hp.n_experts
+            and n_tokens % hp.block_size == 0)
+
+
+class DebugOut:
+    """Host buffers for dmoe_debug."""
+
+    def __init__(self, hp: HParams, n_tokens: int):
+        N, E, K = n_tokens, hp.n_experts, hp.top_k
+        B = N // hp.block_size if use_block_routing(hp, N) else 0
+        self.logits = np.zeros((N, E), np.float32)
+        self.probs = np.zeros((N, E), np.float32)
+        self.bmax = np.zeros((B, E), np.float32)
+        self.thr = np.zeros((B,), np.float32)
+        self.allowed = np.zeros((B, E), np.uint8)
+        self.idx = np.zeros((N, K), np.int32)
+        self.weights = np.zeros((N, K), np.float32)
+        self.counts = np.zeros((E,), np.int32)
+        self.offsets = np.zeros((E,), np.int32)
+        self.perm = np.zeros((N * K,), np.int32)
+        self.use_block = np.zeros((1,), np.int32)
+
+    def struct(self) -> Debug:
+        d = Debug()
+        for name in ("logits", "probs", "bmax", "thr", "allowed", "idx", "weights", "counts",
+                     "offsets", "perm"):
+            a = getattr(self, name)
+            setattr(d, name, a.ctypes.data if a.size else None)
+        d.use_block_routing = self.use_block.ctypes.data
+        return d
+
+    def as_dict(self) -> dict:
+        return {k: getattr(self, k) for k in ("logits", "probs", "bmax", "thr", "allowed", "idx",
+                                              "weights", "counts", "offsets", "perm")} | {
+            "use_block_routing": bool(self.use_block[0])}
+
+
+class Layer:
+    def __init__(self, ctx: "Context", handle: int, weights: LayerWeights):
+        self.ctx, self.handle, self.weights = ctx, handle, weights
+        self.hp = weights.hparams()
+
+    def free(self):
+        if self.handle:
+            load().dmoe_layer_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        lib = load()
+        h = C.c_void_p()
+        rc = lib.dmoe_create(device, C.byref(h))
+        if rc:
+            raise DmoeError(rc, f"dmoe_create({device}) failed")
+        self.handle = h.value
+        self.device = device
+
+    def _check(self, rc: int):
+        if rc:
+            raise DmoeError(rc, load().dmoe_last_error(self.handle).decode())
+
+    def last_error(self) -> str:
+        return load().dmoe_last_error(self.handle).decode()
+
+    def close(self):
+        if getattr(self, "handle", None):
+            load().dmoe_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def upload(self, w: LayerWeights, hp: Optional[HParams] = None,
+               desc: Optional[LayerDesc] = None) -> Layer:
+        """Copy w into HBM.  hp / desc override the structs built from w."""
+        hp = w.hparams() if hp is None else hp
+        d = w.desc() if desc is None else desc
+        out = C.c_void_p()
+        self._check(load().dmoe_layer_upload(self.handle, C.byref(hp), C.byref(d), C.byref(out)))
+        return Layer(self, out.value, w)
+
+    def wrap_device(self, w: LayerWeights) -> Layer:
+        hp, d = w.hparams(), w.desc()
+        out = C.c_void_p()
+        self._check(load().dmoe_layer_wrap_device(self.handle, C.byref(hp), C.byref(d),
+                                                  C.byref(out)))
+        return Layer(self, out.value, w)
+
+    def forward(self, layer: Layer, x: np.ndarray, debug: bool = False):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        N = x.shape[0]
+        y = np.empty_like(x)
+        dbg = DebugOut(layer.hp, N) if debug else None
+        ds = dbg.struct() if dbg else None
+        self._check(load().dmoe_layer_forward(self.handle, layer.handle, x.ctypes.data, N,
+                                              y.ctypes.data, C.byref(ds) if ds else None))
+        return (y, dbg.as_dict()) if debug else y
+
+    def forward_device(self, layer: Layer, x_dev, n_tokens: int, y_dev, stream=None):
+        s = 0 if stream is None else int(stream)
+        self._check(load().dmoe_layer_forward_device(self.handle, layer.handle, _ptr(x_dev),
+                                                     n_tokens, _ptr(y_dev), s or None))
+
+    def route_logits(self, hp: HParams, logits: np.ndarray, bias: Optional[np.ndarray]):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        N = logits.shape[0]
+        dbg = DebugOut(hp, N)
+        ds = dbg.struct()
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self._check(load().dmoe_route_logits(self.handle, C.byref(hp),
+                                             b.ctypes.data if b is not None else None,
+                                             logits.ctypes.data, N, C.byref(ds)))
+        return dbg.as_dict()
+
+    def profile(self, enable: bool):
+        self._check(load().dmoe_profile_enable(self.handle, 1 if enable else 0))
+
+    def profile_read(self) -> dict:
+        """{stage name: (total ms, launches)} since the last read."""
+        ms = np.zeros(N_STAGES, np.float32)
+        calls = np.zeros(N_STAGES, np.int32)
+        self._check(load().dmoe_profile_read(self.handle, ms.ctypes.data, calls.ctypes.data))
+        return {load().dmoe_stage_name(i).decode(): (float(ms[i]), int(calls[i]))
+                for i in range(N_STAGES) if calls[i]}
+
+    def quantize_device(self, ttype: int, src_dev, dst_dev, nrows: int, n_per_row: int,
+                        stream=None):
+        s = 0 if stream is None else int(stream)
+        self._check(load().dmoe_quantize_device(self.handle, ttype, _ptr(src_dev), _ptr(dst_dev),
+                                                nrows, n_per_row, s or None))
+
+
+__all__ = ["Context", "Layer", "LayerWeights", "DmoeError", "load", "tensor_view", "hparams_of",
+           "use_block_routing", "row_size", "TYPE_F32", "TYPE_F16", "TYPE_Q8_0", "TYPE_Q4_K",
+           "TYPE_Q8_K", "TYPE_NAMES", "TYPE_BY_NAME", "EXPORTS", "LIB_PATH"]

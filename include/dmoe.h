@@ -1,0 +1,200 @@
+/*
+ * dmoe.h — C ABI of the MI355X-native LLaDA2 block-routed MoE layer.
+ *
+ * One call computes the MoE segment that Akicou/diffuse-cpp builds out of
+ * ggml ops in src/diffuse-moe-graph.cpp:188-289: sigmoid router with a
+ * selection-only expert bias, per-block expert capacity, per-token top-k inside
+ * the allowed set, renormalised and scaled gate weights, grouped SwiGLU
+ * experts over GGUF block-quantised weights, weighted combine and the
+ * always-on shared expert.  The output is `moe_out` (diffuse-moe-graph.cpp:288),
+ * i.e. the segment output BEFORE the residual add of :291-292.
+ *
+ * Conventions
+ *  - Plain pointers and sizes only.  No exception crosses this boundary; every
+ *    entry point returns a dmoe_status and never calls exit()
+ *    (the reference aborts with DIFFUSE_DIE, src/diffuse-common.h:23-26).
+ *  - Tensor shapes use ggml `ne` order (ne[0] contiguous), byte strides `nb`,
+ *    exactly as the ggml_tensor fields the reference holds in
+ *    diffuse_moe_layer (src/diffuse-common.h:72-82).
+ *  - Activations are row-major float32 [n_tokens][n_embd], i.e. ggml
+ *    [n_embd, N] (diffuse-moe-graph.cpp:200).
+ *  - One dmoe_ctx per host thread / stream: no internal locking
+ *    (the reference serialises callers with a mutex,
+ *    tools/diffuse-server.cpp:462).
+ */
+#ifndef DMOE_H
+#define DMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids, as enumerated in tools/quantize_streaming.py:109-110. */
+#define DMOE_TYPE_F32   0
+#define DMOE_TYPE_F16   1
+#define DMOE_TYPE_Q8_0  8
+#define DMOE_TYPE_Q4_K 12
+
+typedef enum dmoe_status {
+    DMOE_OK                   = 0,
+    DMOE_ERR_INVALID_ARG      = 1, /* null pointer, non-positive size        */
+    DMOE_ERR_UNSUPPORTED_TYPE = 2, /* tensor type outside the list above     */
+    DMOE_ERR_SHAPE            = 3, /* ne/nb inconsistent with the hparams    */
+    DMOE_ERR_HIP              = 4, /* a HIP runtime call failed              */
+    DMOE_ERR_OOM              = 5, /* device allocation failed               */
+    DMOE_ERR_NONFINITE        = 6  /* NaN / Inf in the host input activations */
+} dmoe_status;
+
+/* A view of one ggml tensor (ggml_tensor's type/data/ne/nb).  `data` points at
+ * the unmodified GGUF block bytes. */
+typedef struct dmoe_tensor {
+    int32_t     type;
+    const void *data;
+    int64_t     ne[4];
+    size_t      nb[4];
+} dmoe_tensor;
+
+/* MoE hyper-parameters: the diffuse_model fields of
+ * src/diffuse-common.h:103-118, read from GGUF at src/diffuse-model.cpp:143-158. */
+typedef struct dmoe_hparams {
+    int32_t n_embd;          /* hparams.n_embd                                 */
+    int32_t n_experts;       /* expert_count                                   */
+    int32_t top_k;           /* expert_used_count                              */
+    int32_t capacity;        /* expert_capacity   (default 48)                 */
+    int32_t block_size;      /* moe_block_size    (default 32)                 */
+    int32_t moe_ff;          /* expert_feed_forward_length                     */
+    int32_t n_shared;        /* expert_shared_count (0: no shared expert)      */
+    int32_t shared_ff;       /* ne[1] of moe_shared_gate                       */
+    int32_t norm_topk_prob;  /* norm_topk_prob    (default 1)                  */
+    float   routed_scaling;  /* routed_scaling_factor (2.5 for LLaDA2-flash)   */
+} dmoe_hparams;
+
+/* The MoE tensors of one layer (diffuse_moe_layer, src/diffuse-common.h:72-82):
+ *   gate_w    moe_gate.weight          F32/F16 [n_embd, n_experts]
+ *   gate_bias moe_gate_bias.weight     F32     [n_experts]      (data may be NULL)
+ *   exp_gate  moe_experts_gate.weight  T       [n_embd, moe_ff, n_experts]
+ *   exp_up    moe_experts_up.weight    T       [n_embd, moe_ff, n_experts]
+ *   exp_down  moe_experts_down.weight  T       [moe_ff, n_embd, n_experts]
+ *   sh_gate   moe_shared_gate.weight   Ts      [n_embd, shared_ff]
+ *   sh_up     moe_shared_up.weight     Ts      [n_embd, shared_ff]
+ *   sh_down   moe_shared_down.weight   Ts      [shared_ff, n_embd]
+ * T, Ts in {F32, F16, Q8_0, Q4_K}; the three routed tensors share one T and the
+ * three shared tensors share one Ts.  Shared tensors are ignored when
+ * n_shared == 0. */
+typedef struct dmoe_layer_desc {
+    dmoe_tensor gate_w, gate_bias;
+    dmoe_tensor exp_gate, exp_up, exp_down;
+    dmoe_tensor sh_gate, sh_up, sh_down;
+} dmoe_layer_desc;
+
+/* Optional host-side copies of the routing intermediates (any field may be
+ * NULL).  Sizes with N = n_tokens, E = n_experts, k = top_k, B = N/block_size:
+ *   logits  [N][E] f32  router logits        (diffuse-moe-graph.cpp:203)
+ *   probs   [N][E] f32  sigmoid(logits)      (:204)
+ *   bmax    [B][E] f32  block max fold       (:223-229)   block routing only
+ *   thr     [B]    f32  capacity threshold   (:232-236)   block routing only
+ *   allowed [B][E] u8   1 = expert allowed   (:241-242)   block routing only
+ *   idx     [N][k] i32  selected experts, descending selection score,
+ *                       ties to the lower expert id     (:252)
+ *   weights [N][k] f32  gate weights         (:253-262)
+ *   counts  [E]    i32  (token, slot) pairs per expert
+ *   offsets [E]    i32  exclusive prefix sum of counts
+ *   perm    [N*k]  i32  pair ids t*k+slot grouped by expert: stable counting
+ *                       sort of the t-major pair list (ggml_mul_mat_id order)
+ *   use_block_routing   set to 1 when block routing ran (:215-216), else 0 */
+typedef struct dmoe_debug {
+    float   *logits;
+    float   *probs;
+    float   *bmax;
+    float   *thr;
+    uint8_t *allowed;
+    int32_t *idx;
+    float   *weights;
+    int32_t *counts;
+    int32_t *offsets;
+    int32_t *perm;
+    int32_t *use_block_routing;
+} dmoe_debug;
+
+typedef struct dmoe_ctx   dmoe_ctx;
+typedef struct dmoe_layer dmoe_layer;
+
+/* Create a context bound to HIP device `hip_device`.
+ * Replaces the backend set-up of diffuse_context_new_gpu
+ * (include/diffuse.h:65, src/diffuse-backend.h:76-101) for this segment. */
+int  dmoe_create(int hip_device, dmoe_ctx **out);
+void dmoe_destroy(dmoe_ctx *ctx);
+
+/* Text of the last error on this context (never NULL). */
+const char *dmoe_last_error(const dmoe_ctx *ctx);
+
+/* Copy one layer's MoE tensors from host memory into HBM, once.  The caller
+ * may free its host copy afterwards.  Replaces the (stubbed) weight offload of
+ * src/diffuse-backend.h:104-121 for the MoE tensors of one layer. */
+int  dmoe_layer_upload(dmoe_ctx *ctx, const dmoe_hparams *hp,
+                       const dmoe_layer_desc *desc, dmoe_layer **out);
+
+/* Same, but every `data` pointer in `desc` is already a device pointer on the
+ * context's GPU: the layer refers to that memory without copying (the caller
+ * keeps it alive until dmoe_layer_free).  Strides are taken from nb[]. */
+int  dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp,
+                            const dmoe_layer_desc *desc, dmoe_layer **out);
+
+void dmoe_layer_free(dmoe_layer *layer);
+
+/* moe_out = MoE(x) for host buffers x, y of n_tokens*n_embd floats.
+ * Synchronous.  Replaces src/diffuse-moe-graph.cpp:188-289 (`cur` in,
+ * `moe_out` out).  Host input containing NaN/Inf is rejected with
+ * DMOE_ERR_NONFINITE.  `dbg` may be NULL. */
+int  dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *layer,
+                        const float *x, int32_t n_tokens, float *y,
+                        dmoe_debug *dbg);
+
+/* Device-pointer variant: x_dev, y_dev live on the context's GPU, work is
+ * queued on `stream` (a hipStream_t; NULL = the null stream) and the call
+ * returns without synchronising. */
+int  dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *layer,
+                               const float *x_dev, int32_t n_tokens,
+                               float *y_dev, void *stream);
+
+/* Routing only, from caller-supplied router logits [N][E] (host).  Runs the
+ * GPU router stages that follow the logits product (diffuse-moe-graph.cpp:
+ * 204-262) plus the dispatch grouping; outputs go to `dbg` (logits is
+ * ignored).  Lets routing be checked bit for bit on injected logits. */
+int  dmoe_route_logits(dmoe_ctx *ctx, const dmoe_hparams *hp,
+                       const float *bias /* [E] or NULL */,
+                       const float *logits, int32_t n_tokens,
+                       dmoe_debug *dbg);
+
+/* Bytes of one row of n elements of `type` (ggml_row_size). */
+size_t dmoe_row_size(int32_t type, int64_t n);
+
+/* Quantise nrows rows of n_per_row f32 values (device memory) into `type`
+ * blocks (device memory), on `stream`.  Counterpart of quantize_to_type in
+ * tools/quant_lib.c:16-27 (which wraps ggml_quantize_chunk); used to build
+ * synthetic GGUF expert tensors directly in HBM.  The Q4_K quantiser is a
+ * plain min/max one, not ggml's iterative make_qkx2_quants. */
+int  dmoe_quantize_device(dmoe_ctx *ctx, int32_t type, const float *src_dev,
+                          void *dst_dev, int64_t nrows, int64_t n_per_row,
+                          void *stream);
+
+/* Per-stage timing.  While enabled, every forward records a HIP event pair
+ * around each pipeline stage on the stream it runs on; dmoe_profile_read
+ * waits for the recorded work, adds each stage's elapsed milliseconds and
+ * launch count since the last read into total_ms[s] / calls[s]
+ * (s < DMOE_N_STAGES; either array may be NULL) and resets the tally.
+ * Replaces the per-forward wall-clock timers of the reference
+ * (src/diffuse-sampler.cpp:171-176) at stage granularity. */
+#define DMOE_N_STAGES 10
+int  dmoe_profile_enable(dmoe_ctx *ctx, int enable);
+int  dmoe_profile_read(dmoe_ctx *ctx, float *total_ms, int32_t *calls);
+const char *dmoe_stage_name(int stage);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DMOE_H */

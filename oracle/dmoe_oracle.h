@@ -1,0 +1,109 @@
+/*
+ * dmoe_oracle.h — CPU oracle for the LLaDA2 block-routed MoE layer.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the smoke
+ * entry and the CPU-baseline leg of bench.py may load it; the product library
+ * (libdmoe.so) never links, loads or calls it.
+ *
+ * It restates, in plain C, what src/diffuse-moe-graph.cpp:188-289 computes
+ * when ggml executes that graph on the CPU (every function cites the line it
+ * follows).  ggml itself is absent from the reference checkout (empty git
+ * submodule), so the ggml-internal semantics below are restated from ggml's
+ * published algorithms and are marked "ggml-internal" where they cannot be
+ * checked against the reference's own files.
+ *
+ * Parity status of each function (how it is pinned by tests/):
+ *   dmo_f16_to_f32 / dmo_f32_to_f16  pinned: numpy float16 on all 65536 halves
+ *                                    and on random/edge f32 inputs
+ *   dmo_expf                         pinned: numpy float64 exp rounded to f32
+ *                                    (correctly rounded) on 10^7 inputs + edges
+ *   dmo_dequant_row (F16/Q8_0/Q4_K)  pinned: hand-built blocks with known values,
+ *                                    all 8 get_scale_min_k4 indices
+ *   dmo_quantize_row_act (Q8_K/Q8_0) pinned: hand-computed blocks, half-even /
+ *                                    half-away rounding cases, numpy restatement
+ *   dmo_vec_dot                      pinned: float64 dot of the dequantised rows
+ *                                    (integer parts exact, closed-form bound)
+ *   dmo_router_logits                pinned: float64 matmul bound + a brute-force
+ *                                    numpy emulation of the canonical order
+ *   dmo_route                        pinned: brute force on tiny inputs, fold KAT
+ *                                    (0x3f61fdaf, 0x3ea25e9b), slack / ties /
+ *                                    cap>=E / N%blk!=0 special cases
+ *   dmo_dispatch                     pinned: permutation / histogram / scan
+ *                                    invariants
+ *   dmo_layer_forward                pinned: float64 numpy layer on dequantised
+ *                                    weights within an analytic error budget
+ */
+#ifndef DMOE_ORACLE_H
+#define DMOE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../include/dmoe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- block formats (ggml / GGUF) --------------------------------------- */
+#define DMO_QK_K 256
+#define DMO_QK8_0 32
+
+typedef struct { uint16_t d; int8_t qs[32]; } dmo_block_q8_0;            /* 34 B  */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } dmo_block_q4_K; /* 144 B */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } dmo_block_q8_K;  /* 292 B */
+
+float    dmo_f16_to_f32(uint16_t h);
+uint16_t dmo_f32_to_f16(float f);
+void     dmo_f16_to_f32_n(const uint16_t *h, float *f, int64_t n);
+void     dmo_f32_to_f16_n(const float *f, uint16_t *h, int64_t n);
+
+float    dmo_expf(float x);
+void     dmo_expf_n(const float *x, float *y, int64_t n);
+float    dmo_sigmoid(float x);
+
+size_t   dmo_row_size(int32_t type, int64_t n);
+int32_t  dmo_vec_dot_type(int32_t type);   /* activation type ggml converts to */
+
+/* get_scale_min_k4 of ggml's Q4_K */
+void     dmo_q4K_scale_min(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
+
+int      dmo_dequant_row(int32_t type, const void *src, float *dst, int64_t n);
+/* weight quantisers used to build synthetic GGUF tensors */
+int      dmo_quantize_rows(int32_t type, const float *src, void *dst,
+                           int64_t nrows, int64_t n_per_row, int n_threads);
+/* activation quantisers (ggml vec_dot_type semantics): type is Q8_K (id 15),
+ * Q8_0, F16 or F32 */
+#define DMO_TYPE_Q8_K 15
+int      dmo_quantize_row_act(int32_t act_type, const float *src, void *dst, int64_t n);
+
+/* dot of one weight row (type wtype) with one activation row already in
+ * dmo_vec_dot_type(wtype). */
+float    dmo_vec_dot(int32_t wtype, int64_t n, const void *wrow, const void *xrow);
+
+/* ---- router -------------------------------------------------------------- */
+void dmo_router_logits(const float *W, int64_t w_row_stride, const float *x,
+                       int n_tokens, int n_embd, int n_experts, float *logits);
+
+int  dmo_use_block_routing(const dmoe_hparams *hp, int n_tokens);
+
+/* Routing from logits.  probs [N][E]; bmax [B][E], thr [B], allowed [B][E]
+ * (only written with block routing; may be NULL); idx, weights [N][k]. */
+int  dmo_route(const dmoe_hparams *hp, const float *bias, const float *logits,
+               int n_tokens, float *probs, float *bmax, float *thr,
+               uint8_t *allowed, int32_t *idx, float *weights);
+
+void dmo_dispatch(const int32_t *idx, int n_tokens, int top_k, int n_experts,
+                  int32_t *counts, int32_t *offsets, int32_t *perm);
+
+/* ---- whole segment -------------------------------------------------------
+ * y = moe_out for x [N][n_embd].  dbg may be NULL.  n_threads <= 0: all. */
+int  dmo_layer_forward(const dmoe_hparams *hp, const dmoe_layer_desc *desc,
+                       const float *x, int n_tokens, float *y,
+                       dmoe_debug *dbg, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,231 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Bar (tolerances written here, per the layer contract):
+  * routing — logits, probs, block max, threshold, allowed set, top-k indices,
+    gate weights, per-expert counts/offsets and the dispatch permutation — is
+    bit-exact on identical fp32 inputs;
+  * layer output: max|y - y_oracle| / max|y_oracle| <= 2e-2 for quantised
+    expert weights (Q8_0, Q4_K), <= 1e-3 for F16, <= 1e-4 for F32.
+"""
+import numpy as np
+import pytest
+
+from conftest import max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {0: 1e-4, 1: 1e-3, 8: 2e-2, 12: 2e-2}
+ROUTE_KEYS = ("logits", "probs", "bmax", "thr", "allowed", "idx", "weights", "counts",
+              "offsets", "perm", "use_block_routing")
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _check_routing(dg, dr, keys=ROUTE_KEYS):
+    for k in keys:
+        a, b = dg[k], dr[k]
+        if isinstance(a, np.ndarray):
+            assert a.shape == b.shape, k
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{k} differs"
+        else:
+            assert a == b, k
+
+
+def _small(dmoe, synth, wtype, n_tokens=64, seed=3):
+    return synth.LayerConfig(f"small_{wtype}", 512, 32, 256, 8, 4, 32, 256, wtype, wtype,
+                             n_tokens, -0.05, 0.05)
+
+
+def test_tiny_layer(ctx, O):
+    import dmoe
+    from dmoe import synth
+    _say("case: tiny F32 layer, N=32")
+    cfg = synth.CONFIGS["tiny"]
+    w = synth.host_layer(cfg, 11, O.quantize_rows)
+    x = synth.make_x(cfg, 11)
+    layer = ctx.upload(w)
+    y, dg = ctx.forward(layer, x, debug=True)
+    yr, dr = O.layer_forward(w, x, debug=True)
+    _check_routing(dg, dr)
+    assert max_rel_err(y, yr) <= TOL[0]
+
+
+@pytest.mark.parametrize("wtype", [12, 8, 1], ids=["Q4_K", "Q8_0", "F16"])
+@pytest.mark.parametrize("n_tokens", [32, 96, 40], ids=["N32", "N96", "N40_noblock"])
+def test_small_layer(ctx, O, wtype, n_tokens):
+    import dmoe
+    from dmoe import synth
+    _say(f"case: small layer type={wtype} N={n_tokens}")
+    cfg = _small(dmoe, synth, wtype, n_tokens)
+    w = synth.host_layer(cfg, 5 + wtype, O.quantize_rows)
+    x = synth.make_x(cfg, 5 + wtype, n_tokens)
+    layer = ctx.upload(w)
+    y, dg = ctx.forward(layer, x, debug=True)
+    yr, dr = O.layer_forward(w, x, debug=True)
+    _check_routing(dg, dr)
+    assert dg["use_block_routing"] == (n_tokens % 32 == 0)
+    err = max_rel_err(y, yr)
+    _say(f"  max rel err {err:.3e}")
+    assert err <= TOL[wtype]
+
+
+@pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0"])
+def test_flash_layer(ctx, O, name):
+    import torch
+    import dmoe
+    from dmoe import synth
+    _say(f"case: {name} one 32-token block")
+    cfg = synth.CONFIGS[name]
+    wd = synth.device_layer(cfg, 21, ctx)
+    layer = ctx.wrap_device(wd)
+    x = synth.make_x(cfg, 21)
+    y, dg = ctx.forward(layer, x, debug=True)
+    wh = synth.to_host(wd)
+    yr, dr = O.layer_forward(wh, x, debug=True)
+    _check_routing(dg, dr)
+    touched = int((dr["counts"] > 0).sum())
+    allowed = int(dr["allowed"].sum())
+    err = max_rel_err(y, yr)
+    _say(f"  touched experts {touched}, allowed {allowed}, max rel err {err:.3e}")
+    assert allowed >= cfg.capacity
+    assert err <= TOL[cfg.wtype]
+    del layer, wd
+    torch.cuda.empty_cache()
+
+
+def test_route_logits_flash_shape(ctx, O):
+    import dmoe
+    _say("case: routing from injected logits, flash shape, 8 blocks")
+    rng = np.random.default_rng(0)
+    hp = dmoe.hparams_of(4096, 256, 8, 48, 32)
+    N = 256
+    logits = (rng.standard_normal((N, 256)) * 1.28).astype(np.float32)
+    bias = rng.uniform(-0.1, 0.1, 256).astype(np.float32)
+    dg = ctx.route_logits(hp, logits, bias)
+    dr = O.route(hp, logits, bias)
+    _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
+
+
+def test_route_logits_ties_and_slack(ctx, O):
+    import dmoe
+    _say("case: routing ties / slack")
+    hp = dmoe.hparams_of(256, 64, 4, 8, 32)
+    N = 64
+    # many exact ties: logits from a tiny set of values
+    rng = np.random.default_rng(1)
+    logits = rng.choice(np.array([-1.0, 0.0, 0.5, 0.5, 2.0], np.float32), size=(N, 64))
+    for bias in (None, np.zeros(64, np.float32)):
+        dg = ctx.route_logits(hp, logits, bias)
+        dr = O.route(hp, logits, bias)
+        _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
+        assert dg["allowed"].sum(1).min() >= 8
+
+
+def test_sigmoid_sweep(ctx, O):
+    """GPU sigmoid (binary64 exp) equals the oracle's on a sweep of fp32
+    logits: every 509th bit pattern of [-110, 100] plus 2^20 random values."""
+    import dmoe
+    _say("case: sigmoid sweep")
+    lo = np.float32(-110.0).view(np.uint32)
+    hi = np.float32(100.0).view(np.uint32)
+    neg = np.arange(np.uint32(0x80000000), lo, 509, dtype=np.uint64).astype(np.uint32)
+    pos = np.arange(0, hi, 509, dtype=np.uint64).astype(np.uint32)
+    rng = np.random.default_rng(2)
+    vals = np.concatenate([neg.view(np.float32), pos.view(np.float32),
+                           rng.uniform(-110, 100, 1 << 20).astype(np.float32)])
+    E = 256
+    vals = vals[: (len(vals) // E) * E].reshape(-1, E)
+    hp = dmoe.hparams_of(256, E, 1, 0, 32)   # capacity 0: no block routing
+    probs = np.empty_like(vals)
+    for c0 in range(0, vals.shape[0], 16384):
+        dg = ctx.route_logits(hp, vals[c0:c0 + 16384], None)
+        probs[c0:c0 + 16384] = dg["probs"]
+    ref = np.empty_like(vals)
+    flat = vals.reshape(-1)
+    e = O.expf(-flat)
+    ref = (np.float32(1.0) / (np.float32(1.0) + e)).reshape(vals.shape)
+    assert np.array_equal(probs.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("wtype", [12, 8, 1])
+def test_device_quantizer_matches_oracle(ctx, O, wtype):
+    import torch
+    _say(f"case: device quantizer type {wtype}")
+    rng = np.random.default_rng(4)
+    f = (rng.standard_normal((64, 1024)) * 0.02).astype(np.float32)
+    f[3, :256] = 0.0                         # all-zero super-block
+    f[5, :] = np.abs(f[5, :])                # positive-only rows (min clamps to 0)
+    ref = O.quantize_rows(wtype, f)
+    src = torch.from_numpy(f).cuda()
+    dst = torch.zeros(ref.shape, dtype=torch.uint8, device="cuda")
+    ctx.quantize_device(wtype, src, dst, 64, 1024)
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.cpu().numpy(), ref)
+
+
+def test_forward_device_matches_host(ctx, O):
+    import torch
+    from dmoe import synth
+    _say("case: device-pointer forward == host forward")
+    cfg = _small(None, synth, 12, 64)
+    w = synth.host_layer(cfg, 9, O.quantize_rows)
+    x = synth.make_x(cfg, 9, 64)
+    layer = ctx.upload(w)
+    y = ctx.forward(layer, x)
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty_like(xd)
+    s = torch.cuda.current_stream()
+    ctx.forward_device(layer, xd, 64, yd, s.cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(yd.cpu().numpy(), y)
+    # deterministic: repeat is bit-identical
+    assert np.array_equal(ctx.forward(layer, x), y)
+
+
+def test_error_paths(ctx, O):
+    import dmoe
+    from dmoe import synth
+    _say("case: error paths")
+    cfg = synth.CONFIGS["tiny"]
+    w = synth.host_layer(cfg, 1, O.quantize_rows)
+    bad = synth.replace(w, wtype=2)                      # Q4_0: unsupported
+    with pytest.raises(dmoe.DmoeError) as ei:
+        ctx.upload(bad)
+    assert ei.value.code == dmoe._abi.ERR_UNSUPPORTED_TYPE
+    hp = w.hparams()
+    hp.moe_ff = 64                                       # hparams disagree with ne
+    with pytest.raises(dmoe.DmoeError) as ei:
+        ctx.upload(w, hp=hp)
+    assert ei.value.code == dmoe._abi.ERR_SHAPE
+    d = w.desc()
+    d.exp_down.nb[1] = 8                                 # stride below the row size
+    with pytest.raises(dmoe.DmoeError) as ei:
+        ctx.upload(w, desc=d)
+    assert ei.value.code == dmoe._abi.ERR_SHAPE
+    layer = ctx.upload(w)
+    x = synth.make_x(cfg, 1)
+    x[3, 7] = np.nan
+    with pytest.raises(dmoe.DmoeError) as ei:
+        ctx.forward(layer, x)
+    assert ei.value.code == dmoe._abi.ERR_NONFINITE
+
+
+def test_injected_alloc_failure(O, monkeypatch):
+    import dmoe
+    from dmoe import synth
+    _say("case: injected workspace allocation failure")
+    cfg = synth.CONFIGS["tiny"]
+    w = synth.host_layer(cfg, 1, O.quantize_rows)
+    c = dmoe.Context(0)
+    layer = c.upload(w)
+    monkeypatch.setenv("DMOE_FAIL_ALLOC", "1")
+    with pytest.raises(dmoe.DmoeError) as ei:
+        c.forward(layer, synth.make_x(cfg, 1))
+    assert ei.value.code == dmoe._abi.ERR_OOM
+    monkeypatch.delenv("DMOE_FAIL_ALLOC")
+    y = c.forward(layer, synth.make_x(cfg, 1))
+    assert np.isfinite(y).all()
+    layer.free()
+    c.close()
