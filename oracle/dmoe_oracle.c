@@ -520,6 +520,21 @@ static inline int ranks_before(uint32_t ka, int ea, uint32_t kb, int eb)
     return ka > kb || (ka == kb && ea < eb);
 }
 
+/* :221-229  max over a block's tokens folded as m <- s_j + relu(m - s_j),
+ * j = 1..n-1, starting from s_0 (ggml has no elementwise max).  In binary32
+ * this is not an exact max and not associative. */
+float dmo_block_fold(const float *s, int n, int stride)
+{
+    float m = s[0];
+    for (int j = 1; j < n; j++) {
+        float sj = s[(size_t)j * stride];
+        float r = m - sj;
+        r = r > 0.0f ? r : 0.0f;      /* ggml_relu */
+        m = sj + r;
+    }
+    return m;
+}
+
 int dmo_route(const dmoe_hparams *hp, const float *bias, const float *logits,
               int n_tokens, float *probs, float *bmax, float *thr,
               uint8_t *allowed, int32_t *idx, float *weights)
@@ -544,13 +559,7 @@ int dmo_route(const dmoe_hparams *hp, const float *bias, const float *logits,
         for (int b = 0; b < nb; b++) {
             /* :223-229 bmax = fold_j (s_j + relu(bmax - s_j)), sequential in j */
             for (int e = 0; e < E; e++) {
-                float m = sel[(size_t)(b * blk) * E + e];
-                for (int j = 1; j < blk; j++) {
-                    float s = sel[(size_t)(b * blk + j) * E + e];
-                    float r = m - s;
-                    r = r > 0.0f ? r : 0.0f;      /* ggml_relu */
-                    m = s + r;
-                }
+                float m = dmo_block_fold(sel + (size_t)(b * blk) * E + e, blk, E);
                 bm[e] = m;
                 key[e] = order_key(m);
             }

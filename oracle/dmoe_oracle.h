@@ -87,6 +87,9 @@ void dmo_router_logits(const float *W, int64_t w_row_stride, const float *x,
 
 int  dmo_use_block_routing(const dmoe_hparams *hp, int n_tokens);
 
+/* the block max fold of n scores s[0], s[stride], ... */
+float dmo_block_fold(const float *s, int n, int stride);
+
 /* Routing from logits.  probs [N][E]; bmax [B][E], thr [B], allowed [B][E]
  * (only written with block routing; may be NULL); idx, weights [N][k]. */
 int  dmo_route(const dmoe_hparams *hp, const float *bias, const float *logits,

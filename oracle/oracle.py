@@ -67,6 +67,8 @@ def load() -> C.CDLL:
     lib.dmo_router_logits.argtypes = [P, C.c_int64, P, C.c_int, C.c_int, C.c_int, P]
     lib.dmo_router_logits.restype = None
     lib.dmo_use_block_routing.argtypes = [C.POINTER(HParams), C.c_int]
+    lib.dmo_block_fold.argtypes = [P, C.c_int, C.c_int]
+    lib.dmo_block_fold.restype = C.c_float
     lib.dmo_route.argtypes = [C.POINTER(HParams), P, P, C.c_int, P, P, P, P, P, P]
     lib.dmo_dispatch.argtypes = [P, C.c_int, C.c_int, C.c_int, P, P, P]
     lib.dmo_dispatch.restype = None
@@ -163,6 +165,11 @@ def router_logits(W: np.ndarray, x: np.ndarray) -> np.ndarray:
     out = np.empty((N, E), np.float32)
     load().dmo_router_logits(_p(W), H, _p(x), N, H, E, _p(out))
     return out
+
+
+def block_fold(s: np.ndarray) -> np.float32:
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    return np.float32(load().dmo_block_fold(_p(s), s.size, 1))
 
 
 def route(hp: HParams, logits: np.ndarray, bias=None) -> dict:
