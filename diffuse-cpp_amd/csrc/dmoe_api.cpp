@@ -12,6 +12,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
+#include <functional>
 #include <new>
 #include <string>
 #include <vector>
@@ -254,21 +256,51 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 struct Workspace {
     float *x, *y;
     RouteBufs rb;
-    ActBuf xq, hq;
+    WorkList wl;
+    ActBuf xq, hq;                       // GEMV-path activations
+    ActMfma ax, axs, ah, ahs;            // MFMA-path activations (routed / shared)
     float *h, *ye, *hs, *ys;
     float *bias;
 };
 
-size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, bool shared, int N, uint8_t *base,
-                      Workspace *w)
+// The MFMA expert path covers Q4_K routed experts (and a Q4_K shared expert)
+// with reduction lengths that are whole super-blocks.
+bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared)
+{
+    if (wtype != DMOE_TYPE_Q4_K || hp.n_embd % 256 || hp.moe_ff % 256) return false;
+    if (shared && (stype != DMOE_TYPE_Q4_K || hp.shared_ff % 256)) return false;
+    return true;
+}
+
+ActMfma take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bool split)
+{
+    // split activations keep their lo halves as rows rows..2*rows-1
+    const int r = split ? 2 * rows : rows;
+    ActMfma a{};
+    a.K = K;
+    a.v = (uint16_t *)take((size_t)r * K * 2);
+    a.bs = (uint16_t *)take((size_t)r * (K / 16) * 2);
+    a.d = (float *)take((size_t)r * (K / 256) * 4);
+    if (split && a.v) {
+        a.v_lo = a.v + (size_t)rows * K;
+        a.bs_lo = a.bs + (size_t)rows * (K / 16);
+    }
+    return a;
+}
+
+size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N,
+                      uint8_t *base, Workspace *w)
 {
     const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
     const int SF = shared ? hp.shared_ff : 0;
     const int P = N * K;
     const int B = hp.block_size > 0 ? (N + hp.block_size - 1) / hp.block_size : 1;
+    // routing groups: block_size tokens with block routing, else 32
+    const int gmin = hp.block_size > 1 ? std::min(hp.block_size, 32) : 32;
+    const int groups = (N + gmin - 1) / gmin;
     const int32_t at = act_type_of(wtype);
     size_t off = 0;
-    auto take = [&](size_t bytes) -> uint8_t * {
+    std::function<uint8_t *(size_t)> take = [&](size_t bytes) -> uint8_t * {
         uint8_t *p = base ? base + off : nullptr;
         off += align_up(bytes > 0 ? bytes : 1);
         return p;
@@ -287,6 +319,20 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, bool shared, int N,
     t.rb.counts = (int32_t *)take((size_t)E * 4);
     t.rb.offsets = (int32_t *)take((size_t)(E + 1) * 4);
     t.rb.perm = (int32_t *)take((size_t)P * 4);
+    t.rb.hist = (int32_t *)take((size_t)groups * E * 4);
+    t.rb.lrank = (int32_t *)take((size_t)P * 4);
+    t.wl.chunk = EXPERT_CHUNK;
+    t.wl.n_ec = (int32_t *)take(4);
+    t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
+    t.wl.ec_chunk = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
+    if (use_mfma_path(hp, wtype, stype, shared)) {
+        t.ax = take_act(take, N, H, false);
+        t.ah = take_act(take, P, FF, false);
+        if (shared) {
+            t.axs = take_act(take, N, H, true);
+            t.ahs = take_act(take, N, SF, true);
+        }
+    }
     t.xq.type = at;
     t.xq.n = H;
     t.xq.vals = take((size_t)N * act_row_vals_bytes(at, H));
@@ -307,7 +353,8 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, bool shared, int N,
 
 int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, Workspace *w)
 {
-    const size_t need = plan_workspace(L->hp, L->eg.type, L->has_shared, N, nullptr, nullptr);
+    const size_t need =
+        plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, nullptr, nullptr);
     if (need > ctx->ws_bytes) {
         if (ctx->ws) {
             // work queued on any stream may still read the old workspace
@@ -321,7 +368,7 @@ int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, Workspace *w)
         HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
         ctx->ws_bytes = need;
     }
-    plan_workspace(L->hp, L->eg.type, L->has_shared, N, (uint8_t *)ctx->ws, w);
+    plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
 }
 
@@ -390,7 +437,46 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, id, s, [&] { return call; }))
     STAGE(ST_LOGITS, launch_router_logits(L->gate_w, x, N, H, E, w.rb.logits, s));
     STAGE(ST_ROUTE, launch_route(rp, w.rb.logits, L->gate_bias, w.rb, s));
-    STAGE(ST_DISPATCH, launch_dispatch(rp, w.rb, s));
+    STAGE(ST_DISPATCH, launch_dispatch(rp, w.rb, w.wl, s));
+    if (use_mfma_path(hp, L->eg.type, L->sg.type, L->has_shared)) {
+        // Q4_K experts on MFMA: routed experts and the shared one share a launch
+        const int SF = hp.shared_ff;
+        ExpertJob job{};
+        job.has_shared = L->has_shared;
+        job.n_tokens = N;
+        job.top_k = K;
+        job.perm = w.rb.perm;
+        job.offsets = w.rb.offsets;
+        job.counts = w.rb.counts;
+        job.wl = w.wl;
+        STAGE(ST_ACTQ_X, launch_prep_act(x, N, H, ACT_Q8K, w.ax, s));
+        if (L->has_shared) STAGE(ST_ACTQ_X, launch_prep_act(x, N, H, ACT_SPLIT, w.axs, s));
+        job.w0 = L->eg;
+        job.w1 = L->eu;
+        job.s0 = L->sg;
+        job.s1 = L->su;
+        job.act = w.ax;
+        job.act_sh = w.axs;
+        job.rows = FF;
+        job.rows_sh = SF;
+        job.out = w.h;
+        job.out_sh = w.hs;
+        STAGE(ST_GATEUP, launch_expert_q4k(0, job, s));
+        STAGE(ST_ACTQ_H, launch_prep_act(w.h, N * K, FF, ACT_Q8K, w.ah, s));
+        if (L->has_shared) STAGE(ST_ACTQ_H, launch_prep_act(w.hs, N, SF, ACT_SPLIT, w.ahs, s));
+        job.w0 = L->ed;
+        job.s0 = L->sd;
+        job.act = w.ah;
+        job.act_sh = w.ahs;
+        job.rows = H;
+        job.rows_sh = H;
+        job.out = w.ye;
+        job.out_sh = w.ys;
+        STAGE(ST_DOWN, launch_expert_q4k(1, job, s));
+        STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
+                                         K, H, y, s));
+        return DMOE_OK;
+    }
     STAGE(ST_ACTQ_X, launch_act_quant(x, N, H, w.xq, s));
     STAGE(ST_GATEUP, launch_gateup_routed(L->eg, L->eu, w.xq, rp, w.rb, FF, w.h, s));
     STAGE(ST_ACTQ_H, launch_act_quant(w.h, N * K, FF, w.hq, s));
@@ -647,7 +733,7 @@ int dmoe_route_logits(dmoe_ctx *ctx, const dmoe_hparams *hp, const float *bias,
     }
     const RouteParams rp = route_params(*hp, n_tokens);
     LAUNCH_TRY(ctx, launch_route(rp, w.rb.logits, dbias, w.rb, s));
-    LAUNCH_TRY(ctx, launch_dispatch(rp, w.rb, s));
+    LAUNCH_TRY(ctx, launch_dispatch(rp, w.rb, w.wl, s));
     dmoe_debug d2 = dbg ? *dbg : dmoe_debug{};
     d2.logits = nullptr;
     if ((rc = copy_debug(ctx, *hp, w, n_tokens, &d2, s))) return rc;

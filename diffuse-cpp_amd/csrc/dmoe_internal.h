@@ -53,6 +53,56 @@ struct RouteBufs {
     int32_t *counts;    // [E]
     int32_t *offsets;   // [E+1]
     int32_t *perm;      // [N*K]
+    int32_t *hist;      // [groups][E] pairs of each routing group per expert
+    int32_t *lrank;     // [N*K] rank of a pair among its group's pairs of its expert
+};
+
+// Group scores kept in LDS by the routing kernel (group tokens x experts).
+constexpr int ROUTE_LDS = 8192;
+
+// Work list of the expert kernels: one entry per (expert, chunk of `chunk`
+// consecutive pairs of that expert), in expert order.
+struct WorkList {
+    int32_t chunk;
+    int32_t *n_ec;       // [1]
+    int32_t *ec_expert;  // [E + N*K/chunk + 1]
+    int32_t *ec_chunk;
+};
+
+// Activations in the MFMA operand layout of k_expert.hip.  Per row of K
+// values and per 256-value super-block sb, the f16 values are stored in the
+// order the MFMA lanes read them: position sb*256 + g*64 + s*8 + e holds value
+// 64g + 32*(e/4) + 4s + {0,2,1,3}[e%4] of the super-block (g = lane group,
+// s = MFMA step), matching the nibble order of a Q4_K super-block.
+//   ACT_Q8K  : ggml's Q8_K quantisation (ints exact in f16), d = Q8_K scale,
+//              bs = sums of 16 quants
+//   ACT_SPLIT: f32 value * 2^k split as hi + lo f16 (about 22 significant bits),
+//              d = 2^-k per super-block, bs / bs_lo = split sums of 16 values.
+//              The lo halves are rows `rows`..2*rows-1 of the same arrays
+//              (v_lo = v + rows*K, bs_lo = bs + rows*K/16, d repeated).
+enum ActMode { ACT_Q8K = 0, ACT_SPLIT = 1 };
+struct ActMfma {
+    int32_t K;
+    uint16_t *v;        // [rows][K]
+    uint16_t *v_lo;     // [rows][K]     split only
+    uint16_t *bs;       // [rows][K/16]
+    uint16_t *bs_lo;    // [rows][K/16]  split only
+    float *d;           // [rows][K/256]
+};
+
+// One launch of the grouped expert kernel (routed experts + the shared one).
+struct ExpertJob {
+    WTensor w0, w1;      // routed: gate, up (phase 0) or down, unused (phase 1)
+    WTensor s0, s1;      // shared expert, same roles
+    int32_t has_shared;
+    ActMfma act;         // routed activations (rows: tokens in phase 0, pairs in phase 1)
+    ActMfma act_sh;      // shared activations (rows: tokens)
+    int32_t rows, rows_sh;   // output rows of one routed / shared matrix
+    int32_t n_tokens, top_k;
+    const int32_t *perm, *offsets, *counts;
+    WorkList wl;
+    float *out;          // phase 0: h [N*K][rows]; phase 1: ye [N*K][rows]
+    float *out_sh;       // phase 0: hs [N][rows_sh]; phase 1: ys [N][rows_sh]
 };
 
 struct RouteParams {
@@ -68,7 +118,18 @@ hipError_t launch_router_logits(const float *W, const float *x, int N, int H, in
                                 float *logits, hipStream_t s);
 hipError_t launch_route(const RouteParams &rp, const float *logits, const float *bias,
                         const RouteBufs &rb, hipStream_t s);
-hipError_t launch_dispatch(const RouteParams &rp, const RouteBufs &rb, hipStream_t s);
+hipError_t launch_dispatch(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
+                           hipStream_t s);
+bool route_fits_lds(const RouteParams &rp);
+
+// Activations -> MFMA operand layout (k_prep.hip); K % 256 == 0.
+hipError_t launch_prep_act(const float *src, int rows, int K, int mode, const ActMfma &out,
+                           hipStream_t s);
+// Grouped Q4_K expert products on MFMA (k_expert.hip).  phase 0: h = silu(gate x)
+// * (up x); phase 1: y = down h.
+constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
+constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
+hipError_t launch_expert_q4k(int phase, const ExpertJob &job, hipStream_t s);
 
 hipError_t launch_act_quant(const float *src, int rows, int n, const ActBuf &dst,
                             hipStream_t s);

@@ -1,0 +1,269 @@
+// k_expert.hip — grouped Q4_K expert products on MFMA (gfx950).
+//
+// Computes the routed experts of src/diffuse-moe-graph.cpp:264-269 (ggml's
+// mul_mat_id over Q4_K weights with Q8_K activations) and the shared expert of
+// :280-286 (F32 activations), as one persistent launch per phase:
+//   phase 0: h = silu(W_gate x) * (W_up x)       (gate and up of the same rows)
+//   phase 1: y = W_down h
+//
+// Arithmetic.  Per 256-value super-block, a Q4_K row is  w = d*sc_j*q - dmin*m_j
+// (j = 32-value sub-block).  With activations a (Q8_K quants, or scaled f32
+// for the shared expert):
+//   sum_k w a = d * S1 - dmin * S2,   S1 = sum_k (sc_j q) a,   S2 = sum_j m_j sum_{k in j} a
+// sc_j*q <= 945 and the Q8_K quants are integers, all exact in f16, so
+// v_mfma_f32_16x16x32_f16 gives S1 as an exact integer dot (f32 accumulation of
+// exact products); S2 uses v_mfma_f32_16x16x16_f16 on the 16-value sums.  The
+// super-block result is scaled by the activation scale and accumulated in f32.
+//
+// Operand layout (checked on the hardware): srcA lane l = activation row l%16,
+// k = 8*(l/16)+e; srcB lane l = weight row l%16, same k; D lane l = weight row
+// l%16, activation rows 4*(l/16)+i.  Lane group g = l/16 handles the 32 qs
+// bytes of Q4_K chunk g (sub-blocks 2g, 2g+1); MFMA step s takes qs dword s.
+// A nibble q becomes the f16 1024+q (or 1024+16q for the high nibble) by OR-ing
+// it into the mantissa of 1024.0, and one packed fma subtracts the offset and
+// applies sc exactly: (1024+q)*sc - 1024*sc = q*sc.
+//
+// Work: item = (expert, up to 16 pairs of it, 16 weight rows x R tiles); the
+// wave streams those rows' super-blocks once.
+#include "dmoe_internal.h"
+
+namespace dmoe {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int WPB = 4;           // waves per workgroup
+constexpr int RT_DOWN = 2;       // 16-row tiles per down item
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ float h16f(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (uint16_t)u); }
+
+struct Q4KTile {        // a lane's share of one 16-row tile in one super-block
+    uint4 h;            // d, dmin, scales[12]
+    uint4 q0, q1;       // qs bytes 32g .. 32g+31
+};
+
+__device__ __forceinline__ void load_tile(Q4KTile &t, const uint8_t *row, int sb, int g)
+{
+    const uint8_t *blk = row + (size_t)sb * Q4K_BYTES;
+    t.h = *reinterpret_cast<const uint4 *>(blk);
+    const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * g);
+    t.q0 = qp[0];
+    t.q1 = qp[1];
+}
+
+struct Q4KOps {
+    h8 b[8];            // srcB of the 8 MFMA steps
+    h4 bm;              // srcB of the min term: m_2g, m_2g, m_2g+1, m_2g+1
+    float d, dmin;
+};
+
+__device__ __forceinline__ void dequant_tile(const Q4KTile &t, int g, Q4KOps &o)
+{
+    // 6-bit scale / min of sub-blocks 2g and 2g+1 (bytes jj, jj+1 of each word)
+    const uint32_t shift = 16u * (uint32_t)(g & 1);
+    const uint32_t by = (t.h.y >> shift) & 0xffffu;
+    const uint32_t bz = (t.h.z >> shift) & 0xffffu;
+    const uint32_t bw = (t.h.w >> shift) & 0xffffu;
+    uint32_t sc0, sc1, m0, m1;
+    if (g < 2) {
+        sc0 = by & 63u;
+        sc1 = (by >> 8) & 63u;
+        m0 = bz & 63u;
+        m1 = (bz >> 8) & 63u;
+    } else {
+        sc0 = (bw & 15u) | (((by >> 6) & 3u) << 4);
+        sc1 = ((bw >> 8) & 15u) | (((by >> 14) & 3u) << 4);
+        m0 = ((bw >> 4) & 15u) | (((bz >> 6) & 3u) << 4);
+        m1 = ((bw >> 12) & 15u) | (((bz >> 14) & 3u) << 4);
+    }
+    o.d = h16f(t.h.x & 0xffffu);
+    o.dmin = h16f(t.h.x >> 16);
+    const _Float16 a0 = (_Float16)(float)sc0, n0 = (_Float16)(-1024.0f * (float)sc0);
+    const _Float16 a1 = (_Float16)((float)sc1 * 0.0625f), n1 = (_Float16)(-64.0f * (float)sc1);
+    const h2 SC0 = {a0, a0}, N0 = {n0, n0}, SC1 = {a1, a1}, N1 = {n1, n1};
+    const uint32_t q[8] = {t.q0.x, t.q0.y, t.q0.z, t.q0.w, t.q1.x, t.q1.y, t.q1.z, t.q1.w};
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const uint32_t w = q[s], w8 = w >> 8;
+        const h2 lo02 = __builtin_elementwise_fma(as_h2((w & 0x000F000Fu) | 0x64006400u), SC0, N0);
+        const h2 lo13 = __builtin_elementwise_fma(as_h2((w8 & 0x000F000Fu) | 0x64006400u), SC0, N0);
+        const h2 hi02 = __builtin_elementwise_fma(as_h2((w & 0x00F000F0u) | 0x64006400u), SC1, N1);
+        const h2 hi13 = __builtin_elementwise_fma(as_h2((w8 & 0x00F000F0u) | 0x64006400u), SC1, N1);
+        o.b[s] = (h8){lo02.x, lo02.y, lo13.x, lo13.y, hi02.x, hi02.y, hi13.x, hi13.y};
+    }
+    const _Float16 fm0 = (_Float16)(float)m0, fm1 = (_Float16)(float)m1;
+    o.bm = (h4){fm0, fm0, fm1, fm1};
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Accumulate the item's R weight tiles against one 16-row activation tile over
+// all super-blocks.  arowA: activation row this lane feeds as srcA; arowD[i]:
+// activation row of output row 4g+i (for its per-super-block scale).
+template <int R>
+__device__ __forceinline__ void run_item(const uint8_t *const (&wrow)[R], const ActMfma &act,
+                                         int arowA, const int (&arowD)[4], int g,
+                                         float (&acc)[R][4])
+{
+    const int K = act.K;
+    const int nsb = K / 256;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[r][i] = 0.0f;
+
+    for (int sb = 0; sb < nsb; sb++) {
+        Q4KTile cur[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) load_tile(cur[r], wrow[r], sb, g);
+        const size_t vo = (size_t)arowA * K + sb * 256 + g * 64;
+        const size_t bo = (size_t)arowA * (K / 16) + sb * 16 + 4 * g;
+        float dx[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) dx[i] = act.d[(size_t)arowD[i] * nsb + sb];
+        h8 a[8];
+        const uint4 *av = reinterpret_cast<const uint4 *>(act.v + vo);
+#pragma unroll
+        for (int s = 0; s < 8; s++) a[s] = __builtin_bit_cast(h8, av[s]);
+        const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(act.bs + bo));
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            Q4KOps o;
+            dequant_tile(cur[r], g, o);
+            f4 s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], o.b[s], s1, 0, 0, 0);
+            f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+            s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, o.bm, s2, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[r][i] += dx[i] * (o.d * s1[i] - o.dmin * s2[i]);
+        }
+    }
+}
+
+// Items: routed — (expert, 16 consecutive pairs of it, weight rows); shared —
+// (8 tokens, weight rows), its 16 activation rows being the hi / lo halves of
+// the split activations interleaved (t hi, t lo, ...), so that each lane's
+// four outputs are (t, hi), (t, lo), (t+1, hi), (t+1, lo) and the halves are
+// summed in-lane.
+template <int PHASE>
+__global__ __launch_bounds__(256) void k_expert_q4k(ExpertJob job)
+{
+    constexpr int R = PHASE == 0 ? 2 : RT_DOWN;
+    constexpr int ROWS = PHASE == 0 ? 16 : 16 * RT_DOWN;      // weight rows per item
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int wave = blockIdx.x * WPB + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * WPB;
+    const int K = job.top_k, N = job.n_tokens;
+    const int rg = job.rows / ROWS;
+    const int rg_sh = job.rows_sh / ROWS;
+    const int routed_items = job.wl.n_ec[0] * rg;
+    const int nch_sh = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
+    const int total = routed_items + nch_sh * rg_sh;
+
+    for (int item = wave; item < total; item += nwaves) {
+        const bool shared = item >= routed_items;
+        int row0, arowA, arowD[4], orow[4], nt;
+        const uint8_t *wrow[R];
+        float acc[R][4];
+        if (!shared) {
+            const int ec = item / rg;
+            row0 = (item - ec * rg) * ROWS;
+            const int e = job.wl.ec_expert[ec];
+            const int c0 = job.wl.ec_chunk[ec] * EXPERT_CHUNK;
+            const int t_first = job.offsets[e] + c0;
+            nt = min(EXPERT_CHUNK, job.counts[e] - c0);
+            {
+                const int p = job.perm[t_first + min(r16, nt - 1)];
+                arowA = PHASE == 1 ? p : p / K;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = job.perm[t_first + min(4 * g + i, nt - 1)];
+                arowD[i] = PHASE == 1 ? p : p / K;
+                orow[i] = p;
+            }
+            if (PHASE == 0) {
+                wrow[0] = job.w0.data + (size_t)e * job.w0.nb2 + (size_t)(row0 + r16) * job.w0.nb1;
+                wrow[R - 1] = job.w1.data + (size_t)e * job.w1.nb2 + (size_t)(row0 + r16) * job.w1.nb1;
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    wrow[r] = job.w0.data + (size_t)e * job.w0.nb2 +
+                              (size_t)(row0 + 16 * r + r16) * job.w0.nb1;
+            }
+            run_item<R>(wrow, job.act, arowA, arowD, g, acc);
+        } else {
+            const int j = item - routed_items;
+            const int ch = j / rg_sh;
+            row0 = (j - ch * rg_sh) * ROWS;
+            const int t_first = ch * SHARED_CHUNK;
+            nt = min(SHARED_CHUNK, N - t_first);
+            // activation rows: hi half of token t is row t, lo half is row N + t
+            arowA = t_first + min(r16 >> 1, nt - 1) + (r16 & 1) * N;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = t_first + min(2 * g + (i >> 1), nt - 1);
+                arowD[i] = t + (i & 1) * N;
+                orow[i] = t;
+            }
+            if (PHASE == 0) {
+                wrow[0] = job.s0.data + (size_t)(row0 + r16) * job.s0.nb1;
+                wrow[R - 1] = job.s1.data + (size_t)(row0 + r16) * job.s1.nb1;
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    wrow[r] = job.s0.data + (size_t)(row0 + 16 * r + r16) * job.s0.nb1;
+            }
+            run_item<R>(wrow, job.act_sh, arowA, arowD, g, acc);
+        }
+
+        float *out = shared ? job.out_sh : job.out;
+        const int orows = shared ? job.rows_sh : job.rows;
+        if (!shared) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (4 * g + i >= nt) continue;
+                float *o = out + (size_t)orow[i] * orows + row0 + r16;
+                if (PHASE == 0) {
+                    o[0] = silu(acc[0][i]) * acc[R - 1][i];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; r++) o[16 * r] = acc[r][i];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                if (2 * g + (i >> 1) >= nt) continue;
+                float *o = out + (size_t)orow[i] * orows + row0 + r16;
+                if (PHASE == 0) {
+                    o[0] = silu(acc[0][i] + acc[0][i + 1]) * (acc[R - 1][i] + acc[R - 1][i + 1]);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; r++) o[16 * r] = acc[r][i] + acc[r][i + 1];
+                }
+            }
+        }
+    }
+}
+
+hipError_t launch_expert_q4k(int phase, const ExpertJob &job, hipStream_t s)
+{
+    const int rows_item = phase == 0 ? 16 : 16 * RT_DOWN;
+    if (job.rows % rows_item || (job.has_shared && job.rows_sh % rows_item) || job.act.K % 256)
+        return hipErrorInvalidValue;
+    const int blocks = 1024;
+    if (phase == 0)
+        hipLaunchKernelGGL(k_expert_q4k<0>, dim3(blocks), dim3(WPB * 64), 0, s, job);
+    else
+        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(blocks), dim3(WPB * 64), 0, s, job);
+    return hipGetLastError();
+}
+
+} // namespace dmoe
