@@ -267,8 +267,11 @@ struct Workspace {
 // with reduction lengths that are whole super-blocks.
 bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared)
 {
+    // whole super-blocks along K, whole work items along the output rows
+    const int gu = expert_rows_per_item(0), dn = expert_rows_per_item(1);
     if (wtype != DMOE_TYPE_Q4_K || hp.n_embd % 256 || hp.moe_ff % 256) return false;
-    if (shared && (stype != DMOE_TYPE_Q4_K || hp.shared_ff % 256)) return false;
+    if (hp.moe_ff % gu || hp.n_embd % dn) return false;
+    if (shared && (stype != DMOE_TYPE_Q4_K || hp.shared_ff % 256 || hp.shared_ff % gu)) return false;
     return true;
 }
 
@@ -516,12 +519,45 @@ int copy_debug(dmoe_ctx *ctx, const dmoe_hparams &hp, const Workspace &w, int N,
     return DMOE_OK;
 }
 
+// Rewrites one Q4_K tensor into the tiled layout the MFMA kernels stream
+// (16-row tiles, super-block-major) in a library-owned buffer; a previous
+// library-owned copy is released.
+int tile_tensor(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int mats)
+{
+    const size_t bytes = (size_t)rows * (K / 256) * Q4K_BYTES * mats;
+    void *dev = nullptr;
+    HIP_TRY(ctx, hipMalloc(&dev, bytes));
+    L->owned.push_back(dev);
+    HIP_TRY(ctx, launch_tile_q4k(t.data, t.nb1, t.nb2, rows, K, mats, (uint8_t *)dev, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    auto it = std::find(L->owned.begin(), L->owned.end(), (void *)t.data);
+    if (it != L->owned.end()) {
+        HIP_TRY(ctx, hipFree(*it));
+        L->owned.erase(it);
+    }
+    t.data = (const uint8_t *)dev;
+    t.nb1 = Q4K_BYTES;
+    t.nb2 = (size_t)rows * (K / 256) * Q4K_BYTES;
+    return DMOE_OK;
+}
+
 int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmoe_layer_desc *d)
 {
     L->hp = *hp;
     L->has_shared = hp->n_shared > 0 && d->sh_gate.data != nullptr;
     if (!L->has_shared) L->hp.shared_ff = 0;
-    (void)ctx;
+    if (use_mfma_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) {
+        const int H = hp->n_embd, E = hp->n_experts, FF = hp->moe_ff, SF = L->hp.shared_ff;
+        int rc;
+        if ((rc = tile_tensor(ctx, L, L->eg, FF, H, E))) return rc;
+        if ((rc = tile_tensor(ctx, L, L->eu, FF, H, E))) return rc;
+        if ((rc = tile_tensor(ctx, L, L->ed, H, FF, E))) return rc;
+        if (L->has_shared) {
+            if ((rc = tile_tensor(ctx, L, L->sg, SF, H, 1))) return rc;
+            if ((rc = tile_tensor(ctx, L, L->su, SF, H, 1))) return rc;
+            if ((rc = tile_tensor(ctx, L, L->sd, H, SF, 1))) return rc;
+        }
+    }
     return DMOE_OK;
 }
 

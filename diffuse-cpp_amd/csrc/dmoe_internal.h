@@ -130,6 +130,10 @@ hipError_t launch_prep_act(const float *src, int rows, int K, int mode, const Ac
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
 constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
 hipError_t launch_expert_q4k(int phase, const ExpertJob &job, hipStream_t s);
+int expert_rows_per_item(int phase);     // output rows one work item covers
+// Q4_K row layout -> tiled layout of k_expert.hip (k_quant.hip)
+hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
+                           uint8_t *dst, hipStream_t s);
 
 hipError_t launch_act_quant(const float *src, int rows, int n, const ActBuf &dst,
                             hipStream_t s);

@@ -23,8 +23,13 @@
 // it into the mantissa of 1024.0, and one packed fma subtracts the offset and
 // applies sc exactly: (1024+q)*sc - 1024*sc = q*sc.
 //
-// Work: item = (expert, up to 16 pairs of it, 16 weight rows x R tiles); the
-// wave streams those rows' super-blocks once.
+// Memory.  Weights are in the tiled layout (k_quant.hip: 16-row tiles,
+// super-block-major), so a tile's super-block is one contiguous 2304-byte run
+// and every weight load of a wave is coalesced.  A workgroup's four waves work
+// on the same 16 activation rows (one expert's chunk of pairs, or 8 tokens of
+// the shared expert) and different weight tiles; the activation tile of each
+// super-block is loaded once per workgroup into double-buffered LDS while the
+// previous super-block is computed.
 #include "dmoe_internal.h"
 
 namespace dmoe {
@@ -34,8 +39,20 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int WPB = 4;           // waves per workgroup
-constexpr int RT_DOWN = 2;       // 16-row tiles per down item
+// Tuning constants (measured on MI355X; overridable at compile time).
+#ifndef DMOE_X_RT_DOWN
+#define DMOE_X_RT_DOWN 2         // 16-row tiles per wave in the down phase
+#endif
+#ifndef DMOE_X_PREFETCH
+#define DMOE_X_PREFETCH 1        // keep the next super-block's weights in flight
+#endif
+#ifndef DMOE_X_BLOCKS
+#define DMOE_X_BLOCKS 1024       // persistent grid
+#endif
+constexpr int WAVES = 4;                 // waves per workgroup
+constexpr int RT_DOWN = DMOE_X_RT_DOWN;
+constexpr int A_ROW = 264;               // f16 per LDS activation row (256 + pad)
+constexpr int TILE_BYTES = 16 * Q4K_BYTES;   // one tile x one super-block
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __device__ __forceinline__ float h16f(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (uint16_t)u); }
@@ -45,9 +62,10 @@ struct Q4KTile {        // a lane's share of one 16-row tile in one super-block
     uint4 q0, q1;       // qs bytes 32g .. 32g+31
 };
 
-__device__ __forceinline__ void load_tile(Q4KTile &t, const uint8_t *row, int sb, int g)
+// tile: base of the tile's super-block runs; lane row r16, group g
+__device__ __forceinline__ void load_tile(Q4KTile &t, const uint8_t *tile, int sb, int r16, int g)
 {
-    const uint8_t *blk = row + (size_t)sb * Q4K_BYTES;
+    const uint8_t *blk = tile + (size_t)sb * TILE_BYTES + r16 * Q4K_BYTES;
     t.h = *reinterpret_cast<const uint4 *>(blk);
     const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * g);
     t.q0 = qp[0];
@@ -100,128 +118,187 @@ __device__ __forceinline__ void dequant_tile(const Q4KTile &t, int g, Q4KOps &o)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
-// Accumulate the item's R weight tiles against one 16-row activation tile over
-// all super-blocks.  arowA: activation row this lane feeds as srcA; arowD[i]:
-// activation row of output row 4g+i (for its per-super-block scale).
+// One super-block of the 16 activation rows of a work item, in LDS.
+struct ATile {
+    uint16_t v[16][A_ROW];      // f16 values in operand order (row padded)
+    uint16_t bs[16][16];        // sums of 16
+    float d[16];                // per-row super-block scale
+};
+
+// A thread's share of the per-super-block copy of the activation tile into LDS:
+// value pieces p0 = tid, p1 = tid + 256 (row p/32, 16-byte column p%32), the
+// bs piece for tid < 32 (row tid/2, half tid%2), the scale for tid in 32..47.
+struct AFeed {
+    int rv0, rv1, rbs, rd;      // activation rows (global) of those pieces
+    uint4 v0, v1, bs;
+    float d;
+};
+
+__device__ __forceinline__ void feed_load(AFeed &f, const ActMfma &act, int sb, int tid)
+{
+    const int K = act.K, nsb = K / 256;
+    f.v0 = *reinterpret_cast<const uint4 *>(act.v + (size_t)f.rv0 * K + sb * 256 + (tid & 31) * 8);
+    f.v1 = *reinterpret_cast<const uint4 *>(act.v + (size_t)f.rv1 * K + sb * 256 + (tid & 31) * 8);
+    if (tid < 32)
+        f.bs = *reinterpret_cast<const uint4 *>(act.bs + (size_t)f.rbs * (K / 16) + sb * 16 + (tid & 1) * 8);
+    else if (tid < 48)
+        f.d = act.d[(size_t)f.rd * nsb + sb];
+}
+
+__device__ __forceinline__ void feed_store(const AFeed &f, ATile &a, int tid)
+{
+    *reinterpret_cast<uint4 *>(&a.v[tid >> 5][(tid & 31) * 8]) = f.v0;
+    *reinterpret_cast<uint4 *>(&a.v[(tid >> 5) + 8][(tid & 31) * 8]) = f.v1;
+    if (tid < 32)
+        *reinterpret_cast<uint4 *>(&a.bs[tid >> 1][(tid & 1) * 8]) = f.bs;
+    else if (tid < 48)
+        a.d[tid - 32] = f.d;
+}
+
+// Accumulate R weight tiles (tile[r]: base of the tile's super-block runs)
+// against the item's activation rows, all super-blocks.
 template <int R>
-__device__ __forceinline__ void run_item(const uint8_t *const (&wrow)[R], const ActMfma &act,
-                                         int arowA, const int (&arowD)[4], int g,
+__device__ __forceinline__ void run_item(const uint8_t *const (&tile)[R], const ActMfma &act,
+                                         AFeed &feed, ATile (&sa)[2], int tid, int r16, int g,
                                          float (&acc)[R][4])
 {
-    const int K = act.K;
-    const int nsb = K / 256;
+    const int nsb = act.K / 256;
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[r][i] = 0.0f;
 
+    feed_load(feed, act, 0, tid);
+    feed_store(feed, sa[0], tid);
+    Q4KTile cur[R];
+#if DMOE_X_PREFETCH
+    Q4KTile nxt[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) load_tile(nxt[r], tile[r], 0, r16, g);
+#endif
+    __syncthreads();
+
     for (int sb = 0; sb < nsb; sb++) {
-        Q4KTile cur[R];
+        const int buf = sb & 1;
+#if DMOE_X_PREFETCH
 #pragma unroll
-        for (int r = 0; r < R; r++) load_tile(cur[r], wrow[r], sb, g);
-        const size_t vo = (size_t)arowA * K + sb * 256 + g * 64;
-        const size_t bo = (size_t)arowA * (K / 16) + sb * 16 + 4 * g;
-        float dx[4];
+        for (int r = 0; r < R; r++) cur[r] = nxt[r];
+#else
 #pragma unroll
-        for (int i = 0; i < 4; i++) dx[i] = act.d[(size_t)arowD[i] * nsb + sb];
-        h8 a[8];
-        const uint4 *av = reinterpret_cast<const uint4 *>(act.v + vo);
+        for (int r = 0; r < R; r++) load_tile(cur[r], tile[r], sb, r16, g);
+#endif
+        if (sb + 1 < nsb) {
+            feed_load(feed, act, sb + 1, tid);
+#if DMOE_X_PREFETCH
 #pragma unroll
-        for (int s = 0; s < 8; s++) a[s] = __builtin_bit_cast(h8, av[s]);
-        const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(act.bs + bo));
+            for (int r = 0; r < R; r++) load_tile(nxt[r], tile[r], sb + 1, r16, g);
+#endif
+        }
+        const ATile &a = sa[buf];
+        const float4 dxv = *reinterpret_cast<const float4 *>(&a.d[4 * g]);
+        const float dx[4] = {dxv.x, dxv.y, dxv.z, dxv.w};
+        const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(&a.bs[r16][4 * g]));
 #pragma unroll
         for (int r = 0; r < R; r++) {
             Q4KOps o;
             dequant_tile(cur[r], g, o);
             f4 s1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < 8; s++)
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], o.b[s], s1, 0, 0, 0);
+            for (int s = 0; s < 8; s++) {
+                const h8 av = __builtin_bit_cast(
+                    h8, *reinterpret_cast<const uint4 *>(&a.v[r16][g * 64 + s * 8]));
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, o.b[s], s1, 0, 0, 0);
+            }
             f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
             s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, o.bm, s2, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[r][i] += dx[i] * (o.d * s1[i] - o.dmin * s2[i]);
         }
+        if (sb + 1 < nsb) feed_store(feed, sa[buf ^ 1], tid);
+        __syncthreads();
     }
 }
 
-// Items: routed — (expert, 16 consecutive pairs of it, weight rows); shared —
-// (8 tokens, weight rows), its 16 activation rows being the hi / lo halves of
-// the split activations interleaved (t hi, t lo, ...), so that each lane's
-// four outputs are (t, hi), (t, lo), (t+1, hi), (t+1, lo) and the halves are
-// summed in-lane.
+// Workgroup items: routed — (expert, up to 16 consecutive pairs of it, a group
+// of weight rows); shared — (8 tokens, a group of weight rows), its 16
+// activation rows being the hi / lo halves of the split activations
+// interleaved (t hi, t lo, ...), so that each lane's four outputs are
+// (t, hi), (t, lo), (t+1, hi), (t+1, lo) and the halves are summed in-lane.
 template <int PHASE>
-__global__ __launch_bounds__(256) void k_expert_q4k(ExpertJob job)
+__global__ __launch_bounds__(WAVES * 64) void k_expert_q4k(ExpertJob job)
 {
-    constexpr int R = PHASE == 0 ? 2 : RT_DOWN;
-    constexpr int ROWS = PHASE == 0 ? 16 : 16 * RT_DOWN;      // weight rows per item
-    const int lane = threadIdx.x & 63;
+    constexpr int R = PHASE == 0 ? 2 : RT_DOWN;             // weight tiles per wave
+    constexpr int WROWS = PHASE == 0 ? 16 : 16 * RT_DOWN;   // weight rows per wave
+    constexpr int GROWS = WAVES * WROWS;                    // weight rows per item
+    __shared__ ATile sa[2];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r16 = lane & 15;
-    const int wave = blockIdx.x * WPB + (threadIdx.x >> 6);
-    const int nwaves = gridDim.x * WPB;
     const int K = job.top_k, N = job.n_tokens;
-    const int rg = job.rows / ROWS;
-    const int rg_sh = job.rows_sh / ROWS;
+    const int rg = job.rows / GROWS;
+    const int rg_sh = job.rows_sh / GROWS;
     const int routed_items = job.wl.n_ec[0] * rg;
     const int nch_sh = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
     const int total = routed_items + nch_sh * rg_sh;
+    const int nsb = job.act.K / 256, nsb_sh = job.act_sh.K / 256;
 
-    for (int item = wave; item < total; item += nwaves) {
+    for (int item = blockIdx.x; item < total; item += gridDim.x) {
         const bool shared = item >= routed_items;
-        int row0, arowA, arowD[4], orow[4], nt;
-        const uint8_t *wrow[R];
-        float acc[R][4];
+        int row0, nt, t_first, e = 0;
         if (!shared) {
             const int ec = item / rg;
-            row0 = (item - ec * rg) * ROWS;
-            const int e = job.wl.ec_expert[ec];
+            row0 = (item - ec * rg) * GROWS + wave * WROWS;
+            e = job.wl.ec_expert[ec];
             const int c0 = job.wl.ec_chunk[ec] * EXPERT_CHUNK;
-            const int t_first = job.offsets[e] + c0;
+            t_first = job.offsets[e] + c0;
             nt = min(EXPERT_CHUNK, job.counts[e] - c0);
-            {
-                const int p = job.perm[t_first + min(r16, nt - 1)];
-                arowA = PHASE == 1 ? p : p / K;
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = job.perm[t_first + min(4 * g + i, nt - 1)];
-                arowD[i] = PHASE == 1 ? p : p / K;
-                orow[i] = p;
-            }
-            if (PHASE == 0) {
-                wrow[0] = job.w0.data + (size_t)e * job.w0.nb2 + (size_t)(row0 + r16) * job.w0.nb1;
-                wrow[R - 1] = job.w1.data + (size_t)e * job.w1.nb2 + (size_t)(row0 + r16) * job.w1.nb1;
-            } else {
-#pragma unroll
-                for (int r = 0; r < R; r++)
-                    wrow[r] = job.w0.data + (size_t)e * job.w0.nb2 +
-                              (size_t)(row0 + 16 * r + r16) * job.w0.nb1;
-            }
-            run_item<R>(wrow, job.act, arowA, arowD, g, acc);
         } else {
             const int j = item - routed_items;
             const int ch = j / rg_sh;
-            row0 = (j - ch * rg_sh) * ROWS;
-            const int t_first = ch * SHARED_CHUNK;
+            row0 = (j - ch * rg_sh) * GROWS + wave * WROWS;
+            t_first = ch * SHARED_CHUNK;
             nt = min(SHARED_CHUNK, N - t_first);
-            // activation rows: hi half of token t is row t, lo half is row N + t
-            arowA = t_first + min(r16 >> 1, nt - 1) + (r16 & 1) * N;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = t_first + min(2 * g + (i >> 1), nt - 1);
-                arowD[i] = t + (i & 1) * N;
-                orow[i] = t;
-            }
-            if (PHASE == 0) {
-                wrow[0] = job.s0.data + (size_t)(row0 + r16) * job.s0.nb1;
-                wrow[R - 1] = job.s1.data + (size_t)(row0 + r16) * job.s1.nb1;
-            } else {
-#pragma unroll
-                for (int r = 0; r < R; r++)
-                    wrow[r] = job.s0.data + (size_t)(row0 + 16 * r + r16) * job.s0.nb1;
-            }
-            run_item<R>(wrow, job.act_sh, arowA, arowD, g, acc);
         }
+        // activation row of item row j (0..15)
+        auto arow = [&](int j) {
+            if (shared) return t_first + min(j >> 1, nt - 1) + (j & 1) * N;
+            const int p = job.perm[t_first + min(j, nt - 1)];
+            return PHASE == 1 ? p : p / K;
+        };
+        AFeed feed;
+        feed.rv0 = arow(tid >> 5);
+        feed.rv1 = arow((tid >> 5) + 8);
+        feed.rbs = arow((tid >> 1) & 15);
+        feed.rd = arow(tid >= 32 && tid < 48 ? tid - 32 : 0);
+        // output rows of this lane's four results
+        int orow[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (shared)
+                orow[i] = t_first + min(2 * g + (i >> 1), nt - 1);
+            else
+                orow[i] = job.perm[t_first + min(4 * g + i, nt - 1)];
+        }
+        // this wave's weight tiles
+        const uint8_t *tile[R];
+        if (PHASE == 0) {
+            const WTensor &a = shared ? job.s0 : job.w0;
+            const WTensor &b = shared ? job.s1 : job.w1;
+            const int n = shared ? nsb_sh : nsb;
+            const size_t ea = shared ? 0 : (size_t)e * a.nb2, eb = shared ? 0 : (size_t)e * b.nb2;
+            tile[0] = a.data + ea + (size_t)(row0 / 16) * n * TILE_BYTES;
+            tile[R - 1] = b.data + eb + (size_t)(row0 / 16) * n * TILE_BYTES;
+        } else {
+            const WTensor &a = shared ? job.s0 : job.w0;
+            const int n = shared ? nsb_sh : nsb;
+            const size_t ea = shared ? 0 : (size_t)e * a.nb2;
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                tile[r] = a.data + ea + (size_t)(row0 / 16 + r) * n * TILE_BYTES;
+        }
+        float acc[R][4];
+        run_item<R>(tile, shared ? job.act_sh : job.act, feed, sa, tid, r16, g, acc);
 
         float *out = shared ? job.out_sh : job.out;
         const int orows = shared ? job.rows_sh : job.rows;
@@ -253,16 +330,17 @@ __global__ __launch_bounds__(256) void k_expert_q4k(ExpertJob job)
     }
 }
 
+int expert_rows_per_item(int phase) { return WAVES * (phase == 0 ? 16 : 16 * RT_DOWN); }
+
 hipError_t launch_expert_q4k(int phase, const ExpertJob &job, hipStream_t s)
 {
-    const int rows_item = phase == 0 ? 16 : 16 * RT_DOWN;
+    const int rows_item = expert_rows_per_item(phase);
     if (job.rows % rows_item || (job.has_shared && job.rows_sh % rows_item) || job.act.K % 256)
         return hipErrorInvalidValue;
-    const int blocks = 1024;
     if (phase == 0)
-        hipLaunchKernelGGL(k_expert_q4k<0>, dim3(blocks), dim3(WPB * 64), 0, s, job);
+        hipLaunchKernelGGL(k_expert_q4k<0>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
     else
-        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(blocks), dim3(WPB * 64), 0, s, job);
+        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
     return hipGetLastError();
 }
 

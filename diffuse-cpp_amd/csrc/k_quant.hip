@@ -245,6 +245,43 @@ __global__ __launch_bounds__(256) void k_wq_f16(const float *__restrict__ src, i
     if (i < total) dst[i] = f32_to_f16_bits(src[i]);
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K row layout -> tiled layout: per matrix, 16-row tiles; inside a tile the
+// super-blocks come first, so the 16 rows' blocks of one super-block are one
+// contiguous 2304-byte run:  dst offset of (row r, super-block sb) =
+//   ((r/16) * nsb + sb) * 2304 + (r%16) * 144.
+// The block bytes themselves are unchanged.  One thread per 16-byte piece.
+__global__ __launch_bounds__(256) void k_tile_q4k(const uint8_t *__restrict__ src, size_t nb1,
+                                                  size_t nb2, int rows, int nsb, int mats,
+                                                  uint8_t *__restrict__ dst)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t per_mat = (size_t)rows * nsb * 9;          // 16-byte pieces per matrix
+    if (i >= per_mat * mats) return;
+    const int m = (int)(i / per_mat);
+    size_t j = i - (size_t)m * per_mat;
+    const int piece = (int)(j % 9);
+    j /= 9;
+    const int sb = (int)(j % nsb);
+    const int r = (int)(j / nsb);
+    const uint4 v = *reinterpret_cast<const uint4 *>(src + (size_t)m * nb2 + (size_t)r * nb1 +
+                                                     (size_t)sb * Q4K_BYTES + piece * 16);
+    const size_t o = (size_t)m * rows * nsb * Q4K_BYTES +
+                     ((size_t)(r / 16) * nsb + sb) * (16 * Q4K_BYTES) + (size_t)(r % 16) * Q4K_BYTES +
+                     piece * 16;
+    *reinterpret_cast<uint4 *>(dst + o) = v;
+}
+
+hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
+                           uint8_t *dst, hipStream_t s)
+{
+    if (rows % 16 || K % 256 || nb1 % 16 || (mats > 1 && nb2 % 16)) return hipErrorInvalidValue;
+    const size_t total = (size_t)rows * (K / 256) * 9 * mats;
+    hipLaunchKernelGGL(k_tile_q4k, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
+                       nb1, nb2, rows, K / 256, mats, dst);
+    return hipGetLastError();
+}
+
 hipError_t launch_quantize_weights(int32_t type, const float *src, void *dst, int64_t nrows,
                                    int64_t n_per_row, hipStream_t s)
 {
