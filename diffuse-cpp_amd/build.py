@@ -37,7 +37,7 @@ CFLAGS = [
 ]
 
 SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "dmoe_api.cpp"]
-HEADERS = ["dmoe_internal.h"]
+HEADERS = ["dmoe_internal.h", "dmoe_device.h"]
 
 
 def _needs(obj: Path, deps: list[Path]) -> bool:

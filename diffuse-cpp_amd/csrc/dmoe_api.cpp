@@ -41,6 +41,7 @@ struct dmoe_layer {
     dmoe_hparams hp{};
     float *gate_w = nullptr;       // [E][H] f32
     float *gate_bias = nullptr;    // [E] or null
+    int32_t bias_small = 1;        // no bias, or every bias finite with |bias| < 1e19
     WTensor eg{}, eu{}, ed{};
     WTensor sg{}, su{}, sd{};
     bool has_shared = false;
@@ -261,6 +262,7 @@ struct Workspace {
     ActMfma ax, axs, ah, ahs;            // MFMA-path activations (routed / shared)
     float *h, *ye, *hs, *ys;
     float *bias;
+    int32_t *counter;                    // zeroed once at allocation; routing leaves it zeroed
 };
 
 // The MFMA expert path covers Q4_K routed experts (and a Q4_K shared expert)
@@ -309,11 +311,13 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         return p;
     };
     Workspace t{};
+    t.counter = (int32_t *)take(4);
     t.x = (float *)take((size_t)N * H * 4);
     t.y = (float *)take((size_t)N * H * 4);
     t.bias = (float *)take((size_t)E * 4);
     t.rb.logits = (float *)take((size_t)N * E * 4);
     t.rb.probs = (float *)take((size_t)N * E * 4);
+    t.rb.sel = (float *)take((size_t)N * E * 4);
     t.rb.bmax = (float *)take((size_t)B * E * 4);
     t.rb.thr = (float *)take((size_t)B * 4);
     t.rb.allowed = (uint8_t *)take((size_t)B * E);
@@ -370,14 +374,18 @@ int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, Workspace *w)
             return set_err(ctx, DMOE_ERR_OOM, "workspace allocation of %zu bytes refused (DMOE_FAIL_ALLOC)", need);
         HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
         ctx->ws_bytes = need;
+        // the routing counter sits first in every carve-up
+        HIP_TRY(ctx, hipMemset(ctx->ws, 0, 256));
     }
     plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
 }
 
-RouteParams route_params(const dmoe_hparams &hp, int N)
+RouteParams route_params(const dmoe_layer *L, const dmoe_hparams &hp, int N)
 {
-    RouteParams rp;
+    RouteParams rp{};
+    rp.bias = L ? L->gate_bias : nullptr;
+    rp.bias_small = L ? L->bias_small : 0;
     rp.n_tokens = N;
     rp.n_experts = hp.n_experts;
     rp.top_k = hp.top_k;
@@ -392,10 +400,10 @@ RouteParams route_params(const dmoe_hparams &hp, int N)
 }
 
 const char *const kStageNames[DMOE_N_STAGES] = {
-    "router_logits", "route", "dispatch", "act_quant_x", "gateup_routed",
+    "front", "route", "scores", "act_quant_x", "gateup_routed",
     "act_quant_h", "down_routed", "gateup_shared", "down_shared", "combine"};
 
-enum { ST_LOGITS, ST_ROUTE, ST_DISPATCH, ST_ACTQ_X, ST_GATEUP, ST_ACTQ_H, ST_DOWN, ST_SH_GATEUP,
+enum { ST_FRONT, ST_ROUTE, ST_SCORES, ST_ACTQ_X, ST_GATEUP, ST_ACTQ_H, ST_DOWN, ST_SH_GATEUP,
        ST_SH_DOWN, ST_COMBINE };
 
 hipEvent_t take_event(dmoe_ctx *ctx)
@@ -436,12 +444,20 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
 {
     const dmoe_hparams &hp = L->hp;
     const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
-    const RouteParams rp = route_params(hp, N);
+    const RouteParams rp = route_params(L, hp, N);
+    const bool mfma = use_mfma_path(hp, L->eg.type, L->sg.type, L->has_shared);
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, id, s, [&] { return call; }))
-    STAGE(ST_LOGITS, launch_router_logits(L->gate_w, x, N, H, E, w.rb.logits, s));
-    STAGE(ST_ROUTE, launch_route(rp, w.rb.logits, L->gate_bias, w.rb, s));
-    STAGE(ST_DISPATCH, launch_dispatch(rp, w.rb, w.wl, s));
-    if (use_mfma_path(hp, L->eg.type, L->sg.type, L->has_shared)) {
+    // router logits, sigmoid, selection scores (+ x in the MFMA operand layout)
+    PrepJob xj[2];
+    int nxj = 0;
+    if (mfma) {
+        xj[nxj++] = PrepJob{x, N, H, ACT_Q8K, w.ax};
+        if (L->has_shared) xj[nxj++] = PrepJob{x, N, H, ACT_SPLIT, w.axs};
+    }
+    STAGE(ST_FRONT, launch_front(L->gate_w, L->gate_bias, x, N, H, E, w.rb, xj, nxj, s));
+    // block routing, top-k, gate weights and the dispatch
+    STAGE(ST_ROUTE, launch_route(rp, w.rb, w.wl, w.counter, s));
+    if (mfma) {
         // Q4_K experts on MFMA: routed experts and the shared one share a launch
         const int SF = hp.shared_ff;
         ExpertJob job{};
@@ -452,8 +468,6 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.offsets = w.rb.offsets;
         job.counts = w.rb.counts;
         job.wl = w.wl;
-        STAGE(ST_ACTQ_X, launch_prep_act(x, N, H, ACT_Q8K, w.ax, s));
-        if (L->has_shared) STAGE(ST_ACTQ_X, launch_prep_act(x, N, H, ACT_SPLIT, w.axs, s));
         job.w0 = L->eg;
         job.w1 = L->eu;
         job.s0 = L->sg;
@@ -465,8 +479,11 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.out = w.h;
         job.out_sh = w.hs;
         STAGE(ST_GATEUP, launch_expert_q4k(0, job, s));
-        STAGE(ST_ACTQ_H, launch_prep_act(w.h, N * K, FF, ACT_Q8K, w.ah, s));
-        if (L->has_shared) STAGE(ST_ACTQ_H, launch_prep_act(w.hs, N, SF, ACT_SPLIT, w.ahs, s));
+        PrepJob hj[2];
+        int nhj = 0;
+        hj[nhj++] = PrepJob{w.h, N * K, FF, ACT_Q8K, w.ah};
+        if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, SF, ACT_SPLIT, w.ahs};
+        STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
         job.w0 = L->ed;
         job.s0 = L->sd;
         job.act = w.ah;
@@ -499,7 +516,7 @@ int copy_debug(dmoe_ctx *ctx, const dmoe_hparams &hp, const Workspace &w, int N,
 {
     if (!dbg) return DMOE_OK;
     const int E = hp.n_experts, K = hp.top_k, P = N * K;
-    const RouteParams rp = route_params(hp, N);
+    const RouteParams rp = route_params(nullptr, hp, N);
     const int B = rp.use_block ? N / hp.block_size : 0;
     auto cp = [&](void *dst, const void *src, size_t bytes) -> hipError_t {
         if (!dst || bytes == 0) return hipSuccess;
@@ -544,6 +561,15 @@ int tile_tensor(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int m
 int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmoe_layer_desc *d)
 {
     L->hp = *hp;
+    // Routing keeps a per-token candidate list only when adding the -1e30
+    // mask to a selection score cannot be absorbed by a huge bias.
+    L->bias_small = 1;
+    if (L->gate_bias) {
+        std::vector<float> b(hp->n_experts);
+        HIP_TRY(ctx, hipMemcpy(b.data(), L->gate_bias, b.size() * 4, hipMemcpyDeviceToHost));
+        for (float v : b)
+            if (!(std::fabs(v) < 1e19f)) L->bias_small = 0;
+    }
     L->has_shared = hp->n_shared > 0 && d->sh_gate.data != nullptr;
     if (!L->has_shared) L->hp.shared_ff = 0;
     if (use_mfma_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) {
@@ -663,7 +689,7 @@ int dmoe_layer_upload(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_layer_de
         if ((rc = upload_tensor(ctx, L, d->sh_up, hp->shared_ff, 1, L->su))) return fail(rc);
         if ((rc = upload_tensor(ctx, L, d->sh_down, H, 1, L->sd))) return fail(rc);
     }
-    finish_layer(ctx, L, hp, d);
+    if ((rc = finish_layer(ctx, L, hp, d))) return fail(rc);
     *out = L;
     return DMOE_OK;
 }
@@ -688,7 +714,10 @@ int dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_lay
         L->su = wrap_tensor(d->sh_up);
         L->sd = wrap_tensor(d->sh_down);
     }
-    finish_layer(ctx, L, hp, d);
+    if ((rc = finish_layer(ctx, L, hp, d))) {
+        dmoe_layer_free(L);
+        return rc;
+    }
     *out = L;
     return DMOE_OK;
 }
@@ -767,9 +796,14 @@ int dmoe_route_logits(dmoe_ctx *ctx, const dmoe_hparams *hp, const float *bias,
         HIP_TRY(ctx, hipMemcpyAsync(w.bias, bias, (size_t)E * 4, hipMemcpyHostToDevice, s));
         dbias = w.bias;
     }
-    const RouteParams rp = route_params(*hp, n_tokens);
-    LAUNCH_TRY(ctx, launch_route(rp, w.rb.logits, dbias, w.rb, s));
-    LAUNCH_TRY(ctx, launch_dispatch(rp, w.rb, w.wl, s));
+    RouteParams rp = route_params(nullptr, *hp, n_tokens);
+    rp.bias = dbias;
+    rp.bias_small = 1;
+    if (bias)
+        for (int e = 0; e < E; e++)
+            if (!(std::fabs(bias[e]) < 1e19f)) rp.bias_small = 0;
+    LAUNCH_TRY(ctx, launch_scores(w.rb.logits, dbias, n_tokens, E, w.rb, s));
+    LAUNCH_TRY(ctx, launch_route(rp, w.rb, w.wl, w.counter, s));
     dmoe_debug d2 = dbg ? *dbg : dmoe_debug{};
     d2.logits = nullptr;
     if ((rc = copy_debug(ctx, *hp, w, n_tokens, &d2, s))) return rc;

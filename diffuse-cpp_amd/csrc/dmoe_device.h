@@ -1,0 +1,86 @@
+// dmoe_device.h — device helpers shared by the routing and activation kernels.
+//
+// Everything here is bit-deterministic: single IEEE operations in a fixed
+// order (the including file disables contraction), binary64 exp built from
+// add/mul/fma/rint only, correctly rounded division.
+#pragma once
+
+#include "dmoe_internal.h"
+
+namespace dmoe {
+
+// exp(x) in binary64 rounded once to binary32.  Cody-Waite reduction
+// x = k ln2 + r (ln2 split into a 32-significant-bit head and a tail, so k*head
+// is exact), exp(r) by its degree-13 Taylor polynomial in Horner form with
+// fma, then scaling by 2^k through the exponent field.
+__device__ __forceinline__ double exp_f64(double x)
+{
+    const double inv_ln2 = 1.4426950408889634;
+    const double ln2_hi = 6.93147180369123816490e-01;
+    const double ln2_lo = 1.90821492927058770002e-10;
+    double kd = rint(x * inv_ln2);
+    double r = fma(-kd, ln2_hi, x);
+    r = fma(-kd, ln2_lo, r);
+    double p = 1.0 / 6227020800.0;
+    p = fma(p, r, 1.0 / 479001600.0);
+    p = fma(p, r, 1.0 / 39916800.0);
+    p = fma(p, r, 1.0 / 3628800.0);
+    p = fma(p, r, 1.0 / 362880.0);
+    p = fma(p, r, 1.0 / 40320.0);
+    p = fma(p, r, 1.0 / 5040.0);
+    p = fma(p, r, 1.0 / 720.0);
+    p = fma(p, r, 1.0 / 120.0);
+    p = fma(p, r, 1.0 / 24.0);
+    p = fma(p, r, 1.0 / 6.0);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    long long k = (long long)kd;
+    double two_k = __longlong_as_double((long long)((unsigned long long)(k + 1023) << 52));
+    return p * two_k;
+}
+
+__device__ __forceinline__ float exp_f32(float x)
+{
+    if (x != x) return x;
+    // exp(100) overflows binary32 and exp(-110) rounds to 0: clamping keeps
+    // every result and keeps k in the normal binary64 exponent range.
+    x = x > 100.0f ? 100.0f : x;
+    x = x < -110.0f ? -110.0f : x;
+    return (float)exp_f64((double)x);
+}
+
+// ggml_sigmoid (src/diffuse-moe-graph.cpp:204)
+__device__ __forceinline__ float sigmoid_f32(float x)
+{
+    return 1.0f / (1.0f + exp_f32(-x));
+}
+
+// Descending-value order with ties to the lower expert id; NaN sorts last and
+// -0 equals +0.
+__device__ __forceinline__ uint32_t order_key(float f)
+{
+    if (f != f) return 0u;
+    if (f == 0.0f) f = 0.0f;
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ bool ranks_before(uint32_t ka, int ea, uint32_t kb, int eb)
+{
+    return ka > kb || (ka == kb && ea < eb);
+}
+
+// round half to even for |v| < 2^22 (the magic-number rounding ggml uses)
+__device__ __forceinline__ int nearest_int(float v)
+{
+    const float t = v + 12582912.0f;
+    return (int)(__float_as_uint(t) & 0x007fffffu) - 0x00400000;
+}
+
+__device__ __forceinline__ uint16_t f2h(float f)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+} // namespace dmoe

@@ -55,6 +55,7 @@ struct RouteBufs {
     int32_t *perm;      // [N*K]
     int32_t *hist;      // [groups][E] pairs of each routing group per expert
     int32_t *lrank;     // [N*K] rank of a pair among its group's pairs of its expert
+    float *sel;         // [N][E] selection scores probs + bias
 };
 
 // Group scores kept in LDS by the routing kernel (group tokens x experts).
@@ -110,21 +111,34 @@ struct RouteParams {
     int32_t use_block;      // block routing on (diffuse-moe-graph.cpp:215-216)
     int32_t norm_topk_prob;
     float routed_scaling;
+    int32_t bias_small;     // no bias, or every bias finite with |bias| < 1e19
+    const float *bias;      // [E] or null
 };
 
 // ---------------------------------------------------------------------------
 // Kernel launchers (each returns the hipGetLastError of its launch).
-hipError_t launch_router_logits(const float *W, const float *x, int N, int H, int E,
-                                float *logits, hipStream_t s);
-hipError_t launch_route(const RouteParams &rp, const float *logits, const float *bias,
-                        const RouteBufs &rb, hipStream_t s);
-hipError_t launch_dispatch(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
-                           hipStream_t s);
+// Routing + dispatch (k_router.hip).  counter: a zeroed int the last routing
+// group uses to elect itself (left zeroed again).
+hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
+                        int32_t *counter, hipStream_t s);
 bool route_fits_lds(const RouteParams &rp);
 
-// Activations -> MFMA operand layout (k_prep.hip); K % 256 == 0.
-hipError_t launch_prep_act(const float *src, int rows, int K, int mode, const ActMfma &out,
-                           hipStream_t s);
+// One activation conversion into the MFMA operand layout.
+struct PrepJob {
+    const float *src;
+    int32_t rows, K, mode;   // K % 256 == 0
+    ActMfma out;
+};
+// Front kernel (k_prep.hip): router logits L = Wg x in one fixed fp32 order,
+// probs = sigmoid(L), sel = probs + bias, plus up to two activation
+// conversions of x, in one launch.
+hipError_t launch_front(const float *W, const float *bias, const float *x, int N, int H, int E,
+                        const RouteBufs &rb, const PrepJob *jobs, int njobs, hipStream_t s);
+// probs and sel from given logits (routing-only entry point)
+hipError_t launch_scores(const float *logits, const float *bias, int N, int E,
+                         const RouteBufs &rb, hipStream_t s);
+// Up to two activation conversions in one launch.
+hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s);
 // Grouped Q4_K expert products on MFMA (k_expert.hip).  phase 0: h = silu(gate x)
 // * (up x); phase 1: y = down h.
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item

@@ -1,32 +1,27 @@
-// k_prep.hip — activations into the MFMA operand layout of k_expert.hip.
+// k_prep.hip — the front of the layer and the activation conversions.
+//
+// Front kernel, one launch over three kinds of workgroups:
+//   * router logits L = Wg x (src/diffuse-moe-graph.cpp:203) in one fixed fp32
+//     summation order, with probs = sigmoid(L) (:204) and the selection score
+//     sel = probs + bias (:207-210) computed by the lane that owns each logit;
+//   * up to two conversions of x into the MFMA operand layout of k_expert.hip.
 //
 // ACT_Q8K reproduces ggml's Q8_K conversion of the activations that
-// ggml_mul_mat_id performs before Q4_K dots (src/diffuse-moe-graph.cpp:266-269):
-// per 256 values, the value of largest magnitude (lowest index on ties) maps
-// to -127, iscale = -127/max, q = min(127, nearest_even(iscale*x)),
-// d = 1/iscale, plus sums of 16 quants.  The quants are small integers, exact
-// in f16, so the MFMA products below are exact integer dots.
+// ggml_mul_mat_id performs before Q4_K dots (:266-269): per 256 values, the
+// value of largest magnitude (lowest index on ties) maps to -127,
+// iscale = -127/max, q = min(127, nearest_even(iscale*x)), d = 1/iscale, plus
+// sums of 16 quants.  The quants are small integers, exact in f16.
 //
 // ACT_SPLIT keeps f32 activations (the shared expert, whose weights the
 // reference casts to F32, :8-12, :282-284): per super-block the values are
 // scaled by 2^k into [2^9, 2^10) in magnitude and split into hi = f16(v) and
-// lo = f16(v - hi), about 22 significant bits; d = 2^-k.
-#include "dmoe_internal.h"
+// lo = f16(v - hi), about 22 significant bits; d = 2^-k.  The lo halves are
+// written as rows `rows`..2*rows-1.
+#include "dmoe_device.h"
 
 #pragma clang fp contract(off)
 
 namespace dmoe {
-
-__device__ __forceinline__ uint16_t f2h(float f)
-{
-    return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
-
-__device__ __forceinline__ int nearest_int(float v)
-{
-    const float t = v + 12582912.0f;
-    return (int)(__float_as_uint(t) & 0x007fffffu) - 0x00400000;
-}
 
 // Position p (0..255) of the operand layout -> value index inside the super-block.
 __device__ __forceinline__ int src_index(int p)
@@ -36,19 +31,14 @@ __device__ __forceinline__ int src_index(int p)
     return 64 * g + 32 * (e >> 2) + 4 * s + perm;
 }
 
-// One wavefront per (row, super-block); 4 waves per workgroup.
-__global__ __launch_bounds__(256) void k_prep_act(const float *__restrict__ src, int rows, int K,
-                                                  int mode, ActMfma out)
+// One wavefront converts one (row, super-block) of a job.  sv: 256 floats of LDS.
+__device__ void prep_wave(const PrepJob &job, int wid, float *sv)
 {
-    __shared__ float s_v[4][256];
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int nsb = K / 256;
-    const int wid = blockIdx.x * 4 + w;
-    if (wid >= rows * nsb) return;
+    const int K = job.K, rows = job.rows, nsb = K / 256;
     const int row = wid / nsb, sb = wid - row * nsb;
-    const float *x = src + (size_t)row * K + sb * 256;
-    float *sv = s_v[w];
+    const float *x = job.src + (size_t)row * K + sb * 256;
+    const ActMfma &out = job.out;
 
     float v[4];
     float amax = -1.0f;
@@ -68,7 +58,7 @@ __global__ __launch_bounds__(256) void k_prep_act(const float *__restrict__ src,
 
     const size_t vbase = (size_t)row * K + sb * 256;
     const size_t bbase = (size_t)row * (K / 16) + sb * 16;
-    if (mode == ACT_Q8K) {
+    if (job.mode == ACT_Q8K) {
         float dscale = 0.0f;
         if (amax != 0.0f) {
             const float iscale = -127.0f / x[aidx];
@@ -132,18 +122,197 @@ __global__ __launch_bounds__(256) void k_prep_act(const float *__restrict__ src,
         }
         if (lane == 0) {
             out.d[(size_t)row * nsb + sb] = dinv;             // hi row
-            out.d[(size_t)(rows + row) * nsb + sb] = dinv;    // lo row (v_lo = v + rows*K)
+            out.d[(size_t)(rows + row) * nsb + sb] = dinv;    // lo row
         }
     }
 }
 
-hipError_t launch_prep_act(const float *src, int rows, int K, int mode, const ActMfma &out,
-                           hipStream_t s)
+// ---------------------------------------------------------------------------
+// Router logits.  One wavefront per (2 experts, 4 tokens).  For every
+// (token, expert) lane l keeps one partial:  a_l = fma(W[k], x[k], a_l) for
+// k = 256*i + 4*l + j, i ascending then j = 0..3; the 64 partials are then
+// combined by six xor butterfly rounds (m = 32..1), after which every lane
+// holds the same value (each round adds the same two operands in both
+// partner lanes).  Lane t*LG_E + e then computes sigmoid and the score.
+constexpr int LG_E = 2, LG_T = 4;
+
+__device__ void logits_wave(const float *__restrict__ W, const float *__restrict__ bias,
+                            const float *__restrict__ x, int N, int H, int E, int wave,
+                            const RouteBufs &rb)
 {
-    if (K % 256 || rows <= 0) return hipErrorInvalidValue;
-    const int waves = rows * (K / 256);
-    hipLaunchKernelGGL(k_prep_act, dim3((waves + 3) / 4), dim3(256), 0, s, src, rows, K, mode,
-                       out);
+    const int lane = threadIdx.x & 63;
+    const int ne = (E + LG_E - 1) / LG_E;
+    const int e0 = (wave % ne) * LG_E;
+    const int t0 = (wave / ne) * LG_T;
+
+    float acc[LG_T][LG_E];
+#pragma unroll
+    for (int t = 0; t < LG_T; t++)
+#pragma unroll
+        for (int e = 0; e < LG_E; e++) acc[t][e] = 0.0f;
+
+    const float4 *wr[LG_E];
+    const float4 *xr[LG_T];
+#pragma unroll
+    for (int e = 0; e < LG_E; e++)
+        wr[e] = reinterpret_cast<const float4 *>(W + (size_t)min(e0 + e, E - 1) * H);
+#pragma unroll
+    for (int t = 0; t < LG_T; t++)
+        xr[t] = reinterpret_cast<const float4 *>(x + (size_t)min(t0 + t, N - 1) * H);
+
+#pragma unroll 4
+    for (int i = 0; i < H / 256; i++) {
+        float4 w[LG_E], xv[LG_T];
+#pragma unroll
+        for (int e = 0; e < LG_E; e++) w[e] = wr[e][i * 64 + lane];
+#pragma unroll
+        for (int t = 0; t < LG_T; t++) xv[t] = xr[t][i * 64 + lane];
+#pragma unroll
+        for (int t = 0; t < LG_T; t++)
+#pragma unroll
+            for (int e = 0; e < LG_E; e++) {
+                float a = acc[t][e];
+                a = __builtin_fmaf(w[e].x, xv[t].x, a);
+                a = __builtin_fmaf(w[e].y, xv[t].y, a);
+                a = __builtin_fmaf(w[e].z, xv[t].z, a);
+                a = __builtin_fmaf(w[e].w, xv[t].w, a);
+                acc[t][e] = a;
+            }
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int t = 0; t < LG_T; t++)
+#pragma unroll
+        for (int e = 0; e < LG_E; e++) {
+            float v = acc[t][e];
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+            if (lane == t * LG_E + e) mine = v;
+        }
+    const int t = lane / LG_E, e = lane % LG_E;
+    if (lane < LG_T * LG_E && t0 + t < N && e0 + e < E) {
+        const size_t o = (size_t)(t0 + t) * E + e0 + e;
+        const float p = sigmoid_f32(mine);
+        rb.logits[o] = mine;
+        rb.probs[o] = p;
+        rb.sel[o] = bias ? p + bias[e0 + e] : p;
+    }
+}
+
+__device__ __forceinline__ int prep_blocks(const PrepJob &j)
+{
+    return (j.rows * (j.K / 256) + 3) / 4;
+}
+
+struct FrontArgs {
+    const float *W, *bias, *x;
+    int N, H, E, logit_blocks;
+    RouteBufs rb;
+    PrepJob job[2];
+    int njobs;
+};
+
+__global__ __launch_bounds__(256) void k_front(FrontArgs a)
+{
+    __shared__ float s_v[4][256];
+    const int w = threadIdx.x >> 6;
+    int b = blockIdx.x;
+    if (b < a.logit_blocks) {
+        const int wave = b * 4 + w;
+        const int nw = ((a.E + LG_E - 1) / LG_E) * ((a.N + LG_T - 1) / LG_T);
+        if (wave < nw) logits_wave(a.W, a.bias, a.x, a.N, a.H, a.E, wave, a.rb);
+        return;
+    }
+    b -= a.logit_blocks;
+    for (int j = 0; j < a.njobs; j++) {
+        const int nb = prep_blocks(a.job[j]);
+        if (b < nb) {
+            const int wid = b * 4 + w;
+            if (wid < a.job[j].rows * (a.job[j].K / 256)) prep_wave(a.job[j], wid, s_v[w]);
+            return;
+        }
+        b -= nb;
+    }
+}
+
+hipError_t launch_front(const float *W, const float *bias, const float *x, int N, int H, int E,
+                        const RouteBufs &rb, const PrepJob *jobs, int njobs, hipStream_t s)
+{
+    FrontArgs a{};
+    a.W = W;
+    a.bias = bias;
+    a.x = x;
+    a.N = N;
+    a.H = H;
+    a.E = E;
+    a.rb = rb;
+    const int nw = ((E + LG_E - 1) / LG_E) * ((N + LG_T - 1) / LG_T);
+    a.logit_blocks = (nw + 3) / 4;
+    int blocks = a.logit_blocks;
+    a.njobs = njobs;
+    for (int j = 0; j < njobs; j++) {
+        if (jobs[j].K % 256) return hipErrorInvalidValue;
+        a.job[j] = jobs[j];
+        blocks += (jobs[j].rows * (jobs[j].K / 256) + 3) / 4;
+    }
+    hipLaunchKernelGGL(k_front, dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+struct PrepArgs {
+    PrepJob job[2];
+    int njobs;
+};
+
+__global__ __launch_bounds__(256) void k_prep(PrepArgs a)
+{
+    __shared__ float s_v[4][256];
+    const int w = threadIdx.x >> 6;
+    int b = blockIdx.x;
+    for (int j = 0; j < a.njobs; j++) {
+        const int nb = prep_blocks(a.job[j]);
+        if (b < nb) {
+            const int wid = b * 4 + w;
+            if (wid < a.job[j].rows * (a.job[j].K / 256)) prep_wave(a.job[j], wid, s_v[w]);
+            return;
+        }
+        b -= nb;
+    }
+}
+
+hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s)
+{
+    PrepArgs a{};
+    a.njobs = njobs;
+    int blocks = 0;
+    for (int j = 0; j < njobs; j++) {
+        if (jobs[j].K % 256 || jobs[j].rows <= 0) return hipErrorInvalidValue;
+        a.job[j] = jobs[j];
+        blocks += (jobs[j].rows * (jobs[j].K / 256) + 3) / 4;
+    }
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_prep, dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// probs and sel from given logits
+__global__ __launch_bounds__(256) void k_scores(const float *__restrict__ logits,
+                                                const float *__restrict__ bias, int N, int E,
+                                                RouteBufs rb)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)N * E) return;
+    const float p = sigmoid_f32(logits[i]);
+    rb.probs[i] = p;
+    rb.sel[i] = bias ? p + bias[i % E] : p;
+}
+
+hipError_t launch_scores(const float *logits, const float *bias, int N, int E,
+                         const RouteBufs &rb, hipStream_t s)
+{
+    const size_t total = (size_t)N * E;
+    hipLaunchKernelGGL(k_scores, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, logits,
+                       bias, N, E, rb);
     return hipGetLastError();
 }
 

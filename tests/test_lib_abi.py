@@ -93,5 +93,5 @@ def test_null_context_is_rejected():
     lib.dmoe_destroy(None)
     lib.dmoe_layer_free(None)
     names = [lib.dmoe_stage_name(i).decode() for i in range(dmoe.N_STAGES)]
-    assert names[0] == "router_logits" and "gateup_routed" in names
+    assert names[0] == "front" and "gateup_routed" in names
     assert lib.dmoe_stage_name(99) == b""
