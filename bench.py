@@ -40,7 +40,21 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the bench, run 5 plain device copies of this many MiB "
+                         "(the calibration kernel of the HBM-traffic counters)")
     return ap.parse_args()
+
+
+def traffic_from_profile(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
+    f = ROOT / "profiles" / f"{kernel}_{workload}_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def main():
@@ -105,11 +119,19 @@ def main():
     ctx.profile(False)
     stages = {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.items()}   # us per launch
 
-    # algorithmic bytes of the dominant kernel (routed gate/up): the touched
-    # experts' gate and up matrices, the quantised activations, h written
+    # algorithmic bytes of the dominant kernel, the gate/up launch (routed
+    # experts and the shared expert in one launch): the touched experts' and
+    # the shared expert's gate and up matrices, the activations in their MFMA
+    # layout (f16 values, f16 sums of 16, f32 scale per 256; the shared
+    # expert's in hi/lo pairs), h and the shared h written as f32
     rs_h = dmoe.row_size(cfg.wtype, H)
-    act_bytes = N * (H + 4 * (H // 256) + 2 * (H // 16)) if cfg.wtype == dmoe.TYPE_Q4_K else N * H * 2
-    gu_bytes = touched * 2 * FF * rs_h + act_bytes + N * K * FF * 4
+    SF = cfg.shared_ff
+    act_row = H * 2 + (H // 16) * 2 + (H // 256) * 4
+    if cfg.wtype == dmoe.TYPE_Q4_K:
+        gu_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + N * act_row + 2 * N * act_row
+                    + N * K * FF * 4 + N * SF * 4)
+    else:
+        gu_bytes = touched * 2 * FF * rs_h + N * H * 2 + N * K * FF * 4
     gu_us = stages.get("gateup_routed")
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9 if gu_us else None
 
@@ -150,8 +172,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-            "traffic": None,
+            "traffic": traffic_from_profile("gateup_routed", cfg.name),
             "algorithmic_bytes": gu_bytes,
+            "hip_kernel": "dmoe::k_expert_q4k<0>" if cfg.wtype == dmoe.TYPE_Q4_K else "dmoe::k_gateup_routed",
             "us_per_launch": gu_us,
         },
         "layer": {
@@ -190,6 +213,15 @@ def main():
         torch.cuda.synchronize(dev)
         err = float(np.abs(y.cpu().numpy() - yr).max() / np.abs(yr).max())
         out["check_max_rel_err_vs_oracle"] = err
+
+    if a.copy_probe_mib:
+        n = a.copy_probe_mib * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        out["copy_probe_bytes"] = n * 4
 
     print(json.dumps(out))
 

@@ -71,6 +71,13 @@ __device__ __forceinline__ bool ranks_before(uint32_t ka, int ea, uint32_t kb, i
     return ka > kb || (ka == kb && ea < eb);
 }
 
+// order_key and expert id in one integer: a larger value ranks first, and
+// equal scores rank the lower expert id first (ids below 65536).
+__device__ __forceinline__ uint64_t rank_key(uint32_t key, int e)
+{
+    return ((uint64_t)key << 32) | (uint32_t)(0xFFFFu - (uint32_t)e);
+}
+
 // round half to even for |v| < 2^22 (the magic-number rounding ggml uses)
 __device__ __forceinline__ int nearest_int(float v)
 {

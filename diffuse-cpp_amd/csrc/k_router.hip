@@ -24,12 +24,16 @@ constexpr int MAX_E = 1024;     // experts per layer supported by these kernels
 constexpr int MAX_K = 32;       // top_k supported by these kernels
 constexpr int RT_THREADS = 1024;
 constexpr int RT_WAVES = RT_THREADS / 64;
+// token bitmasks per expert: E * ceil(G/32) words, with G*E <= ROUTE_LDS and E <= 1024
+constexpr int RT_BITS = ROUTE_LDS / 32 + MAX_E;
+// a group has at most ROUTE_LDS / 8 pairs, one per thread
+static_assert(ROUTE_LDS / 8 <= RT_THREADS, "one thread per pair of a routing group");
 
 // Block-wide exclusive scan of one int per thread (blockDim.x == 1024).
 // Returns the exclusive prefix; *total receives the sum.
 __device__ __forceinline__ int block_scan(int v, int *s_tmp, int *total)
 {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int x = v;
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
@@ -38,33 +42,25 @@ __device__ __forceinline__ int block_scan(int v, int *s_tmp, int *total)
     }
     if (lane == 63) s_tmp[w] = x;
     __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int i = 0; i < RT_WAVES; i++) {
-            const int t = s_tmp[i];
-            s_tmp[i] = run;
-            run += t;
-        }
-        s_tmp[RT_WAVES] = run;
+    // every thread adds the wavefront totals itself (independent LDS reads)
+    int before = 0, all = 0;
+#pragma unroll
+    for (int i = 0; i < RT_WAVES; i++) {
+        const int t = s_tmp[i];
+        before += i < w ? t : 0;
+        all += t;
     }
-    __syncthreads();
-    const int excl = s_tmp[w] + x - v;
-    *total = s_tmp[RT_WAVES];
-    __syncthreads();
-    return excl;
+    *total = all;
+    __syncthreads();            // s_tmp is reused by the next scan
+    return before + x - v;
 }
 
-// Dispatch of one forward, run by the last routing group (all 1024 threads).
-__device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
-                             int *s_tmp, int *s_off)
+// Counts, offsets and the expert-chunk work list from each thread's pair
+// count c (threads tid < E), all 1024 threads.  s_off receives the offsets.
+__device__ void dispatch_lists(int c, const RouteParams &rp, const RouteBufs &rb,
+                               const WorkList &wl, int *s_tmp, int *s_off)
 {
-    const int E = rp.n_experts, K = rp.top_k, N = rp.n_tokens;
-    const int G = rp.use_block ? rp.block_size : 32;
-    const int ngroups = (N + G - 1) / G;
-    const int tid = threadIdx.x;
-    int c = 0;
-    if (tid < E)
-        for (int g = 0; g < ngroups; g++) c += rb.hist[(size_t)g * E + tid];
+    const int E = rp.n_experts, tid = threadIdx.x;
     int total;
     const int off = block_scan(c, s_tmp, &total);
     const int nch = (c + wl.chunk - 1) / wl.chunk;
@@ -84,6 +80,23 @@ __device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const W
         wl.n_ec[0] = nec;
     }
     __syncthreads();
+}
+
+// Dispatch of one forward over several routing groups, run by the last group
+// to finish (all 1024 threads), from the groups' histograms and local ranks.
+__device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
+                             int *s_tmp, int *s_off)
+{
+    const int E = rp.n_experts, K = rp.top_k, N = rp.n_tokens;
+    const int G = rp.use_block ? rp.block_size : 32;
+    const int ngroups = (N + G - 1) / G;
+    const int tid = threadIdx.x;
+    int c = 0;
+    if (tid < E) {
+#pragma unroll 8
+        for (int g = 0; g < ngroups; g++) c += rb.hist[(size_t)g * E + tid];
+    }
+    dispatch_lists(c, rp, rb, wl, s_tmp, s_off);
     const int P = N * K;
     for (int p = tid; p < P; p += RT_THREADS) {
         const int g = (p / K) / G;
@@ -94,15 +107,59 @@ __device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const W
     }
 }
 
+// One wavefront: the bmax at position cap-1 of the descending order (ties to
+// the lower expert id).  Lane l keeps the order keys of experts l + 64 r.  A
+// most-significant-bit-first radix select finds the cap-th largest key P
+// (counts by ballot); the expert at position cap-1 is then the
+// (cap - 1 - #{keys > P})-th lowest id among the experts whose key is P.
+template <int R>
+__device__ void find_threshold(int E, int cap, const uint64_t *s_rk, const float *s_bmax,
+                               float *s_thr)
+{
+    const int lane = threadIdx.x & 63;
+    uint32_t k[R];
+    uint64_t valid[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int f = lane + 64 * r;
+        k[r] = f < E ? (uint32_t)(s_rk[f] >> 32) : 0u;
+        valid[r] = __ballot(f < E);
+    }
+    uint32_t P = 0;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t cand = P | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int r = 0; r < R; r++) cnt += __popcll(__ballot(k[r] >= cand) & valid[r]);
+        if (cnt >= cap) P = cand;
+    }
+    int n = cap - 1;
+#pragma unroll
+    for (int r = 0; r < R; r++) n -= __popcll(__ballot(k[r] > P) & valid[r]);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        uint64_t m = __ballot(k[r] == P) & valid[r];
+        const int c = __popcll(m);
+        if (n >= 0 && n < c) {
+            for (int i = 0; i < n; i++) m &= m - 1;
+            const int f = __builtin_ctzll(m) + 64 * r;
+            if (lane == 0) *s_thr = s_bmax[f];
+        }
+        n -= c;
+    }
+}
+
 __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs rb, WorkList wl,
                                                       int32_t *counter)
 {
     __shared__ uint32_t s_key[ROUTE_LDS];         // group scores, then sel' keys
     __shared__ float s_bmax[MAX_E];
-    __shared__ uint32_t s_bkey[MAX_E];
+    __shared__ uint64_t s_rk[MAX_E];              // rank keys of the block maxima
     __shared__ int32_t s_cand[MAX_E];
-    __shared__ int32_t s_slot[RT_WAVES][MAX_K];
     __shared__ int32_t s_idx[ROUTE_LDS / 8];      // group pairs (tokens x slots)
+    __shared__ float s_w[ROUTE_LDS / 8];          // their probs
+    __shared__ uint64_t s_k64[RT_WAVES][64];      // per wavefront: candidate rank keys
+    __shared__ uint32_t s_bits[RT_BITS];          // [e][word]: tokens of the group that chose e
     __shared__ int s_tmp[RT_WAVES + 1];
     __shared__ float s_thr;
     __shared__ int s_nan, s_nc, s_last;
@@ -113,15 +170,33 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     const int t0 = g * G;
     const int nt = min(N, t0 + G) - t0;
     const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int words = (G + 31) / 32;
     float *s_sel = reinterpret_cast<float *>(s_key);
 
     if (tid == 0) s_nan = 0;
+    for (int i = tid; i < E * words; i += RT_THREADS) s_bits[i] = 0u;
     __syncthreads();
-    // selection scores of the group (sel = probs + bias, :207-210)
-    for (int i = tid; i < nt * E; i += RT_THREADS) {
-        const float v = rb.sel[(size_t)t0 * E + i];
-        s_sel[i] = v;
-        if (v != v) s_nan = 1;
+    // selection scores of the group (sel = probs + bias, :207-210); every
+    // load is issued before the first is used
+    {
+        constexpr int R = ROUTE_LDS / RT_THREADS;
+        const int n = nt * E;
+        const float *src = rb.sel + (size_t)t0 * E;
+        float v[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = tid + r * RT_THREADS;
+            v[r] = i < n ? src[i] : 0.0f;
+        }
+        bool nan = false;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = tid + r * RT_THREADS;
+            if (i < n) s_sel[i] = v[r];
+            nan |= v[r] != v[r];
+        }
+        if (nan) s_nan = 1;
     }
     __syncthreads();
 
@@ -137,16 +212,16 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
                 m = sj + r;
             }
             s_bmax[e] = m;
-            s_bkey[e] = order_key(m);
+            s_rk[e] = rank_key(order_key(m), e);
         }
         __syncthreads();
         // :232-236  thr = the cap-th largest bmax (position cap-1 of the
-        // descending order); exactly one expert has that rank
-        for (int e = tid; e < E; e += RT_THREADS) {
-            const uint32_t ke = s_bkey[e];
-            int rank = 0;
-            for (int f = 0; f < E; f++) rank += ranks_before(s_bkey[f], f, ke, e);
-            if (rank == rp.capacity - 1) s_thr = s_bmax[e];
+        // descending order, ties to the lower expert id), found by wavefront 0
+        if (wave == 0) {
+            if (E <= 256)
+                find_threshold<4>(E, rp.capacity, s_rk, s_bmax, &s_thr);
+            else
+                find_threshold<MAX_E / 64>(E, rp.capacity, s_rk, s_bmax, &s_thr);
         }
         __syncthreads();
         // :241-248  keep = step(bmax - (thr + -1e-6)); sel' = sel + (0 | -1e30)
@@ -164,9 +239,17 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
         // allowed experts alone when there are at least k of them.
         restrict_cand = rp.bias_small && !s_nan && nallowed >= K;
         if (restrict_cand && keep) s_cand[pos] = tid;
-        const float add = (float)keep * 1e30f + (-1e30f);
-        for (int t = 0; t < nt; t++)
-            if (tid < E) s_key[t * E + tid] = order_key(s_sel[t * E + tid] + add);
+        if (RT_THREADS % E == 0) {
+            // every thread converts the scores of one expert
+            const int e = tid % E;
+            const float add = (float)((s_bmax[e] - tp) > 0.0f) * 1e30f + (-1e30f);
+            for (int t = tid / E; t < nt; t += RT_THREADS / E)
+                s_key[t * E + e] = order_key(s_sel[t * E + e] + add);
+        } else {
+            const float add = (float)keep * 1e30f + (-1e30f);
+            for (int t = 0; t < nt; t++)
+                if (tid < E) s_key[t * E + tid] = order_key(s_sel[t * E + tid] + add);
+        }
         if (tid == 0) s_nc = restrict_cand ? nallowed : E;
     } else {
         for (int i = tid; i < nt * E; i += RT_THREADS) s_key[i] = order_key(s_sel[i]);
@@ -178,64 +261,89 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
 
     // :252  top-k: a candidate's slot is its rank among the token's candidates
     // (descending sel', ties to the lower expert id)
-    const int lane = tid & 63, wave = tid >> 6;
     const int nc = s_nc;
+    const int my_e = lane < nc ? s_cand[lane] : 0;
     for (int t = wave; t < nt; t += RT_WAVES) {
         const uint32_t *kt = s_key + t * E;
-        for (int c = lane; c < nc; c += 64) {
-            const int e = s_cand[c];
-            const uint32_t k = kt[e];
+        if (nc <= 64) {
+            // lane c holds candidate c's rank key; every other key is an LDS
+            // broadcast and one 64-bit compare
+            const uint64_t mk = lane < nc ? rank_key(kt[my_e], my_e) : 0ull;
+            s_k64[wave][lane] = mk;
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             int rank = 0;
-            for (int c2 = 0; c2 < nc; c2++) {
-                const int e2 = s_cand[c2];
-                rank += ranks_before(kt[e2], e2, k, e);
+#pragma unroll 8
+            for (int c2 = 0; c2 < nc; c2++) rank += s_k64[wave][c2] > mk;
+            if (lane < nc && rank < K) s_idx[t * K + rank] = my_e;
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        } else {
+            for (int c = lane; c < nc; c += 64) {
+                const int e = s_cand[c];
+                const uint32_t k = kt[e];
+                int rank = 0;
+#pragma unroll 8
+                for (int c2 = 0; c2 < nc; c2++) {
+                    const int e2 = s_cand[c2];
+                    rank += ranks_before(kt[e2], e2, k, e);
+                }
+                if (rank < K) s_idx[t * K + rank] = e;
             }
-            if (rank < K) s_slot[wave][rank] = e;
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // :253-262  w = probs[idx]; w /= sum (binary64 row sum); w *= scale
-        const int mine = lane < K ? s_slot[wave][lane] : 0;
-        float w = lane < K ? rb.probs[(size_t)(t0 + t) * E + mine] : 0.0f;
-        double acc = 0.0;
-        for (int s = 0; s < K; s++) acc += (double)__shfl(w, s, 64);
-        if (lane < K) {
-            if (rp.norm_topk_prob) w = w / (float)acc;
-            if (rp.routed_scaling != 1.0f) w = w * rp.routed_scaling;
-            rb.idx[(size_t)(t0 + t) * K + lane] = mine;
-            rb.weights[(size_t)(t0 + t) * K + lane] = w;
-            s_idx[t * K + lane] = mine;
-        }
-        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
 
-    // group histogram and the rank of each pair among the group's pairs of the
-    // same expert (pairs in t-major, slot-minor order)
+    // :253-262  w = probs[idx]; w /= the token's sum (binary64, slot order);
+    // w *= scale.  Thread j owns pair j (token j / K, slot j % K).
     const int np = nt * K;
-    for (int e = tid; e < E; e += RT_THREADS) {
-        int c = 0;
-        for (int j = 0; j < np; j++) c += s_idx[j] == e;
-        rb.hist[(size_t)g * E + e] = c;
+    const int pt = tid / K;
+    int mine = 0;
+    float w = 0.0f;
+    if (tid < np) {
+        mine = s_idx[tid];
+        w = rb.probs[(size_t)(t0 + pt) * E + mine];
+        s_w[tid] = w;
+        atomicOr(&s_bits[mine * words + (pt >> 5)], 1u << (pt & 31));
     }
-    for (int j = tid; j < np; j += RT_THREADS) {
-        const int e = s_idx[j];
-        int r = 0;
-        for (int i = 0; i < j; i++) r += s_idx[i] == e;
-        rb.lrank[(size_t)t0 * K + j] = r;
+    __syncthreads();
+    int lr = 0;
+    if (tid < np) {
+        double acc = 0.0;
+        for (int q = 0; q < K; q++) acc += (double)s_w[pt * K + q];
+        if (rp.norm_topk_prob) w = w / (float)acc;
+        if (rp.routed_scaling != 1.0f) w = w * rp.routed_scaling;
+        rb.idx[(size_t)t0 * K + tid] = mine;
+        rb.weights[(size_t)t0 * K + tid] = w;
+        // rank of the pair among the group's pairs of the same expert (pairs
+        // in t-major, slot-minor order).  A token picks an expert at most
+        // once, so that rank counts the earlier tokens whose bit is set.
+        const uint32_t *bits = s_bits + mine * words;
+        lr = __popc(bits[pt >> 5] & ((1u << (pt & 31)) - 1u));
+        for (int wd = 0; wd < (pt >> 5); wd++) lr += __popc(bits[wd]);
     }
+    int c = 0;                               // pairs of expert tid in this group
+    if (tid < E)
+        for (int wd = 0; wd < words; wd++) c += __popc(s_bits[tid * words + wd]);
+
+    int *s_off = reinterpret_cast<int *>(s_rk);
+    if (gridDim.x == 1) {
+        // one routing group: the dispatch needs nothing beyond this block
+        dispatch_lists(c, rp, rb, wl, s_tmp, s_off);
+        if (tid < np) rb.perm[s_off[mine] + lr] = tid;
+        return;
+    }
+    if (tid < E) rb.hist[(size_t)g * E + tid] = c;
+    if (tid < np) rb.lrank[(size_t)t0 * K + tid] = lr;
 
     // the last group to finish runs the dispatch
     __threadfence();
     __syncthreads();
-    if (tid == 0) {
-        const int ngroups = (N + G - 1) / G;
-        s_last = atomicAdd(counter, 1) == ngroups - 1;
-    }
+    if (tid == 0) s_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    dispatch_all(rp, rb, wl, s_tmp, reinterpret_cast<int *>(s_bkey));
+    dispatch_all(rp, rb, wl, s_tmp, s_off);
     if (tid == 0) *counter = 0;
 }
 
