@@ -126,14 +126,18 @@ def main():
     # expert's in hi/lo pairs), h and the shared h written as f32
     rs_h = dmoe.row_size(cfg.wtype, H)
     SF = cfg.shared_ff
+    P = N * K
     act_row = H * 2 + (H // 16) * 2 + (H // 256) * 4
+    dom_stage = "gateup_routed"
     if cfg.wtype == dmoe.TYPE_Q4_K:
-        gu_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + N * act_row + 2 * N * act_row
-                    + N * K * FF * 4 + N * SF * 4)
+        dom_kernel = "dmoe::k_expert_q4k<0>"
+        dom_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + N * act_row + 2 * N * act_row
+                     + P * FF * 4 + N * SF * 4)
     else:
-        gu_bytes = touched * 2 * FF * rs_h + N * H * 2 + N * K * FF * 4
-    gu_us = stages.get("gateup_routed")
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9 if gu_us else None
+        dom_kernel = "dmoe::k_gateup_routed"
+        dom_bytes = touched * 2 * FF * rs_h + N * H * 2 + P * FF * 4
+    dom_us = stages.get(dom_stage)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9 if dom_us else None
 
     # layer-level: every weight byte the layer must read
     layer_bytes = touched * eb + sb + E * H * 4 + E * 4 + 2 * N * H * 4
@@ -167,15 +171,15 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gateup_routed",
+            "kernel": dom_stage,
             "achieved": round(achieved, 1) if achieved else None,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-            "traffic": traffic_from_profile("gateup_routed", cfg.name),
-            "algorithmic_bytes": gu_bytes,
-            "hip_kernel": "dmoe::k_expert_q4k<0>" if cfg.wtype == dmoe.TYPE_Q4_K else "dmoe::k_gateup_routed",
-            "us_per_launch": gu_us,
+            "traffic": traffic_from_profile(dom_stage, cfg.name),
+            "algorithmic_bytes": dom_bytes,
+            "hip_kernel": dom_kernel,
+            "us_per_launch": dom_us,
         },
         "layer": {
             "bytes": layer_bytes,

@@ -332,6 +332,7 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
     t.wl.n_ec = (int32_t *)take(4);
     t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
     t.wl.ec_chunk = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
+
     if (use_mfma_path(hp, wtype, stype, shared)) {
         t.ax = take_act(take, N, H, false);
         t.ah = take_act(take, P, FF, false);
@@ -459,39 +460,37 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
     STAGE(ST_ROUTE, launch_route(rp, w.rb, w.wl, w.counter, s));
     if (mfma) {
         // Q4_K experts on MFMA: routed experts and the shared one share a launch
-        const int SF = hp.shared_ff;
-        ExpertJob job{};
+        MoeJob job{};
+        job.eg = L->eg;
+        job.eu = L->eu;
+        job.ed = L->ed;
+        job.sg = L->sg;
+        job.su = L->su;
+        job.sd = L->sd;
         job.has_shared = L->has_shared;
+        job.H = H;
+        job.FF = FF;
+        job.SF = hp.shared_ff;
         job.n_tokens = N;
         job.top_k = K;
         job.perm = w.rb.perm;
         job.offsets = w.rb.offsets;
         job.counts = w.rb.counts;
         job.wl = w.wl;
-        job.w0 = L->eg;
-        job.w1 = L->eu;
-        job.s0 = L->sg;
-        job.s1 = L->su;
-        job.act = w.ax;
-        job.act_sh = w.axs;
-        job.rows = FF;
-        job.rows_sh = SF;
-        job.out = w.h;
-        job.out_sh = w.hs;
+        job.ax = w.ax;
+        job.axs = w.axs;
+        job.h = w.h;
+        job.hs = w.hs;
+        job.ah = w.ah;
+        job.ahs = w.ahs;
+        job.ye = w.ye;
+        job.ys = w.ys;
         STAGE(ST_GATEUP, launch_expert_q4k(0, job, s));
         PrepJob hj[2];
         int nhj = 0;
         hj[nhj++] = PrepJob{w.h, N * K, FF, ACT_Q8K, w.ah};
-        if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, SF, ACT_SPLIT, w.ahs};
+        if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, ACT_SPLIT, w.ahs};
         STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
-        job.w0 = L->ed;
-        job.s0 = L->sd;
-        job.act = w.ah;
-        job.act_sh = w.ahs;
-        job.rows = H;
-        job.rows_sh = H;
-        job.out = w.ye;
-        job.out_sh = w.ys;
         STAGE(ST_DOWN, launch_expert_q4k(1, job, s));
         STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
                                          K, H, y, s));

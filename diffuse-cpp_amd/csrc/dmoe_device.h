@@ -1,7 +1,7 @@
 // dmoe_device.h — device helpers shared by the routing and activation kernels.
 //
 // Everything here is bit-deterministic: single IEEE operations in a fixed
-// order (the including file disables contraction), binary64 exp built from
+// order (every function body disables contraction), binary64 exp built from
 // add/mul/fma/rint only, correctly rounded division.
 #pragma once
 
@@ -15,6 +15,7 @@ namespace dmoe {
 // fma, then scaling by 2^k through the exponent field.
 __device__ __forceinline__ double exp_f64(double x)
 {
+#pragma clang fp contract(off)
     const double inv_ln2 = 1.4426950408889634;
     const double ln2_hi = 6.93147180369123816490e-01;
     const double ln2_lo = 1.90821492927058770002e-10;
@@ -42,6 +43,7 @@ __device__ __forceinline__ double exp_f64(double x)
 
 __device__ __forceinline__ float exp_f32(float x)
 {
+#pragma clang fp contract(off)
     if (x != x) return x;
     // exp(100) overflows binary32 and exp(-110) rounds to 0: clamping keeps
     // every result and keeps k in the normal binary64 exponent range.
@@ -53,6 +55,7 @@ __device__ __forceinline__ float exp_f32(float x)
 // ggml_sigmoid (src/diffuse-moe-graph.cpp:204)
 __device__ __forceinline__ float sigmoid_f32(float x)
 {
+#pragma clang fp contract(off)
     return 1.0f / (1.0f + exp_f32(-x));
 }
 
@@ -81,6 +84,7 @@ __device__ __forceinline__ uint64_t rank_key(uint32_t key, int e)
 // round half to even for |v| < 2^22 (the magic-number rounding ggml uses)
 __device__ __forceinline__ int nearest_int(float v)
 {
+#pragma clang fp contract(off)
     const float t = v + 12582912.0f;
     return (int)(__float_as_uint(t) & 0x007fffffu) - 0x00400000;
 }

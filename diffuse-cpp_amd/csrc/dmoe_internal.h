@@ -91,19 +91,20 @@ struct ActMfma {
     float *d;           // [rows][K/256]
 };
 
-// One launch of the grouped expert kernel (routed experts + the shared one).
-struct ExpertJob {
-    WTensor w0, w1;      // routed: gate, up (phase 0) or down, unused (phase 1)
-    WTensor s0, s1;      // shared expert, same roles
+// The expert products of one forward (routed experts + the shared one),
+// k_expert.hip: phase 0 (gate/up) and phase 1 (down) launches.
+struct MoeJob {
+    WTensor eg, eu, ed;      // routed gate, up, down (tiled Q4_K)
+    WTensor sg, su, sd;      // shared expert
     int32_t has_shared;
-    ActMfma act;         // routed activations (rows: tokens in phase 0, pairs in phase 1)
-    ActMfma act_sh;      // shared activations (rows: tokens)
-    int32_t rows, rows_sh;   // output rows of one routed / shared matrix
+    int32_t H, FF, SF;       // n_embd, moe_ff, shared_ff
     int32_t n_tokens, top_k;
     const int32_t *perm, *offsets, *counts;
     WorkList wl;
-    float *out;          // phase 0: h [N*K][rows]; phase 1: ye [N*K][rows]
-    float *out_sh;       // phase 0: hs [N][rows_sh]; phase 1: ys [N][rows_sh]
+    ActMfma ax, axs;         // x converted: Q8_K (rows: tokens), split (shared)
+    float *h, *hs;           // gate/up results [N*K][FF], [N][SF]
+    ActMfma ah, ahs;         // h and hs converted for the down products
+    float *ye, *ys;          // down results [N*K][H], [N][H]
 };
 
 struct RouteParams {
@@ -143,7 +144,7 @@ hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s);
 // * (up x); phase 1: y = down h.
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
 constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
-hipError_t launch_expert_q4k(int phase, const ExpertJob &job, hipStream_t s);
+hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s);
 int expert_rows_per_item(int phase);     // output rows one work item covers
 // Q4_K row layout -> tiled layout of k_expert.hip (k_quant.hip)
 hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,

@@ -5,6 +5,7 @@
 // :280-286 (F32 activations), as one persistent launch per phase:
 //   phase 0: h = silu(W_gate x) * (W_up x)       (gate and up of the same rows)
 //   phase 1: y = W_down h
+// (the conversion of h to the activation layout runs in between, k_prep.hip).
 //
 // Arithmetic.  Per 256-value super-block, a Q4_K row is  w = d*sc_j*q - dmin*m_j
 // (j = 32-value sub-block).  With activations a (Q8_K quants, or scaled f32
@@ -39,18 +40,13 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-// Tuning constants (measured on MI355X; overridable at compile time).
-#ifndef DMOE_X_RT_DOWN
-#define DMOE_X_RT_DOWN 2         // 16-row tiles per wave in the down phase
-#endif
-#ifndef DMOE_X_PREFETCH
-#define DMOE_X_PREFETCH 1        // keep the next super-block's weights in flight
-#endif
-#ifndef DMOE_X_BLOCKS
-#define DMOE_X_BLOCKS 1024       // persistent grid
-#endif
 constexpr int WAVES = 4;                 // waves per workgroup
-constexpr int RT_DOWN = DMOE_X_RT_DOWN;
+constexpr int RT = 2;                    // 16-row weight tiles per wave
+constexpr int GROWS_GU = WAVES * 16;     // weight rows of a gate/up item (gate and up)
+constexpr int GROWS_DN = WAVES * 16 * RT;    // weight rows of a down item
+#ifndef DMOE_X_BLOCKS
+#define DMOE_X_BLOCKS 1024               // persistent grid
+#endif
 constexpr int A_ROW = 264;               // f16 per LDS activation row (256 + pad)
 constexpr int TILE_BYTES = 16 * Q4K_BYTES;   // one tile x one super-block
 
@@ -136,13 +132,14 @@ struct AFeed {
 
 __device__ __forceinline__ void feed_load(AFeed &f, const ActMfma &act, int sb, int tid)
 {
+    // every thread issues the same four loads (pieces it does not store read
+    // valid addresses), so the loads of a pipeline step are branch-free and
+    // the compiler's load counting keeps the next steps in flight
     const int K = act.K, nsb = K / 256;
     f.v0 = *reinterpret_cast<const uint4 *>(act.v + (size_t)f.rv0 * K + sb * 256 + (tid & 31) * 8);
     f.v1 = *reinterpret_cast<const uint4 *>(act.v + (size_t)f.rv1 * K + sb * 256 + (tid & 31) * 8);
-    if (tid < 32)
-        f.bs = *reinterpret_cast<const uint4 *>(act.bs + (size_t)f.rbs * (K / 16) + sb * 16 + (tid & 1) * 8);
-    else if (tid < 48)
-        f.d = act.d[(size_t)f.rd * nsb + sb];
+    f.bs = *reinterpret_cast<const uint4 *>(act.bs + (size_t)f.rbs * (K / 16) + sb * 16 + (tid & 1) * 8);
+    f.d = act.d[(size_t)f.rd * nsb + sb];
 }
 
 __device__ __forceinline__ void feed_store(const AFeed &f, ATile &a, int tid)
@@ -155,8 +152,54 @@ __device__ __forceinline__ void feed_store(const AFeed &f, ATile &a, int tid)
         a.d[tid - 32] = f.d;
 }
 
+// One super-block: R weight tiles against the activation tile a.
+template <int R>
+__device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[R], const ATile &a, int r16, int g,
+                                           float (&acc)[R][4])
+{
+    const float4 dxv = *reinterpret_cast<const float4 *>(&a.d[4 * g]);
+    const float dx[4] = {dxv.x, dxv.y, dxv.z, dxv.w};
+    const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(&a.bs[r16][4 * g]));
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        Q4KOps o;
+        dequant_tile(cur[r], g, o);
+        f4 s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const h8 av = __builtin_bit_cast(
+                h8, *reinterpret_cast<const uint4 *>(&a.v[r16][g * 64 + s * 8]));
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, o.b[s], s1, 0, 0, 0);
+        }
+        f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+        s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, o.bm, s2, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[r][i] += dx[i] * (o.d * s1[i] - o.dmin * s2[i]);
+    }
+}
+
+// One pipeline step: super-block s is computed from cur (skipped past the last
+// super-block) while the weights of s + 1 load into nxt and the activations of
+// s + 1 into the other LDS buffer.  Indices are clamped to the last
+// super-block, whose repeated loads hit the cache, so that every step issues
+// the same loads.
+template <int R>
+__device__ __forceinline__ void step_sb(const Q4KTile (&cur)[R], Q4KTile (&nxt)[R],
+                                        const uint8_t *const (&tile)[R], const ActMfma &act,
+                                        AFeed &feed, ATile (&sa)[2], int s, int nsb, int tid,
+                                        int r16, int g, float (&acc)[R][4])
+{
+    const int sn = min(s + 1, nsb - 1);
+    feed_load(feed, act, sn, tid);
+#pragma unroll
+    for (int r = 0; r < R; r++) load_tile(nxt[r], tile[r], sn, r16, g);
+    if (s < nsb) compute_sb<R>(cur, sa[s & 1], r16, g, acc);
+    if (s + 1 < nsb) feed_store(feed, sa[(s + 1) & 1], tid);
+    __syncthreads();
+}
+
 // Accumulate R weight tiles (tile[r]: base of the tile's super-block runs)
-// against the item's activation rows, all super-blocks.
+// against the item's 16 activation rows, all super-blocks.
 template <int R>
 __device__ __forceinline__ void run_item(const uint8_t *const (&tile)[R], const ActMfma &act,
                                          AFeed &feed, ATile (&sa)[2], int tid, int r16, int g,
@@ -167,175 +210,128 @@ __device__ __forceinline__ void run_item(const uint8_t *const (&tile)[R], const 
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[r][i] = 0.0f;
-
+    Q4KTile t0[R], t1[R];
     feed_load(feed, act, 0, tid);
+#pragma unroll
+    for (int r = 0; r < R; r++) load_tile(t0[r], tile[r], 0, r16, g);
     feed_store(feed, sa[0], tid);
-    Q4KTile cur[R];
-#if DMOE_X_PREFETCH
-    Q4KTile nxt[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) load_tile(nxt[r], tile[r], 0, r16, g);
-#endif
     __syncthreads();
-
-    for (int sb = 0; sb < nsb; sb++) {
-        const int buf = sb & 1;
-#if DMOE_X_PREFETCH
-#pragma unroll
-        for (int r = 0; r < R; r++) cur[r] = nxt[r];
-#else
-#pragma unroll
-        for (int r = 0; r < R; r++) load_tile(cur[r], tile[r], sb, r16, g);
-#endif
-        if (sb + 1 < nsb) {
-            feed_load(feed, act, sb + 1, tid);
-#if DMOE_X_PREFETCH
-#pragma unroll
-            for (int r = 0; r < R; r++) load_tile(nxt[r], tile[r], sb + 1, r16, g);
-#endif
-        }
-        const ATile &a = sa[buf];
-        const float4 dxv = *reinterpret_cast<const float4 *>(&a.d[4 * g]);
-        const float dx[4] = {dxv.x, dxv.y, dxv.z, dxv.w};
-        const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(&a.bs[r16][4 * g]));
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            Q4KOps o;
-            dequant_tile(cur[r], g, o);
-            f4 s1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const h8 av = __builtin_bit_cast(
-                    h8, *reinterpret_cast<const uint4 *>(&a.v[r16][g * 64 + s * 8]));
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, o.b[s], s1, 0, 0, 0);
-            }
-            f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
-            s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, o.bm, s2, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[r][i] += dx[i] * (o.d * s1[i] - o.dmin * s2[i]);
-        }
-        if (sb + 1 < nsb) feed_store(feed, sa[buf ^ 1], tid);
-        __syncthreads();
+    for (int sb = 0; sb < nsb; sb += 2) {
+        step_sb<R>(t0, t1, tile, act, feed, sa, sb, nsb, tid, r16, g, acc);
+        step_sb<R>(t1, t0, tile, act, feed, sa, sb + 1, nsb, tid, r16, g, acc);
     }
 }
 
-// Workgroup items: routed — (expert, up to 16 consecutive pairs of it, a group
-// of weight rows); shared — (8 tokens, a group of weight rows), its 16
-// activation rows being the hi / lo halves of the split activations
-// interleaved (t hi, t lo, ...), so that each lane's four outputs are
-// (t, hi), (t, lo), (t+1, hi), (t+1, lo) and the halves are summed in-lane.
+// Workgroup items of phase 0: routed (work-list entry ec, group of 64 rows),
+// then shared (chunk of 8 tokens, group of 64 rows); phase 1 the same with
+// groups of 128 rows.  A routed item's 16 activation rows are the pairs of its
+// entry (one expert, up to 16 consecutive pairs of it); a shared item's are the
+// hi / lo halves of its 8 tokens' split activations interleaved (t hi, t lo,
+// ...), so that each lane's four outputs are (t, hi), (t, lo), (t+1, hi),
+// (t+1, lo) and the halves are summed in-lane.
 template <int PHASE>
-__global__ __launch_bounds__(WAVES * 64) void k_expert_q4k(ExpertJob job)
+__global__ __launch_bounds__(WAVES * 64) void k_expert_q4k(MoeJob job)
 {
-    constexpr int R = PHASE == 0 ? 2 : RT_DOWN;             // weight tiles per wave
-    constexpr int WROWS = PHASE == 0 ? 16 : 16 * RT_DOWN;   // weight rows per wave
-    constexpr int GROWS = WAVES * WROWS;                    // weight rows per item
+    constexpr bool DOWN = PHASE == 1;
+    constexpr int GROWS = DOWN ? GROWS_DN : GROWS_GU;
     __shared__ ATile sa[2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r16 = lane & 15;
-    const int K = job.top_k, N = job.n_tokens;
-    const int rg = job.rows / GROWS;
-    const int rg_sh = job.rows_sh / GROWS;
-    const int routed_items = job.wl.n_ec[0] * rg;
-    const int nch_sh = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
-    const int total = routed_items + nch_sh * rg_sh;
-    const int nsb = job.act.K / 256, nsb_sh = job.act_sh.K / 256;
+    const int N = job.n_tokens, K = job.top_k;
+    const int H = job.H, FF = job.FF, SF = job.SF;
+    const int n_ec = job.wl.n_ec[0];
+    const int nch = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
+    const int rg = (DOWN ? H : FF) / GROWS, rg_sh = (DOWN ? H : SF) / GROWS;
+    const int routed_items = n_ec * rg;
+    const int total = routed_items + nch * rg_sh;
+    const int nsbH = H / 256, nsbF = FF / 256, nsbS = SF / 256;
 
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
         const bool shared = item >= routed_items;
-        int row0, nt, t_first, e = 0;
+        const int j = shared ? item - routed_items : item;
+        const int rgn = shared ? rg_sh : rg;
+        const int unit = j / rgn;                 // work-list entry or shared chunk
+        const int row0 = (j - unit * rgn) * GROWS + wave * (GROWS / WAVES);
+        int t_first, nt, e = 0;
         if (!shared) {
-            const int ec = item / rg;
-            row0 = (item - ec * rg) * GROWS + wave * WROWS;
-            e = job.wl.ec_expert[ec];
-            const int c0 = job.wl.ec_chunk[ec] * EXPERT_CHUNK;
+            e = job.wl.ec_expert[unit];
+            const int c0 = job.wl.ec_chunk[unit] * EXPERT_CHUNK;
             t_first = job.offsets[e] + c0;
             nt = min(EXPERT_CHUNK, job.counts[e] - c0);
         } else {
-            const int j = item - routed_items;
-            const int ch = j / rg_sh;
-            row0 = (j - ch * rg_sh) * GROWS + wave * WROWS;
-            t_first = ch * SHARED_CHUNK;
+            t_first = unit * SHARED_CHUNK;
             nt = min(SHARED_CHUNK, N - t_first);
         }
-        // activation row of item row j (0..15)
-        auto arow = [&](int j) {
-            if (shared) return t_first + min(j >> 1, nt - 1) + (j & 1) * N;
-            const int p = job.perm[t_first + min(j, nt - 1)];
-            return PHASE == 1 ? p : p / K;
+        // activation row of item row jr (0..15): tokens in phase 0, pairs in
+        // phase 1; shared rows interleave hi and lo (lo rows start at N)
+        auto arow = [&](int jr) {
+            if (shared) return t_first + min(jr >> 1, nt - 1) + (jr & 1) * N;
+            const int p = job.perm[t_first + min(jr, nt - 1)];
+            return DOWN ? p : p / K;
         };
         AFeed feed;
         feed.rv0 = arow(tid >> 5);
         feed.rv1 = arow((tid >> 5) + 8);
         feed.rbs = arow((tid >> 1) & 15);
         feed.rd = arow(tid >= 32 && tid < 48 ? tid - 32 : 0);
-        // output rows of this lane's four results
-        int orow[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (shared)
-                orow[i] = t_first + min(2 * g + (i >> 1), nt - 1);
-            else
-                orow[i] = job.perm[t_first + min(4 * g + i, nt - 1)];
-        }
-        // this wave's weight tiles
-        const uint8_t *tile[R];
-        if (PHASE == 0) {
-            const WTensor &a = shared ? job.s0 : job.w0;
-            const WTensor &b = shared ? job.s1 : job.w1;
-            const int n = shared ? nsb_sh : nsb;
-            const size_t ea = shared ? 0 : (size_t)e * a.nb2, eb = shared ? 0 : (size_t)e * b.nb2;
-            tile[0] = a.data + ea + (size_t)(row0 / 16) * n * TILE_BYTES;
-            tile[R - 1] = b.data + eb + (size_t)(row0 / 16) * n * TILE_BYTES;
-        } else {
-            const WTensor &a = shared ? job.s0 : job.w0;
-            const int n = shared ? nsb_sh : nsb;
-            const size_t ea = shared ? 0 : (size_t)e * a.nb2;
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                tile[r] = a.data + ea + (size_t)(row0 / 16 + r) * n * TILE_BYTES;
-        }
-        float acc[R][4];
-        run_item<R>(tile, shared ? job.act_sh : job.act, feed, sa, tid, r16, g, acc);
 
-        float *out = shared ? job.out_sh : job.out;
-        const int orows = shared ? job.rows_sh : job.rows;
+        const uint8_t *tile[RT];
+        if (!DOWN) {
+            const WTensor &a = shared ? job.sg : job.eg;
+            const WTensor &b = shared ? job.su : job.eu;
+            tile[0] = a.data + (size_t)e * a.nb2 + (size_t)(row0 / 16) * nsbH * TILE_BYTES;
+            tile[1] = b.data + (size_t)e * b.nb2 + (size_t)(row0 / 16) * nsbH * TILE_BYTES;
+        } else {
+            const WTensor &a = shared ? job.sd : job.ed;
+            const int n = shared ? nsbS : nsbF;
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                tile[r] = a.data + (size_t)e * a.nb2 + (size_t)(row0 / 16 + r) * n * TILE_BYTES;
+        }
+        const ActMfma &act = DOWN ? (shared ? job.ahs : job.ah) : (shared ? job.axs : job.ax);
+        float acc[RT][4];
+        run_item<RT>(tile, act, feed, sa, tid, r16, g, acc);
+
         if (!shared) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 if (4 * g + i >= nt) continue;
-                float *o = out + (size_t)orow[i] * orows + row0 + r16;
-                if (PHASE == 0) {
-                    o[0] = silu(acc[0][i]) * acc[R - 1][i];
+                const int p = job.perm[t_first + 4 * g + i];
+                if (!DOWN) {
+                    job.h[(size_t)p * FF + row0 + r16] = silu(acc[0][i]) * acc[1][i];
                 } else {
+                    float *o = job.ye + (size_t)p * H + row0 + r16;
 #pragma unroll
-                    for (int r = 0; r < R; r++) o[16 * r] = acc[r][i];
+                    for (int r = 0; r < RT; r++) o[16 * r] = acc[r][i];
                 }
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i += 2) {
                 if (2 * g + (i >> 1) >= nt) continue;
-                float *o = out + (size_t)orow[i] * orows + row0 + r16;
-                if (PHASE == 0) {
-                    o[0] = silu(acc[0][i] + acc[0][i + 1]) * (acc[R - 1][i] + acc[R - 1][i + 1]);
+                const int t = t_first + 2 * g + (i >> 1);
+                if (!DOWN) {
+                    job.hs[(size_t)t * SF + row0 + r16] =
+                        silu(acc[0][i] + acc[0][i + 1]) * (acc[1][i] + acc[1][i + 1]);
                 } else {
+                    float *o = job.ys + (size_t)t * H + row0 + r16;
 #pragma unroll
-                    for (int r = 0; r < R; r++) o[16 * r] = acc[r][i] + acc[r][i + 1];
+                    for (int r = 0; r < RT; r++) o[16 * r] = acc[r][i] + acc[r][i + 1];
                 }
             }
         }
     }
 }
 
-int expert_rows_per_item(int phase) { return WAVES * (phase == 0 ? 16 : 16 * RT_DOWN); }
+int expert_rows_per_item(int phase) { return phase == 0 ? GROWS_GU : GROWS_DN; }
 
-hipError_t launch_expert_q4k(int phase, const ExpertJob &job, hipStream_t s)
+hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s)
 {
-    const int rows_item = expert_rows_per_item(phase);
-    if (job.rows % rows_item || (job.has_shared && job.rows_sh % rows_item) || job.act.K % 256)
+    if (job.FF % GROWS_GU || job.FF % 256 || job.H % GROWS_DN || job.H % 256 ||
+        job.ax.K != job.H || job.ah.K != job.FF ||
+        (job.has_shared && (job.SF % GROWS_GU || job.SF % 256 || job.ahs.K != job.SF)))
         return hipErrorInvalidValue;
     if (phase == 0)
         hipLaunchKernelGGL(k_expert_q4k<0>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);

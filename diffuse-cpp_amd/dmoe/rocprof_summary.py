@@ -8,8 +8,10 @@ Two reports:
   ``FETCH_SIZE`` then ``WRITE_SIZE`` (both in KiB per dispatch).  Each counter
   is scaled by what it reads for a plain device copy of known size run in the
   same process (``bench.py --copy-probe-mib``): the copy reads and writes
-  exactly its size, so ``size / counter`` converts the counter to bytes.  The
-  report carries a ``traffic_bytes_per_launch:`` line that bench.py reads.
+  exactly its size, so ``size / counter`` converts the counter to bytes.  Only
+  the copy kernel's large dispatches (at least half its largest) count as the
+  probe.  The report carries a ``traffic_bytes_per_launch:`` line that
+  bench.py reads.
 
     python -m dmoe.rocprof_summary kernels --dir D --cmd "..." --out F
     python -m dmoe.rocprof_summary traffic --fetch D1 --write D2 \\
@@ -99,6 +101,10 @@ def report_traffic(a):
     _, kw = _pick(write, a.kernel)
     cname, cf = _pick(fetch, a.copy_kernel, largest=True)
     _, cw = _pick(write, cname)
+    # the probe's dispatches are the large ones (the same kernel also serves
+    # small runtime copies)
+    cf = [v for v in cf if v >= 0.5 * max(cf)]
+    cw = [v for v in cw if v >= 0.5 * max(cw)]
     cb = a.copy_bytes
     f_read = cb / (statistics.mean(cf) * 1024.0)
     f_write = cb / (statistics.mean(cw) * 1024.0)
