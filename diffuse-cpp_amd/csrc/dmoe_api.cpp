@@ -259,7 +259,7 @@ struct Workspace {
     RouteBufs rb;
     WorkList wl;
     ActBuf xq, hq;                       // GEMV-path activations
-    ActMfma ax, axs, ah, ahs;            // MFMA-path activations (routed / shared)
+    ActI8 ax, axs, ah, ahs;              // MFMA-path activations (routed / shared)
     float *h, *ye, *hs, *ys;
     float *bias;
     int32_t *counter;                    // zeroed once at allocation; routing leaves it zeroed
@@ -273,23 +273,22 @@ bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
     const int gu = expert_rows_per_item(0), dn = expert_rows_per_item(1);
     if (wtype != DMOE_TYPE_Q4_K || hp.n_embd % 256 || hp.moe_ff % 256) return false;
     if (hp.moe_ff % gu || hp.n_embd % dn) return false;
-    if (shared && (stype != DMOE_TYPE_Q4_K || hp.shared_ff % 256 || hp.shared_ff % gu)) return false;
+    // the shared expert's down product runs in the routed one's launch plan
+    if (shared && (stype != DMOE_TYPE_Q4_K || hp.shared_ff != hp.moe_ff)) return false;
+    // an item's activation rows are held whole in LDS
+    if (!expert_k_ok(hp.n_embd) || !expert_k_ok(hp.moe_ff)) return false;
     return true;
 }
 
-ActMfma take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bool split)
+ActI8 take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bool split)
 {
-    // split activations keep their lo halves as rows rows..2*rows-1
+    // split activations keep their a0 digit rows as rows rows..2*rows-1
     const int r = split ? 2 * rows : rows;
-    ActMfma a{};
+    ActI8 a{};
     a.K = K;
-    a.v = (uint16_t *)take((size_t)r * K * 2);
+    a.q = (int8_t *)take((size_t)r * K);
     a.bs = (uint16_t *)take((size_t)r * (K / 16) * 2);
     a.d = (float *)take((size_t)r * (K / 256) * 4);
-    if (split && a.v) {
-        a.v_lo = a.v + (size_t)rows * K;
-        a.bs_lo = a.bs + (size_t)rows * (K / 16);
-    }
     return a;
 }
 

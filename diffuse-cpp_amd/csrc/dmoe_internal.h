@@ -70,24 +70,22 @@ struct WorkList {
     int32_t *ec_chunk;
 };
 
-// Activations in the MFMA operand layout of k_expert.hip.  Per row of K
-// values and per 256-value super-block sb, the f16 values are stored in the
-// order the MFMA lanes read them: position sb*256 + g*64 + s*8 + e holds value
-// 64g + 32*(e/4) + 4s + {0,2,1,3}[e%4] of the super-block (g = lane group,
-// s = MFMA step), matching the nibble order of a Q4_K super-block.
-//   ACT_Q8K  : ggml's Q8_K quantisation (ints exact in f16), d = Q8_K scale,
-//              bs = sums of 16 quants
-//   ACT_SPLIT: f32 value * 2^k split as hi + lo f16 (about 22 significant bits),
-//              d = 2^-k per super-block, bs / bs_lo = split sums of 16 values.
-//              The lo halves are rows `rows`..2*rows-1 of the same arrays
-//              (v_lo = v + rows*K, bs_lo = bs + rows*K/16, d repeated).
+// Activations of the Q4_K expert products (k_expert.hip), int8 per value.
+// Per row of K values and per 256-value super-block the bytes are stored in the
+// order the MFMA lanes read them: position 64g + 8j + b holds value
+// 32j + 8g + b of the super-block (j = 32-value sub-block, g = lane group,
+// b = byte), so that a lane group's eight 8-byte pieces are contiguous.
+//   ACT_Q8K  : ggml's Q8_K quantisation (d = Q8_K scale, q in [-127, 127]).
+//   ACT_SPLIT: f32 values (the shared expert) as two int8 digits: with a
+//              power-of-two scale s per super-block, X = round(v / s),
+//              |X| <= 32512, X = 256*a1 + a0; rows 0..rows-1 hold a1 (d = 256 s)
+//              and rows rows..2*rows-1 hold a0 (d = s).
+// bs holds the f16 sums of each 16 consecutive values (exact: |sum| <= 2048).
 enum ActMode { ACT_Q8K = 0, ACT_SPLIT = 1 };
-struct ActMfma {
+struct ActI8 {
     int32_t K;
-    uint16_t *v;        // [rows][K]
-    uint16_t *v_lo;     // [rows][K]     split only
+    int8_t *q;          // [rows][K]
     uint16_t *bs;       // [rows][K/16]
-    uint16_t *bs_lo;    // [rows][K/16]  split only
     float *d;           // [rows][K/256]
 };
 
@@ -101,9 +99,9 @@ struct MoeJob {
     int32_t n_tokens, top_k;
     const int32_t *perm, *offsets, *counts;
     WorkList wl;
-    ActMfma ax, axs;         // x converted: Q8_K (rows: tokens), split (shared)
+    ActI8 ax, axs;         // x converted: Q8_K (rows: tokens), split (shared)
     float *h, *hs;           // gate/up results [N*K][FF], [N][SF]
-    ActMfma ah, ahs;         // h and hs converted for the down products
+    ActI8 ah, ahs;         // h and hs converted for the down products
     float *ye, *ys;          // down results [N*K][H], [N][H]
 };
 
@@ -128,7 +126,7 @@ bool route_fits_lds(const RouteParams &rp);
 struct PrepJob {
     const float *src;
     int32_t rows, K, mode;   // K % 256 == 0
-    ActMfma out;
+    ActI8 out;
 };
 // Front kernel (k_prep.hip): router logits L = Wg x in one fixed fp32 order,
 // probs = sigmoid(L), sel = probs + bias, plus up to two activation
@@ -146,7 +144,14 @@ constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
 constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
 hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s);
 int expert_rows_per_item(int phase);     // output rows one work item covers
-// Q4_K row layout -> tiled layout of k_expert.hip (k_quant.hip)
+bool expert_k_ok(int K);                 // reduction length the expert kernels accept
+// Q4_K row layout -> tiled layout of k_expert.hip (k_quant.hip): per matrix,
+// 16-row tiles, super-block-major (row r, super-block sb at
+// ((r/16)*nsb + sb)*2304 + (r%16)*144); inside each 144-byte block d and dmin
+// stay in bytes 0..3, the twelve scale bytes are repacked (dword 1:
+// sc0..sc4, dword 2: sc5..sc7 m0 m1, dword 3: m2..m6, six bits each; m7 in
+// bits 30..31 of the three dwords, low bits first) and the 128 quant bytes
+// are reordered so that byte 16 + 32g + 8c + b holds quant byte 32c + 8g + b.
 hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
                            uint8_t *dst, hipStream_t s);
 

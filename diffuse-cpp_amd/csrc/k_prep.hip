@@ -6,17 +6,8 @@
 //     sel = probs + bias (:207-210) computed by the lane that owns each logit;
 //   * up to two conversions of x into the MFMA operand layout of k_expert.hip.
 //
-// ACT_Q8K reproduces ggml's Q8_K conversion of the activations that
-// ggml_mul_mat_id performs before Q4_K dots (:266-269): per 256 values, the
-// value of largest magnitude (lowest index on ties) maps to -127,
-// iscale = -127/max, q = min(127, nearest_even(iscale*x)), d = 1/iscale, plus
-// sums of 16 quants.  The quants are small integers, exact in f16.
-//
-// ACT_SPLIT keeps f32 activations (the shared expert, whose weights the
-// reference casts to F32, :8-12, :282-284): per super-block the values are
-// scaled by 2^k into [2^9, 2^10) in magnitude and split into hi = f16(v) and
-// lo = f16(v - hi), about 22 significant bits; d = 2^-k.  The lo halves are
-// written as rows `rows`..2*rows-1.
+// The conversions themselves (Q8_K for the routed experts, two int8 digits
+// for the shared expert) are in dmoe_prep.h.
 #include "dmoe_prep.h"
 
 #pragma clang fp contract(off)

@@ -255,28 +255,56 @@ __global__ __launch_bounds__(256) void k_tile_q4k(const uint8_t *__restrict__ sr
                                                   size_t nb2, int rows, int nsb, int mats,
                                                   uint8_t *__restrict__ dst)
 {
+    // one thread per 144-byte block
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t per_mat = (size_t)rows * nsb * 9;          // 16-byte pieces per matrix
+    const size_t per_mat = (size_t)rows * nsb;
     if (i >= per_mat * mats) return;
     const int m = (int)(i / per_mat);
-    size_t j = i - (size_t)m * per_mat;
-    const int piece = (int)(j % 9);
-    j /= 9;
+    const size_t j = i - (size_t)m * per_mat;
     const int sb = (int)(j % nsb);
     const int r = (int)(j / nsb);
-    const uint4 v = *reinterpret_cast<const uint4 *>(src + (size_t)m * nb2 + (size_t)r * nb1 +
-                                                     (size_t)sb * Q4K_BYTES + piece * 16);
-    const size_t o = (size_t)m * rows * nsb * Q4K_BYTES +
-                     ((size_t)(r / 16) * nsb + sb) * (16 * Q4K_BYTES) + (size_t)(r % 16) * Q4K_BYTES +
-                     piece * 16;
-    *reinterpret_cast<uint4 *>(dst + o) = v;
+    const uint8_t *in = src + (size_t)m * nb2 + (size_t)r * nb1 + (size_t)sb * Q4K_BYTES;
+    uint8_t *out = dst + (size_t)m * rows * nsb * Q4K_BYTES +
+                   ((size_t)(r / 16) * nsb + sb) * (16 * Q4K_BYTES) + (size_t)(r % 16) * Q4K_BYTES;
+    uint8_t blk[Q4K_BYTES];
+#pragma unroll
+    for (int p = 0; p < 9; p++)
+        *reinterpret_cast<uint4 *>(blk + 16 * p) = *reinterpret_cast<const uint4 *>(in + 16 * p);
+    // get_scale_min_k4 of the twelve scale bytes
+    const uint8_t *q = blk + 4;
+    uint32_t sc[8], mn[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        if (k < 4) {
+            sc[k] = q[k] & 63u;
+            mn[k] = q[k + 4] & 63u;
+        } else {
+            sc[k] = (q[k + 4] & 0xFu) | ((uint32_t)(q[k - 4] >> 6) << 4);
+            mn[k] = (uint32_t)(q[k + 4] >> 4) | ((uint32_t)(q[k] >> 6) << 4);
+        }
+    }
+    uint32_t w[9 * 4];
+    w[0] = *reinterpret_cast<const uint32_t *>(blk);          // d, dmin
+    w[1] = sc[0] | sc[1] << 6 | sc[2] << 12 | sc[3] << 18 | sc[4] << 24 | (mn[7] & 3u) << 30;
+    w[2] = sc[5] | sc[6] << 6 | sc[7] << 12 | mn[0] << 18 | mn[1] << 24 | ((mn[7] >> 2) & 3u) << 30;
+    w[3] = mn[2] | mn[3] << 6 | mn[4] << 12 | mn[5] << 18 | mn[6] << 24 | ((mn[7] >> 4) & 3u) << 30;
+    // quant bytes: 16 + 32g + 8c + b  <-  32c + 8g + b (as 8-byte pieces)
+    const uint64_t *qs = reinterpret_cast<const uint64_t *>(blk + 16);
+    uint64_t *ws = reinterpret_cast<uint64_t *>(w + 4);
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) ws[4 * g + c] = qs[4 * c + g];
+#pragma unroll
+    for (int p = 0; p < 9; p++)
+        *reinterpret_cast<uint4 *>(out + 16 * p) = *reinterpret_cast<const uint4 *>(w + 4 * p);
 }
 
 hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
                            uint8_t *dst, hipStream_t s)
 {
     if (rows % 16 || K % 256 || nb1 % 16 || (mats > 1 && nb2 % 16)) return hipErrorInvalidValue;
-    const size_t total = (size_t)rows * (K / 256) * 9 * mats;
+    const size_t total = (size_t)rows * (K / 256) * mats;
     hipLaunchKernelGGL(k_tile_q4k, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
                        nb1, nb2, rows, K / 256, mats, dst);
     return hipGetLastError();
