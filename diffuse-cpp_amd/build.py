@@ -36,7 +36,8 @@ CFLAGS = [
     f"-I{ROOT / 'include'}",
 ]
 
-SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "dmoe_api.cpp"]
+SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "k_gemm.hip",
+           "dmoe_api.cpp"]
 HEADERS = ["dmoe_internal.h", "dmoe_device.h"]
 
 

@@ -260,6 +260,7 @@ struct Workspace {
     WorkList wl;
     ActBuf xq, hq;                       // GEMV-path activations
     ActI8 ax, axs, ah, ahs;              // MFMA-path activations (routed / shared)
+    uint16_t *x16, *xs16, *h16, *hs16;   // GEMM-path f16 activations (split: hi / lo rows)
     float *h, *ye, *hs, *ys;
     float *bias;
     int32_t *counter;                    // zeroed once at allocation; routing leaves it zeroed
@@ -278,6 +279,13 @@ bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
     // an item's activation rows are held whole in LDS
     if (!expert_k_ok(hp.n_embd) || !expert_k_ok(hp.moe_ff)) return false;
     return true;
+}
+
+// F16 experts (and an F16 shared expert) run on the MFMA grouped-GEMM path.
+bool use_gemm_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared)
+{
+    if (wtype != DMOE_TYPE_F16 || (shared && stype != DMOE_TYPE_F16)) return false;
+    return gemm_shapes_ok(hp.n_embd, hp.moe_ff, shared ? hp.shared_ff : 0, shared);
 }
 
 ActI8 take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bool split)
@@ -327,7 +335,8 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
     t.rb.perm = (int32_t *)take((size_t)P * 4);
     t.rb.hist = (int32_t *)take((size_t)groups * E * 4);
     t.rb.lrank = (int32_t *)take((size_t)P * 4);
-    t.wl.chunk = EXPERT_CHUNK;
+    const bool gemm = use_gemm_path(hp, wtype, stype, shared);
+    t.wl.chunk = gemm ? GM : EXPERT_CHUNK;
     t.wl.n_ec = (int32_t *)take(4);
     t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
     t.wl.ec_chunk = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
@@ -338,6 +347,14 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         if (shared) {
             t.axs = take_act(take, N, H, true);
             t.ahs = take_act(take, N, SF, true);
+        }
+    }
+    if (gemm) {
+        t.x16 = (uint16_t *)take((size_t)N * H * 2);
+        t.h16 = (uint16_t *)take((size_t)P * FF * 2);
+        if (shared) {
+            t.xs16 = (uint16_t *)take((size_t)2 * N * H * 2);
+            t.hs16 = (uint16_t *)take((size_t)2 * N * SF * 2);
         }
     }
     t.xq.type = at;
@@ -446,6 +463,7 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
     const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
     const RouteParams rp = route_params(L, hp, N);
     const bool mfma = use_mfma_path(hp, L->eg.type, L->sg.type, L->has_shared);
+    const bool gemm = use_gemm_path(hp, L->eg.type, L->sg.type, L->has_shared);
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, id, s, [&] { return call; }))
     // router logits, sigmoid, selection scores (+ x in the MFMA operand layout)
     PrepJob xj[2];
@@ -491,6 +509,39 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, ACT_SPLIT, w.ahs};
         STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
         STAGE(ST_DOWN, launch_expert_q4k(1, job, s));
+        STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
+                                         K, H, y, s));
+        return DMOE_OK;
+    }
+    if (gemm) {
+        // F16 experts on MFMA tiles (the prefill path)
+        GemmJob job{};
+        job.eg = L->eg;
+        job.eu = L->eu;
+        job.ed = L->ed;
+        job.sg = L->sg;
+        job.su = L->su;
+        job.sd = L->sd;
+        job.has_shared = L->has_shared;
+        job.H = H;
+        job.FF = FF;
+        job.SF = hp.shared_ff;
+        job.n_tokens = N;
+        job.top_k = K;
+        job.perm = w.rb.perm;
+        job.offsets = w.rb.offsets;
+        job.counts = w.rb.counts;
+        job.wl = w.wl;
+        job.x16 = w.x16;
+        job.xs16 = w.xs16;
+        job.h16 = w.h16;
+        job.hs16 = w.hs16;
+        job.ye = w.ye;
+        job.ys = w.ys;
+        STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 0, w.x16, s));
+        if (L->has_shared) STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 1, w.xs16, s));
+        STAGE(ST_GATEUP, launch_gemm_f16(0, job, s));
+        STAGE(ST_DOWN, launch_gemm_f16(1, job, s));
         STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
                                          K, H, y, s));
         return DMOE_OK;

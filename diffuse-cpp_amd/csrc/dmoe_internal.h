@@ -116,6 +116,31 @@ struct RouteParams {
 
 // ---------------------------------------------------------------------------
 // Kernel launchers (each returns the hipGetLastError of its launch).
+// F16 expert products on MFMA, the prefill path (k_gemm.hip).
+constexpr int GM = 128;             // (token, slot) pairs per work item
+constexpr int GK = 32;              // k per pipeline step
+constexpr int GN_GU = 64;           // moe_ff rows of a gate/up item (gate and up)
+constexpr int GN_DN = 128;          // n_embd rows of a down item
+constexpr int GEMM_BLOCKS = 1024;   // persistent grid
+struct GemmJob {
+    WTensor eg, eu, ed;      // routed gate, up, down (F16, ggml row layout)
+    WTensor sg, su, sd;      // shared expert (F16)
+    int32_t has_shared;
+    int32_t H, FF, SF;       // n_embd, moe_ff, shared_ff
+    int32_t n_tokens, top_k;
+    const int32_t *perm, *offsets, *counts;
+    WorkList wl;             // chunk == GM
+    const uint16_t *x16;     // [N][H]  f16(x)
+    const uint16_t *xs16;    // [2N][H] hi / lo pair of x (shared expert)
+    uint16_t *h16;           // [N*K][FF] f16(h)
+    uint16_t *hs16;          // [2N][SF] hi / lo pair of the shared h
+    float *ye, *ys;          // down results [N*K][H], [N][H]
+};
+hipError_t launch_gemm_f16(int phase, const GemmJob &job, hipStream_t s);
+bool gemm_shapes_ok(int H, int FF, int SF, bool shared);
+// x (f32) -> f16, or its hi / lo f16 pair (lo rows after the hi rows)
+hipError_t launch_cvt_f16(const float *src, int rows, int K, int split, uint16_t *dst, hipStream_t s);
+
 // Routing + dispatch (k_router.hip).  counter: a zeroed int the last routing
 // group uses to elect itself (left zeroed again).
 hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,

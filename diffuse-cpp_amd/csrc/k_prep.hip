@@ -28,49 +28,54 @@ __device__ void prep_wave(const PrepJob &job, int wid, float *sv)
 }
 
 // ---------------------------------------------------------------------------
-// Router logits.  One wavefront per (2 experts, 4 tokens).  For every
+// Router logits.  One wavefront per (LE experts, LT tokens).  For every
 // (token, expert) lane l keeps one partial:  a_l = fma(W[k], x[k], a_l) for
 // k = 256*i + 4*l + j, i ascending then j = 0..3; the 64 partials are then
 // combined by six xor butterfly rounds (m = 32..1), after which every lane
 // holds the same value (each round adds the same two operands in both
-// partner lanes).  Lane t*LG_E + e then computes sigmoid and the score.
-constexpr int LG_E = 2, LG_T = 4;
+// partner lanes).  Lane t*LE + e then computes sigmoid and the score.  The
+// tile shape only changes which rows a wavefront reads, not the order.
+constexpr int LG_E = 2, LG_T = 4;        // up to a few hundred tokens
+constexpr int LW_E = 8, LW_T = 8;        // more tokens: fewer re-reads of x
 
+template <int LE, int LT>
 __device__ void logits_wave(const float *__restrict__ W, const float *__restrict__ bias,
                             const float *__restrict__ x, int N, int H, int E, int wave,
                             const RouteBufs &rb)
 {
+    static_assert(LE * LT <= 64, "one lane per output");
     const int lane = threadIdx.x & 63;
-    const int ne = (E + LG_E - 1) / LG_E;
-    const int e0 = (wave % ne) * LG_E;
-    const int t0 = (wave / ne) * LG_T;
+    const int ne = (E + LE - 1) / LE;
+    const int e0 = (wave % ne) * LE;
+    const int t0 = (wave / ne) * LT;
 
-    float acc[LG_T][LG_E];
+    float acc[LT][LE];
 #pragma unroll
-    for (int t = 0; t < LG_T; t++)
+    for (int t = 0; t < LT; t++)
 #pragma unroll
-        for (int e = 0; e < LG_E; e++) acc[t][e] = 0.0f;
+        for (int e = 0; e < LE; e++) acc[t][e] = 0.0f;
 
-    const float4 *wr[LG_E];
-    const float4 *xr[LG_T];
+    const float4 *wr[LE];
+    const float4 *xr[LT];
 #pragma unroll
-    for (int e = 0; e < LG_E; e++)
+    for (int e = 0; e < LE; e++)
         wr[e] = reinterpret_cast<const float4 *>(W + (size_t)min(e0 + e, E - 1) * H);
 #pragma unroll
-    for (int t = 0; t < LG_T; t++)
+    for (int t = 0; t < LT; t++)
         xr[t] = reinterpret_cast<const float4 *>(x + (size_t)min(t0 + t, N - 1) * H);
 
-#pragma unroll 4
+    constexpr int UNR = LE * LT > 8 ? 1 : 4;
+#pragma unroll UNR
     for (int i = 0; i < H / 256; i++) {
-        float4 w[LG_E], xv[LG_T];
+        float4 w[LE], xv[LT];
 #pragma unroll
-        for (int e = 0; e < LG_E; e++) w[e] = wr[e][i * 64 + lane];
+        for (int e = 0; e < LE; e++) w[e] = wr[e][i * 64 + lane];
 #pragma unroll
-        for (int t = 0; t < LG_T; t++) xv[t] = xr[t][i * 64 + lane];
+        for (int t = 0; t < LT; t++) xv[t] = xr[t][i * 64 + lane];
 #pragma unroll
-        for (int t = 0; t < LG_T; t++)
+        for (int t = 0; t < LT; t++)
 #pragma unroll
-            for (int e = 0; e < LG_E; e++) {
+            for (int e = 0; e < LE; e++) {
                 float a = acc[t][e];
                 a = __builtin_fmaf(w[e].x, xv[t].x, a);
                 a = __builtin_fmaf(w[e].y, xv[t].y, a);
@@ -81,22 +86,29 @@ __device__ void logits_wave(const float *__restrict__ W, const float *__restrict
     }
     float mine = 0.0f;
 #pragma unroll
-    for (int t = 0; t < LG_T; t++)
+    for (int t = 0; t < LT; t++)
 #pragma unroll
-        for (int e = 0; e < LG_E; e++) {
+        for (int e = 0; e < LE; e++) {
             float v = acc[t][e];
 #pragma unroll
             for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-            if (lane == t * LG_E + e) mine = v;
+            if (lane == t * LE + e) mine = v;
         }
-    const int t = lane / LG_E, e = lane % LG_E;
-    if (lane < LG_T * LG_E && t0 + t < N && e0 + e < E) {
+    const int t = lane / LE, e = lane % LE;
+    if (lane < LT * LE && t0 + t < N && e0 + e < E) {
         const size_t o = (size_t)(t0 + t) * E + e0 + e;
         const float p = sigmoid_f32(mine);
         rb.logits[o] = mine;
         rb.probs[o] = p;
         rb.sel[o] = bias ? p + bias[e0 + e] : p;
     }
+}
+
+// logit wavefronts of a launch (wide: the 8 x 8 tiles)
+__host__ __device__ __forceinline__ int logit_waves(int N, int E, bool wide)
+{
+    return wide ? ((E + LW_E - 1) / LW_E) * ((N + LW_T - 1) / LW_T)
+                : ((E + LG_E - 1) / LG_E) * ((N + LG_T - 1) / LG_T);
 }
 
 __device__ __forceinline__ int prep_blocks(const PrepJob &j)
@@ -106,7 +118,7 @@ __device__ __forceinline__ int prep_blocks(const PrepJob &j)
 
 struct FrontArgs {
     const float *W, *bias, *x;
-    int N, H, E, logit_blocks;
+    int N, H, E, logit_blocks, wide;
     RouteBufs rb;
     PrepJob job[2];
     int njobs;
@@ -119,8 +131,12 @@ __global__ __launch_bounds__(256) void k_front(FrontArgs a)
     int b = blockIdx.x;
     if (b < a.logit_blocks) {
         const int wave = b * 4 + w;
-        const int nw = ((a.E + LG_E - 1) / LG_E) * ((a.N + LG_T - 1) / LG_T);
-        if (wave < nw) logits_wave(a.W, a.bias, a.x, a.N, a.H, a.E, wave, a.rb);
+        if (wave < logit_waves(a.N, a.E, a.wide)) {
+            if (a.wide)
+                logits_wave<LW_E, LW_T>(a.W, a.bias, a.x, a.N, a.H, a.E, wave, a.rb);
+            else
+                logits_wave<LG_E, LG_T>(a.W, a.bias, a.x, a.N, a.H, a.E, wave, a.rb);
+        }
         return;
     }
     b -= a.logit_blocks;
@@ -146,8 +162,8 @@ hipError_t launch_front(const float *W, const float *bias, const float *x, int N
     a.H = H;
     a.E = E;
     a.rb = rb;
-    const int nw = ((E + LG_E - 1) / LG_E) * ((N + LG_T - 1) / LG_T);
-    a.logit_blocks = (nw + 3) / 4;
+    a.wide = N >= 256;
+    a.logit_blocks = (logit_waves(N, E, a.wide) + 3) / 4;
     int blocks = a.logit_blocks;
     a.njobs = njobs;
     for (int j = 0; j < njobs; j++) {

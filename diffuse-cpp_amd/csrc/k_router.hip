@@ -26,6 +26,8 @@ constexpr int RT_THREADS = 1024;
 constexpr int RT_WAVES = RT_THREADS / 64;
 // token bitmasks per expert: E * ceil(G/32) words, with G*E <= ROUTE_LDS and E <= 1024
 constexpr int RT_BITS = ROUTE_LDS / 32 + MAX_E;
+// per-(group, expert) prefix table of the dispatch (64 x 256 at 2048 tokens)
+constexpr int ROUTE_PREF = 16384;
 // a group has at most ROUTE_LDS / 8 pairs, one per thread
 static_assert(ROUTE_LDS / 8 <= RT_THREADS, "one thread per pair of a routing group");
 
@@ -85,16 +87,26 @@ __device__ void dispatch_lists(int c, const RouteParams &rp, const RouteBufs &rb
 // Dispatch of one forward over several routing groups, run by the last group
 // to finish (all 1024 threads), from the groups' histograms and local ranks.
 __device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
-                             int *s_tmp, int *s_off)
+                             int *s_tmp, int *s_off, int *s_pref)
 {
     const int E = rp.n_experts, K = rp.top_k, N = rp.n_tokens;
     const int G = rp.use_block ? rp.block_size : 32;
     const int ngroups = (N + G - 1) / G;
+    const bool table = ngroups * E <= ROUTE_PREF;
     const int tid = threadIdx.x;
+    // pairs of expert tid per group; the exclusive prefix over groups goes to
+    // s_pref[g][e] when it fits
     int c = 0;
     if (tid < E) {
+        if (table) {
+            for (int g = 0; g < ngroups; g++) {
+                s_pref[g * E + tid] = c;
+                c += rb.hist[(size_t)g * E + tid];
+            }
+        } else {
 #pragma unroll 8
-        for (int g = 0; g < ngroups; g++) c += rb.hist[(size_t)g * E + tid];
+            for (int g = 0; g < ngroups; g++) c += rb.hist[(size_t)g * E + tid];
+        }
     }
     dispatch_lists(c, rp, rb, wl, s_tmp, s_off);
     const int P = N * K;
@@ -102,7 +114,11 @@ __device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const W
         const int g = (p / K) / G;
         const int e = rb.idx[p];
         int base = s_off[e];
-        for (int h = 0; h < g; h++) base += rb.hist[(size_t)h * E + e];
+        if (table) {
+            base += s_pref[g * E + e];
+        } else {
+            for (int h = 0; h < g; h++) base += rb.hist[(size_t)h * E + e];
+        }
         rb.perm[base + rb.lrank[p]] = p;
     }
 }
@@ -159,6 +175,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     __shared__ int32_t s_idx[ROUTE_LDS / 8];      // group pairs (tokens x slots)
     __shared__ float s_w[ROUTE_LDS / 8];          // their probs
     __shared__ uint64_t s_k64[RT_WAVES][64];      // per wavefront: candidate rank keys
+    __shared__ int s_pref[ROUTE_PREF];            // dispatch: pairs of earlier groups per expert
     __shared__ uint32_t s_bits[RT_BITS];          // [e][word]: tokens of the group that chose e
     __shared__ int s_tmp[RT_WAVES + 1];
     __shared__ float s_thr;
@@ -343,7 +360,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    dispatch_all(rp, rb, wl, s_tmp, s_off);
+    dispatch_all(rp, rb, wl, s_tmp, s_off, s_pref);
     if (tid == 0) *counter = 0;
 }
 

@@ -71,12 +71,15 @@ def test_small_layer(ctx, O, wtype, n_tokens):
     assert err <= TOL[wtype]
 
 
-@pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0"])
+@pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "prefill_f16"])
 def test_flash_layer(ctx, O, name):
+    """Flash-shaped layers: one 32-token block (Q4_K, Q8_0), eight blocks
+    (Q4_K, 256 tokens, each block its own allowed set) and the 2048-token F16
+    prefill with a hot expert set."""
     import torch
     import dmoe
     from dmoe import synth
-    _say(f"case: {name} one 32-token block")
+    _say(f"case: {name}, {synth.CONFIGS[name].n_tokens} tokens")
     cfg = synth.CONFIGS[name]
     wd = synth.device_layer(cfg, 21, ctx)
     layer = ctx.wrap_device(wd)
