@@ -232,3 +232,60 @@ def test_injected_alloc_failure(O, monkeypatch):
     assert np.isfinite(y).all()
     layer.free()
     c.close()
+
+
+def _rmsnorm_np(h, eps=1e-6):
+    """RMSNorm without weight (float64 mean of the float32 squares, ggml_rms_norm)."""
+    sq = (h * h).astype(np.float64).sum(axis=1, keepdims=True)
+    mean = (sq / h.shape[1]).astype(np.float32)
+    return (h * (np.float32(1.0) / np.sqrt(mean + np.float32(eps)))).astype(np.float32)
+
+
+def test_stack32_chain(ctx, O):
+    """32 stacked flash-shaped Q4_K layers with Zipf-skewed routing over one
+    32-token block, chained through a synthetic residual RMSNorm (eps 1e-6).
+    Every layer is checked on the chain's own input: routing bit-exact, output
+    within 2e-2.  The final hidden state is checked against h0 plus the
+    oracle's outputs on the same per-layer inputs (the chain's accumulated
+    error).  An independent CPU chain is run for information only: layer
+    outputs agree to tolerance, not bit for bit, so a near-tie selection score
+    deep in the stack can route differently and the two chains then part."""
+    import torch
+    from dmoe import synth
+    cfg = synth.CONFIGS["stack32_q4k"]
+    _say(f"case: {cfg.n_layers} stacked layers, {cfg.n_tokens} tokens")
+    dev = torch.device("cuda:0")
+    h0 = synth.make_x(cfg, 5)
+    h = torch.from_numpy(h0).to(dev)
+    h_ref = h0.copy()                           # h0 + oracle outputs on the chain's inputs
+    h_cpu = h0.copy()                           # independent CPU chain
+    keep = []                                   # router / bias referenced by the wrapped layers
+    worst, split_at = 0.0, None
+    for li in range(cfg.n_layers):
+        wd = synth.device_layer(cfg, 5, ctx, layer=li)
+        layer = ctx.wrap_device(wd)
+        wh = synth.to_host(wd)
+        keep.append((layer, wd.gate_w, wd.gate_bias))
+        wd.exp_gate = wd.exp_up = wd.exp_down = wd.sh_gate = wd.sh_up = wd.sh_down = None
+        x = _rmsnorm_np(h.cpu().numpy())
+        y, dg = ctx.forward(layer, x, debug=True)
+        yr, dr = O.layer_forward(wh, x, debug=True)
+        _check_routing(dg, dr)
+        err = max_rel_err(y, yr)
+        worst = max(worst, err)
+        assert err <= TOL[cfg.wtype], f"layer {li}: max rel err {err}"
+        h = h + torch.from_numpy(y).to(dev)
+        h_ref = h_ref + yr
+        yc, dc = O.layer_forward(wh, _rmsnorm_np(h_cpu), debug=True)
+        if split_at is None and not np.array_equal(dc["idx"], dg["idx"]):
+            split_at = li
+        h_cpu = h_cpu + yc
+        del wh
+        torch.cuda.empty_cache()
+    hf = h.cpu().numpy()
+    final = float(np.abs(hf - h_ref).max() / np.abs(h_ref).max())
+    indep = float(np.abs(hf - h_cpu).max() / np.abs(h_cpu).max())
+    _say(f"  per-layer max rel err {worst:.3e}; final hidden state {final:.3e}; "
+         f"independent CPU chain: first routing difference at layer {split_at}, "
+         f"final difference {indep:.3e}")
+    assert final <= TOL[cfg.wtype]
