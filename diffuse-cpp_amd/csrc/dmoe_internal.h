@@ -117,10 +117,10 @@ struct RouteParams {
 // ---------------------------------------------------------------------------
 // Kernel launchers (each returns the hipGetLastError of its launch).
 // F16 expert products on MFMA, the prefill path (k_gemm.hip).
-constexpr int GM = 128;             // (token, slot) pairs per work item
+constexpr int GM = 256;             // (token, slot) pairs per work item
 constexpr int GK = 32;              // k per pipeline step
-constexpr int GN_GU = 64;           // moe_ff rows of a gate/up item (gate and up)
-constexpr int GN_DN = 128;          // n_embd rows of a down item
+constexpr int GN_GU = 128;          // moe_ff rows of a gate/up item (gate and up)
+constexpr int GN_DN = 256;          // n_embd rows of a down item
 constexpr int GEMM_BLOCKS = 1024;   // persistent grid
 struct GemmJob {
     WTensor eg, eu, ed;      // routed gate, up, down (F16, ggml row layout)
@@ -171,12 +171,14 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s);
 int expert_rows_per_item(int phase);     // output rows one work item covers
 bool expert_k_ok(int K);                 // reduction length the expert kernels accept
 // Q4_K row layout -> tiled layout of k_expert.hip (k_quant.hip): per matrix,
-// 16-row tiles, super-block-major (row r, super-block sb at
-// ((r/16)*nsb + sb)*2304 + (r%16)*144); inside each 144-byte block d and dmin
-// stay in bytes 0..3, the twelve scale bytes are repacked (dword 1:
-// sc0..sc4, dword 2: sc5..sc7 m0 m1, dword 3: m2..m6, six bits each; m7 in
-// bits 30..31 of the three dwords, low bits first) and the 128 quant bytes
-// are reordered so that byte 16 + 32g + 8c + b holds quant byte 32c + 8g + b.
+// 16-row tiles, super-block-major (the 16 rows of super-block sb of tile t
+// are the 2304-byte run at (t*nsb + sb)*2304); inside a run, byte b of the
+// repacked block of row r (r < 16) is at ((b/16)*16 + r)*16 + b%16.  In the
+// repacked 144-byte block d and dmin stay in bytes 0..3, the twelve scale
+// bytes are repacked (dword 1: sc0..sc4, dword 2: sc5..sc7 m0 m1, dword 3:
+// m2..m6, six bits each; m7 in bits 30..31 of the three dwords, low bits
+// first) and the 128 quant bytes are reordered so that byte 16 + 32g + 8c + b
+// holds quant byte 32c + 8g + b.
 hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
                            uint8_t *dst, hipStream_t s);
 

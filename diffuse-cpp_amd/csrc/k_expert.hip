@@ -25,10 +25,12 @@
 // 32-byte chunk c: low nibbles = sub-block 2c, high = 2c+1) side by side, and
 // repacks the 6-bit scales so that each is one bit-field extract.
 //
-// Memory.  A workgroup's four wavefronts share one work item: 16 activation
-// rows, held whole (all K) in LDS for the item, so the wavefronts stream their
-// weight tiles (coalesced 2304-byte runs) through a register ring with no
-// workgroup barrier inside the item.
+// Memory.  A workgroup's eight wavefronts share one work item (16 activation
+// rows).  Per step (one super-block) each wavefront copies its own weight
+// tiles (contiguous 2304-byte runs) into a private ring of LDS stages, and six
+// of them copy the step's activations into the workgroup's activation ring,
+// with LDS-direct loads (global_load_lds_dwordx4): two steps stay in flight
+// without holding registers.
 #include "dmoe_internal.h"
 
 namespace dmoe {
@@ -38,8 +40,8 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // Tuning constants (overridable at compile time).
-#ifndef DMOE_X_STAGES
-#define DMOE_X_STAGES 2          // register stages of the weight ring
+#ifndef DMOE_X_WSTAGES
+#define DMOE_X_WSTAGES 3         // LDS stages of each wavefront's weight ring
 #endif
 #ifndef DMOE_X_DN_IT
 #define DMOE_X_DN_IT 2           // row passes of a down item (shared activation tile)
@@ -47,20 +49,20 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 #ifndef DMOE_X_BLOCKS
 #define DMOE_X_BLOCKS 1024       // persistent grid
 #endif
-#ifndef DMOE_X_KC
-#define DMOE_X_KC 2048           // activation values per row held in LDS at a time
+#ifndef DMOE_X_WAVES
+#define DMOE_X_WAVES 8           // wavefronts per workgroup (one workgroup per CU)
 #endif
-#ifndef DMOE_X_WPE
-#define DMOE_X_WPE 2             // wavefronts per SIMD the kernel is compiled for
-#endif
-constexpr int WAVES = 4;                     // waves per workgroup
+constexpr int WAVES = DMOE_X_WAVES;
 constexpr int RT = 2;                        // 16-row weight tiles per wave per step
-constexpr int STAGES = DMOE_X_STAGES;
+constexpr int WSTAGES = DMOE_X_WSTAGES;
 constexpr int DN_IT = DMOE_X_DN_IT;
 constexpr int GROWS_GU = WAVES * 16;             // gate/up rows of an item (gate and up tiles)
 constexpr int GROWS_DN = WAVES * 16 * RT * DN_IT;   // down rows of an item
 constexpr int TILE_BYTES = 16 * Q4K_BYTES;   // one tile x one super-block
-constexpr int KC = DMOE_X_KC;
+constexpr int WSTEP_BYTES = RT * TILE_BYTES;             // one wave's weights of one step
+constexpr int WPIECES = WSTEP_BYTES / 16;                // 16-byte pieces of a step
+constexpr int WDMA = (WPIECES + 63) / 64;                // LDS-direct loads per step
+static_assert(WSTEP_BYTES % 16 == 0 && Q4K_BYTES == 144, "tile pieces");
 
 __device__ __forceinline__ float h16f(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (uint16_t)u); }
 
@@ -69,14 +71,32 @@ struct Q4KTile {        // a lane's share of one 16-row tile in one super-block
     uint4 q0, q1;       // the 32 quant bytes of lane group g
 };
 
-__device__ __forceinline__ void load_tile(Q4KTile &t, const uint8_t *tile, int sb, int r16, int g)
+// A weight tile of one super-block (a 2304-byte run of the tiled layout,
+// copied to a ring stage as it lies): piece k of row r16's repacked block at
+// slot 16 k + r16 (k = 0: d, dmin, scales; k = 1 + 2g, 2 + 2g: the quant bytes
+// of lane group g), so that every read below is free of LDS bank conflicts.
+__device__ __forceinline__ void read_tile(Q4KTile &t, const uint8_t *tile, int r16, int g)
 {
-    const uint8_t *blk = tile + (size_t)sb * TILE_BYTES + r16 * Q4K_BYTES;
-    t.h = *reinterpret_cast<const uint4 *>(blk);
-    const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * g);
-    t.q0 = qp[0];
-    t.q1 = qp[1];
+    const uint4 *p = reinterpret_cast<const uint4 *>(tile);
+    t.h = p[r16];
+    t.q0 = p[(1 + 2 * g) * 16 + r16];
+    t.q1 = p[(2 + 2 * g) * 16 + r16];
 }
+
+// LDS-direct load of 16 bytes per active lane: lane l's bytes go to LDS address
+// lds + 16 l (lds wave-uniform).  Inline assembly, so that the compiler does not
+// order every later LDS read after it (it cannot tell the ring's stages apart
+// and would wait for all loads in flight); completion is awaited with an
+// explicit s_waitcnt on the vector-memory counter.
+__device__ __forceinline__ void lds_load16(const void *src, const void *lds)
+{
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+}
+
+// s_waitcnt with vmcnt(n), lgkmcnt(0), expcnt untouched (n < 16)
+#define EXPERT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x70 | (n))
 
 __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w)
 {
@@ -85,87 +105,40 @@ __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
-// The item's activation rows in LDS (dynamic shared memory):
-//   q  [16][K + 16] int8   (row padding spreads the rows over the banks)
-//   bs [16][K/16 + 8] f16
-//   d  [nsb][16] f32
-struct ATileView {
-    int8_t *q;
-    uint16_t *bs;
-    float *d;
-    int qs, bss;        // row strides (bytes, f16 elements)
-};
+// Activations of one step (one super-block of the item's 16 rows) in a stage
+// of the workgroup's activation ring:
+//   q  [16][256] int8 at 0: 16-byte unit u of row r at unit u ^ (r & 11), which
+//      makes the operand reads (lane l: row l % 16, units 4 (l / 16) .. + 3)
+//      free of LDS bank conflicts
+//   bs [16][16] f16 at ABS_OFF (sums of 16)
+//   d  [16] f32 at AD_OFF
+constexpr int ABS_OFF = 4096, AD_OFF = 4608, ASTEP_BYTES = 4672;
+constexpr int ADMA_WAVES = 6;       // wavefronts that load a step's activations
 
-__device__ __forceinline__ ATileView atile_view(uint8_t *lds, int K)
+// LDS-direct load of 4 bytes per active lane (to lds + 4 l).
+__device__ __forceinline__ void lds_load4(const void *src, const void *lds)
 {
-    ATileView v;
-    v.qs = K + 16;
-    v.bss = K / 16 + 8;
-    v.q = reinterpret_cast<int8_t *>(lds);
-    v.bs = reinterpret_cast<uint16_t *>(lds + 16 * v.qs);
-    v.d = reinterpret_cast<float *>(lds + 16 * v.qs + 16 * v.bss * 2);
-    return v;
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
 }
 
-size_t atile_bytes(int K)
-{
-    return (size_t)16 * (K + 16) + (size_t)16 * (K / 16 + 8) * 2 + (size_t)(K / 256) * 16 * 4;
-}
-
-// Copies values [k0, k0 + kc) of the item's 16 activation rows (global row
-// rows[j], j < 16, in LDS) into the LDS tile; loads go out in rounds of eight
-// 16-byte pieces per thread.
-__device__ __forceinline__ void load_atile(const ActI8 &act, const int *rows, const ATileView &at,
-                                           int k0, int kc, int tid)
-{
-    constexpr int T = WAVES * 64;
-    const int K = act.K, nsb = K / 256;
-    const int per_row = kc / 16;                 // 16-byte pieces of a q row
-    const int nq = 16 * per_row;
-    for (int base = 0; base < nq; base += 8 * T) {
-        uint4 v[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = min(base + i * T + tid, nq - 1);
-            const int r = c / per_row, col = c - r * per_row;
-            v[i] = *reinterpret_cast<const uint4 *>(act.q + (size_t)rows[r] * K + k0 + col * 16);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = base + i * T + tid;
-            if (c < nq) {
-                const int r = c / per_row, col = c - r * per_row;
-                *reinterpret_cast<uint4 *>(at.q + r * at.qs + col * 16) = v[i];
-            }
-        }
-    }
-    const int bs_pieces = kc / 128;              // 16-byte pieces of a bs row
-    for (int c = tid; c < 16 * bs_pieces; c += T) {
-        const int r = c / bs_pieces, col = c - r * bs_pieces;
-        const uint4 v = *reinterpret_cast<const uint4 *>(act.bs + (size_t)rows[r] * (K / 16) + k0 / 16 + col * 8);
-        *reinterpret_cast<uint4 *>(at.bs + r * at.bss + col * 8) = v;
-    }
-    const int nsbc = kc / 256, sb0 = k0 / 256;
-    for (int c = tid; c < 16 * nsbc; c += T) {
-        const int r = c / nsbc, sb = c - r * nsbc;
-        at.d[sb * 16 + r] = act.d[(size_t)rows[r] * nsb + sb0 + sb];
-    }
-}
-
-// One super-block of RT weight tiles against the activation tile.
-__device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[RT], const ATileView &at, int sb,
-                                           int r16, int g, float (&acc)[RT][4])
+// One super-block of RT weight tiles against the step's activations.
+__device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[RT], const uint8_t *ast, int r16, int g,
+                                           float (&acc)[RT][4])
 {
     // activation operands of the 8 sub-blocks: row r16, bytes 64g .. 64g+63
-    const uint4 *ap = reinterpret_cast<const uint4 *>(at.q + r16 * at.qs + sb * 256 + 64 * g);
-    const uint4 a01 = ap[0], a23 = ap[1], a45 = ap[2], a67 = ap[3];
+    // (16-byte units 4g .. 4g+3, swizzled)
+    const uint4 *ap = reinterpret_cast<const uint4 *>(ast + r16 * 256);
+    const uint4 a01 = ap[(4 * g + 0) ^ (r16 & 11)], a23 = ap[(4 * g + 1) ^ (r16 & 11)];
+    const uint4 a45 = ap[(4 * g + 2) ^ (r16 & 11)], a67 = ap[(4 * g + 3) ^ (r16 & 11)];
     const long a[8] = {
         (long)((uint64_t)a01.y << 32 | a01.x), (long)((uint64_t)a01.w << 32 | a01.z),
         (long)((uint64_t)a23.y << 32 | a23.x), (long)((uint64_t)a23.w << 32 | a23.z),
         (long)((uint64_t)a45.y << 32 | a45.x), (long)((uint64_t)a45.w << 32 | a45.z),
         (long)((uint64_t)a67.y << 32 | a67.x), (long)((uint64_t)a67.w << 32 | a67.z)};
-    const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(at.bs + r16 * at.bss + sb * 16 + 4 * g));
-    const float4 dxv = *reinterpret_cast<const float4 *>(at.d + sb * 16 + 4 * g);
+    const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(ast + ABS_OFF + r16 * 32 + 8 * g));
+    const float4 dxv = *reinterpret_cast<const float4 *>(ast + AD_OFF + 16 * g);
     const float dx[4] = {dxv.x, dxv.y, dxv.z, dxv.w};
 #pragma unroll
     for (int r = 0; r < RT; r++) {
@@ -192,8 +165,11 @@ __device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[RT], const ATile
             v4i s_lo = {0, 0, 0, 0}, s_hi = {0, 0, 0, 0};
             s_lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[2 * c], blo, s_lo, 0, 0, 0);
             s_hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[2 * c + 1], bhi, s_hi, 0, 0, 0);
+            // |S_j| <= 32 * 15 * 127 and sc_j < 64: 24-bit products are exact
+            // (v_mad_i32_i24, full rate; a 32-bit multiply is quarter rate)
 #pragma unroll
-            for (int i = 0; i < 4; i++) isum[i] += (int)sc[2 * c] * s_lo[i] + (int)sc[2 * c + 1] * s_hi[i];
+            for (int i = 0; i < 4; i++)
+                isum[i] += __mul24((int)sc[2 * c], s_lo[i]) + __mul24((int)sc[2 * c + 1], s_hi[i]);
         }
         f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
         s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, bm, s2, 0, 0, 0);
@@ -203,21 +179,27 @@ __device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[RT], const ATile
     }
 }
 
-// Work items of phase 0: routed (work-list entry ec, group of 64 rows), then
-// shared (chunk of 8 tokens, group of 64 rows); phase 1 the same with groups of
-// GROWS_DN rows.  A routed item's 16 activation rows are the pairs of its
-// entry (one expert, up to 16 consecutive pairs of it); a shared item's are the
-// a1 / a0 digit rows of its 8 tokens interleaved (t a1, t a0, ...), so that each
-// lane's four outputs are (t, a1), (t, a0), (t+1, a1), (t+1, a0) and the two
-// digits' products are summed in-lane.
+// Work items of phase 0: routed (work-list entry ec, group of GROWS_GU rows),
+// then shared (chunk of 8 tokens, group of GROWS_GU rows); phase 1 the same
+// with groups of GROWS_DN rows.  A routed item's 16 activation rows are the
+// pairs of its entry (one expert, up to 16 consecutive pairs of it); a shared
+// item's are the a1 / a0 digit rows of its 8 tokens interleaved (t a1, t a0,
+// ...), so that each lane's four outputs are (t, a1), (t, a0), (t+1, a1),
+// (t+1, a0) and the two digits' products are summed in-lane.
+//
+// Step s of an item is super-block s % nsb of row pass s / nsb.  Its weights
+// (each wavefront's own tiles) and its activations (the workgroup's 16 rows,
+// loaded by wavefronts 0..5) go to ring stage s % WSTAGES with LDS-direct
+// loads issued WSTAGES - 1 steps ahead; one barrier per step makes the
+// activations visible to all wavefronts and frees the stage for refilling.
 template <int PHASE>
-__global__ __launch_bounds__(WAVES * 64, DMOE_X_WPE) void k_expert_q4k(MoeJob job)
+__global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
 {
     constexpr bool DOWN = PHASE == 1;
     constexpr int IT = DOWN ? DN_IT : 1;             // row passes per item
     constexpr int GROWS = DOWN ? GROWS_DN : GROWS_GU;
-    extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int s_rows[16];
+    __shared__ __align__(16) uint8_t s_act[WSTAGES][ASTEP_BYTES];
+    __shared__ __align__(16) uint8_t s_w[WAVES][WSTAGES][WSTEP_BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -232,9 +214,20 @@ __global__ __launch_bounds__(WAVES * 64, DMOE_X_WPE) void k_expert_q4k(MoeJob jo
     const int Kin = DOWN ? FF : H;                   // reduction length (SF == FF when shared)
     const int nsb = Kin / 256;
     const int steps = IT * nsb;
-    const int kc = min(Kin, KC);                     // values per LDS chunk (Kin % kc == 0)
-    const int nsbc = kc / 256;
-    const ATileView at = atile_view(lds, kc);
+    // weight load jd of a step: lane's piece p = 64 jd + lane (p < WPIECES) is
+    // piece p % 144 of tile p / 144, copied to slot p of the stage
+    int goff[WDMA], gtile[WDMA];
+#pragma unroll
+    for (int jd = 0; jd < WDMA; jd++) {
+        const int p = min(64 * jd + lane, WPIECES - 1);
+        gtile[jd] = p / 144;
+        goff[jd] = (p % 144) * 16;
+    }
+    // activation load of this wavefront (wavefronts 0..5): which item row
+    // (ar) and piece; 0..3: q units of rows 4w .. 4w+3, 4: bs halves, 5: d
+    const int ar = wave < 4 ? 4 * wave + (lane >> 4) : (wave == 4 ? (lane >> 1) & 15 : lane & 15);
+    const int aunit = (lane & 15) ^ (ar & 11);       // q: logical unit of this lane's slot
+    const bool aload = wave < 4 || (wave == 4 && lane < 32) || (wave == 5 && lane < 16);
 
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
         const bool shared = item >= routed_items;
@@ -270,41 +263,48 @@ __global__ __launch_bounds__(WAVES * 64, DMOE_X_WPE) void k_expert_q4k(MoeJob jo
                     tb[it][r] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
                 }
         }
-        auto load_step = [&](Q4KTile (&t)[RT], int s) {
-            const int sc = min(s, steps - 1);
-            const int it = sc / nsb, sb = sc - it * nsb;
+        // the activation row of item row ar: tokens in phase 0, pairs in phase
+        // 1; shared rows interleave the a1 and a0 digit rows (a0 rows start at N)
+        const ActI8 &act = DOWN ? (shared ? job.ahs : job.ah) : (shared ? job.axs : job.ax);
+        int arow;
+        if (shared) {
+            arow = t_first + min(ar >> 1, nt - 1) + (ar & 1) * N;
+        } else {
+            const int p = job.perm[t_first + min(ar, nt - 1)];
+            arow = DOWN ? p : p / K;
+        }
+        const int8_t *aq = act.q + (size_t)arow * Kin + aunit * 16;
+        const uint16_t *abs_ = act.bs + (size_t)arow * (Kin / 16) + (lane & 1) * 8;
+        const float *ad = act.d + (size_t)arow * nsb;
+
+        auto issue = [&](int s) {
+            if (s >= steps) return;
+            const int it = s / nsb, sb = s - it * nsb;
+            const int stg = s % WSTAGES;
+            const uint8_t *t0 = tb[0][0], *t1 = tb[0][1];
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
-                const uint8_t *p = tb[0][r];
+            for (int q = 1; q < IT; q++)
+                if (it == q) { t0 = tb[q][0]; t1 = tb[q][1]; }
 #pragma unroll
-                for (int q = 1; q < IT; q++)
-                    if (it == q) p = tb[q][r];
-                load_tile(t[r], p, sb, r16, g);
+            for (int jd = 0; jd < WDMA; jd++) {
+                const uint8_t *src = (gtile[jd] ? t1 : t0) + (size_t)sb * TILE_BYTES + goff[jd];
+                if (64 * (jd + 1) <= WPIECES || 64 * jd + lane < WPIECES)
+                    lds_load16(src, &s_w[wave][stg][1024 * jd]);
             }
+            if (wave < 4)
+                lds_load16(aq + sb * 256, &s_act[stg][1024 * wave]);
+            else if (wave == 4 && aload)
+                lds_load16(abs_ + sb * 16, &s_act[stg][ABS_OFF]);
+            else if (wave == 5 && aload)
+                lds_load4(ad + sb, &s_act[stg][AD_OFF]);
         };
 
-        // weights of the first steps in flight while the activation tile loads
-        Q4KTile ring[STAGES][RT];
+        // the previous item's reads of the rings are done in every wavefront
+        EXPERT_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
 #pragma unroll
-        for (int st = 0; st < STAGES; st++) load_step(ring[st], st);
-        const ActI8 &act = DOWN ? (shared ? job.ahs : job.ah) : (shared ? job.axs : job.ax);
-        __syncthreads();                          // the previous item's LDS reads are done
-        // activation row of item row jr: tokens in phase 0, pairs in phase 1;
-        // shared rows interleave the a1 and a0 digit rows (a0 rows start at N)
-        if (tid < 16) {
-            int row;
-            if (shared) {
-                row = t_first + min(tid >> 1, nt - 1) + (tid & 1) * N;
-            } else {
-                const int p = job.perm[t_first + min(tid, nt - 1)];
-                row = DOWN ? p : p / K;
-            }
-            s_rows[tid] = row;
-        }
-        __syncthreads();
-        load_atile(act, s_rows, at, 0, kc, tid);
-        __syncthreads();
-        int chunk = 0;                            // K chunk in LDS
+        for (int s = 0; s < WSTAGES - 1; s++) issue(s);
 
         float acc[IT][RT][4];
 #pragma unroll
@@ -313,28 +313,31 @@ __global__ __launch_bounds__(WAVES * 64, DMOE_X_WPE) void k_expert_q4k(MoeJob jo
             for (int r = 0; r < RT; r++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[it][r][i] = 0.0f;
-        // weight ring: compute step s from its stage, then refill that stage
-        // with step s + STAGES (clamped: every step issues the same loads)
-        for (int s0 = 0; s0 < steps; s0 += STAGES) {
-#pragma unroll
-            for (int st = 0; st < STAGES; st++) {
-                const int s = s0 + st;
-                if (s < steps) {
-                    const int it = s / nsb, sb = s - it * nsb;
-                    const int ck = sb / nsbc;
-                    if (ck != chunk) {
-                        // next K chunk of the activation rows (the weights stay in flight)
-                        __syncthreads();
-                        load_atile(act, s_rows, at, ck * kc, kc, tid);
-                        __syncthreads();
-                        chunk = ck;
-                    }
-#pragma unroll
-                    for (int q = 0; q < IT; q++)
-                        if (it == q) compute_sb(ring[st], at, sb - ck * nsbc, r16, g, acc[q]);
-                }
-                load_step(ring[st], s + STAGES);
+        for (int s = 0; s < steps; s++) {
+            // step s's loads have landed once the WSTAGES - 2 later steps' are
+            // all that may be in flight (a wavefront issues WDMA loads per step,
+            // plus one when it loads activations); in the last steps fewer
+            // follow: wait for all.  The barrier makes that true of every
+            // wavefront and frees the stage read in step s - 1.
+            if (s + WSTAGES - 2 < steps) {
+                if (wave < ADMA_WAVES)
+                    EXPERT_WAIT_VM((WDMA + 1) * (WSTAGES - 2));
+                else
+                    EXPERT_WAIT_VM(WDMA * (WSTAGES - 2));
+            } else {
+                EXPERT_WAIT_VM(0);
             }
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            issue(s + WSTAGES - 1);
+            const int it = s / nsb;
+            const int stg = s % WSTAGES;
+            Q4KTile cur[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) read_tile(cur[r], &s_w[wave][stg][r * TILE_BYTES], r16, g);
+#pragma unroll
+            for (int q = 0; q < IT; q++)
+                if (it == q) compute_sb(cur, s_act[stg], r16, g, acc[q]);
         }
 
         // results
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(WAVES * 64, DMOE_X_WPE) void k_expert_q4k(MoeJob jo
 
 int expert_rows_per_item(int phase) { return phase == 0 ? GROWS_GU : GROWS_DN; }
 
-bool expert_k_ok(int K) { return K % 256 == 0 && (K <= KC || K % KC == 0); }
+bool expert_k_ok(int K) { return K % 256 == 0; }
 
 hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s)
 {
@@ -383,20 +386,10 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s)
         job.ax.K != job.H || job.ah.K != job.FF ||
         (job.has_shared && (job.SF != job.FF || job.ahs.K != job.SF)))
         return hipErrorInvalidValue;
-    const int Kin = phase == 0 ? job.H : job.FF;
-    if (Kin > KC && Kin % KC) return hipErrorInvalidValue;
-    const size_t lds = atile_bytes(Kin < KC ? Kin : KC);
-    static bool attr[2] = {false, false};
-    if (!attr[phase]) {
-        const void *k = phase == 0 ? (const void *)k_expert_q4k<0> : (const void *)k_expert_q4k<1>;
-        const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 156 * 1024);
-        if (e != hipSuccess) return e;
-        attr[phase] = true;
-    }
     if (phase == 0)
-        hipLaunchKernelGGL(k_expert_q4k<0>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), lds, s, job);
+        hipLaunchKernelGGL(k_expert_q4k<0>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
     else
-        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), lds, s, job);
+        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
     return hipGetLastError();
 }
 

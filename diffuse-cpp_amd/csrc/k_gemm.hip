@@ -9,14 +9,16 @@
 //            phase 1 (routed) or as their hi / lo pair (shared)
 //   phase 1: y = W_down h
 //
-// Work item: one expert, a block of up to 128 of its (token, slot) pairs (or
-// 128 tokens of the shared expert) and a group of output rows (64 moe_ff rows
-// of gate and of up, or 128 n_embd rows of down).  Items of one expert and
+// Work item: one expert, a block of up to 256 of its (token, slot) pairs (or
+// 256 tokens of the shared expert) and a group of output rows (128 moe_ff rows
+// of gate and of up, or 256 n_embd rows of down).  Items of one expert and
 // row group but different pair blocks are a row-group count apart, so they run
 // together and share the weight rows through the caches.  Each 32-wide k
-// step stages the 128 activation rows and the 128 weight rows through
-// double-buffered LDS; every wavefront computes a 64 x 64 output tile as 4 x 4
-// v_mfma_f32_16x16x32_f16 (operand layout as in k_expert.hip: srcA lane l =
+// step stages the 256 activation rows and the 256 weight rows in LDS with the
+// LDS-direct global loads (global_load_lds_dwordx4: no registers held, so a
+// 4-stage ring keeps three steps of loads in flight to cover HBM latency);
+// each of the 8 wavefronts computes a 128 x 64 output
+// tile as 8 x 4 v_mfma_f32_16x16x32_f16 (operand layout as in k_expert.hip: srcA lane l =
 // activation row l%16, k = 8*(l/16)+e; srcB = weight row, same k; D lane l =
 // weight row l%16, activation rows 4*(l/16)+i).
 #include "dmoe_internal.h"
@@ -26,21 +28,49 @@ namespace dmoe {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int GWAVES = 4;
+constexpr int GWAVES = 8;
 constexpr int GT = GWAVES * 64;      // threads per workgroup
-constexpr int GROW = GK + 8;         // LDS row (f16) with padding: 80 bytes, conflict-free reads
+constexpr int GNW = 256;             // weight rows per item (gate/up: 128 moe_ff rows of each)
+constexpr int GS = 4;                // LDS pipeline stages
+constexpr int GTILE = GM * GK * 2;   // bytes of one operand tile of a stage (64-byte rows)
+constexpr int GP = GM * GK / 8 / GT; // 16-byte pieces per thread per tile and stage
 
 __device__ __forceinline__ float gsilu(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ uint16_t f2h_rn(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// The 16-byte k-chunk q (0..3) of tile row r sits in slot q ^ swz(r) of the
+// row.  A ds_read_b128 serves 16 lanes per cycle over the 64 banks: the four
+// lane quads (4 consecutive lanes) of one half-wave whose quad indices have
+// equal bit parity (measured on gfx950 with the LDS bank-conflict counter).
+// The operand reads (lane l: row l % 16, chunk l / 16) are conflict-free
+// with the slot flipped by row bits 1..2.
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
+
+// s_waitcnt with vmcnt(n), lgkmcnt(0), expcnt untouched (n < 16)
+#define GEMM_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x70 | (n))
+
+// LDS-direct load of 16 bytes per lane: lane l's bytes go to LDS address
+// lds + 16 l (lds wave-uniform).  Written as inline assembly so that the
+// compiler does not order every later LDS read after it (it cannot tell the
+// ring's buffers apart and would wait for all loads in flight); completion is
+// awaited explicitly with GEMM_WAIT_VM before the barrier of each step.
+__device__ __forceinline__ void lds_load16(const void *src, const void *lds)
+{
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+}
 
 template <int PHASE>
 __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
 {
     constexpr bool DOWN = PHASE == 1;
     constexpr int GN = DOWN ? GN_DN : GN_GU;         // output rows per item
-    __shared__ __align__(16) uint16_t As[2][GM][GROW];
-    __shared__ __align__(16) uint16_t Bs[2][128][GROW];
+    static_assert(GP * GT * 8 == GM * GK && GNW == GM && GP == 2, "tile shapes");
+    // stage s: activation tile at S[s][0], weight tile at S[s][1]; row r of a
+    // tile is 64 bytes at r * 64, its k-chunks swizzled by swz(r)
+    __shared__ __align__(16) uint8_t S[GS][2][GTILE];
     __shared__ int s_arow[GM];
 
     const int tid = threadIdx.x;
@@ -51,15 +81,53 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
     const int n_ec = job.wl.n_ec[0];
     const int nch = job.has_shared ? (N + GM - 1) / GM : 0;
     const int rg = (DOWN ? H : FF) / GN, rg_sh = (DOWN ? H : SF) / GN;
-    const int routed_items = n_ec * rg;
-    const int total = routed_items + nch * rg_sh;
-    const int tok0 = 64 * (wave >> 1);               // this wave's 64 activation rows
+    // Items by XCD: workgroup b runs on XCD b % 8 (round-robin dispatch).  The
+    // units (expert chunks, expert-major, then the shared expert's token
+    // chunks) are split into 8 contiguous segments of equal work (a shared
+    // unit does two passes), one per XCD, so that the row groups of a unit
+    // (one activation block) and the chunks of an expert (one weight slice)
+    // meet in the same L2.  Within a segment, item m is unit m / row-groups,
+    // row group m % row-groups.
+    static_assert(GEMM_BLOCKS % 8 == 0, "grid by XCD");
+    const int xcd = blockIdx.x & 7, G8 = gridDim.x >> 3, lb = blockIdx.x >> 3;
+    const long w_routed = (long)n_ec * rg, w_total = w_routed + 2L * nch * rg_sh;
+    auto seg = [&](int x) -> int {
+        const long t = w_total * x / 8;
+        return t <= w_routed ? (int)((t + rg - 1) / rg)
+                             : n_ec + (int)((t - w_routed + 2 * rg_sh - 1) / (2 * rg_sh));
+    };
+    const int u0 = seg(xcd), u1 = seg(xcd + 1);
+    const int nr = max(0, min(u1, n_ec) - u0);                             // routed units
+    const int s0 = max(u0, n_ec) - n_ec, ns = max(0, u1 - max(u0, n_ec)); // shared chunks
+    const int seg_items = nr * rg + ns * rg_sh;
+    // wave grid 2 (activation rows) x 4 (weight rows): 128 x 64 per wave
+    const int tok0 = 128 * (wave >> 2);
+    const int wq = wave & 3;
+    // weight rows of this wave's four 16-row tiles in the weight tile: gate/up:
+    // 32 moe_ff rows of gate (tiles 0, 1) and the same rows of up (tiles 2, 3)
+    int brow[4];
+#pragma unroll
+    for (int tw = 0; tw < 4; tw++)
+        brow[tw] = DOWN ? 64 * wq + 16 * tw
+                        : (tw < 2 ? 32 * wq + 16 * tw : GN + 32 * wq + 16 * (tw - 2));
+    // byte offsets of this lane's operand chunk g in a tile
+    int aoff[8], boff[4];
+#pragma unroll
+    for (int ti = 0; ti < 8; ti++) {
+        const int r = tok0 + 16 * ti + r16;
+        aoff[ti] = r * 64 + ((g ^ swz(r)) << 4);
+    }
+#pragma unroll
+    for (int tw = 0; tw < 4; tw++) {
+        const int r = brow[tw] + r16;
+        boff[tw] = r * 64 + ((g ^ swz(r)) << 4);
+    }
 
-    for (int item = blockIdx.x; item < total; item += gridDim.x) {
-        const bool shared = item >= routed_items;
-        const int j = shared ? item - routed_items : item;
+    for (int m = lb; m < seg_items; m += G8) {
+        const bool shared = m >= nr * rg;
+        const int mm = shared ? m - nr * rg : m;
         const int rgn = shared ? rg_sh : rg;
-        const int unit = j / rgn, rb = j - unit * rgn;
+        const int unit = (shared ? s0 : u0) + mm / rgn, rb = mm % rgn;
         int t_first, nt, e = 0;
         if (!shared) {
             e = job.wl.ec_expert[unit];
@@ -77,7 +145,9 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         const uint16_t *A = DOWN ? (shared ? job.hs16 : job.h16) : (shared ? job.xs16 : job.x16);
         const size_t lo_off = (size_t)N * Kin;           // split arrays only
 
-        __syncthreads();                                  // previous item's LDS reads are done
+        // the previous item's loads into LDS, its stores and its LDS reads are
+        // complete after this barrier (its fence waits for all memory counters)
+        __syncthreads();
         if (tid < GM) {
             const int i = min(tid, nt - 1);
             int row;
@@ -91,80 +161,78 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         }
         __syncthreads();
 
-        // this thread's two 16-byte pieces of each tile: row c >> 2, column (c & 3) * 8
-        const int pr0 = tid >> 2, pr1 = (tid + GT) >> 2, pc = (tid & 3) * 8;
-        const uint16_t *a0 = A + (size_t)s_arow[pr0] * Kin + pc;
-        const uint16_t *a1 = A + (size_t)s_arow[pr1] * Kin + pc;
-        // weight row r (0..127) of this item: gate rows 0..63 and up rows 64..127
-        // of the same moe_ff rows, or 128 down rows
-        auto wrow = [&](int r) -> const uint8_t * {
-            if (!DOWN) {
-                const WTensor &w = r < 64 ? (shared ? job.sg : job.eg) : (shared ? job.su : job.eu);
-                const int rr = r < 64 ? r : r - 64;
-                return w.data + (size_t)e * w.nb2 + (size_t)(rb * GN + rr) * w.nb1;
-            }
-            const WTensor &w = shared ? job.sd : job.ed;
-            return w.data + (size_t)e * w.nb2 + (size_t)(rb * GN + r) * w.nb1;
-        };
-        const uint8_t *b0 = wrow(pr0) + pc * 2, *b1 = wrow(pr1) + pc * 2;
-
-        auto gload = [&](int st, uint4 (&va)[2], uint4 (&vb)[2]) {
-            const int pass = st >= nsteps ? 1 : 0;
-            const int k0 = (st - pass * nsteps) * GK;
-            const size_t off = pass ? lo_off : 0;
-            va[0] = *reinterpret_cast<const uint4 *>(a0 + off + k0);
-            va[1] = *reinterpret_cast<const uint4 *>(a1 + off + k0);
-            vb[0] = *reinterpret_cast<const uint4 *>(b0 + (size_t)k0 * 2);
-            vb[1] = *reinterpret_cast<const uint4 *>(b1 + (size_t)k0 * 2);
-        };
-        auto lstore = [&](int buf, const uint4 (&va)[2], const uint4 (&vb)[2]) {
-            *reinterpret_cast<uint4 *>(&As[buf][pr0][pc]) = va[0];
-            *reinterpret_cast<uint4 *>(&As[buf][pr1][pc]) = va[1];
-            *reinterpret_cast<uint4 *>(&Bs[buf][pr0][pc]) = vb[0];
-            *reinterpret_cast<uint4 *>(&Bs[buf][pr1][pc]) = vb[1];
-        };
-
-        f4 acc[4][4];
+        // weight rows of the item: gate rows 0..127 and up rows 128..255 of
+        // the same moe_ff rows, or 256 down rows.  (The fields are selected
+        // here, not in a lambda: a lambda that captured the argument struct
+        // would copy it to private memory.)
+        const WTensor &w0 = DOWN ? (shared ? job.sd : job.ed) : (shared ? job.sg : job.eg);
+        const WTensor &w1 = DOWN ? (shared ? job.sd : job.ed) : (shared ? job.su : job.eu);
+        const uint8_t *wb0 = w0.data + (size_t)e * w0.nb2 + (size_t)(rb * GN) * w0.nb1;
+        const uint8_t *wb1 = w1.data + (size_t)e * w1.nb2 + (size_t)(rb * GN) * w1.nb1;
+        const size_t wnb0 = w0.nb1, wnb1 = w1.nb1;
+        // piece c = i * GT + tid of a tile (16 bytes at c * 16): row c >> 2,
+        // slot c & 3, holding k-chunk (c & 3) ^ swz(row).  A wavefront's pieces
+        // of one load are 1 KB of consecutive LDS, as the LDS-direct load writes.
+        const uint8_t *ap[GP], *bp[GP];
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++)
+        for (int i = 0; i < GP; i++) {
+            const int c = i * GT + tid, row = c >> 2;
+            const int q = (c & 3) ^ swz(row);
+            ap[i] = reinterpret_cast<const uint8_t *>(A + (size_t)s_arow[row] * Kin) + q * 16;
+            const bool up = !DOWN && row >= GN;
+            bp[i] = (up ? wb1 + (size_t)(row - GN) * wnb1 : wb0 + (size_t)row * wnb0) + q * 16;
+        }
+        // stage st of the k loop into LDS buffer buf: 2 GP loads per thread
+        // (none past the last stage, so nothing is in flight when the item ends)
+        auto issue = [&](int st, int buf) {
+            if (st >= total_steps) return;
+            const int pass = st >= nsteps ? 1 : 0;
+            const size_t kb = (size_t)(st - pass * nsteps) * GK * 2;
+            const size_t ab = kb + (pass ? lo_off * 2 : 0);
+#pragma unroll
+            for (int i = 0; i < GP; i++) {
+                const int dst = (i * GT + wave * 64) * 16;
+                lds_load16(ap[i] + ab, &S[buf][0][dst]);
+                lds_load16(bp[i] + kb, &S[buf][1][dst]);
+            }
+        };
+
+        f4 acc[8][4];
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++)
 #pragma unroll
             for (int tw = 0; tw < 4; tw++) acc[ti][tw] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-        // weight rows of this wave's four 16-row tiles in Bs
-        int brow[4];
-#pragma unroll
-        for (int tw = 0; tw < 4; tw++)
-            brow[tw] = DOWN ? 64 * (wave & 1) + 16 * tw
-                            : (tw < 2 ? 32 * (wave & 1) + 16 * tw : 64 + 32 * (wave & 1) + 16 * (tw - 2));
 
-        {
-            uint4 va[2], vb[2];
-            gload(0, va, vb);
-            lstore(0, va, vb);
-        }
-        __syncthreads();
+#pragma unroll
+        for (int s0 = 0; s0 < GS - 1; s0++) issue(s0, s0);
         for (int st = 0; st < total_steps; st++) {
-            const int buf = st & 1;
-            uint4 va[2], vb[2];
-            gload(min(st + 1, total_steps - 1), va, vb);  // clamped: every step loads
-            h8 a[4], b[4];
+            const int buf = st % GS;
+            // stage st has landed (the GS - 2 later stages may be in flight) in
+            // this wavefront's pieces; the barrier makes that true of all, and
+            // frees the buffer read in step st - 1 for stage st + GS - 1.  In
+            // the last steps fewer stages follow: wait for all.
+            if (st + GS - 2 < total_steps)
+                GEMM_WAIT_VM(2 * GP * (GS - 2));
+            else
+                GEMM_WAIT_VM(0);
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            issue(st + GS - 1, (st + GS - 1) % GS);
+            h8 b[4];
 #pragma unroll
-            for (int ti = 0; ti < 4; ti++)
-                a[ti] = *reinterpret_cast<const h8 *>(&As[buf][tok0 + 16 * ti + r16][8 * g]);
+            for (int tw = 0; tw < 4; tw++) b[tw] = *reinterpret_cast<const h8 *>(&S[buf][1][boff[tw]]);
 #pragma unroll
-            for (int tw = 0; tw < 4; tw++)
-                b[tw] = *reinterpret_cast<const h8 *>(&Bs[buf][brow[tw] + r16][8 * g]);
-#pragma unroll
-            for (int ti = 0; ti < 4; ti++)
+            for (int ti = 0; ti < 8; ti++) {
+                const h8 a = *reinterpret_cast<const h8 *>(&S[buf][0][aoff[ti]]);
 #pragma unroll
                 for (int tw = 0; tw < 4; tw++)
-                    acc[ti][tw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ti], b[tw], acc[ti][tw], 0, 0, 0);
-            if (st + 1 < total_steps) lstore(buf ^ 1, va, vb);
-            __syncthreads();
+                    acc[ti][tw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[tw], acc[ti][tw], 0, 0, 0);
+            }
         }
 
         // results: output row of tile tw for lane r16; activation rows 16 ti + 4 g + i
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++)
+        for (int ti = 0; ti < 8; ti++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int tt = tok0 + 16 * ti + 4 * g + i;
@@ -172,7 +240,7 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
                 if (!DOWN) {
 #pragma unroll
                     for (int tj = 0; tj < 2; tj++) {
-                        const int row = rb * GN + 32 * (wave & 1) + 16 * tj + r16;
+                        const int row = rb * GN + 32 * wq + 16 * tj + r16;
                         const float hv = gsilu(acc[ti][tj][i]) * acc[ti][2 + tj][i];
                         if (!shared) {
                             const int p = job.perm[t_first + tt];

@@ -248,9 +248,10 @@ __global__ __launch_bounds__(256) void k_wq_f16(const float *__restrict__ src, i
 // ---------------------------------------------------------------------------
 // Q4_K row layout -> tiled layout: per matrix, 16-row tiles; inside a tile the
 // super-blocks come first, so the 16 rows' blocks of one super-block are one
-// contiguous 2304-byte run:  dst offset of (row r, super-block sb) =
-//   ((r/16) * nsb + sb) * 2304 + (r%16) * 144.
-// The block bytes themselves are unchanged.  One thread per 16-byte piece.
+// contiguous 2304-byte run starting at ((r/16) * nsb + sb) * 2304.  Inside the
+// run, the repacked 144-byte block of row r % 16 is nine 16-byte pieces, piece
+// k at byte (16 k + r % 16) * 16 (piece-major, so that a kernel copying the
+// run to LDS as it lies reads each piece without bank conflicts).
 __global__ __launch_bounds__(256) void k_tile_q4k(const uint8_t *__restrict__ src, size_t nb1,
                                                   size_t nb2, int rows, int nsb, int mats,
                                                   uint8_t *__restrict__ dst)
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(256) void k_tile_q4k(const uint8_t *__restrict__ sr
     const int r = (int)(j / nsb);
     const uint8_t *in = src + (size_t)m * nb2 + (size_t)r * nb1 + (size_t)sb * Q4K_BYTES;
     uint8_t *out = dst + (size_t)m * rows * nsb * Q4K_BYTES +
-                   ((size_t)(r / 16) * nsb + sb) * (16 * Q4K_BYTES) + (size_t)(r % 16) * Q4K_BYTES;
+                   ((size_t)(r / 16) * nsb + sb) * (16 * Q4K_BYTES) + (size_t)(r % 16) * 16;
     uint8_t blk[Q4K_BYTES];
 #pragma unroll
     for (int p = 0; p < 9; p++)
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(256) void k_tile_q4k(const uint8_t *__restrict__ sr
         for (int c = 0; c < 4; c++) ws[4 * g + c] = qs[4 * c + g];
 #pragma unroll
     for (int p = 0; p < 9; p++)
-        *reinterpret_cast<uint4 *>(out + 16 * p) = *reinterpret_cast<const uint4 *>(w + 4 * p);
+        *reinterpret_cast<uint4 *>(out + 256 * p) = *reinterpret_cast<const uint4 *>(w + 4 * p);
 }
 
 hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
