@@ -56,6 +56,7 @@ constexpr int WAVES = DMOE_X_WAVES;
 constexpr int RT = 2;                        // 16-row weight tiles per wave per step
 constexpr int WSTAGES = DMOE_X_WSTAGES;
 constexpr int DN_IT = DMOE_X_DN_IT;
+static_assert(DN_IT == 1 || DN_IT == 2, "row passes of a down item");
 constexpr int GROWS_GU = WAVES * 16;             // gate/up rows of an item (gate and up tiles)
 constexpr int GROWS_DN = WAVES * 16 * RT * DN_IT;   // down rows of an item
 constexpr int TILE_BYTES = 16 * Q4K_BYTES;   // one tile x one super-block
@@ -277,9 +278,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         const uint16_t *abs_ = act.bs + (size_t)arow * (Kin / 16) + (lane & 1) * 8;
         const float *ad = act.d + (size_t)arow * nsb;
 
+        // row pass of step s (at most two passes: no division)
+        auto pass_of = [&](int s) -> int { return IT == 1 ? 0 : (s >= nsb ? 1 : 0); };
         auto issue = [&](int s) {
             if (s >= steps) return;
-            const int it = s / nsb, sb = s - it * nsb;
+            const int it = pass_of(s), sb = s - it * nsb;
             const int stg = s % WSTAGES;
             const uint8_t *t0 = tb[0][0], *t1 = tb[0][1];
 #pragma unroll
@@ -330,7 +333,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             issue(s + WSTAGES - 1);
-            const int it = s / nsb;
+            const int it = pass_of(s);
             const int stg = s % WSTAGES;
             Q4KTile cur[RT];
 #pragma unroll
