@@ -607,6 +607,27 @@ int tile_tensor(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int m
     return DMOE_OK;
 }
 
+// F16 [mats][rows][K] -> the tiled layout of the grouped GEMM (k_gemm.hip), in
+// a library-owned copy (a library-owned original is freed).
+int tile_tensor_f16(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int mats)
+{
+    const size_t bytes = (size_t)rows * K * 2 * mats;
+    void *dev = nullptr;
+    HIP_TRY(ctx, hipMalloc(&dev, bytes));
+    L->owned.push_back(dev);
+    HIP_TRY(ctx, launch_tile_f16(t.data, t.nb1, t.nb2, rows, K, mats, (uint8_t *)dev, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    auto it = std::find(L->owned.begin(), L->owned.end(), (void *)t.data);
+    if (it != L->owned.end()) {
+        HIP_TRY(ctx, hipFree(*it));
+        L->owned.erase(it);
+    }
+    t.data = (const uint8_t *)dev;
+    t.nb1 = (size_t)K * 2;                          // bytes per row (blocks of 128 rows)
+    t.nb2 = (size_t)rows * K * 2;
+    return DMOE_OK;
+}
+
 int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmoe_layer_desc *d)
 {
     L->hp = *hp;
@@ -631,6 +652,18 @@ int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmo
             if ((rc = tile_tensor(ctx, L, L->sg, SF, H, 1))) return rc;
             if ((rc = tile_tensor(ctx, L, L->su, SF, H, 1))) return rc;
             if ((rc = tile_tensor(ctx, L, L->sd, H, SF, 1))) return rc;
+        }
+    }
+    if (use_gemm_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) {
+        const int H = hp->n_embd, E = hp->n_experts, FF = hp->moe_ff, SF = L->hp.shared_ff;
+        int rc;
+        if ((rc = tile_tensor_f16(ctx, L, L->eg, FF, H, E))) return rc;
+        if ((rc = tile_tensor_f16(ctx, L, L->eu, FF, H, E))) return rc;
+        if ((rc = tile_tensor_f16(ctx, L, L->ed, H, FF, E))) return rc;
+        if (L->has_shared) {
+            if ((rc = tile_tensor_f16(ctx, L, L->sg, SF, H, 1))) return rc;
+            if ((rc = tile_tensor_f16(ctx, L, L->su, SF, H, 1))) return rc;
+            if ((rc = tile_tensor_f16(ctx, L, L->sd, H, SF, 1))) return rc;
         }
     }
     return DMOE_OK;

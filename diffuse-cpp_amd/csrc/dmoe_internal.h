@@ -140,6 +140,12 @@ hipError_t launch_gemm_f16(int phase, const GemmJob &job, hipStream_t s);
 bool gemm_shapes_ok(int H, int FF, int SF, bool shared);
 // x (f32) -> f16, or its hi / lo f16 pair (lo rows after the hi rows)
 hipError_t launch_cvt_f16(const float *src, int rows, int K, int split, uint16_t *dst, hipStream_t s);
+// F16 matrices -> the tiled layout of k_gemm.hip: per matrix, 128-row blocks,
+// k-step-major (rows x 32 values of k step ks of block b at
+// (b*K/32 + ks)*8192), row r of a step at (r%128)*64 with 16-byte chunk q at
+// slot q ^ ((r >> 1) & 3).
+hipError_t launch_tile_f16(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
+                           uint8_t *dst, hipStream_t s);
 
 // Routing + dispatch (k_router.hip).  counter: a zeroed int the last routing
 // group uses to elect itself (left zeroed again).

@@ -31,7 +31,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int GWAVES = 8;
 constexpr int GT = GWAVES * 64;      // threads per workgroup
 constexpr int GNW = 256;             // weight rows per item (gate/up: 128 moe_ff rows of each)
-constexpr int GS = 4;                // LDS pipeline stages
+constexpr int GS = 5;                // LDS pipeline stages (5 x 32 KB: all of the CU's LDS)
 constexpr int GTILE = GM * GK * 2;   // bytes of one operand tile of a stage (64-byte rows)
 constexpr int GP = GM * GK / 8 / GT; // 16-byte pieces per thread per tile and stage
 
@@ -47,19 +47,26 @@ __device__ __forceinline__ uint16_t f2h_rn(float f) { return __builtin_bit_cast(
 // with the slot flipped by row bits 1..2.
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
 
-// s_waitcnt with vmcnt(n), lgkmcnt(0), expcnt untouched (n < 16)
-#define GEMM_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x70 | (n))
+// s_waitcnt with vmcnt(n) (n < 64); lgkmcnt(0) or untouched (LDS reads may
+// stay in flight); expcnt untouched
+#define GEMM_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70)
+#define GEMM_WAIT_VM_ONLY(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0xF70)
 
 // LDS-direct load of 16 bytes per lane: lane l's bytes go to LDS address
-// lds + 16 l (lds wave-uniform).  Written as inline assembly so that the
+// lds + 16 l (lds: a wave-uniform LDS byte address).  Written as inline assembly so that the
 // compiler does not order every later LDS read after it (it cannot tell the
 // ring's buffers apart and would wait for all loads in flight); completion is
 // awaited explicitly with GEMM_WAIT_VM before the barrier of each step.
-__device__ __forceinline__ void lds_load16(const void *src, const void *lds)
+__device__ __forceinline__ void lds_load16(const void *src, uint32_t lds)
 {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+
+// LDS byte address of a shared-memory object
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
 template <int PHASE>
@@ -67,11 +74,12 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
 {
     constexpr bool DOWN = PHASE == 1;
     constexpr int GN = DOWN ? GN_DN : GN_GU;         // output rows per item
-    static_assert(GP * GT * 8 == GM * GK && GNW == GM && GP == 2, "tile shapes");
+    static_assert(GP * GT * 8 == GM * GK && GNW == GM && GP == 2 && GN_GU == 128 && GK == 32,
+                  "tile shapes: a stage's weight tile is two 128-row blocks of the tiled layout");
     // stage s: activation tile at S[s][0], weight tile at S[s][1]; row r of a
     // tile is 64 bytes at r * 64, its k-chunks swizzled by swz(r)
     __shared__ __align__(16) uint8_t S[GS][2][GTILE];
-    __shared__ int s_arow[GM];
+    const uint32_t s_base = __builtin_amdgcn_readfirstlane(lds_addr(&S[0][0][0]));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -103,25 +111,14 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
     // wave grid 2 (activation rows) x 4 (weight rows): 128 x 64 per wave
     const int tok0 = 128 * (wave >> 2);
     const int wq = wave & 3;
-    // weight rows of this wave's four 16-row tiles in the weight tile: gate/up:
-    // 32 moe_ff rows of gate (tiles 0, 1) and the same rows of up (tiles 2, 3)
-    int brow[4];
-#pragma unroll
-    for (int tw = 0; tw < 4; tw++)
-        brow[tw] = DOWN ? 64 * wq + 16 * tw
-                        : (tw < 2 ? 32 * wq + 16 * tw : GN + 32 * wq + 16 * (tw - 2));
-    // byte offsets of this lane's operand chunk g in a tile
-    int aoff[8], boff[4];
-#pragma unroll
-    for (int ti = 0; ti < 8; ti++) {
-        const int r = tok0 + 16 * ti + r16;
-        aoff[ti] = r * 64 + ((g ^ swz(r)) << 4);
-    }
-#pragma unroll
-    for (int tw = 0; tw < 4; tw++) {
-        const int r = brow[tw] + r16;
-        boff[tw] = r * 64 + ((g ^ swz(r)) << 4);
-    }
+    // byte offsets of this lane's operand chunk g in a tile (swz depends on
+    // row bits 1..2 only: the same for every 16-row tile): activation rows
+    // tok0 + 16 ti + r16 at aoff + 1024 ti; the wave's four 16-row weight
+    // tiles at boff + bstep(tw): down: rows 64 wq + 16 tw; gate/up: 32 moe_ff
+    // rows of gate (tiles 0, 1) and the same rows of up (tiles 2, 3)
+    const int aoff = (tok0 + r16) * 64 + ((g ^ swz(r16)) << 4);
+    const int boff = ((DOWN ? 64 : 32) * wq + r16) * 64 + ((g ^ swz(r16)) << 4);
+    auto bstep = [](int tw) -> int { return DOWN ? 1024 * tw : (tw < 2 ? 1024 * tw : GN * 64 + 1024 * (tw - 2)); };
 
     for (int m = lb; m < seg_items; m += G8) {
         const bool shared = m >= nr * rg;
@@ -145,56 +142,56 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         const uint16_t *A = DOWN ? (shared ? job.hs16 : job.h16) : (shared ? job.xs16 : job.x16);
         const size_t lo_off = (size_t)N * Kin;           // split arrays only
 
-        // the previous item's loads into LDS, its stores and its LDS reads are
-        // complete after this barrier (its fence waits for all memory counters)
-        __syncthreads();
-        if (tid < GM) {
-            const int i = min(tid, nt - 1);
-            int row;
-            if (shared) {
-                row = t_first + i;
-            } else {
-                const int p = job.perm[t_first + i];
-                row = DOWN ? p : p / K;
-            }
-            s_arow[tid] = row;
-        }
-        __syncthreads();
-
-        // weight rows of the item: gate rows 0..127 and up rows 128..255 of
-        // the same moe_ff rows, or 256 down rows.  (The fields are selected
-        // here, not in a lambda: a lambda that captured the argument struct
-        // would copy it to private memory.)
+        // weight rows of the item (tiled layout, 128-row blocks of 8 KB per k
+        // step): gate rows 0..127 and up rows 128..255 of the same moe_ff rows
+        // (block rb of each), or 256 down rows (blocks 2 rb, 2 rb + 1).  (The
+        // fields are selected here, not in a lambda: a lambda that captured
+        // the argument struct would copy it to private memory.)
         const WTensor &w0 = DOWN ? (shared ? job.sd : job.ed) : (shared ? job.sg : job.eg);
         const WTensor &w1 = DOWN ? (shared ? job.sd : job.ed) : (shared ? job.su : job.eu);
-        const uint8_t *wb0 = w0.data + (size_t)e * w0.nb2 + (size_t)(rb * GN) * w0.nb1;
-        const uint8_t *wb1 = w1.data + (size_t)e * w1.nb2 + (size_t)(rb * GN) * w1.nb1;
-        const size_t wnb0 = w0.nb1, wnb1 = w1.nb1;
+        const size_t kblk = (size_t)nsteps * 8192;       // one 128-row block
+        const uint8_t *wb0 = w0.data + (size_t)e * w0.nb2 + (size_t)(DOWN ? 2 * rb : rb) * kblk;
+        const uint8_t *wb1 = DOWN ? wb0 + kblk : w1.data + (size_t)e * w1.nb2 + (size_t)rb * kblk;
         // piece c = i * GT + tid of a tile (16 bytes at c * 16): row c >> 2,
         // slot c & 3, holding k-chunk (c & 3) ^ swz(row).  A wavefront's pieces
-        // of one load are 1 KB of consecutive LDS, as the LDS-direct load writes.
+        // of one load are 1 KB of consecutive LDS, as the LDS-direct load
+        // writes, and of the tiled weights in HBM.
         const uint8_t *ap[GP], *bp[GP];
 #pragma unroll
         for (int i = 0; i < GP; i++) {
             const int c = i * GT + tid, row = c >> 2;
             const int q = (c & 3) ^ swz(row);
-            ap[i] = reinterpret_cast<const uint8_t *>(A + (size_t)s_arow[row] * Kin) + q * 16;
-            const bool up = !DOWN && row >= GN;
-            bp[i] = (up ? wb1 + (size_t)(row - GN) * wnb1 : wb0 + (size_t)row * wnb0) + q * 16;
+            int arow;
+            if (shared) {
+                arow = t_first + min(row, nt - 1);
+            } else {
+                const int p = job.perm[t_first + min(row, nt - 1)];
+                arow = DOWN ? p : p / K;
+            }
+            ap[i] = reinterpret_cast<const uint8_t *>(A + (size_t)arow * Kin) + q * 16;
+            bp[i] = (c < 512 ? wb0 : wb1) + (size_t)(c & 511) * 16;
         }
-        // stage st of the k loop into LDS buffer buf: 2 GP loads per thread
+        // stage st of the k loop into LDS buffer st % GS: 2 GP loads per thread
         // (none past the last stage, so nothing is in flight when the item ends)
-        auto issue = [&](int st, int buf) {
+        auto issue = [&](int st) {
             if (st >= total_steps) return;
             const int pass = st >= nsteps ? 1 : 0;
-            const size_t kb = (size_t)(st - pass * nsteps) * GK * 2;
-            const size_t ab = kb + (pass ? lo_off * 2 : 0);
+            const int ks = st - pass * nsteps;
+            const size_t ab = (size_t)ks * GK * 2 + (pass ? lo_off * 2 : 0);
+            const size_t wbk = (size_t)ks * 8192;
+            const uint32_t sb = s_base + (uint32_t)((st % GS) * 2 * GTILE + wave * 1024);
 #pragma unroll
             for (int i = 0; i < GP; i++) {
-                const int dst = (i * GT + wave * 64) * 16;
-                lds_load16(ap[i] + ab, &S[buf][0][dst]);
-                lds_load16(bp[i] + kb, &S[buf][1][dst]);
+                lds_load16(ap[i] + ab, sb + i * GT * 16);
+                lds_load16(bp[i] + wbk, sb + GTILE + i * GT * 16);
             }
+        };
+        auto read_w = [&](int buf, h8 (&rw)[4]) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) rw[t] = *reinterpret_cast<const h8 *>(&S[buf][1][boff + bstep(t)]);
+        };
+        auto read_a = [&](int buf, int ti) -> h8 {
+            return *reinterpret_cast<const h8 *>(&S[buf][0][aoff + 1024 * ti]);
         };
 
         f4 acc[8][4];
@@ -202,32 +199,89 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         for (int ti = 0; ti < 8; ti++)
 #pragma unroll
             for (int tw = 0; tw < 4; tw++) acc[ti][tw] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-
-#pragma unroll
-        for (int s0 = 0; s0 < GS - 1; s0++) issue(s0, s0);
-        for (int st = 0; st < total_steps; st++) {
-            const int buf = st % GS;
-            // stage st has landed (the GS - 2 later stages may be in flight) in
-            // this wavefront's pieces; the barrier makes that true of all, and
-            // frees the buffer read in step st - 1 for stage st + GS - 1.  In
-            // the last steps fewer stages follow: wait for all.
-            if (st + GS - 2 < total_steps)
-                GEMM_WAIT_VM(2 * GP * (GS - 2));
-            else
-                GEMM_WAIT_VM(0);
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            issue(st + GS - 1, (st + GS - 1) % GS);
-            h8 b[4];
-#pragma unroll
-            for (int tw = 0; tw < 4; tw++) b[tw] = *reinterpret_cast<const h8 *>(&S[buf][1][boff[tw]]);
+        // MFMAs of one step: weight operands rw (read a step ahead), activation
+        // operands of buffer buf read two 16-row tiles ahead; a0, a1 hold tiles
+        // 0, 1 on entry and the next step's tiles 0, 1 (buffer nbuf) on exit
+        auto mfma_step = [&](int buf, int nbuf, bool next, h8 &a0, h8 &a1, const h8 (&rw)[4]) {
+            h8 a = a0, b = a1;
 #pragma unroll
             for (int ti = 0; ti < 8; ti++) {
-                const h8 a = *reinterpret_cast<const h8 *>(&S[buf][0][aoff[ti]]);
+                h8 an;
+                if (ti < 6)
+                    an = read_a(buf, ti + 2);
+                else if (next)
+                    an = read_a(nbuf, ti - 6);
 #pragma unroll
                 for (int tw = 0; tw < 4; tw++)
-                    acc[ti][tw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[tw], acc[ti][tw], 0, 0, 0);
+                    acc[ti][tw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, rw[tw], acc[ti][tw], 0, 0, 0);
+                a = b;
+                if (ti < 6 || next) b = an;
             }
+            a0 = a;
+            a1 = b;
+        };
+        // Step st: wait until stage st + 1 has landed (the GS - 3 stages after
+        // it may be in flight; in the last steps fewer follow: wait for all),
+        // barrier (all wavefronts' loads of stage st + 1 are in LDS, and the
+        // buffer of stage st - 1, last read in step st - 1, is free), refill
+        // that buffer with stage st + GS - 1, then read stage st + 1's weight
+        // operands into the spare registers while the MFMAs of stage st run.
+        // Operand reads stay in flight across a barrier (the compiler waits for
+        // them before their MFMAs); the scheduling barriers keep each step's
+        // MFMAs between its barriers.
+        auto sync_step = [&](int st, bool tail) {
+            if (!tail)
+                GEMM_WAIT_VM_ONLY(2 * GP * (GS - 3));
+            else
+                GEMM_WAIT_VM_ONLY(0);
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (!tail) issue(st + GS - 1);
+        };
+
+        // the previous item's LDS reads are done in every wavefront
+        GEMM_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int st = 0; st < GS - 1; st++) issue(st);
+        // stage 0 in LDS, its first operands in registers
+        if (GS - 1 < total_steps)
+            GEMM_WAIT_VM(2 * GP * (GS - 2));
+        else
+            GEMM_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        h8 a0, a1, rw0[4], rw1[4];
+        read_w(0, rw0);
+        a0 = read_a(0, 0);
+        a1 = read_a(0, 1);
+        // total_steps is even (Kin % 64 == 0): two steps per iteration, one
+        // weight register set each.  Steps st with st + GS - 1 < total_steps
+        // refill the ring and wait for a fixed count; the last ones do neither.
+        int st = 0;
+        for (; st + 1 + GS - 1 < total_steps; st += 2) {
+            sync_step(st, false);
+            read_w((st + 1) % GS, rw1);
+            mfma_step(st % GS, (st + 1) % GS, true, a0, a1, rw0);
+            __builtin_amdgcn_sched_barrier(0);
+            sync_step(st + 1, false);
+            read_w((st + 2) % GS, rw0);
+            mfma_step((st + 1) % GS, (st + 2) % GS, true, a0, a1, rw1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (; st < total_steps; st += 2) {
+            // every stage is issued by now, except that the pair's first step
+            // may still issue the last one
+            const bool more = st + 2 < total_steps;
+            sync_step(st, st + GS - 1 >= total_steps);
+            read_w((st + 1) % GS, rw1);
+            mfma_step(st % GS, (st + 1) % GS, true, a0, a1, rw0);
+            __builtin_amdgcn_sched_barrier(0);
+            sync_step(st + 1, true);
+            if (more) read_w((st + 2) % GS, rw0);
+            mfma_step((st + 1) % GS, (st + 2) % GS, more, a0, a1, rw1);
+            __builtin_amdgcn_sched_barrier(0);
         }
 
         // results: output row of tile tw for lane r16; activation rows 16 ti + 4 g + i
@@ -257,10 +311,43 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
                     float *o = shared ? job.ys + (size_t)(t_first + tt) * H
                                       : job.ye + (size_t)job.perm[t_first + tt] * H;
 #pragma unroll
-                    for (int tw = 0; tw < 4; tw++) o[rb * GN + brow[tw] + r16] = acc[ti][tw][i];
+                    for (int tw = 0; tw < 4; tw++) o[rb * GN + 64 * wq + 16 * tw + r16] = acc[ti][tw][i];
                 }
             }
     }
+}
+
+// F16 matrices [rows][K] (ggml row layout, mats of them) -> the tiled layout
+// the GEMM streams: per matrix, 128-row blocks, k-step-major inside a block
+// (the 128 rows x 32 values of k step ks of block b are the 8 KB at
+// (b * K/32 + ks) * 8192), row r of the 8 KB at r * 64 with its 16-byte chunk
+// q at slot q ^ swz(r) -- the LDS layout of a stage, so the GEMM copies a
+// block's k step to LDS as it lies.  One thread per 16-byte chunk.
+__global__ __launch_bounds__(256) void k_tile_f16(const uint8_t *__restrict__ src, size_t nb1, size_t nb2,
+                                                  int rows, int K, int mats, uint8_t *__restrict__ dst)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int cpr = K / 8;                            // 16-byte chunks of a row
+    const size_t per_mat = (size_t)rows * cpr;
+    if (i >= per_mat * mats) return;
+    const int m = (int)(i / per_mat);
+    const size_t j = i - (size_t)m * per_mat;
+    const int r = (int)(j / cpr), c = (int)(j % cpr);
+    const int ks = c >> 2, q = c & 3, rl = r & 127;
+    const uint4 v = *reinterpret_cast<const uint4 *>(src + (size_t)m * nb2 + (size_t)r * nb1 + (size_t)c * 16);
+    uint8_t *out = dst + (size_t)m * rows * K * 2 + ((size_t)(r >> 7) * (K / GK) + ks) * 8192 +
+                   rl * 64 + ((q ^ swz(rl)) << 4);
+    *reinterpret_cast<uint4 *>(out) = v;
+}
+
+hipError_t launch_tile_f16(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
+                           uint8_t *dst, hipStream_t s)
+{
+    if (rows % 128 || K % GK || nb1 % 16 || (mats > 1 && nb2 % 16)) return hipErrorInvalidValue;
+    const size_t total = (size_t)rows * (K / 8) * mats;
+    hipLaunchKernelGGL(k_tile_f16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, nb1, nb2,
+                       rows, K, mats, dst);
+    return hipGetLastError();
 }
 
 // x (f32 rows) -> f16 rows, or the hi / lo f16 pair (lo rows after the hi rows)
@@ -298,8 +385,9 @@ hipError_t launch_cvt_f16(const float *src, int rows, int K, int split, uint16_t
 
 bool gemm_shapes_ok(int H, int FF, int SF, bool shared)
 {
-    return H % GN_DN == 0 && H % GK == 0 && FF % GN_GU == 0 && FF % GK == 0 &&
-           (!shared || (SF % GN_GU == 0 && SF % GK == 0));
+    // whole row groups; an even number of k steps per pass
+    return H % GN_DN == 0 && H % (2 * GK) == 0 && FF % GN_GU == 0 && FF % (2 * GK) == 0 &&
+           (!shared || (SF % GN_GU == 0 && SF % (2 * GK) == 0));
 }
 
 hipError_t launch_gemm_f16(int phase, const GemmJob &job, hipStream_t s)

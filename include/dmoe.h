@@ -138,11 +138,12 @@ int  dmoe_layer_upload(dmoe_ctx *ctx, const dmoe_hparams *hp,
                        const dmoe_layer_desc *desc, dmoe_layer **out);
 
 /* Same, but every `data` pointer in `desc` is already a device pointer on the
- * context's GPU.  Strides are taken from nb[].  Q4_K expert tensors whose
- * sizes fit the MFMA kernels (n_embd, moe_ff, shared_ff multiples of 256) are
- * rewritten once into a library-owned tiled copy in HBM; every other tensor
- * is referenced without copying (the caller keeps it alive until
- * dmoe_layer_free). */
+ * context's GPU.  Strides are taken from nb[].  Expert tensors whose type and
+ * sizes fit the MFMA kernels (Q4_K: n_embd, moe_ff, shared_ff multiples of
+ * 256 and of the kernels' row groups; F16: n_embd a multiple of 256, moe_ff
+ * and shared_ff of 128) are rewritten once into a library-owned tiled copy in
+ * HBM; every other tensor is referenced without copying (the caller keeps it
+ * alive until dmoe_layer_free). */
 int  dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp,
                             const dmoe_layer_desc *desc, dmoe_layer **out);
 
