@@ -26,6 +26,7 @@ sys.path.insert(0, str(ROOT / "diffuse-cpp_amd"))
 
 METRIC = "MoE-layer tokens/s + % HBM-BW roofline (32-tok block, Q4_K); prefill % MFMA"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 
 
@@ -119,25 +120,45 @@ def main():
     ctx.profile(False)
     stages = {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.items()}   # us per launch
 
-    # algorithmic bytes of the dominant kernel, the gate/up launch (routed
-    # experts and the shared expert in one launch): the touched experts' and
-    # the shared expert's gate and up matrices, the activations in their MFMA
-    # layout (f16 values, f16 sums of 16, f32 scale per 256; the shared
-    # expert's in hi/lo pairs), h and the shared h written as f32
+    # The dominant kernel is the gate/up launch (routed experts and the shared
+    # expert in one launch).  Q4_K / Q8_0 (HBM-bound): its algorithmic bytes
+    # are the touched experts' and the shared expert's gate and up matrices,
+    # the activations in their operand layout (Q4_K: int8 values, f16 sums of
+    # 16, an f32 scale per 256; the shared expert's as two int8 digit rows)
+    # and h written as f32.  F16 (the prefill, MFMA-bound): its algorithmic
+    # FLOPs, 2 per multiply-add of the routed pairs' and the tokens' shared
+    # gate and up products (the shared expert's two f16 passes count once).
     rs_h = dmoe.row_size(cfg.wtype, H)
     SF = cfg.shared_ff
     P = N * K
-    act_row = H * 2 + (H // 16) * 2 + (H // 256) * 4
     dom_stage = "gateup_routed"
-    if cfg.wtype == dmoe.TYPE_Q4_K:
-        dom_kernel = "dmoe::k_expert_q4k<0>"
-        dom_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + N * act_row + 2 * N * act_row
-                     + P * FF * 4 + N * SF * 4)
-    else:
-        dom_kernel = "dmoe::k_gateup_routed"
-        dom_bytes = touched * 2 * FF * rs_h + N * H * 2 + P * FF * 4
     dom_us = stages.get(dom_stage)
-    achieved = dom_bytes / (dom_us * 1e-6) / 1e9 if dom_us else None
+    if cfg.wtype == dmoe.TYPE_F16:
+        dom_kernel = "dmoe::k_gemm_f16<0>"
+        dom_flops = 2.0 * (P * 2 * H * FF + N * 2 * H * SF)
+        achieved = dom_flops / (dom_us * 1e-6) / 1e12 if dom_us else None
+        roofline = {"bound": "mfma", "kernel": dom_stage,
+                    "achieved": round(achieved, 1) if achieved else None,
+                    "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4) if achieved else None,
+                    "traffic": traffic_from_profile(dom_stage, cfg.name),
+                    "algorithmic_flops": dom_flops, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
+    else:
+        if cfg.wtype == dmoe.TYPE_Q4_K:
+            act_row = H + (H // 16) * 2 + (H // 256) * 4
+            dom_kernel = "dmoe::k_expert_q4k<0>"
+            dom_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + N * act_row + 2 * N * act_row
+                         + P * FF * 4 + N * SF * 4)
+        else:
+            dom_kernel = "dmoe::k_gateup_routed"
+            dom_bytes = touched * 2 * FF * rs_h + N * H * 2 + P * FF * 4
+        achieved = dom_bytes / (dom_us * 1e-6) / 1e9 if dom_us else None
+        roofline = {"bound": "hbm", "kernel": dom_stage,
+                    "achieved": round(achieved, 1) if achieved else None,
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+                    "traffic": traffic_from_profile(dom_stage, cfg.name),
+                    "algorithmic_bytes": dom_bytes, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
 
     # layer-level: every weight byte the layer must read
     layer_bytes = touched * eb + sb + E * H * 4 + E * 4 + 2 * N * H * 4
@@ -169,18 +190,7 @@ def main():
             "max_tokens_per_expert": int(counts.max()),
             "weight_copies_rotated": a.copies,
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dom_stage,
-            "achieved": round(achieved, 1) if achieved else None,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-            "traffic": traffic_from_profile(dom_stage, cfg.name),
-            "algorithmic_bytes": dom_bytes,
-            "hip_kernel": dom_kernel,
-            "us_per_launch": dom_us,
-        },
+        "roofline": roofline,
         "layer": {
             "bytes": layer_bytes,
             "touched_expert_bytes": touched * eb,
