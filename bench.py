@@ -123,9 +123,9 @@ def main():
     # The dominant kernel is the gate/up launch (routed experts and the shared
     # expert in one launch).  Q4_K / Q8_0 (HBM-bound): its algorithmic bytes
     # are the touched experts' and the shared expert's gate and up matrices,
-    # the activations in their operand layout (Q4_K: int8 values, f16 sums of
-    # 16, an f32 scale per 256; the shared expert's as two int8 digit rows)
-    # and h written as f32.  F16 (the prefill, MFMA-bound): its algorithmic
+    # the activations in their operand layout (int8 values with, for Q4_K, f16
+    # sums of 16 and an f32 scale per 256, for Q8_0 an f32 scale per 32; the
+    # shared expert's as two int8 digit rows) and h written as f32.  F16 (the prefill, MFMA-bound): its algorithmic
     # FLOPs, 2 per multiply-add of the routed pairs' and the tokens' shared
     # gate and up products (the shared expert's two f16 passes count once).
     rs_h = dmoe.row_size(cfg.wtype, H)
@@ -144,9 +144,13 @@ def main():
                     "traffic": traffic_from_profile(dom_stage, cfg.name),
                     "algorithmic_flops": dom_flops, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
     else:
-        if cfg.wtype == dmoe.TYPE_Q4_K:
-            act_row = H + (H // 16) * 2 + (H // 256) * 4
-            dom_kernel = "dmoe::k_expert_q4k<0>"
+        if cfg.wtype in (dmoe.TYPE_Q4_K, dmoe.TYPE_Q8_0):
+            if cfg.wtype == dmoe.TYPE_Q4_K:
+                act_row = H + (H // 16) * 2 + (H // 256) * 4
+                dom_kernel = "dmoe::k_expert_q4k<0>"
+            else:
+                act_row = H + (H // 32) * 4
+                dom_kernel = "dmoe::k_expert_q80<0>"
             dom_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + N * act_row + 2 * N * act_row
                          + P * FF * 4 + N * SF * 4)
         else:

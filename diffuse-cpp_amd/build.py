@@ -36,9 +36,9 @@ CFLAGS = [
     f"-I{ROOT / 'include'}",
 ]
 
-SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "k_gemm.hip",
-           "dmoe_api.cpp"]
-HEADERS = ["dmoe_internal.h", "dmoe_device.h"]
+SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "k_expert_q80.hip",
+           "k_gemm.hip", "dmoe_api.cpp"]
+HEADERS = ["dmoe_internal.h", "dmoe_device.h", "dmoe_prep.h"]
 
 
 def _needs(obj: Path, deps: list[Path]) -> bool:

@@ -281,6 +281,17 @@ bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
     return true;
 }
 
+// Q8_0 experts (and a Q8_0 shared expert of the same width) run on the int8
+// MFMA kernels of k_expert_q80.hip.
+bool use_q80_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared)
+{
+    const int gu = expert_q80_rows_per_item(0), dn = expert_q80_rows_per_item(1);
+    if (wtype != DMOE_TYPE_Q8_0 || hp.n_embd % 256 || hp.moe_ff % 256) return false;
+    if (hp.moe_ff % gu || hp.n_embd % dn) return false;
+    if (shared && (stype != DMOE_TYPE_Q8_0 || hp.shared_ff != hp.moe_ff)) return false;
+    return true;
+}
+
 // F16 experts (and an F16 shared expert) run on the MFMA grouped-GEMM path.
 bool use_gemm_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared)
 {
@@ -288,15 +299,17 @@ bool use_gemm_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
     return gemm_shapes_ok(hp.n_embd, hp.moe_ff, shared ? hp.shared_ff : 0, shared);
 }
 
-ActI8 take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bool split)
+ActI8 take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bool split,
+               bool per32 = false)
 {
-    // split activations keep their a0 digit rows as rows rows..2*rows-1
+    // split activations keep their a0 digit rows as rows rows..2*rows-1;
+    // per32: one scale per 32 values and no sums (the Q8_0 kernels)
     const int r = split ? 2 * rows : rows;
     ActI8 a{};
     a.K = K;
     a.q = (int8_t *)take((size_t)r * K);
-    a.bs = (uint16_t *)take((size_t)r * (K / 16) * 2);
-    a.d = (float *)take((size_t)r * (K / 256) * 4);
+    a.bs = per32 ? nullptr : (uint16_t *)take((size_t)r * (K / 16) * 2);
+    a.d = (float *)take((size_t)r * (K / (per32 ? 32 : 256)) * 4);
     return a;
 }
 
@@ -347,6 +360,14 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         if (shared) {
             t.axs = take_act(take, N, H, true);
             t.ahs = take_act(take, N, SF, true);
+        }
+    }
+    if (use_q80_path(hp, wtype, stype, shared)) {
+        t.ax = take_act(take, N, H, false, true);
+        t.ah = take_act(take, P, FF, false, true);
+        if (shared) {
+            t.axs = take_act(take, N, H, true, true);
+            t.ahs = take_act(take, N, SF, true, true);
         }
     }
     if (gemm) {
@@ -462,21 +483,29 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
     const dmoe_hparams &hp = L->hp;
     const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
     const RouteParams rp = route_params(L, hp, N);
-    const bool mfma = use_mfma_path(hp, L->eg.type, L->sg.type, L->has_shared);
+    const bool q4 = use_mfma_path(hp, L->eg.type, L->sg.type, L->has_shared);
+    const bool q8 = use_q80_path(hp, L->eg.type, L->sg.type, L->has_shared);
+    const bool mfma = q4 || q8;
     const bool gemm = use_gemm_path(hp, L->eg.type, L->sg.type, L->has_shared);
+    // activation layouts of the int8 MFMA kernels (routed, shared expert)
+    const int mode_r = q8 ? ACT_Q80 : ACT_Q8K, mode_s = q8 ? ACT_SPLIT32 : ACT_SPLIT;
+    auto expert = [&](int phase, const MoeJob &j) {
+        return q8 ? launch_expert_q80(phase, j, s) : launch_expert_q4k(phase, j, s);
+    };
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, id, s, [&] { return call; }))
     // router logits, sigmoid, selection scores (+ x in the MFMA operand layout)
     PrepJob xj[2];
     int nxj = 0;
     if (mfma) {
-        xj[nxj++] = PrepJob{x, N, H, ACT_Q8K, w.ax};
-        if (L->has_shared) xj[nxj++] = PrepJob{x, N, H, ACT_SPLIT, w.axs};
+        xj[nxj++] = PrepJob{x, N, H, mode_r, w.ax};
+        if (L->has_shared) xj[nxj++] = PrepJob{x, N, H, mode_s, w.axs};
     }
     STAGE(ST_FRONT, launch_front(L->gate_w, L->gate_bias, x, N, H, E, w.rb, xj, nxj, s));
     // block routing, top-k, gate weights and the dispatch
     STAGE(ST_ROUTE, launch_route(rp, w.rb, w.wl, w.counter, s));
     if (mfma) {
-        // Q4_K experts on MFMA: routed experts and the shared one share a launch
+        // Q4_K / Q8_0 experts on int8 MFMA: routed experts and the shared one
+        // share a launch
         MoeJob job{};
         job.eg = L->eg;
         job.eu = L->eu;
@@ -502,13 +531,13 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.ahs = w.ahs;
         job.ye = w.ye;
         job.ys = w.ys;
-        STAGE(ST_GATEUP, launch_expert_q4k(0, job, s));
+        STAGE(ST_GATEUP, expert(0, job));
         PrepJob hj[2];
         int nhj = 0;
-        hj[nhj++] = PrepJob{w.h, N * K, FF, ACT_Q8K, w.ah};
-        if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, ACT_SPLIT, w.ahs};
+        hj[nhj++] = PrepJob{w.h, N * K, FF, mode_r, w.ah};
+        if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, mode_s, w.ahs};
         STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
-        STAGE(ST_DOWN, launch_expert_q4k(1, job, s));
+        STAGE(ST_DOWN, expert(1, job));
         STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
                                          K, H, y, s));
         return DMOE_OK;
@@ -607,6 +636,28 @@ int tile_tensor(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int m
     return DMOE_OK;
 }
 
+// Q8_0 [mats][rows][K] -> the tiled layout of k_expert_q80.hip, in a
+// library-owned copy (a library-owned original is freed).
+int tile_tensor_q80(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int mats)
+{
+    const size_t row_bytes = (size_t)(K / 32) * Q8_0_BYTES;
+    const size_t bytes = (size_t)rows * row_bytes * mats;
+    void *dev = nullptr;
+    HIP_TRY(ctx, hipMalloc(&dev, bytes));
+    L->owned.push_back(dev);
+    HIP_TRY(ctx, launch_tile_q80(t.data, t.nb1, t.nb2, rows, K, mats, (uint8_t *)dev, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    auto it = std::find(L->owned.begin(), L->owned.end(), (void *)t.data);
+    if (it != L->owned.end()) {
+        HIP_TRY(ctx, hipFree(*it));
+        L->owned.erase(it);
+    }
+    t.data = (const uint8_t *)dev;
+    t.nb1 = row_bytes;
+    t.nb2 = (size_t)rows * row_bytes;
+    return DMOE_OK;
+}
+
 // F16 [mats][rows][K] -> the tiled layout of the grouped GEMM (k_gemm.hip), in
 // a library-owned copy (a library-owned original is freed).
 int tile_tensor_f16(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int mats)
@@ -652,6 +703,18 @@ int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmo
             if ((rc = tile_tensor(ctx, L, L->sg, SF, H, 1))) return rc;
             if ((rc = tile_tensor(ctx, L, L->su, SF, H, 1))) return rc;
             if ((rc = tile_tensor(ctx, L, L->sd, H, SF, 1))) return rc;
+        }
+    }
+    if (use_q80_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) {
+        const int H = hp->n_embd, E = hp->n_experts, FF = hp->moe_ff, SF = L->hp.shared_ff;
+        int rc;
+        if ((rc = tile_tensor_q80(ctx, L, L->eg, FF, H, E))) return rc;
+        if ((rc = tile_tensor_q80(ctx, L, L->eu, FF, H, E))) return rc;
+        if ((rc = tile_tensor_q80(ctx, L, L->ed, H, FF, E))) return rc;
+        if (L->has_shared) {
+            if ((rc = tile_tensor_q80(ctx, L, L->sg, SF, H, 1))) return rc;
+            if ((rc = tile_tensor_q80(ctx, L, L->su, SF, H, 1))) return rc;
+            if ((rc = tile_tensor_q80(ctx, L, L->sd, H, SF, 1))) return rc;
         }
     }
     if (use_gemm_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) {

@@ -81,12 +81,18 @@ struct WorkList {
 //              |X| <= 32512, X = 256*a1 + a0; rows 0..rows-1 hold a1 (d = 256 s)
 //              and rows rows..2*rows-1 hold a0 (d = s).
 // bs holds the f16 sums of each 16 consecutive values (exact: |sum| <= 2048).
-enum ActMode { ACT_Q8K = 0, ACT_SPLIT = 1 };
+//   ACT_Q80  : ggml's Q8_0 quantisation per 32 values (d = amax/127,
+//              q = roundf(v * (1/d)), d kept as its fp16 rounding); d holds
+//              one scale per 32 values and bs is unused (the Q8_0 expert
+//              kernel, k_expert_q80.hip).
+//   ACT_SPLIT32: ACT_SPLIT with the power-of-two scale chosen per 32 values,
+//              d per 32 values, bs unused (the Q8_0 kernel's shared expert).
+enum ActMode { ACT_Q8K = 0, ACT_SPLIT = 1, ACT_Q80 = 2, ACT_SPLIT32 = 3 };
 struct ActI8 {
     int32_t K;
     int8_t *q;          // [rows][K]
-    uint16_t *bs;       // [rows][K/16]
-    float *d;           // [rows][K/256]
+    uint16_t *bs;       // [rows][K/16] (Q8K, SPLIT)
+    float *d;           // [rows][K/256] (Q8K, SPLIT) or [rows][K/32] (Q80, SPLIT32)
 };
 
 // The expert products of one forward (routed experts + the shared one),
@@ -174,6 +180,18 @@ hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s);
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
 constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
 hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s);
+// The same products for Q8_0 experts (k_expert_q80.hip): activations in the
+// ActI8 layout with ACT_Q80 / ACT_SPLIT32 scales, weights in the Q8_0 tiled
+// layout of launch_tile_q80.
+hipError_t launch_expert_q80(int phase, const MoeJob &job, hipStream_t s);
+int expert_q80_rows_per_item(int phase);
+// GGUF Q8_0 rows -> tiled layout: per matrix, 16-row tiles, 256-value-step-
+// major (16 rows x 256 values of step sb of tile t: the 4352-byte run at
+// (t*nsb + sb)*4352); a row's 272 bytes of a step are seventeen 16-byte
+// pieces, piece k of row r at (16k + r)*16: piece 0 the eight fp16 scales,
+// pieces 1+4g .. 4+4g the quants 8g .. 8g+7 of blocks 0..7 (8 bytes each).
+hipError_t launch_tile_q80(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
+                           uint8_t *dst, hipStream_t s);
 int expert_rows_per_item(int phase);     // output rows one work item covers
 bool expert_k_ok(int K);                 // reduction length the expert kernels accept
 // Q4_K row layout -> tiled layout of k_expert.hip (k_quant.hip): per matrix,

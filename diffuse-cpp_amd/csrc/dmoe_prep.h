@@ -14,6 +14,11 @@
 // super-block into [2^14, 2^15) (one step lower if it would round above
 // 32512), X = nearest_even(v / s) = 256*a1 + a0 with a0 in [-128, 127]; the a1
 // digits are row `row` (d = 256 s), the a0 digits row `rows + row` (d = s).
+//
+// ACT_Q80 reproduces ggml's Q8_0 conversion (the vec_dot_type of Q8_0 weights):
+// per 32 values d = amax/127, q = roundf(v * (1/d)) (half away from zero), d
+// kept as its fp16 rounding.  ACT_SPLIT32 is ACT_SPLIT with the scale chosen
+// per 32 values.  Both write one scale per 32 values and no sums.
 #pragma once
 
 #include "dmoe_device.h"
@@ -54,7 +59,73 @@ __device__ __forceinline__ void prep_values(const float (&v)[4], const ActI8 &ou
     const int K = nsb * 256;
     const size_t qbase = (size_t)row * K + sb * 256;
     const size_t bbase = (size_t)row * (K / 16) + sb * 16;
-    if (mode == ACT_Q8K) {
+    if (mode == ACT_Q80 || mode == ACT_SPLIT32) {
+        // per 32-value block: value lane + 64c is in block 2c + lane / 32
+        float bmax[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float a = fabsf(v[c]);
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
+            bmax[c] = a;
+        }
+        const size_t dbase = (size_t)row * (K / 32) + sb * 8;
+        if (mode == ACT_Q80) {
+            float dq[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float d = bmax[c] / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                sv[lane + 64 * c] = roundf(v[c] * id);
+                dq[c] = (float)(_Float16)d;
+            }
+            if ((lane & 31) == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) out.d[dbase + 2 * c + (lane >> 5)] = dq[c];
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            uint32_t pk = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                pk |= ((uint32_t)(int)sv[src_index(4 * lane + i)] & 0xffu) << (8 * i);
+            *reinterpret_cast<uint32_t *>(out.q + qbase + 4 * lane) = pk;
+        } else {
+            int kc[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                int k = 0;
+                if (bmax[c] != 0.0f) {
+                    int ex = 0;
+                    (void)frexpf(bmax[c], &ex);
+                    k = 15 - ex;
+                    if (nearest_int(ldexpf(bmax[c], k)) > 32512) k -= 1;
+                }
+                kc[c] = k;
+                sv[lane + 64 * c] = (float)nearest_int(ldexpf(v[c], k));
+            }
+            if ((lane & 31) == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const size_t b = dbase + 2 * c + (lane >> 5);
+                    out.d[b] = ldexpf(1.0f, 8 - kc[c]);                       // a1 row
+                    out.d[(size_t)rows * (K / 32) + b] = ldexpf(1.0f, -kc[c]);  // a0 row
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            uint32_t phi = 0, plo = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int X = (int)sv[src_index(4 * lane + i)];
+                const int a1 = (X + 128) >> 8, a0 = X - (a1 << 8);
+                phi |= ((uint32_t)a1 & 0xffu) << (8 * i);
+                plo |= ((uint32_t)a0 & 0xffu) << (8 * i);
+            }
+            *reinterpret_cast<uint32_t *>(out.q + qbase + 4 * lane) = phi;
+            *reinterpret_cast<uint32_t *>(out.q + (size_t)rows * K + qbase + 4 * lane) = plo;
+        }
+    } else if (mode == ACT_Q8K) {
         float dscale = 0.0f;
         if (amax != 0.0f) {
             const float iscale = -127.0f / aval;
