@@ -443,9 +443,53 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ye,
     y[i] = acc;
 }
 
+// The same, four consecutive outputs per thread (H % 4 == 0, 16-byte aligned
+// buffers): each output's operations and their order are those of k_combine.
+__global__ __launch_bounds__(256) void k_combine4(const float4 *__restrict__ ye,
+                                                  const float *__restrict__ weights,
+                                                  const float4 *__restrict__ ys, int N, int K, int H4,
+                                                  float4 *__restrict__ y)
+{
+#pragma clang fp contract(off)
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)N * H4) return;
+    const int t = (int)(i / H4), r = (int)(i % H4);
+    float4 v[8];
+    const int kk = K < 8 ? K : 8;
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+        if (s < kk) v[s] = ye[(size_t)(t * K + s) * H4 + r];
+    const float w0 = weights[t * K];
+    float4 acc = make_float4(v[0].x * w0, v[0].y * w0, v[0].z * w0, v[0].w * w0);
+    for (int s = 1; s < K; s++) {
+        const float ws = weights[t * K + s];
+        const float4 e = s < 8 ? v[s] : ye[(size_t)(t * K + s) * H4 + r];
+        acc.x = acc.x + e.x * ws;
+        acc.y = acc.y + e.y * ws;
+        acc.z = acc.z + e.z * ws;
+        acc.w = acc.w + e.w * ws;
+    }
+    if (ys) {
+        const float4 b = ys[i];
+        acc.x = acc.x + b.x;
+        acc.y = acc.y + b.y;
+        acc.z = acc.z + b.z;
+        acc.w = acc.w + b.w;
+    }
+    y[i] = acc;
+}
+
 hipError_t launch_combine(const float *ye, const float *weights, const float *ys, int N, int K,
                           int H, float *y, hipStream_t s)
 {
+    const auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (H % 4 == 0 && al16(ye) && al16(y) && (!ys || al16(ys))) {
+        const size_t total = (size_t)N * (H / 4);
+        hipLaunchKernelGGL(k_combine4, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(ye), weights,
+                           reinterpret_cast<const float4 *>(ys), N, K, H / 4, reinterpret_cast<float4 *>(y));
+        return hipGetLastError();
+    }
     const size_t total = (size_t)N * H;
     hipLaunchKernelGGL(k_combine, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ye,
                        weights, ys, N, K, H, y);
