@@ -31,7 +31,7 @@
 // of them copy the step's activations into the workgroup's activation ring,
 // with LDS-direct loads (global_load_lds_dwordx4): two steps stay in flight
 // without holding registers.
-#include "dmoe_internal.h"
+#include "dmoe_prep.h"
 
 namespace dmoe {
 
@@ -57,7 +57,8 @@ constexpr int RT = 2;                        // 16-row weight tiles per wave per
 constexpr int WSTAGES = DMOE_X_WSTAGES;
 constexpr int DN_IT = DMOE_X_DN_IT;
 static_assert(DN_IT == 1 || DN_IT == 2, "row passes of a down item");
-constexpr int GROWS_GU = WAVES * 16;             // gate/up rows of an item (gate and up tiles)
+constexpr int GU_IT = 2;                         // row passes of a gate/up item
+constexpr int GROWS_GU = WAVES * 16 * GU_IT;     // gate/up rows of an item: one h super-block
 constexpr int GROWS_DN = WAVES * 16 * RT * DN_IT;   // down rows of an item
 constexpr int TILE_BYTES = 16 * Q4K_BYTES;   // one tile x one super-block
 constexpr int WSTEP_BYTES = RT * TILE_BYTES;             // one wave's weights of one step
@@ -197,7 +198,7 @@ template <int PHASE>
 __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
 {
     constexpr bool DOWN = PHASE == 1;
-    constexpr int IT = DOWN ? DN_IT : 1;             // row passes per item
+    constexpr int IT = DOWN ? DN_IT : GU_IT;         // row passes per item
     constexpr int GROWS = DOWN ? GROWS_DN : GROWS_GU;
     __shared__ __align__(16) uint8_t s_act[WSTAGES][ASTEP_BYTES];
     __shared__ __align__(16) uint8_t s_w[WAVES][WSTAGES][WSTEP_BYTES];
@@ -251,9 +252,12 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         if (!DOWN) {
             const WTensor &a = shared ? job.sg : job.eg;
             const WTensor &b = shared ? job.su : job.eu;
-            const int t16 = (rbase + wave * 16) / 16;
-            tb[0][0] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
-            tb[0][1] = b.data + (size_t)e * b.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+                const int t16 = (rbase + it * (WAVES * 16) + wave * 16) / 16;
+                tb[it][0] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+                tb[it][1] = b.data + (size_t)e * b.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+            }
         } else {
             const WTensor &a = shared ? job.sd : job.ed;
 #pragma unroll
@@ -343,36 +347,65 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
                 if (it == q) compute_sb(cur, s_act[stg], r16, g, acc[q]);
         }
 
-        // results
-        float *out = DOWN ? (shared ? job.ys : job.ye) : (shared ? job.hs : job.h);
-        const int orows = DOWN ? H : (shared ? SF : FF);
+        if (!DOWN) {
+            // h = silu(gate) * up for the item's activation rows and its 256
+            // moe_ff rows (one super-block), then converted in place to the
+            // down products' operand layout (routed: Q8_K, shared: two int8
+            // digits; dmoe_prep.h) -- no f32 h in HBM.  The rings are idle
+            // (no loads in flight after the last step): h goes through the
+            // weight-ring LDS, the conversion scratch through the activation
+            // ring's.
+            float *s_h = reinterpret_cast<float *>(&s_w[0][0][0]);      // [16][256]
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+                const int col = it * (WAVES * 16) + wave * 16 + r16;
+                if (!shared) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s_h[(4 * g + i) * 256 + col] = silu(acc[it][0][i]) * acc[it][1][i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i += 2)
+                        s_h[(2 * g + (i >> 1)) * 256 + col] =
+                            silu(acc[it][0][i] + acc[it][0][i + 1]) * (acc[it][1][i] + acc[it][1][i + 1]);
+                }
+            }
+            __syncthreads();
+            float *sv = reinterpret_cast<float *>(&s_act[0][0]) + wave * 256;
+            const int sb = rbase / 256, nsb_h = (shared ? SF : FF) / 256;
+            for (int t = wave; t < nt; t += WAVES) {
+                float v[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) v[c] = s_h[t * 256 + lane + 64 * c];
+                if (!shared)
+                    prep_values(v, job.ah, ACT_Q8K, job.perm[t_first + t], N * K, sb, nsb_h, sv);
+                else
+                    prep_values(v, job.ahs, ACT_SPLIT, t_first + t, N, sb, nsb_h, sv);
+            }
+            continue;
+        }
+
+        // results of the down products
+        float *out = shared ? job.ys : job.ye;
 #pragma unroll
         for (int it = 0; it < IT; it++) {
-            const int row0 = DOWN ? rbase + it * (WAVES * 32) + wave * 32 : rbase + wave * 16;
+            const int row0 = rbase + it * (WAVES * 32) + wave * 32;
             if (!shared) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     if (4 * g + i >= nt) continue;
-                    float *o = out + (size_t)job.perm[t_first + 4 * g + i] * orows + row0 + r16;
-                    if (!DOWN) {
-                        o[0] = silu(acc[it][0][i]) * acc[it][1][i];
-                    } else {
+                    float *o = out + (size_t)job.perm[t_first + 4 * g + i] * H + row0 + r16;
 #pragma unroll
-                        for (int r = 0; r < RT; r++) o[16 * r] = acc[it][r][i];
-                    }
+                    for (int r = 0; r < RT; r++) o[16 * r] = acc[it][r][i];
                 }
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; i += 2) {
                     if (2 * g + (i >> 1) >= nt) continue;
-                    float *o = out + (size_t)(t_first + 2 * g + (i >> 1)) * orows + row0 + r16;
-                    if (!DOWN) {
-                        o[0] = silu(acc[it][0][i] + acc[it][0][i + 1]) *
-                               (acc[it][1][i] + acc[it][1][i + 1]);
-                    } else {
+                    float *o = out + (size_t)(t_first + 2 * g + (i >> 1)) * H + row0 + r16;
 #pragma unroll
-                        for (int r = 0; r < RT; r++) o[16 * r] = acc[it][r][i] + acc[it][r][i + 1];
-                    }
+                    for (int r = 0; r < RT; r++) o[16 * r] = acc[it][r][i] + acc[it][r][i + 1];
                 }
             }
         }
