@@ -531,16 +531,8 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.ahs = w.ahs;
         job.ye = w.ye;
         job.ys = w.ys;
+        // the gate/up launch converts h to the down products' layout itself
         STAGE(ST_GATEUP, expert(0, job));
-        if (q8) {
-            // the Q8_0 gate/up launch writes h in f32; the Q4_K one converts
-            // h to the down products' layout itself
-            PrepJob hj[2];
-            int nhj = 0;
-            hj[nhj++] = PrepJob{w.h, N * K, FF, mode_r, w.ah};
-            if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, mode_s, w.ahs};
-            STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
-        }
         STAGE(ST_DOWN, expert(1, job));
         STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
                                          K, H, y, s));

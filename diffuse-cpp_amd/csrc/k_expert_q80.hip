@@ -32,16 +32,17 @@
 // private 3-stage LDS ring, and six of them copy the step's activations (16
 // rows x 256 int8, 16 x 8 scales) into the workgroup's 3-stage ring, with
 // LDS-direct loads; one barrier per step publishes the activations.
-#include "dmoe_internal.h"
+#include "dmoe_prep.h"
 
 namespace dmoe {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int Q8_WAVES = 8;                          // wavefronts per workgroup
-constexpr int Q8_IT = 2;                             // row passes per item
-constexpr int Q8_GROWS_GU = Q8_WAVES * 16;           // gate/up rows (pass 0 gate, pass 1 up)
-constexpr int Q8_GROWS_DN = Q8_WAVES * 16 * Q8_IT;   // down rows
+constexpr int Q8_IT_GU = 4;                          // gate/up passes: gate, up of rows 0..127, of 128..255
+constexpr int Q8_IT_DN = 2;                          // down passes: two 16-row tiles a wavefront
+constexpr int Q8_GROWS_GU = Q8_WAVES * 16 * 2;       // gate/up rows of an item: one h super-block
+constexpr int Q8_GROWS_DN = Q8_WAVES * 16 * Q8_IT_DN; // down rows
 constexpr int Q8_STEP_ROW = 8 * Q8_0_BYTES;          // 272 bytes of a row per 256 values
 constexpr int Q8_TILE = 16 * Q8_STEP_ROW;            // 4352 bytes: one tile, one step
 constexpr int Q8_WPIECES = Q8_TILE / 16;             // 272
@@ -122,16 +123,19 @@ hipError_t launch_tile_q80(const uint8_t *src, size_t nb1, size_t nb2, int rows,
     return hipGetLastError();
 }
 
-// Work items of phase 0: routed (work-list entry ec, group of 128 rows), then
-// shared (chunk of 8 tokens, group of 128 rows); each wavefront 16 rows, pass 0
-// of gate, pass 1 of up.  Phase 1: groups of 256 rows, each wavefront two
-// 16-row tiles (one per pass).  A shared item's 16 activation rows are the a1 /
-// a0 digit rows of its 8 tokens interleaved, as in k_expert.hip.
+// Work items of phase 0: routed (work-list entry ec, group of 256 rows), then
+// shared (chunk of 8 tokens, group of 256 rows); each wavefront 16 rows of
+// each 128-row half, passes gate / up of the first half, gate / up of the
+// second; the epilogue converts h to the down products' layout.  Phase 1:
+// groups of 256 rows, each wavefront two 16-row tiles (one per pass).  A shared
+// item's 16 activation rows are the a1 / a0 digit rows of its 8 tokens
+// interleaved, as in k_expert.hip.
 template <int PHASE>
 __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
 {
     constexpr bool DOWN = PHASE == 1;
     constexpr int GROWS = DOWN ? Q8_GROWS_DN : Q8_GROWS_GU;
+    constexpr int IT = DOWN ? Q8_IT_DN : Q8_IT_GU;
     __shared__ __align__(16) uint8_t s_act[Q8_STAGES][Q8_ABYTES];
     __shared__ __align__(16) uint8_t s_w[Q8_WAVES][Q8_STAGES][Q8_TILE];
 
@@ -147,7 +151,7 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
     const int total = routed_items + nch * rg_sh;
     const int Kin = DOWN ? FF : H;                   // reduction length (SF == FF when shared)
     const int nsb = Kin / 256;
-    const int steps = Q8_IT * nsb;
+    const int steps = IT * nsb;
     const uint32_t act_base = q8_lds_addr(&s_act[0][0]);
     const uint32_t w_base = q8_lds_addr(&s_w[wave][0][0]);
     // weight load jd of a step: lane's piece p = 64 jd + lane (p < 272) of the
@@ -179,13 +183,16 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
             nt = min(SHARED_CHUNK, N - t_first);
         }
         // this wavefront's tile of pass it: tb[it]
-        const uint8_t *tb[Q8_IT];
+        const uint8_t *tb[IT];
         if (!DOWN) {
             const WTensor &a = shared ? job.sg : job.eg;
             const WTensor &b = shared ? job.su : job.eu;
-            const int t16 = rbase / 16 + wave;
-            tb[0] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * Q8_TILE;
-            tb[1] = b.data + (size_t)e * b.nb2 + (size_t)t16 * nsb * Q8_TILE;
+#pragma unroll
+            for (int p = 0; p < IT; p++) {
+                const int t16 = (rbase + 128 * (p >> 1)) / 16 + wave;
+                const WTensor &w = (p & 1) ? b : a;
+                tb[p] = w.data + (size_t)e * w.nb2 + (size_t)t16 * nsb * Q8_TILE;
+            }
         } else {
             const WTensor &a = shared ? job.sd : job.ed;
             const int t16 = rbase / 16 + 2 * wave;
@@ -205,11 +212,26 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
 
         // step s (pass s / nsb, 256-value step s % nsb): the wavefront's tile
         // run into its ring stage, its activation loads into the workgroup's
+        // pass of step s and its 256-value step (no division: at most 3 passes
+        // to skip)
+        auto pass_of = [&](int s, int &sb) -> int {
+            int it = 0;
+            sb = s;
+#pragma unroll
+            for (int q = 1; q < IT; q++)
+                if (sb >= nsb) { sb -= nsb; it++; }
+            return it;
+        };
         auto issue = [&](int s) {
             if (s >= steps) return;
-            const int it = s >= nsb ? 1 : 0, sb = s - it * nsb;
+            int sb;
+            const int it = pass_of(s, sb);
             const int stg = s % Q8_STAGES;
-            const uint8_t *run = tb[it] + (size_t)sb * Q8_TILE;
+            const uint8_t *t0 = tb[0];
+#pragma unroll
+            for (int q = 1; q < IT; q++)
+                if (it == q) t0 = tb[q];
+            const uint8_t *run = t0 + (size_t)sb * Q8_TILE;
             const uint32_t wst = w_base + (uint32_t)(stg * Q8_TILE);
 #pragma unroll
             for (int jd = 0; jd < Q8_WDMA; jd++) {
@@ -229,9 +251,9 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
 #pragma unroll
         for (int s = 0; s < Q8_STAGES - 1; s++) issue(s);
 
-        float acc[Q8_IT][4];
+        float acc[IT][4];
 #pragma unroll
-        for (int it = 0; it < Q8_IT; it++)
+        for (int it = 0; it < IT; it++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[it][i] = 0.0f;
         for (int s = 0; s < steps; s++) {
@@ -250,7 +272,8 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             issue(s + Q8_STAGES - 1);
-            const int it = s >= nsb ? 1 : 0;
+            int sbc;
+            const int it = pass_of(s, sbc);
             const int stg = s % Q8_STAGES;
             const uint4 *wt = reinterpret_cast<const uint4 *>(&s_w[wave][stg][0]);
             const uint8_t *ast = s_act[stg];
@@ -286,39 +309,69 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
                 for (int i = 0; i < 4; i++) sum[i] += (float)si[i] * (dw * dxa[i]);
             }
 #pragma unroll
-            for (int q = 0; q < Q8_IT; q++)
+            for (int q = 0; q < IT; q++)
                 if (it == q)
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[q][i] += sum[i];
         }
 
-        // results
-        float *out = DOWN ? (shared ? job.ys : job.ye) : (shared ? job.hs : job.h);
-        const int orows = DOWN ? H : (shared ? SF : FF);
-        const int row0 = DOWN ? rbase + 32 * wave : rbase + 16 * wave;
+        if (!DOWN) {
+            // h = silu(gate) * up for the item's activation rows and its 256
+            // moe_ff rows, converted in place to the down products' operand
+            // layout (routed: Q8_0, shared: two int8 digits per 32 values;
+            // dmoe_prep.h).  No loads are in flight after the last step: h
+            // goes through the weight-ring LDS, the conversion scratch through
+            // the activation ring's.
+            float *s_h = reinterpret_cast<float *>(&s_w[0][0][0]);      // [16][256]
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int col = 128 * hh + 16 * wave + r16;
+                if (!shared) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        s_h[(4 * g + i) * 256 + col] = q8_silu(acc[2 * hh][i]) * acc[2 * hh + 1][i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i += 2)
+                        s_h[(2 * g + (i >> 1)) * 256 + col] = q8_silu(acc[2 * hh][i] + acc[2 * hh][i + 1]) *
+                                                              (acc[2 * hh + 1][i] + acc[2 * hh + 1][i + 1]);
+                }
+            }
+            __syncthreads();
+            float *sv = reinterpret_cast<float *>(&s_act[0][0]) + wave * 256;
+            const int sb = rbase / 256, nsb_h = (shared ? SF : FF) / 256;
+            for (int t = wave; t < nt; t += Q8_WAVES) {
+                float v[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) v[c] = s_h[t * 256 + lane + 64 * c];
+                if (!shared)
+                    prep_values(v, job.ah, ACT_Q80, job.perm[t_first + t], N * K, sb, nsb_h, sv);
+                else
+                    prep_values(v, job.ahs, ACT_SPLIT32, t_first + t, N, sb, nsb_h, sv);
+            }
+            continue;
+        }
+
+        // results of the down products
+        float *out = shared ? job.ys : job.ye;
+        const int row0 = rbase + 32 * wave;
         if (!shared) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 if (4 * g + i >= nt) continue;
-                float *o = out + (size_t)job.perm[t_first + 4 * g + i] * orows + row0 + r16;
-                if (!DOWN) {
-                    o[0] = q8_silu(acc[0][i]) * acc[1][i];
-                } else {
-                    o[0] = acc[0][i];
-                    o[16] = acc[1][i];
-                }
+                float *o = out + (size_t)job.perm[t_first + 4 * g + i] * H + row0 + r16;
+                o[0] = acc[0][i];
+                o[16] = acc[1][i];
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i += 2) {
                 if (2 * g + (i >> 1) >= nt) continue;
-                float *o = out + (size_t)(t_first + 2 * g + (i >> 1)) * orows + row0 + r16;
-                if (!DOWN) {
-                    o[0] = q8_silu(acc[0][i] + acc[0][i + 1]) * (acc[1][i] + acc[1][i + 1]);
-                } else {
-                    o[0] = acc[0][i] + acc[0][i + 1];
-                    o[16] = acc[1][i] + acc[1][i + 1];
-                }
+                float *o = out + (size_t)(t_first + 2 * g + (i >> 1)) * H + row0 + r16;
+                o[0] = acc[0][i] + acc[0][i + 1];
+                o[16] = acc[1][i] + acc[1][i + 1];
             }
         }
     }
