@@ -125,7 +125,8 @@ def main():
     # are the touched experts' and the shared expert's gate and up matrices,
     # the activations in their operand layout (int8 values with, for Q4_K, f16
     # sums of 16 and an f32 scale per 256, for Q8_0 an f32 scale per 32; the
-    # shared expert's as two int8 digit rows) and h written as f32.  F16 (the prefill, MFMA-bound): its algorithmic
+    # shared expert's as two int8 digit rows) and h written in the down
+    # products' operand layout.  F16 (the prefill, MFMA-bound): its algorithmic
     # FLOPs, 2 per multiply-add of the routed pairs' and the tokens' shared
     # gate and up products (the shared expert's two f16 passes count once).
     rs_h = dmoe.row_size(cfg.wtype, H)
@@ -146,13 +147,17 @@ def main():
     else:
         if cfg.wtype in (dmoe.TYPE_Q4_K, dmoe.TYPE_Q8_0):
             if cfg.wtype == dmoe.TYPE_Q4_K:
-                act_row = H + (H // 16) * 2 + (H // 256) * 4
+                def act_row(n):
+                    return n + (n // 16) * 2 + (n // 256) * 4
                 dom_kernel = "dmoe::k_expert_q4k<0>"
             else:
-                act_row = H + (H // 32) * 4
+                def act_row(n):
+                    return n + (n // 32) * 4
                 dom_kernel = "dmoe::k_expert_q80<0>"
-            dom_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + N * act_row + 2 * N * act_row
-                         + P * FF * 4 + N * SF * 4)
+            # x rows in (routed, shared digit rows), h rows out in the down
+            # products' layout (routed pairs, shared digit rows)
+            dom_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + 3 * N * act_row(H)
+                         + P * act_row(FF) + 2 * N * act_row(SF))
         else:
             dom_kernel = "dmoe::k_gateup_routed"
             dom_bytes = touched * 2 * FF * rs_h + N * H * 2 + P * FF * 4

@@ -56,7 +56,7 @@ constexpr int WAVES = DMOE_X_WAVES;
 constexpr int RT = 2;                        // 16-row weight tiles per wave per step
 constexpr int WSTAGES = DMOE_X_WSTAGES;
 constexpr int DN_IT = DMOE_X_DN_IT;
-static_assert(DN_IT == 1 || DN_IT == 2, "row passes of a down item");
+static_assert(DN_IT >= 1 && DN_IT <= 4, "row passes of a down item");
 constexpr int GU_IT = 2;                         // row passes of a gate/up item
 constexpr int GROWS_GU = WAVES * 16 * GU_IT;     // gate/up rows of an item: one h super-block
 constexpr int GROWS_DN = WAVES * 16 * RT * DN_IT;   // down rows of an item
@@ -282,8 +282,13 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         const uint16_t *abs_ = act.bs + (size_t)arow * (Kin / 16) + (lane & 1) * 8;
         const float *ad = act.d + (size_t)arow * nsb;
 
-        // row pass of step s (at most two passes: no division)
-        auto pass_of = [&](int s) -> int { return IT == 1 ? 0 : (s >= nsb ? 1 : 0); };
+        // row pass of step s (at most four passes: no division)
+        auto pass_of = [&](int s) -> int {
+            int it = 0;
+#pragma unroll
+            for (int q = 1; q < IT; q++) it += s >= q * nsb ? 1 : 0;
+            return it;
+        };
         auto issue = [&](int s) {
             if (s >= steps) return;
             const int it = pass_of(s), sb = s - it * nsb;
