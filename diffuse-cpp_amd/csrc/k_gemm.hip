@@ -186,12 +186,15 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
                 lds_load16(bp[i] + wbk, sb + GTILE + i * GT * 16);
             }
         };
-        auto read_w = [&](int buf, h8 (&rw)[4]) {
-#pragma unroll
-            for (int t = 0; t < 4; t++) rw[t] = *reinterpret_cast<const h8 *>(&S[buf][1][boff + bstep(t)]);
+        // Operand reads of a stage (buffer buf, at the LDS byte offset of the
+        // buffer in S): the lane offsets go through an empty asm so that the
+        // compiler keeps one register each and adds the buffer offset per
+        // step, instead of holding a precomputed address per buffer.
+        auto read_w = [&](uint32_t boffs, int t) -> h8 {
+            return *reinterpret_cast<const h8 *>(&S[0][0][0] + boffs + bstep(t));
         };
-        auto read_a = [&](int buf, int ti) -> h8 {
-            return *reinterpret_cast<const h8 *>(&S[buf][0][aoff + 1024 * ti]);
+        auto read_a = [&](uint32_t aoffs, int ti) -> h8 {
+            return *reinterpret_cast<const h8 *>(&S[0][0][0] + aoffs + 1024 * ti);
         };
 
         f4 acc[8][4];
@@ -199,37 +202,21 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         for (int ti = 0; ti < 8; ti++)
 #pragma unroll
             for (int tw = 0; tw < 4; tw++) acc[ti][tw] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-        // MFMAs of one step: weight operands rw (read a step ahead), activation
-        // operands of buffer buf read two 16-row tiles ahead; a0, a1 hold tiles
-        // 0, 1 on entry and the next step's tiles 0, 1 (buffer nbuf) on exit
-        auto mfma_step = [&](int buf, int nbuf, bool next, h8 &a0, h8 &a1, const h8 (&rw)[4]) {
-            h8 a = a0, b = a1;
-#pragma unroll
-            for (int ti = 0; ti < 8; ti++) {
-                h8 an;
-                if (ti < 6)
-                    an = read_a(buf, ti + 2);
-                else if (next)
-                    an = read_a(nbuf, ti - 6);
-#pragma unroll
-                for (int tw = 0; tw < 4; tw++)
-                    acc[ti][tw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, rw[tw], acc[ti][tw], 0, 0, 0);
-                a = b;
-                if (ti < 6 || next) b = an;
-            }
-            a0 = a;
-            a1 = b;
-        };
+        // operand register sets: set c holds a stage's 8 activation and 4
+        // weight operands; step st computes from set st & 1 and reads stage
+        // st + 1 into the other set between its MFMAs
+        h8 ra[2][8], rw[2][4];
         // Step st: wait until stage st + 1 has landed (the GS - 3 stages after
         // it may be in flight; in the last steps fewer follow: wait for all),
         // barrier (all wavefronts' loads of stage st + 1 are in LDS, and the
-        // buffer of stage st - 1, last read in step st - 1, is free), refill
-        // that buffer with stage st + GS - 1, then read stage st + 1's weight
-        // operands into the spare registers while the MFMAs of stage st run.
-        // Operand reads stay in flight across a barrier (the compiler waits for
-        // them before their MFMAs); the scheduling barriers keep each step's
-        // MFMAs between its barriers.
-        auto sync_step = [&](int st, bool tail) {
+        // buffer of stage st - 1, whose operands were read in step st - 2 and
+        // consumed in step st - 1, is free), refill that buffer with stage
+        // st + GS - 1, then run the 32 MFMAs of stage st from registers,
+        // reading stage st + 1's operands (if next) in between: one or two
+        // reads ahead of each group of four MFMAs.  The scheduling groups fix
+        // that interleave; the reads complete during the step and are awaited
+        // before the next step's first MFMA.
+        auto step = [&](int st, int c, bool tail, bool next) {
             if (!tail)
                 GEMM_WAIT_VM_ONLY(2 * GP * (GS - 3));
             else
@@ -237,6 +224,28 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             if (!tail) issue(st + GS - 1);
+            uint32_t al = aoff, bl = boff;
+            asm volatile("" : "+v"(al), "+v"(bl));
+            const uint32_t nb = (uint32_t)(((st + 1) % GS) * 2 * GTILE);
+            const uint32_t aoffs = al + nb, boffs = bl + nb + GTILE;
+#pragma unroll
+            for (int ti = 0; ti < 8; ti++) {
+                if (next) {
+                    if (ti < 4) rw[c ^ 1][ti] = read_w(boffs, ti);
+                    ra[c ^ 1][ti] = read_a(aoffs, ti);
+                }
+#pragma unroll
+                for (int tw = 0; tw < 4; tw++)
+                    acc[ti][tw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ra[c][ti], rw[c][tw], acc[ti][tw], 0, 0, 0);
+                if (next) {
+                    if (ti < 4)
+                        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    else
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         };
 
         // the previous item's LDS reads are done in every wavefront
@@ -245,56 +254,47 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int st = 0; st < GS - 1; st++) issue(st);
-        // stage 0 in LDS, its first operands in registers
+        // stage 0 in LDS, its operands in set 0
         if (GS - 1 < total_steps)
             GEMM_WAIT_VM(2 * GP * (GS - 2));
         else
             GEMM_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        h8 a0, a1, rw0[4], rw1[4];
-        read_w(0, rw0);
-        a0 = read_a(0, 0);
-        a1 = read_a(0, 1);
+#pragma unroll
+        for (int t = 0; t < 4; t++) rw[0][t] = read_w(boff + GTILE, t);
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++) ra[0][ti] = read_a(aoff, ti);
         // total_steps is even (Kin % 64 == 0): two steps per iteration, one
-        // weight register set each.  Steps st with st + GS - 1 < total_steps
-        // refill the ring and wait for a fixed count; the last ones do neither.
+        // operand set each.  Steps st with st + GS - 1 < total_steps refill
+        // the ring and wait for a fixed count; the last ones do neither.
         int st = 0;
         for (; st + 1 + GS - 1 < total_steps; st += 2) {
-            sync_step(st, false);
-            read_w((st + 1) % GS, rw1);
-            mfma_step(st % GS, (st + 1) % GS, true, a0, a1, rw0);
-            __builtin_amdgcn_sched_barrier(0);
-            sync_step(st + 1, false);
-            read_w((st + 2) % GS, rw0);
-            mfma_step((st + 1) % GS, (st + 2) % GS, true, a0, a1, rw1);
-            __builtin_amdgcn_sched_barrier(0);
+            step(st, 0, false, true);
+            step(st + 1, 1, false, true);
         }
         for (; st < total_steps; st += 2) {
             // every stage is issued by now, except that the pair's first step
             // may still issue the last one
-            const bool more = st + 2 < total_steps;
-            sync_step(st, st + GS - 1 >= total_steps);
-            read_w((st + 1) % GS, rw1);
-            mfma_step(st % GS, (st + 1) % GS, true, a0, a1, rw0);
-            __builtin_amdgcn_sched_barrier(0);
-            sync_step(st + 1, true);
-            if (more) read_w((st + 2) % GS, rw0);
-            mfma_step((st + 1) % GS, (st + 2) % GS, more, a0, a1, rw1);
-            __builtin_amdgcn_sched_barrier(0);
+            step(st, 0, st + GS - 1 >= total_steps, true);
+            step(st + 1, 1, true, st + 2 < total_steps);
         }
 
         // results: output row of tile tw for lane r16; activation rows 16 ti + 4 g + i
+        // (the row base goes through an empty asm so that the compiler does not
+        // hold the 32 row indices in registers across the item loop)
+        int ebase = tok0 + 4 * g, erow = r16;
+        asm volatile("" : "+v"(ebase), "+v"(erow));
 #pragma unroll
         for (int ti = 0; ti < 8; ti++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int tt = tok0 + 16 * ti + 4 * g + i;
+                const int tt = ebase + 16 * ti + i;
                 if (tt >= nt) continue;
                 if (!DOWN) {
 #pragma unroll
                     for (int tj = 0; tj < 2; tj++) {
-                        const int row = rb * GN + 32 * wq + 16 * tj + r16;
+                        const int row = rb * GN + 32 * wq + 16 * tj + erow;
                         const float hv = gsilu(acc[ti][tj][i]) * acc[ti][2 + tj][i];
                         if (!shared) {
                             const int p = job.perm[t_first + tt];
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
                     float *o = shared ? job.ys + (size_t)(t_first + tt) * H
                                       : job.ye + (size_t)job.perm[t_first + tt] * H;
 #pragma unroll
-                    for (int tw = 0; tw < 4; tw++) o[rb * GN + 64 * wq + 16 * tw + r16] = acc[ti][tw][i];
+                    for (int tw = 0; tw < 4; tw++) o[rb * GN + 64 * wq + 16 * tw + erow] = acc[ti][tw][i];
                 }
             }
     }

@@ -63,11 +63,21 @@ __device__ void dispatch_lists(int c, const RouteParams &rp, const RouteBufs &rb
                                const WorkList &wl, int *s_tmp, int *s_off)
 {
     const int E = rp.n_experts, tid = threadIdx.x;
-    int total;
-    const int off = block_scan(c, s_tmp, &total);
+    int total, nec, off, ecb;
     const int nch = (c + wl.chunk - 1) / wl.chunk;
-    int nec;
-    const int ecb = block_scan(nch, s_tmp, &nec);
+    if (rp.n_tokens * rp.top_k < 32768 && E + rp.n_tokens * rp.top_k / wl.chunk + 1 < 32768) {
+        // both prefixes in one scan (pair counts in the low 16 bits, chunk
+        // counts in the high ones): every partial sum of either is below 2^15
+        int both;
+        const int p = block_scan(c | (nch << 16), s_tmp, &both);
+        off = p & 0xFFFF;
+        ecb = p >> 16;
+        total = both & 0xFFFF;
+        nec = both >> 16;
+    } else {
+        off = block_scan(c, s_tmp, &total);
+        ecb = block_scan(nch, s_tmp, &nec);
+    }
     if (tid < E) {
         rb.counts[tid] = c;
         rb.offsets[tid] = off;
@@ -123,31 +133,71 @@ __device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const W
     }
 }
 
+// Wavefront reductions of unsigned ints over 64 lanes (DPP row shifts and
+// broadcasts; the result is read from lane 63).
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v)
+{
+    const int id = MAX ? 0 : -1;
+    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x111, 0xF, 0xF, false));   // row_shr:1
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x112, 0xF, 0xF, false));   // row_shr:2
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x114, 0xF, 0xF, false));   // row_shr:4
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x118, 0xF, 0xF, false));   // row_shr:8
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xA, 0xF, false));   // row_bcast:15
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v)
+{
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // One wavefront: the bmax at position cap-1 of the descending order (ties to
 // the lower expert id).  Lane l keeps the order keys of experts l + 64 r.  A
 // most-significant-bit-first radix select finds the cap-th largest key P
-// (counts by ballot); the expert at position cap-1 is then the
-// (cap - 1 - #{keys > P})-th lowest id among the experts whose key is P.
-template <int R>
+// (counts by ballot), starting below the bits that every key shares; the
+// expert at position cap-1 is then the (cap - 1 - #{keys > P})-th lowest id
+// among the experts whose key is P.
+template <int R, bool FULL>
 __device__ void find_threshold(int E, int cap, const uint64_t *s_rk, const float *s_bmax,
                                float *s_thr)
 {
     const int lane = threadIdx.x & 63;
     uint32_t k[R];
     uint64_t valid[R];
+    uint32_t hi = 0u, lo = ~0u;
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const int f = lane + 64 * r;
         k[r] = f < E ? (uint32_t)(s_rk[f] >> 32) : 0u;
         valid[r] = __ballot(f < E);
+        if (f < E) {
+            hi = k[r] > hi ? k[r] : hi;
+            lo = k[r] < lo ? k[r] : lo;
+        }
     }
-    uint32_t P = 0;
-    for (int b = 31; b >= 0; b--) {
-        const uint32_t cand = P | (1u << b);
+    hi = wave_reduce_u32<true>(hi);
+    lo = wave_reduce_u32<false>(lo);
+    // every key lies in [lo, hi]: they share the bits above the highest bit
+    // where lo and hi differ, so P starts as that prefix (all keys >= P)
+    const uint32_t diff = hi ^ lo;
+    const int top = diff ? 31 - __builtin_clz(diff) : -1;
+    uint32_t P = top >= 0 ? (hi & ~((2u << top) - 1u)) : hi;
+    for (uint32_t bit = top >= 0 ? 1u << top : 0u; bit; bit >>= 1) {
+        const uint32_t cand = P | bit;
         int cnt = 0;
 #pragma unroll
-        for (int r = 0; r < R; r++) cnt += __popcll(__ballot(k[r] >= cand) & valid[r]);
-        if (cnt >= cap) P = cand;
+        for (int r = 0; r < R; r++)
+            cnt += __popcll(FULL ? __ballot(k[r] >= cand) : __ballot(k[r] >= cand) & valid[r]);
+        P = cnt >= cap ? cand : P;
     }
     int n = cap - 1;
 #pragma unroll
@@ -165,6 +215,29 @@ __device__ void find_threshold(int E, int cap, const uint64_t *s_rk, const float
     }
 }
 
+// Exclusive prefix of a 0/1 flag over threads tid < 256 (any block size):
+// ballots and lane counts, four wavefront totals through LDS (s_w4: 4 ints).
+__device__ __forceinline__ int flag_scan256(int flag, int *s_w4, int *total)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t b = __ballot(flag);
+    const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+    if (lane == 0 && wave < 4) s_w4[wave] = __popcll(b);
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const int t = s_w4[w];
+        before += w < wave ? t : 0;
+        all += t;
+    }
+    *total = all;
+    return before + below;
+}
+
+// SINGLE: the forward is one routing group (the dispatch needs nothing
+// beyond this block; the token probabilities are staged in LDS).
+template <bool SINGLE>
 __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs rb, WorkList wl,
                                                       int32_t *counter)
 {
@@ -174,10 +247,10 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     __shared__ int32_t s_cand[MAX_E];
     __shared__ int32_t s_idx[ROUTE_LDS / 8];      // group pairs (tokens x slots)
     __shared__ float s_w[ROUTE_LDS / 8];          // their probs
-    __shared__ uint64_t s_k64[RT_WAVES][64];      // per wavefront: candidate rank keys
-    __shared__ int s_pref[ROUTE_PREF];            // dispatch: pairs of earlier groups per expert
+    __shared__ __align__(16) uint32_t s_k32[RT_WAVES][2][64];   // per wavefront: order keys of two tokens
     __shared__ uint32_t s_bits[RT_BITS];          // [e][word]: tokens of the group that chose e
     __shared__ int s_tmp[RT_WAVES + 1];
+    __shared__ float s_probs[SINGLE ? ROUTE_LDS : 1];   // the group's probs (one group)
     __shared__ float s_thr;
     __shared__ int s_nan, s_nc, s_last;
 
@@ -191,13 +264,46 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     const int words = (G + 31) / 32;
     float *s_sel = reinterpret_cast<float *>(s_key);
 
+    // one forward = one group: the group's probs go to LDS, loaded with the scores
+    constexpr int R = ROUTE_LDS / RT_THREADS;
+    float pv[R];
+    if constexpr (SINGLE) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = tid + r * RT_THREADS;
+            pv[r] = i < nt * E ? rb.probs[(size_t)t0 * E + i] : 0.0f;
+        }
+    }
     if (tid == 0) s_nan = 0;
     for (int i = tid; i < E * words; i += RT_THREADS) s_bits[i] = 0u;
-    __syncthreads();
+
     // selection scores of the group (sel = probs + bias, :207-210); every
-    // load is issued before the first is used
-    {
-        constexpr int R = ROUTE_LDS / RT_THREADS;
+    // load is issued before the first is used.  Blocks of 32 tokens: thread
+    // e loads the 32 scores of expert e and folds them in registers.
+    const bool fold32 = rp.use_block && G == 32 && nt == 32;
+    bool nan = false;
+    if (fold32) {
+        if (tid < E) {
+            const float *src = rb.sel + (size_t)t0 * E + tid;
+            float v[32];
+#pragma unroll
+            for (int t = 0; t < 32; t++) v[t] = src[(size_t)t * E];
+            // :223-229  bmax = s_0 folded with m <- s_j + relu(m - s_j), j = 1..blk-1
+            float m = v[0];
+            nan = v[0] != v[0];
+#pragma unroll
+            for (int j = 1; j < 32; j++) {
+                s_sel[j * E + tid] = v[j];
+                nan |= v[j] != v[j];
+                float r = m - v[j];
+                r = r > 0.0f ? r : 0.0f;          // ggml_relu
+                m = v[j] + r;
+            }
+            s_sel[tid] = v[0];
+            s_bmax[tid] = m;
+            s_rk[tid] = rank_key(order_key(m), tid);
+        }
+    } else {
         const int n = nt * E;
         const float *src = rb.sel + (size_t)t0 * E;
         float v[R];
@@ -206,39 +312,48 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
             const int i = tid + r * RT_THREADS;
             v[r] = i < n ? src[i] : 0.0f;
         }
-        bool nan = false;
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int i = tid + r * RT_THREADS;
             if (i < n) s_sel[i] = v[r];
             nan |= v[r] != v[r];
         }
-        if (nan) s_nan = 1;
+    }
+    if constexpr (SINGLE) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = tid + r * RT_THREADS;
+            if (i < nt * E) s_probs[i] = pv[r];
+        }
     }
     __syncthreads();
+    if (nan) s_nan = 1;
 
     bool restrict_cand = false;
     if (rp.use_block) {
-        // :223-229  bmax = s_0 folded with m <- s_j + relu(m - s_j), j = 1..blk-1
-        for (int e = tid; e < E; e += RT_THREADS) {
-            float m = s_sel[e];
-            for (int j = 1; j < G; j++) {
-                const float sj = s_sel[j * E + e];
-                float r = m - sj;
-                r = r > 0.0f ? r : 0.0f;          // ggml_relu
-                m = sj + r;
+        if (!fold32) {
+            for (int e = tid; e < E; e += RT_THREADS) {
+                float m = s_sel[e];
+                for (int j = 1; j < G; j++) {
+                    const float sj = s_sel[j * E + e];
+                    float r = m - sj;
+                    r = r > 0.0f ? r : 0.0f;      // ggml_relu
+                    m = sj + r;
+                }
+                s_bmax[e] = m;
+                s_rk[e] = rank_key(order_key(m), e);
             }
-            s_bmax[e] = m;
-            s_rk[e] = rank_key(order_key(m), e);
+            __syncthreads();
         }
-        __syncthreads();
         // :232-236  thr = the cap-th largest bmax (position cap-1 of the
-        // descending order, ties to the lower expert id), found by wavefront 0
+        // descending order, ties to the lower expert id)
         if (wave == 0) {
-            if (E <= 256)
-                find_threshold<4>(E, rp.capacity, s_rk, s_bmax, &s_thr);
+            if (E == 256)
+                find_threshold<4, true>(E, rp.capacity, s_rk, s_bmax, &s_thr);
+            else if (E < 256)
+                find_threshold<4, false>(E, rp.capacity, s_rk, s_bmax, &s_thr);
             else
-                find_threshold<MAX_E / 64>(E, rp.capacity, s_rk, s_bmax, &s_thr);
+                find_threshold<MAX_E / 64, false>(E, rp.capacity, s_rk, s_bmax, &s_thr);
         }
         __syncthreads();
         // :241-248  keep = step(bmax - (thr + -1e-6)); sel' = sel + (0 | -1e30)
@@ -250,22 +365,25 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
         }
         if (tid == 0) rb.thr[g] = s_thr;
         int nallowed;
-        const int pos = block_scan(keep, s_tmp, &nallowed);
+        const int pos = E <= 256 ? flag_scan256(keep, s_tmp, &nallowed) : block_scan(keep, s_tmp, &nallowed);
         // Every allowed score (finite, |sel| < 1e20) ranks above every masked
         // one (sel - 1e30 < -9e29), so the top-k can be taken among the
-        // allowed experts alone when there are at least k of them.
+        // allowed experts alone when there are at least k of them; their
+        // sel' = sel + 0 has the order key of sel.
         restrict_cand = rp.bias_small && !s_nan && nallowed >= K;
         if (restrict_cand && keep) s_cand[pos] = tid;
-        if (RT_THREADS % E == 0) {
-            // every thread converts the scores of one expert
-            const int e = tid % E;
-            const float add = (float)((s_bmax[e] - tp) > 0.0f) * 1e30f + (-1e30f);
-            for (int t = tid / E; t < nt; t += RT_THREADS / E)
-                s_key[t * E + e] = order_key(s_sel[t * E + e] + add);
-        } else {
-            const float add = (float)keep * 1e30f + (-1e30f);
-            for (int t = 0; t < nt; t++)
-                if (tid < E) s_key[t * E + tid] = order_key(s_sel[t * E + tid] + add);
+        if (!restrict_cand) {
+            if (RT_THREADS % E == 0) {
+                // every thread converts the scores of one expert
+                const int e = tid % E;
+                const float add = (float)((s_bmax[e] - tp) > 0.0f) * 1e30f + (-1e30f);
+                for (int t = tid / E; t < nt; t += RT_THREADS / E)
+                    s_key[t * E + e] = order_key(s_sel[t * E + e] + add);
+            } else {
+                const float add = (float)keep * 1e30f + (-1e30f);
+                for (int t = 0; t < nt; t++)
+                    if (tid < E) s_key[t * E + tid] = order_key(s_sel[t * E + tid] + add);
+            }
         }
         if (tid == 0) s_nc = restrict_cand ? nallowed : E;
     } else {
@@ -279,31 +397,59 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     // :252  top-k: a candidate's slot is its rank among the token's candidates
     // (descending sel', ties to the lower expert id)
     const int nc = s_nc;
-    const int my_e = lane < nc ? s_cand[lane] : 0;
-    for (int t = wave; t < nt; t += RT_WAVES) {
-        const uint32_t *kt = s_key + t * E;
-        if (nc <= 64) {
-            // lane c holds candidate c's rank key; every other key is an LDS
-            // broadcast and one 64-bit compare
-            const uint64_t mk = lane < nc ? rank_key(kt[my_e], my_e) : 0ull;
-            s_k64[wave][lane] = mk;
+    if (nc <= 64) {
+        // lane c holds candidate c's order key for two tokens of the
+        // wavefront at a time; a candidate's slot is the number of keys
+        // above its own (LDS broadcasts, four keys per read) plus, when keys
+        // tie, the tied candidates of lower id (lower lane).  Without ties
+        // the counts are a permutation of 0 .. nc-1, which their sum tests.
+        const bool act = lane < nc;
+        const int my_e = act ? s_cand[lane] : 0;
+        auto okey = [&](int t) -> uint32_t {
+            if (!act || t >= nt) return 0u;
+            return restrict_cand ? order_key(s_sel[t * E + my_e]) : s_key[t * E + my_e];
+        };
+        const int nc4 = (nc + 3) & ~3;
+        const int perm_sum = nc * (nc - 1) / 2;
+        for (int t = wave; t < nt; t += 2 * RT_WAVES) {
+            const int t2 = t + RT_WAVES;
+            const uint32_t k0 = okey(t), k1 = okey(t2);
+            s_k32[wave][0][lane] = k0;
+            s_k32[wave][1][lane] = k1;
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            int rank = 0;
-#pragma unroll 8
-            for (int c2 = 0; c2 < nc; c2++) rank += s_k64[wave][c2] > mk;
-            if (lane < nc && rank < K) s_idx[t * K + rank] = my_e;
+            int r0 = 0, r1 = 0;
+            // keys past nc are 0 and never above a candidate's
+#pragma unroll 4
+            for (int c2 = 0; c2 < nc4; c2 += 4) {
+                const uint4 a = *reinterpret_cast<const uint4 *>(&s_k32[wave][0][c2]);
+                const uint4 b = *reinterpret_cast<const uint4 *>(&s_k32[wave][1][c2]);
+                r0 += (a.x > k0 ? 1 : 0) + (a.y > k0 ? 1 : 0) + (a.z > k0 ? 1 : 0) + (a.w > k0 ? 1 : 0);
+                r1 += (b.x > k1 ? 1 : 0) + (b.y > k1 ? 1 : 0) + (b.z > k1 ? 1 : 0) + (b.w > k1 ? 1 : 0);
+            }
+            if (wave_sum_i32(act ? r0 : 0) != perm_sum)
+                for (int c2 = 0; c2 < lane; c2++) r0 += s_k32[wave][0][c2] == k0 ? 1 : 0;
+            if (t2 < nt && wave_sum_i32(act ? r1 : 0) != perm_sum)
+                for (int c2 = 0; c2 < lane; c2++) r1 += s_k32[wave][1][c2] == k1 ? 1 : 0;
+            if (act && r0 < K) s_idx[t * K + r0] = my_e;
+            if (act && t2 < nt && r1 < K) s_idx[t2 * K + r1] = my_e;
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        } else {
+        }
+    } else {
+        // keys: the sel' keys, or with restricted candidates the keys of sel
+        auto key = [&](int t, int e) -> uint32_t {
+            return restrict_cand ? order_key(s_sel[t * E + e]) : s_key[t * E + e];
+        };
+        for (int t = wave; t < nt; t += RT_WAVES) {
             for (int c = lane; c < nc; c += 64) {
                 const int e = s_cand[c];
-                const uint32_t k = kt[e];
+                const uint32_t k = key(t, e);
                 int rank = 0;
 #pragma unroll 8
                 for (int c2 = 0; c2 < nc; c2++) {
                     const int e2 = s_cand[c2];
-                    rank += ranks_before(kt[e2], e2, k, e);
+                    rank += ranks_before(key(t, e2), e2, k, e);
                 }
                 if (rank < K) s_idx[t * K + rank] = e;
             }
@@ -319,7 +465,10 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     float w = 0.0f;
     if (tid < np) {
         mine = s_idx[tid];
-        w = rb.probs[(size_t)(t0 + pt) * E + mine];
+        if constexpr (SINGLE)
+            w = s_probs[pt * E + mine];
+        else
+            w = rb.probs[(size_t)(t0 + pt) * E + mine];
         s_w[tid] = w;
         atomicOr(&s_bits[mine * words + (pt >> 5)], 1u << (pt & 31));
     }
@@ -344,24 +493,26 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
         for (int wd = 0; wd < words; wd++) c += __popc(s_bits[tid * words + wd]);
 
     int *s_off = reinterpret_cast<int *>(s_rk);
-    if (gridDim.x == 1) {
+    if constexpr (SINGLE) {
         // one routing group: the dispatch needs nothing beyond this block
         dispatch_lists(c, rp, rb, wl, s_tmp, s_off);
         if (tid < np) rb.perm[s_off[mine] + lr] = tid;
         return;
-    }
-    if (tid < E) rb.hist[(size_t)g * E + tid] = c;
-    if (tid < np) rb.lrank[(size_t)t0 * K + tid] = lr;
+    } else {
+        if (tid < E) rb.hist[(size_t)g * E + tid] = c;
+        if (tid < np) rb.lrank[(size_t)t0 * K + tid] = lr;
 
-    // the last group to finish runs the dispatch
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    dispatch_all(rp, rb, wl, s_tmp, s_off, s_pref);
-    if (tid == 0) *counter = 0;
+        // the last group to finish runs the dispatch
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
+        __syncthreads();
+        if (!s_last) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __shared__ int s_pref[ROUTE_PREF];   // dispatch: pairs of earlier groups per expert
+        dispatch_all(rp, rb, wl, s_tmp, s_off, s_pref);
+        if (tid == 0) *counter = 0;
+    }
 }
 
 // General-shape routing (groups too large for LDS): selection scores are
@@ -499,7 +650,11 @@ hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkLi
     const int G = rp.use_block ? rp.block_size : 32;
     const int ngroups = (rp.n_tokens + G - 1) / G;
     if (route_fits_lds(rp)) {
-        hipLaunchKernelGGL(k_route, dim3(ngroups), dim3(RT_THREADS), 0, s, rp, rb, wl, counter);
+        if (ngroups == 1)
+            hipLaunchKernelGGL(k_route<true>, dim3(1), dim3(RT_THREADS), 0, s, rp, rb, wl, counter);
+        else
+            hipLaunchKernelGGL(k_route<false>, dim3(ngroups), dim3(RT_THREADS), 0, s, rp, rb, wl,
+                               counter);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_route_general, dim3(ngroups), dim3(256), 0, s, rp, rb.logits,
