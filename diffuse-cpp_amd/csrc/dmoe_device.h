@@ -94,4 +94,46 @@ __device__ __forceinline__ uint16_t f2h(float f)
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// DPP reductions (results exact whatever the order: max of floats, sums of
+// integers).  wave_max_f32: the maximum over the 64 lanes (lanes with NaN
+// contribute nothing unless every lane holds NaN).  row_sum16_i32: lane 15
+// of every 16-lane row receives the sum of its row.  half_max_f32: lanes 31
+// and 63 receive the maxima of lanes 0..31 and 32..63.
+#define DMOE_DPP(old, v, ctrl, rmask) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, (float)(old)), \
+                                                          __builtin_bit_cast(int, (float)(v)), ctrl, rmask, 0xF, false))
+
+__device__ __forceinline__ float row_prefix_max_f32(float v, float id)
+{
+    v = fmaxf(v, DMOE_DPP(id, v, 0x111, 0xF));   // row_shr:1
+    v = fmaxf(v, DMOE_DPP(id, v, 0x112, 0xF));   // row_shr:2
+    v = fmaxf(v, DMOE_DPP(id, v, 0x114, 0xF));   // row_shr:4
+    v = fmaxf(v, DMOE_DPP(id, v, 0x118, 0xF));   // row_shr:8
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v, float id)
+{
+    v = row_prefix_max_f32(v, id);
+    v = fmaxf(v, DMOE_DPP(id, v, 0x142, 0xA));   // row_bcast:15
+    v = fmaxf(v, DMOE_DPP(id, v, 0x143, 0xC));   // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// lanes 31 and 63 hold the maxima of the two 32-lane halves
+__device__ __forceinline__ float half_max_f32(float v, float id)
+{
+    v = row_prefix_max_f32(v, id);
+    return fmaxf(v, DMOE_DPP(id, v, 0x142, 0xA));  // row_bcast:15
+}
+
+__device__ __forceinline__ int row_sum16_i32(int v)
+{
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    return v;
+}
+
 } // namespace dmoe

@@ -40,20 +40,23 @@ __device__ __forceinline__ void prep_values(const float (&v)[4], const ActI8 &ou
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    // value of largest magnitude, lowest index on ties
-    float amax = -1.0f, aval = 0.0f;
-    int aidx = 0;
+    // value of largest magnitude, lowest index on ties (index lane + 64 c:
+    // the first c whose ballot has a match, then its lowest lane); NaNs
+    // never match, and with every value NaN amax stays -1 and aval 0
+    float lmax = -1.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) lmax = fmaxf(lmax, fabsf(v[c]));
+    const float amax = wave_max_f32(lmax, -1.0f);
+    float aval = 0.0f;
+    bool found = false;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        const float a = fabsf(v[c]);
-        if (a > amax) { amax = a; aval = v[c]; aidx = lane + 64 * c; }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float oa = __shfl_xor(amax, m, 64);
-        const float ov = __shfl_xor(aval, m, 64);
-        const int oi = __shfl_xor(aidx, m, 64);
-        if (oa > amax || (oa == amax && oi < aidx)) { amax = oa; aval = ov; aidx = oi; }
+        const uint64_t m = __ballot(fabsf(v[c]) == amax);
+        if (!found && m) {
+            found = true;
+            aval = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[c]),
+                                                                       __builtin_ctzll(m)));
+        }
     }
 
     const int K = nsb * 256;
@@ -64,10 +67,10 @@ __device__ __forceinline__ void prep_values(const float (&v)[4], const ActI8 &ou
         float bmax[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            float a = fabsf(v[c]);
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
-            bmax[c] = a;
+            const float h = half_max_f32(fabsf(v[c]), __builtin_nanf(""));
+            const float m0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, h), 31));
+            const float m1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, h), 63));
+            bmax[c] = lane < 32 ? m0 : m1;
         }
         const size_t dbase = (size_t)row * (K / 32) + sb * 8;
         if (mode == ACT_Q80) {
@@ -127,18 +130,18 @@ __device__ __forceinline__ void prep_values(const float (&v)[4], const ActI8 &ou
         }
     } else if (mode == ACT_Q8K) {
         float dscale = 0.0f;
+        int qc[4] = {0, 0, 0, 0};
         if (amax != 0.0f) {
             const float iscale = -127.0f / aval;
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const int q = nearest_int(iscale * v[c]);
-                sv[lane + 64 * c] = (float)(q < 127 ? q : 127);
+                qc[c] = q < 127 ? q : 127;
             }
             dscale = 1.0f / iscale;
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; c++) sv[lane + 64 * c] = 0.0f;
         }
+#pragma unroll
+        for (int c = 0; c < 4; c++) sv[lane + 64 * c] = (float)qc[c];
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         uint32_t pk = 0;
@@ -146,10 +149,12 @@ __device__ __forceinline__ void prep_values(const float (&v)[4], const ActI8 &ou
         for (int i = 0; i < 4; i++)
             pk |= ((uint32_t)(int)sv[src_index(4 * lane + i)] & 0xffu) << (8 * i);
         *reinterpret_cast<uint32_t *>(out.q + qbase + 4 * lane) = pk;
-        if (lane < 16) {
-            float s = 0.0f;                 // integer sum, exact
-            for (int i = 0; i < 16; i++) s += sv[16 * lane + i];
-            out.bs[bbase + lane] = f2h(s);
+        // sums of 16 quants: values 16 g .. 16 g + 15 are lanes 16 r .. 16 r + 15
+        // of c = g / 4, r = g % 4 (integers, exact in any order)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int s16 = row_sum16_i32(qc[c]);
+            if ((lane & 15) == 15) out.bs[bbase + 4 * c + (lane >> 4)] = f2h((float)s16);
         }
         if (lane == 0) out.d[(size_t)row * nsb + sb] = dscale;
     } else {
@@ -160,8 +165,12 @@ __device__ __forceinline__ void prep_values(const float (&v)[4], const ActI8 &ou
             k = 15 - ex;                      // amax * 2^k in [2^14, 2^15)
             if (nearest_int(ldexpf(amax, k)) > 32512) k -= 1;
         }
+        int xc[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) sv[lane + 64 * c] = (float)nearest_int(ldexpf(v[c], k));
+        for (int c = 0; c < 4; c++) {
+            xc[c] = nearest_int(ldexpf(v[c], k));
+            sv[lane + 64 * c] = (float)xc[c];
+        }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         uint32_t phi = 0, plo = 0;
@@ -175,16 +184,16 @@ __device__ __forceinline__ void prep_values(const float (&v)[4], const ActI8 &ou
         const size_t lo_off = (size_t)rows * K;
         *reinterpret_cast<uint32_t *>(out.q + qbase + 4 * lane) = phi;
         *reinterpret_cast<uint32_t *>(out.q + lo_off + qbase + 4 * lane) = plo;
-        if (lane < 16) {
-            int s1 = 0, s0 = 0;
-            for (int i = 0; i < 16; i++) {
-                const int X = (int)sv[16 * lane + i];
-                const int a1 = (X + 128) >> 8;
-                s1 += a1;
-                s0 += X - (a1 << 8);
+        // digit sums of 16 values (lanes 16 r .. 16 r + 15 of c: group 4 c + r)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int a1 = (xc[c] + 128) >> 8, a0 = xc[c] - (a1 << 8);
+            const int s1 = row_sum16_i32(a1), s0 = row_sum16_i32(a0);
+            if ((lane & 15) == 15) {
+                const int g = 4 * c + (lane >> 4);
+                out.bs[bbase + g] = f2h((float)s1);
+                out.bs[(size_t)rows * (K / 16) + bbase + g] = f2h((float)s0);
             }
-            out.bs[bbase + lane] = f2h((float)s1);
-            out.bs[(size_t)rows * (K / 16) + bbase + lane] = f2h((float)s0);
         }
         if (lane == 0) {
             out.d[(size_t)row * nsb + sb] = ldexpf(1.0f, 8 - k);           // a1 row
