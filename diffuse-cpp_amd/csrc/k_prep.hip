@@ -125,16 +125,39 @@ __device__ void logits_wave(const float *__restrict__ W, const float *__restrict
                 acc[t][e] = a;
             }
     }
-    constexpr int NV = LT * LE, SH = 6 - __builtin_ctz(NV);
+    // Few outputs: the transposed butterfly (fewer shuffles).  Many (the
+    // 64 of the wide tile): the plain one, whose 64 independent chains hide
+    // the shuffle latency better (measured faster).  Same sums either way.
+    constexpr int NV = LT * LE;
     static_assert((NV & (NV - 1)) == 0, "a power-of-two tile");
-    float v[NV];
+    float mine = 0.0f;
+    int j;
+    bool writer;
+    if constexpr (NV <= 8) {
+        constexpr int SH = 6 - __builtin_ctz(NV);
+        float v[NV];
 #pragma unroll
-    for (int t = 0; t < LT; t++)
+        for (int t = 0; t < LT; t++)
 #pragma unroll
-        for (int e = 0; e < LE; e++) v[t * LE + e] = acc[t][e];
-    const float mine = butterfly_sum<NV>(v);
-    const int j = lane >> SH, t = j / LE, e = j % LE;
-    if ((lane & ((1 << SH) - 1)) == 0 && t0 + t < N && e0 + e < E) {
+            for (int e = 0; e < LE; e++) v[t * LE + e] = acc[t][e];
+        mine = butterfly_sum<NV>(v);
+        j = lane >> SH;
+        writer = (lane & ((1 << SH) - 1)) == 0;
+    } else {
+#pragma unroll
+        for (int t = 0; t < LT; t++)
+#pragma unroll
+            for (int e = 0; e < LE; e++) {
+                float v = acc[t][e];
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+                if (lane == t * LE + e) mine = v;
+            }
+        j = lane;
+        writer = lane < NV;
+    }
+    const int t = j / LE, e = j % LE;
+    if (writer && t0 + t < N && e0 + e < E) {
         const size_t o = (size_t)(t0 + t) * E + e0 + e;
         const float p = sigmoid_f32(mine);
         rb.logits[o] = mine;
