@@ -26,7 +26,6 @@ sys.path.insert(0, str(ROOT / "diffuse-cpp_amd"))
 
 METRIC = "MoE-layer tokens/s + % HBM-BW roofline (32-tok block, Q4_K); prefill % MFMA"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 
 

@@ -158,21 +158,30 @@ __device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[RT], const uint8
         const h4 bm = {fa, fa, fb, fb};
         // nibbles -> int8 operands: dwords 2c, 2c+1 hold chunk c of lane group g
         const uint32_t w[8] = {t.q0.x, t.q0.y, t.q0.z, t.q0.w, t.q1.x, t.q1.y, t.q1.z, t.q1.w};
-        int isum[4] = {0, 0, 0, 0};
+        // all eight sub-block products of the tile first, then their scales
+        // (the MFMA results are read only after the last one is issued)
+        v4i sj[8];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t l0 = w[2 * c] & 0x0F0F0F0Fu, l1 = w[2 * c + 1] & 0x0F0F0F0Fu;
             const uint32_t h0 = (w[2 * c] >> 4) & 0x0F0F0F0Fu, h1 = (w[2 * c + 1] >> 4) & 0x0F0F0F0Fu;
             const long blo = (long)((uint64_t)l1 << 32 | l0), bhi = (long)((uint64_t)h1 << 32 | h0);
-            v4i s_lo = {0, 0, 0, 0}, s_hi = {0, 0, 0, 0};
-            s_lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[2 * c], blo, s_lo, 0, 0, 0);
-            s_hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[2 * c + 1], bhi, s_hi, 0, 0, 0);
-            // |S_j| <= 32 * 15 * 127 and sc_j < 64: 24-bit products are exact
-            // (v_mad_i32_i24, full rate; a 32-bit multiply is quarter rate)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                isum[i] += __mul24((int)sc[2 * c], s_lo[i]) + __mul24((int)sc[2 * c + 1], s_hi[i]);
+            const v4i z = {0, 0, 0, 0};
+            sj[2 * c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[2 * c], blo, z, 0, 0, 0);
+            sj[2 * c + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[2 * c + 1], bhi, z, 0, 0, 0);
         }
+        // |S_j| <= 32 * 15 * 127 and sc_j < 64: 24-bit products are exact
+        // (v_mad_i32_i24, full rate; a 32-bit multiply is quarter rate). The
+        // empty asm pins each step as one multiply-add: left free, the
+        // compiler splits the chain into v_mul_i32_i24 + v_add3 pairs.
+        int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                isum[i] = __mul24((int)sc[j], sj[j][i]) + isum[i];
+                asm volatile("" : "+v"(isum[i]));
+            }
         f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
         s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, bm, s2, 0, 0, 0);
         const float d = h16f(t.h.x & 0xffffu), dmin = h16f(t.h.x >> 16);
