@@ -296,11 +296,18 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
                 (long)((uint64_t)w45.y << 32 | w45.x), (long)((uint64_t)w45.w << 32 | w45.z),
                 (long)((uint64_t)w67.y << 32 | w67.x), (long)((uint64_t)w67.w << 32 | w67.z)};
             const uint32_t wds[4] = {wd.x, wd.y, wd.z, wd.w};
+            // all eight block products first, then their scales (the MFMA
+            // results are read only after the last one is issued)
+            v4i sj[8];
+#pragma unroll
+            for (int jb = 0; jb < 8; jb++) {
+                const v4i z = {0, 0, 0, 0};
+                sj[jb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[jb], w[jb], z, 0, 0, 0);
+            }
             float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int jb = 0; jb < 8; jb++) {
-                v4i si = {0, 0, 0, 0};
-                si = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[jb], w[jb], si, 0, 0, 0);
+                const v4i si = sj[jb];
                 const float dw = q8_h2f(jb & 1 ? wds[jb >> 1] >> 16 : wds[jb >> 1] & 0xffffu);
                 // scales of block jb for activation rows 4g .. 4g+3
                 const float4 dx = *reinterpret_cast<const float4 *>(ast + Q8_AD_OFF + jb * 64 + 16 * g);

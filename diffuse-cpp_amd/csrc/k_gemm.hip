@@ -16,7 +16,7 @@
 // together and share the weight rows through the caches.  Each 32-wide k
 // step stages the 256 activation rows and the 256 weight rows in LDS with the
 // LDS-direct global loads (global_load_lds_dwordx4: no registers held, so a
-// 4-stage ring keeps three steps of loads in flight to cover HBM latency);
+// 5-stage ring keeps four steps of loads in flight to cover HBM latency);
 // each of the 8 wavefronts computes a 128 x 64 output
 // tile as 8 x 4 v_mfma_f32_16x16x32_f16 (operand layout as in k_expert.hip: srcA lane l =
 // activation row l%16, k = 8*(l/16)+e; srcB = weight row, same k; D lane l =
@@ -47,10 +47,8 @@ __device__ __forceinline__ uint16_t f2h_rn(float f) { return __builtin_bit_cast(
 // with the slot flipped by row bits 1..2.
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
 
-// s_waitcnt with vmcnt(n) (n < 64); lgkmcnt(0) or untouched (LDS reads may
-// stay in flight); expcnt untouched
+// s_waitcnt with vmcnt(n) (n < 64) and lgkmcnt(0); expcnt untouched
 #define GEMM_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70)
-#define GEMM_WAIT_VM_ONLY(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0xF70)
 
 // LDS-direct load of 16 bytes per lane: lane l's bytes go to LDS address
 // lds + 16 l (lds: a wave-uniform LDS byte address).  Written as inline assembly so that the
@@ -94,8 +92,11 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
     // chunks) are split into 8 contiguous segments of equal work (a shared
     // unit does two passes), one per XCD, so that the row groups of a unit
     // (one activation block) and the chunks of an expert (one weight slice)
-    // meet in the same L2.  Within a segment, item m is unit m / row-groups,
-    // row group m % row-groups.
+    // meet in the same L2.  Within a segment the shared units' items come
+    // first (twice as long: started first, the routed items fill in behind
+    // them; dispatched last, they would finish a round after the rest), then
+    // the routed ones; item m of either part is unit m / row-groups, row group
+    // m % row-groups.
     static_assert(GEMM_BLOCKS % 8 == 0, "grid by XCD");
     const int xcd = blockIdx.x & 7, G8 = gridDim.x >> 3, lb = blockIdx.x >> 3;
     const long w_routed = (long)n_ec * rg, w_total = w_routed + 2L * nch * rg_sh;
@@ -121,8 +122,8 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
     auto bstep = [](int tw) -> int { return DOWN ? 1024 * tw : (tw < 2 ? 1024 * tw : GN * 64 + 1024 * (tw - 2)); };
 
     for (int m = lb; m < seg_items; m += G8) {
-        const bool shared = m >= nr * rg;
-        const int mm = shared ? m - nr * rg : m;
+        const bool shared = m < ns * rg_sh;
+        const int mm = shared ? m : m - ns * rg_sh;
         const int rgn = shared ? rg_sh : rg;
         const int unit = (shared ? s0 : u0) + mm / rgn, rb = mm % rgn;
         int t_first, nt, e = 0;
@@ -206,24 +207,25 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         // weight operands; step st computes from set st & 1 and reads stage
         // st + 1 into the other set between its MFMAs
         h8 ra[2][8], rw[2][4];
-        // Step st: wait until stage st + 1 has landed (the GS - 3 stages after
-        // it may be in flight; in the last steps fewer follow: wait for all),
-        // barrier (all wavefronts' loads of stage st + 1 are in LDS, and the
-        // buffer of stage st - 1, whose operands were read in step st - 2 and
-        // consumed in step st - 1, is free), refill that buffer with stage
-        // st + GS - 1, then run the 32 MFMAs of stage st from registers,
+        // Step st: wait until stage st + 1 has landed (the GS - 2 stages after
+        // it may be in flight; in the last steps fewer follow: wait for all)
+        // and until this wavefront's reads of stage st (issued in step st - 1)
+        // are done, barrier (all wavefronts' loads of stage st + 1 are in LDS,
+        // and the buffer of stage st, whose operands are all in registers, is
+        // free), refill that buffer with stage st + GS, then run the 32 MFMAs
+        // of stage st from registers,
         // reading stage st + 1's operands (if next) in between: one or two
         // reads ahead of each group of four MFMAs.  The scheduling groups fix
         // that interleave; the reads complete during the step and are awaited
         // before the next step's first MFMA.
         auto step = [&](int st, int c, bool tail, bool next) {
             if (!tail)
-                GEMM_WAIT_VM_ONLY(2 * GP * (GS - 3));
+                GEMM_WAIT_VM(2 * GP * (GS - 2));
             else
-                GEMM_WAIT_VM_ONLY(0);
+                GEMM_WAIT_VM(0);
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (!tail) issue(st + GS - 1);
+            if (!tail) issue(st + GS);
             uint32_t al = aoff, bl = boff;
             asm volatile("" : "+v"(al), "+v"(bl));
             const uint32_t nb = (uint32_t)(((st + 1) % GS) * 2 * GTILE);
@@ -253,10 +255,10 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
 #pragma unroll
-        for (int st = 0; st < GS - 1; st++) issue(st);
+        for (int st = 0; st < GS; st++) issue(st);
         // stage 0 in LDS, its operands in set 0
         if (GS - 1 < total_steps)
-            GEMM_WAIT_VM(2 * GP * (GS - 2));
+            GEMM_WAIT_VM(2 * GP * (GS - 1));
         else
             GEMM_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
@@ -267,15 +269,15 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         for (int ti = 0; ti < 8; ti++) ra[0][ti] = read_a(aoff, ti);
         // total_steps is even (Kin % 64 == 0): two steps per iteration, one
         // operand set each.  Steps st with st + GS - 1 < total_steps refill
-        // the ring and wait for a fixed count; the last ones do neither.
+        // the ring (when a stage is left) and wait for a fixed count; the last
+        // ones wait for all loads.
         int st = 0;
         for (; st + 1 + GS - 1 < total_steps; st += 2) {
             step(st, 0, false, true);
             step(st + 1, 1, false, true);
         }
         for (; st < total_steps; st += 2) {
-            // every stage is issued by now, except that the pair's first step
-            // may still issue the last one
+            // every stage is issued by now
             step(st, 0, st + GS - 1 >= total_steps, true);
             step(st + 1, 1, true, st + 2 < total_steps);
         }
