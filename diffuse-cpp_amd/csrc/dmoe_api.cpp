@@ -263,7 +263,6 @@ struct Workspace {
     uint16_t *x16, *xs16, *h16, *hs16;   // GEMM-path f16 activations (split: hi / lo rows)
     float *h, *ye, *hs, *ys;
     float *bias;
-    int32_t *counter;                    // zeroed once at allocation; routing leaves it zeroed
 };
 
 // The MFMA expert path covers Q4_K routed experts (and a Q4_K shared expert)
@@ -331,7 +330,6 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         return p;
     };
     Workspace t{};
-    t.counter = (int32_t *)take(4);
     t.x = (float *)take((size_t)N * H * 4);
     t.y = (float *)take((size_t)N * H * 4);
     t.bias = (float *)take((size_t)E * 4);
@@ -412,8 +410,6 @@ int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, Workspace *w)
             return set_err(ctx, DMOE_ERR_OOM, "workspace allocation of %zu bytes refused (DMOE_FAIL_ALLOC)", need);
         HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
         ctx->ws_bytes = need;
-        // the routing counter sits first in every carve-up
-        HIP_TRY(ctx, hipMemset(ctx->ws, 0, 256));
     }
     plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
@@ -502,7 +498,7 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
     }
     STAGE(ST_FRONT, launch_front(L->gate_w, L->gate_bias, x, N, H, E, w.rb, xj, nxj, s));
     // block routing, top-k, gate weights and the dispatch
-    STAGE(ST_ROUTE, launch_route(rp, w.rb, w.wl, w.counter, s));
+    STAGE(ST_ROUTE, launch_route(rp, w.rb, w.wl, s));
     if (mfma) {
         // Q4_K / Q8_0 experts on int8 MFMA: routed experts and the shared one
         // share a launch
@@ -944,7 +940,7 @@ int dmoe_route_logits(dmoe_ctx *ctx, const dmoe_hparams *hp, const float *bias,
         for (int e = 0; e < E; e++)
             if (!(std::fabs(bias[e]) < 1e19f)) rp.bias_small = 0;
     LAUNCH_TRY(ctx, launch_scores(w.rb.logits, dbias, n_tokens, E, w.rb, s));
-    LAUNCH_TRY(ctx, launch_route(rp, w.rb, w.wl, w.counter, s));
+    LAUNCH_TRY(ctx, launch_route(rp, w.rb, w.wl, s));
     dmoe_debug d2 = dbg ? *dbg : dmoe_debug{};
     d2.logits = nullptr;
     if ((rc = copy_debug(ctx, *hp, w, n_tokens, &d2, s))) return rc;

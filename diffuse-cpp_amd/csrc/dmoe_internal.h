@@ -153,10 +153,8 @@ hipError_t launch_cvt_f16(const float *src, int rows, int K, int split, uint16_t
 hipError_t launch_tile_f16(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
                            uint8_t *dst, hipStream_t s);
 
-// Routing + dispatch (k_router.hip).  counter: a zeroed int the last routing
-// group uses to elect itself (left zeroed again).
-hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
-                        int32_t *counter, hipStream_t s);
+// Routing + dispatch (k_router.hip).
+hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl, hipStream_t s);
 bool route_fits_lds(const RouteParams &rp);
 
 // One activation conversion into the MFMA operand layout.

@@ -5,15 +5,17 @@
 //   route    : per routing group (a block of block_size tokens with block
 //              routing, else 32 tokens): block max fold, capacity threshold,
 //              allowed mask, per-token top-k and gate weights (:212-262), the
-//              group's expert histogram and the local rank of its pairs; the
-//              last group to finish then runs the dispatch: counts, offsets,
-//              the stable grouping of (token, slot) pairs by expert (the row
-//              grouping ggml_mul_mat_id performs, :266-269) and the work list
-//              of the expert kernels.
+//              group's expert histogram and the local rank of its pairs
+//   dispatch : counts, offsets, the stable grouping of (token, slot) pairs by
+//              expert (the row grouping ggml_mul_mat_id performs, :266-269)
+//              and the work list of the expert kernels; in the route kernel
+//              itself when the forward is one group, else in one workgroup
+//              launched after it (the launch boundary makes every group's
+//              results visible to it without a device-scope fence per group)
 //
 // Bit-exactness: single IEEE operations in a fixed order (no contraction),
 // order decisions on exact integer keys, counts and ranks without atomics on
-// the results (one atomic counter only elects the group that dispatches).
+// the results.
 #include "dmoe_device.h"
 
 #pragma clang fp contract(off)
@@ -58,9 +60,10 @@ __device__ __forceinline__ int block_scan(int v, int *s_tmp, int *total)
 }
 
 // Counts, offsets and the expert-chunk work list from each thread's pair
-// count c (threads tid < E), all 1024 threads.  s_off receives the offsets.
+// count c (threads tid < E), all 1024 threads.  s_off receives the offsets;
+// the global outputs are written when publish is set.
 __device__ void dispatch_lists(int c, const RouteParams &rp, const RouteBufs &rb,
-                               const WorkList &wl, int *s_tmp, int *s_off)
+                               const WorkList &wl, int *s_tmp, int *s_off, bool publish)
 {
     const int E = rp.n_experts, tid = threadIdx.x;
     int total, nec, off, ecb;
@@ -78,58 +81,146 @@ __device__ void dispatch_lists(int c, const RouteParams &rp, const RouteBufs &rb
         off = block_scan(c, s_tmp, &total);
         ecb = block_scan(nch, s_tmp, &nec);
     }
-    if (tid < E) {
+    if (tid < E) s_off[tid] = off;
+    if (publish && tid < E) {
         rb.counts[tid] = c;
         rb.offsets[tid] = off;
-        s_off[tid] = off;
         for (int k = 0; k < nch; k++) {
             wl.ec_expert[ecb + k] = tid;
             wl.ec_chunk[ecb + k] = k;
         }
     }
-    if (tid == 0) {
+    if (publish && tid == 0) {
         rb.offsets[E] = total;
         wl.n_ec[0] = nec;
     }
     __syncthreads();
 }
 
-// Dispatch of one forward over several routing groups, run by the last group
-// to finish (all 1024 threads), from the groups' histograms and local ranks.
+// Dispatch of one forward over several routing groups, from the groups'
+// histograms (pairs per expert) and the pairs' local ranks, by one workgroup
+// of 1024 threads for the pairs of groups g_lo .. g_hi - 1 (every workgroup
+// derives the offsets from all histograms; the one with publish set writes
+// counts, offsets and the work list).  The groups are taken in chunks of
+// ROUTE_PREF / E: a chunk's histograms are copied to LDS by all threads
+// (eight loads in flight each), scanned over its groups by thread e (the
+// exclusive prefix, carried from chunk to chunk), and the pairs of the
+// workgroup's groups in the chunk are then scattered to their slots, eight per
+// thread at a time.  One chunk holds every group up to ROUTE_PREF / E groups;
+// beyond that the totals take one more pass.
 __device__ void dispatch_all(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
-                             int *s_tmp, int *s_off, int *s_pref)
+                             int *s_tmp, int *s_off, int *s_pref, int g_lo, int g_hi, bool publish)
 {
     const int E = rp.n_experts, K = rp.top_k, N = rp.n_tokens;
     const int G = rp.use_block ? rp.block_size : 32;
     const int ngroups = (N + G - 1) / G;
-    const bool table = ngroups * E <= ROUTE_PREF;
+    const int gchunk = ROUTE_PREF / E;
     const int tid = threadIdx.x;
-    // pairs of expert tid per group; the exclusive prefix over groups goes to
-    // s_pref[g][e] when it fits
-    int c = 0;
-    if (tid < E) {
-        if (table) {
-            for (int g = 0; g < ngroups; g++) {
-                s_pref[g * E + tid] = c;
-                c += rb.hist[(size_t)g * E + tid];
+    auto load_chunk = [&](int gb, int ng) {
+        const int n = ng * E;
+        const int *src = rb.hist + (size_t)gb * E;
+        for (int i0 = 0; i0 < n; i0 += 8 * RT_THREADS) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * RT_THREADS + tid;
+                v[j] = i < n ? src[i] : 0;
             }
-        } else {
-#pragma unroll 8
-            for (int g = 0; g < ngroups; g++) c += rb.hist[(size_t)g * E + tid];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * RT_THREADS + tid;
+                if (i < n) s_pref[i] = v[j];
+            }
         }
+        __syncthreads();
+    };
+    // thread e: s_pref[g][e] <- pairs of expert e in earlier groups (from
+    // *run on), *run advanced past the chunk
+    auto scan_chunk = [&](int ng, int *run) {
+        if (tid >= E) return;
+        int c = *run, g = 0;
+        for (; g + 8 <= ng; g += 8) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = s_pref[(g + j) * E + tid];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                s_pref[(g + j) * E + tid] = c;
+                c += v[j];
+            }
+        }
+        for (; g < ng; g++) {
+            const int v = s_pref[g * E + tid];
+            s_pref[g * E + tid] = c;
+            c += v;
+        }
+        *run = c;
+    };
+
+    int c = 0;                         // pairs of expert tid
+    if (ngroups <= gchunk) {
+        load_chunk(0, ngroups);
+        scan_chunk(ngroups, &c);
+    } else {
+        // totals first: all threads add histogram entries into LDS counters
+        int *s_cnt = s_pref;
+        for (int e = tid; e < E; e += RT_THREADS) s_cnt[e] = 0;
+        __syncthreads();
+        const int n = ngroups * E;
+        for (int i0 = 0; i0 < n; i0 += 8 * RT_THREADS) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * RT_THREADS + tid;
+                v[j] = i < n ? rb.hist[i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * RT_THREADS + tid;
+                if (i < n && v[j]) atomicAdd(&s_cnt[i % E], v[j]);
+            }
+        }
+        __syncthreads();
+        if (tid < E) c = s_cnt[tid];
+        __syncthreads();               // s_pref is reused by the chunks below
     }
-    dispatch_lists(c, rp, rb, wl, s_tmp, s_off);
-    const int P = N * K;
-    for (int p = tid; p < P; p += RT_THREADS) {
-        const int g = (p / K) / G;
-        const int e = rb.idx[p];
-        int base = s_off[e];
-        if (table) {
-            base += s_pref[g * E + e];
-        } else {
-            for (int h = 0; h < g; h++) base += rb.hist[(size_t)h * E + e];
+    dispatch_lists(c, rp, rb, wl, s_tmp, s_off, publish);
+
+    // a pair's group p / (K G) by a float reciprocal, made exact by one
+    // correction each way (pair indices below 2^24)
+    const int KG = K * G;
+    const float rkg = 1.0f / (float)KG;
+    int run = 0;                       // thread e: pairs of expert e before the chunk
+    for (int gb = 0; gb < g_hi; gb += gchunk) {
+        const int ng = min(gchunk, ngroups - gb);
+        if (ngroups > gchunk) {
+            load_chunk(gb, ng);
+            scan_chunk(ng, &run);
         }
-        rb.perm[base + rb.lrank[p]] = p;
+        __syncthreads();
+        // this workgroup's pairs in the chunk: tokens lo * G .. hi * G, K slots each
+        const int lo = max(gb, g_lo), hi = min(gb + ng, g_hi);
+        const int p_lo = lo * KG, p_hi = lo < hi ? min(N, hi * G) * K : p_lo;
+        for (int p0 = p_lo; p0 < p_hi; p0 += 8 * RT_THREADS) {
+            int ev[8], lv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int p = p0 + j * RT_THREADS + tid;
+                ev[j] = p < p_hi ? rb.idx[p] : 0;
+                lv[j] = p < p_hi ? rb.lrank[p] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int p = p0 + j * RT_THREADS + tid;
+                if (p >= p_hi) continue;
+                int q = (int)((float)p * rkg);
+                q -= q * KG > p ? 1 : 0;
+                q += (q + 1) * KG <= p ? 1 : 0;
+                const int g = q - gb, e = ev[j];
+                rb.perm[s_off[e] + s_pref[g * E + e] + lv[j]] = p;
+            }
+        }
+        __syncthreads();               // before the next chunk overwrites s_pref
     }
 }
 
@@ -238,8 +329,7 @@ __device__ __forceinline__ int flag_scan256(int flag, int *s_w4, int *total)
 // SINGLE: the forward is one routing group (the dispatch needs nothing
 // beyond this block; the token probabilities are staged in LDS).
 template <bool SINGLE>
-__global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs rb, WorkList wl,
-                                                      int32_t *counter)
+__global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs rb, WorkList wl)
 {
     __shared__ uint32_t s_key[ROUTE_LDS];         // group scores, then sel' keys
     __shared__ float s_bmax[MAX_E];
@@ -252,7 +342,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     __shared__ int s_tmp[RT_WAVES + 1];
     __shared__ float s_probs[SINGLE ? ROUTE_LDS : 1];   // the group's probs (one group)
     __shared__ float s_thr;
-    __shared__ int s_nan, s_nc, s_last;
+    __shared__ int s_nan, s_nc;
 
     const int E = rp.n_experts, K = rp.top_k, N = rp.n_tokens;
     const int G = rp.use_block ? rp.block_size : 32;
@@ -495,24 +585,30 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     int *s_off = reinterpret_cast<int *>(s_rk);
     if constexpr (SINGLE) {
         // one routing group: the dispatch needs nothing beyond this block
-        dispatch_lists(c, rp, rb, wl, s_tmp, s_off);
+        dispatch_lists(c, rp, rb, wl, s_tmp, s_off, true);
         if (tid < np) rb.perm[s_off[mine] + lr] = tid;
         return;
     } else {
+        // several groups: k_dispatch_groups, the next launch, dispatches them
         if (tid < E) rb.hist[(size_t)g * E + tid] = c;
         if (tid < np) rb.lrank[(size_t)t0 * K + tid] = lr;
-
-        // the last group to finish runs the dispatch
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) s_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
-        __syncthreads();
-        if (!s_last) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        __shared__ int s_pref[ROUTE_PREF];   // dispatch: pairs of earlier groups per expert
-        dispatch_all(rp, rb, wl, s_tmp, s_off, s_pref);
-        if (tid == 0) *counter = 0;
     }
+}
+
+// The dispatch of a forward of several routing groups, after their k_route
+// launch (which leaves hist and lrank for it): workgroup b scatters the pairs
+// of groups DISP_GROUPS b .. DISP_GROUPS (b + 1) - 1, workgroup 0 also writes
+// counts, offsets and the work list.
+constexpr int DISP_GROUPS = 4;
+__global__ __launch_bounds__(RT_THREADS) void k_dispatch_groups(RouteParams rp, RouteBufs rb, WorkList wl)
+{
+    __shared__ int s_tmp[RT_WAVES + 1];
+    __shared__ int s_off[MAX_E];
+    __shared__ int s_pref[ROUTE_PREF];
+    const int G = rp.use_block ? rp.block_size : 32;
+    const int ngroups = (rp.n_tokens + G - 1) / G;
+    const int g_lo = blockIdx.x * DISP_GROUPS, g_hi = min(ngroups, g_lo + DISP_GROUPS);
+    dispatch_all(rp, rb, wl, s_tmp, s_off, s_pref, g_lo, g_hi, blockIdx.x == 0);
 }
 
 // General-shape routing (groups too large for LDS): selection scores are
@@ -640,21 +736,25 @@ __global__ __launch_bounds__(DISP_THREADS) void k_dispatch_general(RouteParams r
 bool route_fits_lds(const RouteParams &rp)
 {
     const int G = rp.use_block ? rp.block_size : 32;
+    // (pair indices below 2^24: the dispatch's float reciprocal is exact there)
     return (size_t)G * rp.n_experts <= ROUTE_LDS && (size_t)G * rp.top_k <= ROUTE_LDS / 8 &&
-           rp.top_k <= MAX_K && rp.n_experts <= RT_THREADS;
+           rp.top_k <= MAX_K && rp.n_experts <= RT_THREADS && (size_t)rp.n_tokens * rp.top_k < (1u << 24);
 }
 
-hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl,
-                        int32_t *counter, hipStream_t s)
+hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl, hipStream_t s)
 {
     const int G = rp.use_block ? rp.block_size : 32;
     const int ngroups = (rp.n_tokens + G - 1) / G;
     if (route_fits_lds(rp)) {
-        if (ngroups == 1)
-            hipLaunchKernelGGL(k_route<true>, dim3(1), dim3(RT_THREADS), 0, s, rp, rb, wl, counter);
-        else
-            hipLaunchKernelGGL(k_route<false>, dim3(ngroups), dim3(RT_THREADS), 0, s, rp, rb, wl,
-                               counter);
+        if (ngroups == 1) {
+            hipLaunchKernelGGL(k_route<true>, dim3(1), dim3(RT_THREADS), 0, s, rp, rb, wl);
+            return hipGetLastError();
+        }
+        hipLaunchKernelGGL(k_route<false>, dim3(ngroups), dim3(RT_THREADS), 0, s, rp, rb, wl);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_dispatch_groups, dim3((ngroups + DISP_GROUPS - 1) / DISP_GROUPS), dim3(RT_THREADS),
+                           0, s, rp, rb, wl);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_route_general, dim3(ngroups), dim3(256), 0, s, rp, rb.logits,

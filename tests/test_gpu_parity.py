@@ -111,6 +111,23 @@ def test_route_logits_flash_shape(ctx, O):
     _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
 
 
+@pytest.mark.parametrize("N", [2304, 4128, 2312], ids=["72groups", "129groups", "73groups_noblock"])
+def test_route_logits_many_groups(ctx, O, N):
+    """More routing groups than one LDS chunk of the dispatch holds (64
+    groups of 256 experts): the histograms are scanned chunk by chunk, the
+    last chunk partial (one group; a partial group without block routing)."""
+    import dmoe
+    _say(f"case: routing from injected logits, 256 experts, N={N}")
+    rng = np.random.default_rng(N)
+    hp = dmoe.hparams_of(4096, 256, 8, 48, 32)
+    logits = (rng.standard_normal((N, 256)) * 1.28).astype(np.float32)
+    bias = rng.uniform(-0.1, 0.1, 256).astype(np.float32)
+    dg = ctx.route_logits(hp, logits, bias)
+    dr = O.route(hp, logits, bias)
+    assert dg["use_block_routing"] == (N % 32 == 0)
+    _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
+
+
 def test_route_logits_ties_and_slack(ctx, O):
     import dmoe
     _say("case: routing ties / slack")
