@@ -62,9 +62,9 @@ constexpr int GROWS_GU = WAVES * 16 * GU_IT;     // gate/up rows of an item: one
 constexpr int GROWS_DN = WAVES * 16 * RT * DN_IT;   // down rows of an item
 constexpr int TILE_BYTES = 16 * Q4K_BYTES;   // one tile x one super-block
 constexpr int WSTEP_BYTES = RT * TILE_BYTES;             // one wave's weights of one step
-constexpr int WPIECES = WSTEP_BYTES / 16;                // 16-byte pieces of a step
-constexpr int WDMA = (WPIECES + 63) / 64;                // LDS-direct loads per step
-static_assert(WSTEP_BYTES % 16 == 0 && Q4K_BYTES == 144, "tile pieces");
+constexpr int TPIECES = TILE_BYTES / 16;                 // 16-byte pieces of a tile (144)
+constexpr int WLOADS = RT * 3;                           // LDS-direct loads per step: 64 + 64 + 16 pieces a tile
+static_assert(TILE_BYTES % 16 == 0 && TPIECES > 128 && TPIECES <= 192, "tile pieces");
 
 __device__ __forceinline__ float h16f(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (uint16_t)u); }
 
@@ -95,6 +95,16 @@ __device__ __forceinline__ void lds_load16(const void *src, const void *lds)
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+}
+
+// The same with the source as a wave-uniform base (an SGPR pair) plus a
+// 32-bit per-lane byte offset (global_load's saddr form): the base advances by
+// scalar adds, the offsets stay fixed, so issuing a step costs no VALU.
+__device__ __forceinline__ void lds_load16_sa(const void *base, uint32_t voff, const void *lds)
+{
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
 }
 
 // s_waitcnt with vmcnt(n), lgkmcnt(0), expcnt untouched (n < 16)
@@ -213,7 +223,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     __shared__ __align__(16) uint8_t s_w[WAVES][WSTAGES][WSTEP_BYTES];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r16 = lane & 15;
     const int N = job.n_tokens, K = job.top_k;
     const int H = job.H, FF = job.FF, SF = job.SF;
@@ -225,15 +235,10 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     const int Kin = DOWN ? FF : H;                   // reduction length (SF == FF when shared)
     const int nsb = Kin / 256;
     const int steps = IT * nsb;
-    // weight load jd of a step: lane's piece p = 64 jd + lane (p < WPIECES) is
-    // piece p % 144 of tile p / 144, copied to slot p of the stage
-    int goff[WDMA], gtile[WDMA];
-#pragma unroll
-    for (int jd = 0; jd < WDMA; jd++) {
-        const int p = min(64 * jd + lane, WPIECES - 1);
-        gtile[jd] = p / 144;
-        goff[jd] = (p % 144) * 16;
-    }
+    // weight loads of a step: tile r's pieces 64 j + lane (j = 0, 1, and 2 for
+    // lanes below TPIECES - 128) from the tile's step run, to slot 64 j + lane
+    // of the tile's place in the stage
+    const uint32_t loff = lane * 16;
     // activation load of this wavefront (wavefronts 0..5): which item row
     // (ar) and piece; 0..3: q units of rows 4w .. 4w+3, 4: bs halves, 5: d
     const int ar = wave < 4 ? 4 * wave + (lane >> 4) : (wave == 4 ? (lane >> 1) & 15 : lane & 15);
@@ -302,15 +307,17 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             if (s >= steps) return;
             const int it = pass_of(s), sb = s - it * nsb;
             const int stg = s % WSTAGES;
-            const uint8_t *t0 = tb[0][0], *t1 = tb[0][1];
 #pragma unroll
-            for (int q = 1; q < IT; q++)
-                if (it == q) { t0 = tb[q][0]; t1 = tb[q][1]; }
+            for (int r = 0; r < RT; r++) {
+                const uint8_t *t = tb[0][r];
 #pragma unroll
-            for (int jd = 0; jd < WDMA; jd++) {
-                const uint8_t *src = (gtile[jd] ? t1 : t0) + (size_t)sb * TILE_BYTES + goff[jd];
-                if (64 * (jd + 1) <= WPIECES || 64 * jd + lane < WPIECES)
-                    lds_load16(src, &s_w[wave][stg][1024 * jd]);
+                for (int q = 1; q < IT; q++)
+                    if (it == q) t = tb[q][r];
+                t += (size_t)sb * TILE_BYTES;
+                const uint8_t *d = &s_w[wave][stg][r * TILE_BYTES];
+                lds_load16_sa(t, loff, d);
+                lds_load16_sa(t, loff + 1024, d + 1024);
+                if (lane < TPIECES - 128) lds_load16_sa(t, loff + 2048, d + 2048);
             }
             if (wave < 4)
                 lds_load16(aq + sb * 256, &s_act[stg][1024 * wave]);
@@ -336,15 +343,15 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
                 for (int i = 0; i < 4; i++) acc[it][r][i] = 0.0f;
         for (int s = 0; s < steps; s++) {
             // step s's loads have landed once the WSTAGES - 2 later steps' are
-            // all that may be in flight (a wavefront issues WDMA loads per step,
+            // all that may be in flight (a wavefront issues WLOADS loads per step,
             // plus one when it loads activations); in the last steps fewer
             // follow: wait for all.  The barrier makes that true of every
             // wavefront and frees the stage read in step s - 1.
             if (s + WSTAGES - 2 < steps) {
                 if (wave < ADMA_WAVES)
-                    EXPERT_WAIT_VM((WDMA + 1) * (WSTAGES - 2));
+                    EXPERT_WAIT_VM((WLOADS + 1) * (WSTAGES - 2));
                 else
-                    EXPERT_WAIT_VM(WDMA * (WSTAGES - 2));
+                    EXPERT_WAIT_VM(WLOADS * (WSTAGES - 2));
             } else {
                 EXPERT_WAIT_VM(0);
             }
