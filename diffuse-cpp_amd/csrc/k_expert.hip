@@ -104,7 +104,15 @@ __device__ __forceinline__ void lds_load16_sa(const void *base, uint32_t voff, c
 {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+    // the base is wave-uniform by construction; readfirstlane makes that
+    // visible to the compiler, so the operand is always an SGPR pair (the
+    // builtin returns a signed int: each half is widened as uint32_t, never
+    // sign-extended)
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    const uint64_t sb = (uint64_t)lo | ((uint64_t)hi << 32);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sb), "s"(m0) : "memory", "m0");
 }
 
 // s_waitcnt with vmcnt(n), lgkmcnt(0), expcnt untouched (n < 16)
