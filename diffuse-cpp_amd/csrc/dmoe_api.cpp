@@ -965,6 +965,29 @@ int dmoe_quantize_device(dmoe_ctx *ctx, int32_t type, const float *src_dev, void
     return DMOE_OK;
 }
 
+int dmoe_residual_rmsnorm(dmoe_ctx *ctx, float *h_dev, const float *y_dev, const float *gain_dev,
+                          float *x_dev, int32_t n_rows, int32_t n_embd, float eps, void *stream)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!h_dev || !x_dev || n_rows < 0 || n_embd <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "residual_rmsnorm: NULL pointer or empty shape");
+    if (n_embd % 4)
+        return set_err(ctx, DMOE_ERR_SHAPE, "residual_rmsnorm: n_embd = %d not a multiple of 4", n_embd);
+    auto misaligned = [](const void *p) { return p && ((uintptr_t)p & 15) != 0; };
+    if (misaligned(h_dev) || misaligned(y_dev) || misaligned(gain_dev) || misaligned(x_dev))
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "residual_rmsnorm: pointers must be 16-byte aligned");
+    const size_t bytes = (size_t)n_rows * n_embd * 4;
+    const uintptr_t h0 = (uintptr_t)h_dev, x0 = (uintptr_t)x_dev;
+    if (n_rows > 0 && h0 < x0 + bytes && x0 < h0 + bytes)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "residual_rmsnorm: h and x overlap");
+    if (!(eps >= 0.0f) || eps > 1.0f)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "residual_rmsnorm: eps = %g outside [0, 1]", (double)eps);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    LAUNCH_TRY(ctx, launch_residual_rmsnorm(h_dev, y_dev, gain_dev, x_dev, n_rows, n_embd, eps,
+                                            (hipStream_t)stream));
+    return DMOE_OK;
+}
+
 int dmoe_profile_enable(dmoe_ctx *ctx, int enable)
 {
     if (!ctx) return DMOE_ERR_INVALID_ARG;

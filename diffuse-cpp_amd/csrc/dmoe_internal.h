@@ -153,6 +153,12 @@ hipError_t launch_cvt_f16(const float *src, int rows, int K, int split, uint16_t
 hipError_t launch_tile_f16(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
                            uint8_t *dst, hipStream_t s);
 
+// Residual add and RMSNorm of the residual stream (k_norm.hip): per row of H
+// floats (H % 4 == 0, 16-byte aligned rows), h += y (y may be null), then
+// x = rms_norm(h, eps) * gain (gain may be null).
+hipError_t launch_residual_rmsnorm(float *h, const float *y, const float *gain, float *x, int rows, int H,
+                                   float eps, hipStream_t s);
+
 // Routing + dispatch (k_router.hip).
 hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl, hipStream_t s);
 bool route_fits_lds(const RouteParams &rp);

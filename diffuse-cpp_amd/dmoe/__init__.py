@@ -29,8 +29,8 @@ LIB_PATH = PKG_DIR / "libdmoe.so"
 EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload",
            "dmoe_layer_wrap_device", "dmoe_layer_free", "dmoe_layer_forward",
            "dmoe_layer_forward_device", "dmoe_route_logits", "dmoe_row_size",
-           "dmoe_quantize_device", "dmoe_profile_enable", "dmoe_profile_read",
-           "dmoe_stage_name")
+           "dmoe_quantize_device", "dmoe_residual_rmsnorm", "dmoe_profile_enable",
+           "dmoe_profile_read", "dmoe_stage_name")
 N_STAGES = 10
 
 
@@ -76,6 +76,7 @@ def load() -> C.CDLL:
     lib.dmoe_row_size.argtypes = [C.c_int32, C.c_int64]
     lib.dmoe_row_size.restype = C.c_size_t
     lib.dmoe_quantize_device.argtypes = [P, C.c_int32, P, P, C.c_int64, C.c_int64, P]
+    lib.dmoe_residual_rmsnorm.argtypes = [P, P, P, P, P, C.c_int32, C.c_int32, C.c_float, P]
     lib.dmoe_profile_enable.argtypes = [P, C.c_int]
     lib.dmoe_profile_read.argtypes = [P, P, P]
     lib.dmoe_stage_name.argtypes = [C.c_int]
@@ -328,6 +329,17 @@ class Context:
         self._check(load().dmoe_profile_read(self.handle, ms.ctypes.data, calls.ctypes.data))
         return {load().dmoe_stage_name(i).decode(): (float(ms[i]), int(calls[i]))
                 for i in range(N_STAGES) if calls[i]}
+
+    def residual_rmsnorm(self, h_dev, y_dev, x_dev, n_rows: int, n_embd: int, eps: float,
+                         gain_dev=None, stream=None):
+        """h += y (y_dev may be None), then x = rms_norm(h, eps) [* gain], on
+        device tensors (src/diffuse-moe-graph.cpp:292, :175-178); queued on
+        `stream` (None: the null stream)."""
+        s = 0 if stream is None else int(stream)
+        self._check(load().dmoe_residual_rmsnorm(
+            self.handle, _ptr(h_dev), _ptr(y_dev) if y_dev is not None else None,
+            _ptr(gain_dev) if gain_dev is not None else None, _ptr(x_dev), n_rows, n_embd,
+            float(eps), s or None))
 
     def quantize_device(self, ttype: int, src_dev, dst_dev, nrows: int, n_per_row: int,
                         stream=None):

@@ -185,6 +185,17 @@ int  dmoe_quantize_device(dmoe_ctx *ctx, int32_t type, const float *src_dev,
                           void *dst_dev, int64_t nrows, int64_t n_per_row,
                           void *stream);
 
+/* The residual stream around the segment, on device pointers: per row of
+ * n_embd floats, h += y (skipped when y is NULL; the segment output added to
+ * the residual, src/diffuse-moe-graph.cpp:292), then x = rms_norm(h, eps),
+ * times gain[n_embd] when gain is not NULL (the next segment's input,
+ * :175-178: ggml_rms_norm then ggml_mul by the norm weight).  h and x must
+ * not overlap; n_embd % 4 == 0 and 16-byte aligned pointers.  Queued on
+ * `stream` without synchronising. */
+int  dmoe_residual_rmsnorm(dmoe_ctx *ctx, float *h_dev, const float *y_dev,
+                           const float *gain_dev, float *x_dev, int32_t n_rows,
+                           int32_t n_embd, float eps, void *stream);
+
 /* Per-stage timing.  While enabled, every forward records a HIP event pair
  * around each pipeline stage on the stream it runs on; dmoe_profile_read
  * waits for the recorded work, adds each stage's elapsed milliseconds and

@@ -232,6 +232,46 @@ def test_error_paths(ctx, O):
     assert ei.value.code == dmoe._abi.ERR_NONFINITE
 
 
+@pytest.mark.parametrize("rows,H,with_y,with_gain", [(32, 4096, True, False), (96, 512, True, True),
+                                                     (7, 4096, False, True)])
+def test_residual_rmsnorm(ctx, rows, H, with_y, with_gain):
+    """h += y, x = rms_norm(h) [* gain] (src/diffuse-moe-graph.cpp:292,
+    :175-178) against ggml_rms_norm's definition evaluated in numpy: the f32
+    squares summed in float64, the mean rounded to f32, scale = 1 / sqrt(mean +
+    eps) in f32.  h is bit-exact (one f32 add per element); x within 2 ulp
+    (the double sum runs in another order than ggml's sequential one, which
+    can move the f32 mean by one ulp)."""
+    import torch
+    import dmoe
+    _say(f"case: residual rmsnorm rows={rows} H={H} y={with_y} gain={with_gain}")
+    rng = np.random.default_rng(rows + H)
+    h0 = (rng.standard_normal((rows, H)) * 3).astype(np.float32)
+    y = rng.standard_normal((rows, H)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    dev = torch.device("cuda:0")
+    hd = torch.from_numpy(h0).to(dev)
+    yd = torch.from_numpy(y).to(dev) if with_y else None
+    gd = torch.from_numpy(g).to(dev) if with_gain else None
+    xd = torch.empty_like(hd)
+    ctx.residual_rmsnorm(hd, yd, xd, rows, H, 1e-6, gain_dev=gd)
+    torch.cuda.synchronize()
+    h_ref = (h0 + y).astype(np.float32) if with_y else h0
+    x_ref = _rmsnorm_np(h_ref)
+    if with_gain:
+        x_ref = (x_ref * g).astype(np.float32)
+    assert np.array_equal(hd.cpu().numpy().view(np.uint32), h_ref.view(np.uint32))
+    x = xd.cpu().numpy()
+    ulp = np.spacing(np.abs(x_ref).astype(np.float32))
+    assert np.all(np.abs(x - x_ref) <= 2 * ulp)
+    # argument checks (before any launch)
+    with pytest.raises(dmoe.DmoeError) as ei:
+        ctx.residual_rmsnorm(hd, yd, hd, rows, H, 1e-6)            # h and x overlap
+    assert ei.value.code == dmoe._abi.ERR_INVALID_ARG
+    with pytest.raises(dmoe.DmoeError) as ei:
+        ctx.residual_rmsnorm(hd, yd, xd, rows, H - 2, 1e-6)        # n_embd % 4
+    assert ei.value.code == dmoe._abi.ERR_SHAPE
+
+
 def test_injected_alloc_failure(O, monkeypatch):
     import dmoe
     from dmoe import synth

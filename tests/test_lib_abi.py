@@ -87,6 +87,7 @@ def test_null_context_is_rejected():
     assert lib.dmoe_layer_forward_device(None, None, None, 32, None, None) == E
     assert lib.dmoe_route_logits(None, C.byref(hp), None, None, 32, None) == E
     assert lib.dmoe_quantize_device(None, 12, None, None, 1, 256, None) == E
+    assert lib.dmoe_residual_rmsnorm(None, None, None, None, None, 32, 4096, 1e-6, None) == E
     assert lib.dmoe_profile_enable(None, 1) == E
     assert lib.dmoe_profile_read(None, None, None) == E
     assert lib.dmoe_last_error(None) == b"null context"
