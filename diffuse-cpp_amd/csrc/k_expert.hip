@@ -253,7 +253,16 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     const int aunit = (lane & 15) ^ (ar & 11);       // q: logical unit of this lane's slot
     const bool aload = wave < 4 || (wave == 4 && lane < 32) || (wave == 5 && lane < 16);
 
-    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    // The pointers of one work item.
+    struct ItemPtrs {
+        const uint8_t *tb[IT][RT];   // this wave's weight tiles of pass it
+        const int8_t *aq;            // the lane's activation load sources
+        const uint16_t *abs_;
+        const float *ad;
+        int t_first, nt, rbase;
+        bool shared;
+    };
+    auto setup = [&](int item, ItemPtrs &P) {
         const bool shared = item >= routed_items;
         const int j = shared ? item - routed_items : item;
         const int rgn = shared ? rg_sh : rg;
@@ -269,16 +278,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             t_first = unit * SHARED_CHUNK;
             nt = min(SHARED_CHUNK, N - t_first);
         }
-        // this wave's weight tiles of pass it: tb[it][r]
-        const uint8_t *tb[IT][RT];
         if (!DOWN) {
             const WTensor &a = shared ? job.sg : job.eg;
             const WTensor &b = shared ? job.su : job.eu;
 #pragma unroll
             for (int it = 0; it < IT; it++) {
                 const int t16 = (rbase + it * (WAVES * 16) + wave * 16) / 16;
-                tb[it][0] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
-                tb[it][1] = b.data + (size_t)e * b.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+                P.tb[it][0] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+                P.tb[it][1] = b.data + (size_t)e * b.nb2 + (size_t)t16 * nsb * TILE_BYTES;
             }
         } else {
             const WTensor &a = shared ? job.sd : job.ed;
@@ -287,7 +294,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
                     const int t16 = (rbase + it * (WAVES * 32) + wave * 32) / 16 + r;
-                    tb[it][r] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+                    P.tb[it][r] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
                 }
         }
         // the activation row of item row ar: tokens in phase 0, pairs in phase
@@ -300,47 +307,76 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             const int p = job.perm[t_first + min(ar, nt - 1)];
             arow = DOWN ? p : p / K;
         }
-        const int8_t *aq = act.q + (size_t)arow * Kin + aunit * 16;
-        const uint16_t *abs_ = act.bs + (size_t)arow * (Kin / 16) + (lane & 1) * 8;
-        const float *ad = act.d + (size_t)arow * nsb;
+        P.aq = act.q + (size_t)arow * Kin + aunit * 16;
+        P.abs_ = act.bs + (size_t)arow * (Kin / 16) + (lane & 1) * 8;
+        P.ad = act.d + (size_t)arow * nsb;
+        P.t_first = t_first;
+        P.nt = nt;
+        P.rbase = rbase;
+        P.shared = shared;
+    };
 
-        // row pass of step s (at most four passes: no division)
-        auto pass_of = [&](int s) -> int {
-            int it = 0;
+    // row pass of step s (at most four passes: no division)
+    auto pass_of = [&](int s) -> int {
+        int it = 0;
 #pragma unroll
-            for (int q = 1; q < IT; q++) it += s >= q * nsb ? 1 : 0;
-            return it;
-        };
-        auto issue = [&](int s) {
-            if (s >= steps) return;
-            const int it = pass_of(s), sb = s - it * nsb;
-            const int stg = s % WSTAGES;
+        for (int q = 1; q < IT; q++) it += s >= q * nsb ? 1 : 0;
+        return it;
+    };
+    // step s of item P to ring stage gstep % WSTAGES
+    auto issue = [&](const ItemPtrs &P, int s, int gstep) {
+        if (s >= steps) return;
+        const int it = pass_of(s), sb = s - it * nsb;
+        const int stg = gstep % WSTAGES;
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
-                const uint8_t *t = tb[0][r];
+        for (int r = 0; r < RT; r++) {
+            const uint8_t *t = P.tb[0][r];
 #pragma unroll
-                for (int q = 1; q < IT; q++)
-                    if (it == q) t = tb[q][r];
-                t += (size_t)sb * TILE_BYTES;
-                const uint8_t *d = &s_w[wave][stg][r * TILE_BYTES];
-                lds_load16_sa(t, loff, d);
-                lds_load16_sa(t, loff + 1024, d + 1024);
-                if (lane < TPIECES - 128) lds_load16_sa(t, loff + 2048, d + 2048);
-            }
-            if (wave < 4)
-                lds_load16(aq + sb * 256, &s_act[stg][1024 * wave]);
-            else if (wave == 4 && aload)
-                lds_load16(abs_ + sb * 16, &s_act[stg][ABS_OFF]);
-            else if (wave == 5 && aload)
-                lds_load4(ad + sb, &s_act[stg][AD_OFF]);
-        };
+            for (int q = 1; q < IT; q++)
+                if (it == q) t = P.tb[q][r];
+            t += (size_t)sb * TILE_BYTES;
+            const uint8_t *d = &s_w[wave][stg][r * TILE_BYTES];
+            lds_load16_sa(t, loff, d);
+            lds_load16_sa(t, loff + 1024, d + 1024);
+            if (lane < TPIECES - 128) lds_load16_sa(t, loff + 2048, d + 2048);
+        }
+        if (wave < 4)
+            lds_load16(P.aq + sb * 256, &s_act[stg][1024 * wave]);
+        else if (wave == 4 && aload)
+            lds_load16(P.abs_ + sb * 16, &s_act[stg][ABS_OFF]);
+        else if (wave == 5 && aload)
+            lds_load4(P.ad + sb, &s_act[stg][AD_OFF]);
+    };
 
-        // the previous item's reads of the rings are done in every wavefront
-        EXPERT_WAIT_VM(0);
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
+    // Down items end with global stores only, so the rings run on from one
+    // item of this workgroup to its next: the last steps of an item issue
+    // the next item's first WSTAGES - 1 steps (ring positions continue), and
+    // the next item starts without draining.  Gate/up items convert h through
+    // the rings after their last step, so each starts from drained rings.
+    constexpr bool XPF = DOWN;
+    ItemPtrs cur, nx;
+    bool primed = false;             // cur's first WSTAGES - 1 steps are issued
+    int g0 = 0;                      // ring position of cur's step 0
+    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+        if (primed)
+            cur = nx;
+        else
+            setup(item, cur);
+        const int nitem = item + gridDim.x;
+        const bool has_next = XPF && steps >= WSTAGES - 1 && nitem < total;
+        if (has_next) setup(nitem, nx);
+        const bool shared = cur.shared;
+        const int t_first = cur.t_first, nt = cur.nt, rbase = cur.rbase;
+
+        if (!primed) {
+            // the previous item's reads of the rings are done in every wavefront
+            g0 = 0;
+            EXPERT_WAIT_VM(0);
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
 #pragma unroll
-        for (int s = 0; s < WSTAGES - 1; s++) issue(s);
+            for (int s = 0; s < WSTAGES - 1; s++) issue(cur, s, s);
+        }
 
         float acc[IT][RT][4];
 #pragma unroll
@@ -352,10 +388,12 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         for (int s = 0; s < steps; s++) {
             // step s's loads have landed once the WSTAGES - 2 later steps' are
             // all that may be in flight (a wavefront issues WLOADS loads per step,
-            // plus one when it loads activations); in the last steps fewer
-            // follow: wait for all.  The barrier makes that true of every
-            // wavefront and frees the stage read in step s - 1.
-            if (s + WSTAGES - 2 < steps) {
+            // plus one when it loads activations; the previous item's output
+            // stores, when they follow, only make this stricter); when fewer
+            // later steps were issued (the item's last steps, no next item
+            // primed): wait for all.  The barrier makes that true of every
+            // wavefront and frees the stage read in the step before.
+            if (s + WSTAGES - 2 < steps || has_next) {
                 if (wave < ADMA_WAVES)
                     EXPERT_WAIT_VM((WLOADS + 1) * (WSTAGES - 2));
                 else
@@ -365,16 +403,22 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             }
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            issue(s + WSTAGES - 1);
+            const int sn = s + WSTAGES - 1;
+            if (sn < steps)
+                issue(cur, sn, g0 + sn);
+            else if (has_next)
+                issue(nx, sn - steps, g0 + sn);
             const int it = pass_of(s);
-            const int stg = s % WSTAGES;
-            Q4KTile cur[RT];
+            const int stg = (g0 + s) % WSTAGES;
+            Q4KTile cur_t[RT];
 #pragma unroll
-            for (int r = 0; r < RT; r++) read_tile(cur[r], &s_w[wave][stg][r * TILE_BYTES], r16, g);
+            for (int r = 0; r < RT; r++) read_tile(cur_t[r], &s_w[wave][stg][r * TILE_BYTES], r16, g);
 #pragma unroll
             for (int q = 0; q < IT; q++)
-                if (it == q) compute_sb(cur, s_act[stg], r16, g, acc[q]);
+                if (it == q) compute_sb(cur_t, s_act[stg], r16, g, acc[q]);
         }
+        primed = has_next;
+        g0 += steps;
 
         if (!DOWN) {
             // h = silu(gate) * up for the item's activation rows and its 256
@@ -451,10 +495,24 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s)
         job.ax.K != job.H || job.ah.K != job.FF ||
         (job.has_shared && (job.SF != job.FF || job.ahs.K != job.SF)))
         return hipErrorInvalidValue;
-    if (phase == 0)
+    if (phase == 0) {
         hipLaunchKernelGGL(k_expert_q4k<0>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
-    else
-        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
+    } else {
+        // one workgroup per compute unit (one fits at a time), so that each
+        // runs its items back to back with the rings running on between them
+        static int n_cu[64] = {0};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+        if (n_cu[dev] <= 0) {
+            int n = 0;
+            e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+            if (e != hipSuccess) return e;
+            n_cu[dev] = n > 0 ? n : DMOE_X_BLOCKS;
+        }
+        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(n_cu[dev]), dim3(WAVES * 64), 0, s, job);
+    }
     return hipGetLastError();
 }
 
