@@ -227,7 +227,7 @@ __device__ void logits_tile_small(const float *__restrict__ W, const float *__re
             asm volatile("" ::: "memory");
         }
         // at most the 2 * NK expert-row loads still in flight
-        __builtin_amdgcn_s_waitcnt((2 * NK) & 15 | (((2 * NK) >> 4) << 14) | 0xF70);
+        __builtin_amdgcn_s_waitcnt(((2 * NK) & 15) | (((2 * NK) >> 4) << 14) | 0xF70);
         __syncthreads();
 
         {
