@@ -369,12 +369,16 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         }
     }
     if (gemm) {
-        t.x16 = (uint16_t *)take((size_t)N * H * 2);
-        t.h16 = (uint16_t *)take((size_t)P * FF * 2);
+        // with a shared expert, the hi rows of its split x (f16(x)) are the
+        // routed experts' f16 x as well: no separate copy
         if (shared) {
             t.xs16 = (uint16_t *)take((size_t)2 * N * H * 2);
             t.hs16 = (uint16_t *)take((size_t)2 * N * SF * 2);
+            t.x16 = t.xs16;
+        } else {
+            t.x16 = (uint16_t *)take((size_t)N * H * 2);
         }
+        t.h16 = (uint16_t *)take((size_t)P * FF * 2);
     }
     t.xq.type = at;
     t.xq.n = H;
@@ -559,8 +563,12 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.hs16 = w.hs16;
         job.ye = w.ye;
         job.ys = w.ys;
-        STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 0, w.x16, s));
-        if (L->has_shared) STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 1, w.xs16, s));
+        // one conversion: f16(x), or with a shared expert its (hi, lo) pair,
+        // whose hi rows are x16
+        if (L->has_shared)
+            STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 1, w.xs16, s));
+        else
+            STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 0, w.x16, s));
         STAGE(ST_GATEUP, launch_gemm_f16(0, job, s));
         STAGE(ST_DOWN, launch_gemm_f16(1, job, s));
         STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
