@@ -1,7 +1,7 @@
 /*
  * dmoe_oracle.h — CPU oracle for the LLaDA2 block-routed MoE layer.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the smoke
+ * TEST INFRASTRUCTURE ONLY.  The parity tests compare against it: tests/, the smoke
  * entry and the CPU-baseline leg of bench.py may load it; the product library
  * (libdmoe.so) never links, loads or calls it.
  *

@@ -1,7 +1,7 @@
 """Shared test set-up.
 
 Markers: `gpu` — needs an MI355X (HIP device 0); everything else runs on the
-CPU.  The CPU oracle (oracle/) is the checker for every parity test.
+CPU.  Every parity test compares against the CPU oracle (oracle/).
 """
 import sys
 from pathlib import Path
