@@ -71,6 +71,26 @@ def test_small_layer(ctx, O, wtype, n_tokens):
     assert err <= TOL[wtype]
 
 
+def test_small_layer_many_items(ctx, O):
+    """Q4_K at moe_ff 256 over 2048 tokens: down items of two steps (the
+    fewest the LDS rings can run on across) and several items per workgroup,
+    so each item's first steps are issued by the previous item's."""
+    import dmoe
+    from dmoe import synth
+    n_tokens = 2048
+    _say(f"case: small layer Q4_K N={n_tokens}, many down items per workgroup")
+    cfg = _small(dmoe, synth, 12, n_tokens)
+    w = synth.host_layer(cfg, 31, O.quantize_rows)
+    x = synth.make_x(cfg, 31, n_tokens)
+    layer = ctx.upload(w)
+    y, dg = ctx.forward(layer, x, debug=True)
+    yr, dr = O.layer_forward(w, x, debug=True)
+    _check_routing(dg, dr)
+    err = max_rel_err(y, yr)
+    _say(f"  max rel err {err:.3e}")
+    assert err <= TOL[12]
+
+
 @pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "prefill_f16"])
 def test_flash_layer(ctx, O, name):
     """Flash-shaped layers: one 32-token block (Q4_K, Q8_0), eight blocks
