@@ -71,15 +71,18 @@ def test_small_layer(ctx, O, wtype, n_tokens):
     assert err <= TOL[wtype]
 
 
-def test_small_layer_many_items(ctx, O):
-    """Q4_K at moe_ff 256 over 2048 tokens: down items of two steps (the
-    fewest the LDS rings can run on across) and several items per workgroup,
-    so each item's first steps are issued by the previous item's."""
+@pytest.mark.parametrize("wtype", [12, 8, 1], ids=["Q4_K", "Q8_0", "F16"])
+def test_small_layer_many_items(ctx, O, wtype):
+    """Layers of moe_ff 256 over 2048 tokens.  Q4_K: down items of two steps
+    (the fewest the LDS rings can run on across) and several items per
+    workgroup, so each item's first steps are issued by the previous item's.
+    Q8_0: more items than the persistent grid.  F16: the grouped GEMM with
+    8 and 16 k steps per item, so its ring's first and last steps overlap."""
     import dmoe
     from dmoe import synth
     n_tokens = 2048
-    _say(f"case: small layer Q4_K N={n_tokens}, many down items per workgroup")
-    cfg = _small(dmoe, synth, 12, n_tokens)
+    _say(f"case: small layer type={wtype} N={n_tokens}, many items per workgroup")
+    cfg = _small(dmoe, synth, wtype, n_tokens)
     w = synth.host_layer(cfg, 31, O.quantize_rows)
     x = synth.make_x(cfg, 31, n_tokens)
     layer = ctx.upload(w)
@@ -88,7 +91,7 @@ def test_small_layer_many_items(ctx, O):
     _check_routing(dg, dr)
     err = max_rel_err(y, yr)
     _say(f"  max rel err {err:.3e}")
-    assert err <= TOL[12]
+    assert err <= TOL[wtype]
 
 
 @pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "prefill_f16"])
