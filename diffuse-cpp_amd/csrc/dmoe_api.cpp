@@ -37,7 +37,8 @@ struct dmoe_ctx {
 };
 
 struct dmoe_layer {
-    dmoe_ctx *ctx = nullptr;
+    dmoe_ctx *ctx = nullptr;       // creating context (not used by dmoe_layer_free)
+    int device = 0;                // HIP device holding the layer's buffers
     dmoe_hparams hp{};
     float *gate_w = nullptr;       // [E][H] f32
     float *gate_bias = nullptr;    // [E] or null
@@ -312,8 +313,10 @@ ActI8 take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bo
     return a;
 }
 
+// host_io: room for x and y (the host-buffer forward copies them through HBM).
+// Buffers only one kernel family reads are planned only for that family.
 size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N,
-                      uint8_t *base, Workspace *w)
+                      bool host_io, uint8_t *base, Workspace *w)
 {
     const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
     const int SF = shared ? hp.shared_ff : 0;
@@ -330,8 +333,10 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         return p;
     };
     Workspace t{};
-    t.x = (float *)take((size_t)N * H * 4);
-    t.y = (float *)take((size_t)N * H * 4);
+    if (host_io) {
+        t.x = (float *)take((size_t)N * H * 4);
+        t.y = (float *)take((size_t)N * H * 4);
+    }
     t.bias = (float *)take((size_t)E * 4);
     t.rb.logits = (float *)take((size_t)N * E * 4);
     t.rb.probs = (float *)take((size_t)N * E * 4);
@@ -347,6 +352,8 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
     t.rb.hist = (int32_t *)take((size_t)groups * E * 4);
     t.rb.lrank = (int32_t *)take((size_t)P * 4);
     const bool gemm = use_gemm_path(hp, wtype, stype, shared);
+    const bool gemv = !gemm && !use_mfma_path(hp, wtype, stype, shared) &&
+                      !use_q80_path(hp, wtype, stype, shared);
     t.wl.chunk = gemm ? GM : EXPERT_CHUNK;
     t.wl.n_ec = (int32_t *)take(4);
     t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
@@ -380,28 +387,31 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         }
         t.h16 = (uint16_t *)take((size_t)P * FF * 2);
     }
-    t.xq.type = at;
-    t.xq.n = H;
-    t.xq.vals = take((size_t)N * act_row_vals_bytes(at, H));
-    t.xq.d = (float *)take((size_t)N * (H / 32) * 4);
-    t.xq.bsums = (int16_t *)take((size_t)N * (H / 16) * 2);
-    t.h = (float *)take((size_t)P * FF * 4);
-    t.hq.type = at;
-    t.hq.n = FF;
-    t.hq.vals = take((size_t)P * act_row_vals_bytes(at, FF));
-    t.hq.d = (float *)take((size_t)P * (FF / 32 + 1) * 4);
-    t.hq.bsums = (int16_t *)take((size_t)P * (FF / 16 + 1) * 2);
+    if (gemv) {
+        // activations of the GEMV kernels (k_gemv.hip) and their f32 h
+        t.xq.type = at;
+        t.xq.n = H;
+        t.xq.vals = take((size_t)N * act_row_vals_bytes(at, H));
+        t.xq.d = (float *)take((size_t)N * (H / 32) * 4);
+        t.xq.bsums = (int16_t *)take((size_t)N * (H / 16) * 2);
+        t.h = (float *)take((size_t)P * FF * 4);
+        t.hq.type = at;
+        t.hq.n = FF;
+        t.hq.vals = take((size_t)P * act_row_vals_bytes(at, FF));
+        t.hq.d = (float *)take((size_t)P * (FF / 32 + 1) * 4);
+        t.hq.bsums = (int16_t *)take((size_t)P * (FF / 16 + 1) * 2);
+        t.hs = (float *)take((size_t)N * (SF > 0 ? SF : 1) * 4);
+    }
     t.ye = (float *)take((size_t)P * H * 4);
-    t.hs = (float *)take((size_t)N * (SF > 0 ? SF : 1) * 4);
     t.ys = (float *)take((size_t)N * H * 4);
     if (w) *w = t;
     return off;
 }
 
-int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, Workspace *w)
+int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, Workspace *w)
 {
     const size_t need =
-        plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, nullptr, nullptr);
+        plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, host_io, nullptr, nullptr);
     if (need > ctx->ws_bytes) {
         if (ctx->ws) {
             // work queued on any stream may still read the old workspace
@@ -415,7 +425,7 @@ int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, Workspace *w)
         HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
         ctx->ws_bytes = need;
     }
-    plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, (uint8_t *)ctx->ws, w);
+    plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, host_io, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
 }
 
@@ -792,6 +802,7 @@ int dmoe_layer_upload(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_layer_de
     dmoe_layer *L = new (std::nothrow) dmoe_layer();
     if (!L) return set_err(ctx, DMOE_ERR_OOM, "host allocation failed");
     L->ctx = ctx;
+    L->device = ctx->device;
     const int H = hp->n_embd, E = hp->n_experts, FF = hp->moe_ff;
     auto fail = [&](int code) {
         dmoe_layer_free(L);
@@ -849,6 +860,7 @@ int dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_lay
     dmoe_layer *L = new (std::nothrow) dmoe_layer();
     if (!L) return set_err(ctx, DMOE_ERR_OOM, "host allocation failed");
     L->ctx = ctx;
+    L->device = ctx->device;
     L->gate_w = (float *)d->gate_w.data;
     L->gate_bias = (float *)d->gate_bias.data;
     L->eg = wrap_tensor(d->exp_gate);
@@ -870,9 +882,20 @@ int dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_lay
 void dmoe_layer_free(dmoe_layer *L)
 {
     if (!L) return;
-    if (L->ctx) (void)hipSetDevice(L->ctx->device);
+    // the layer keeps its own device id: freeing it after its context was
+    // destroyed touches nothing of the context
+    (void)hipSetDevice(L->device);
     for (void *p : L->owned) (void)hipFree(p);
     delete L;
+}
+
+int dmoe_layer_kernel_path(const dmoe_layer *L)
+{
+    if (!L) return -1;
+    if (use_mfma_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q4K_MFMA;
+    if (use_q80_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q80_MFMA;
+    if (use_gemm_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_F16_GEMM;
+    return DMOE_PATH_GEMV;
 }
 
 int dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *x, int32_t n_tokens,
@@ -887,7 +910,7 @@ int dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *x, int32
             return set_err(ctx, DMOE_ERR_NONFINITE, "x[%zu] = %g is not finite", i, (double)x[i]);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     Workspace w;
-    int rc = ensure_workspace(ctx, L, n_tokens, &w);
+    int rc = ensure_workspace(ctx, L, n_tokens, true, &w);
     if (rc) return rc;
     hipStream_t s = ctx->stream;
     HIP_TRY(ctx, hipMemcpyAsync(w.x, x, (size_t)n_tokens * H * 4, hipMemcpyHostToDevice, s));
@@ -908,7 +931,7 @@ int dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *x
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "x_dev must be 16-byte aligned");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     Workspace w;
-    int rc = ensure_workspace(ctx, L, n_tokens, &w);
+    int rc = ensure_workspace(ctx, L, n_tokens, false, &w);
     if (rc) return rc;
     return enqueue_forward(ctx, L, w, x_dev, n_tokens, y_dev, (hipStream_t)stream);
 }
@@ -931,7 +954,7 @@ int dmoe_route_logits(dmoe_ctx *ctx, const dmoe_hparams *hp, const float *bias,
     L.hp.moe_ff = 32;
     L.eg.type = DMOE_TYPE_F32;
     Workspace w;
-    int rc = ensure_workspace(ctx, &L, n_tokens, &w);
+    int rc = ensure_workspace(ctx, &L, n_tokens, false, &w);
     if (rc) return rc;
     hipStream_t s = ctx->stream;
     HIP_TRY(ctx, hipMemcpyAsync(w.rb.logits, logits, (size_t)n_tokens * E * 4,

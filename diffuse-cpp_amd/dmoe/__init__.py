@@ -30,8 +30,9 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_layer_wrap_device", "dmoe_layer_free", "dmoe_layer_forward",
            "dmoe_layer_forward_device", "dmoe_route_logits", "dmoe_row_size",
            "dmoe_quantize_device", "dmoe_residual_rmsnorm", "dmoe_profile_enable",
-           "dmoe_profile_read", "dmoe_stage_name")
+           "dmoe_profile_read", "dmoe_stage_name", "dmoe_layer_kernel_path")
 N_STAGES = 10
+PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}
 
 
 class DmoeError(RuntimeError):
@@ -70,6 +71,7 @@ def load() -> C.CDLL:
                                            C.POINTER(P)]
     lib.dmoe_layer_free.argtypes = [P]
     lib.dmoe_layer_free.restype = None
+    lib.dmoe_layer_kernel_path.argtypes = [P]
     lib.dmoe_layer_forward.argtypes = [P, P, P, C.c_int32, P, C.POINTER(Debug)]
     lib.dmoe_layer_forward_device.argtypes = [P, P, P, C.c_int32, P, P]
     lib.dmoe_route_logits.argtypes = [P, C.POINTER(HParams), P, P, C.c_int32, C.POINTER(Debug)]
@@ -236,6 +238,10 @@ class Layer:
     def __init__(self, ctx: "Context", handle: int, weights: LayerWeights):
         self.ctx, self.handle, self.weights = ctx, handle, weights
         self.hp = weights.hparams()
+
+    def kernel_path(self) -> str:
+        """Expert kernels this layer runs (dmoe_layer_kernel_path)."""
+        return PATH_NAMES[load().dmoe_layer_kernel_path(self.handle)]
 
     def free(self):
         if self.handle:

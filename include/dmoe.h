@@ -147,7 +147,26 @@ int  dmoe_layer_upload(dmoe_ctx *ctx, const dmoe_hparams *hp,
 int  dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp,
                             const dmoe_layer_desc *desc, dmoe_layer **out);
 
+/* Release a layer's device buffers.  The layer records its own device, so it
+ * may be freed before or after the context that created it. */
 void dmoe_layer_free(dmoe_layer *layer);
+
+/* Which expert kernels a layer's forward runs, chosen at upload from the
+ * weight types and shapes (a diagnostic without a counterpart in the
+ * reference, whose expert products all run in ggml_mul_mat_id,
+ * src/diffuse-moe-graph.cpp:266-269 and :282-285):
+ *   DMOE_PATH_Q4K_MFMA  Q4_K routed + shared experts on int8 MFMA tiles
+ *   DMOE_PATH_Q80_MFMA  Q8_0 routed + shared experts on int8 MFMA tiles
+ *   DMOE_PATH_F16_GEMM  F16 experts on the f16 MFMA grouped GEMM
+ *   DMOE_PATH_GEMV      every other type / shape mix (F32 experts; widths
+ *                       that are not whole MFMA work items; a shared expert
+ *                       whose type or width differs from the routed ones)
+ * Returns -1 for a NULL layer. */
+#define DMOE_PATH_GEMV      0
+#define DMOE_PATH_Q4K_MFMA  1
+#define DMOE_PATH_Q80_MFMA  2
+#define DMOE_PATH_F16_GEMM  3
+int  dmoe_layer_kernel_path(const dmoe_layer *layer);
 
 /* moe_out = MoE(x) for host buffers x, y of n_tokens*n_embd floats.
  * Synchronous.  Replaces src/diffuse-moe-graph.cpp:188-289 (`cur` in,

@@ -4,8 +4,11 @@ Bar (tolerances written here, per the layer contract):
   * routing — logits, probs, block max, threshold, allowed set, top-k indices,
     gate weights, per-expert counts/offsets and the dispatch permutation — is
     bit-exact on identical fp32 inputs;
-  * layer output: max|y - y_oracle| / max|y_oracle| <= 2e-2 for quantised
-    expert weights (Q8_0, Q4_K), <= 1e-3 for F16, <= 1e-4 for F32.
+  * layer output: max|y - y_oracle| / max|y_oracle| <= 3e-3 for one layer
+    with quantised expert weights (Q8_0, Q4_K; the layer contract allows
+    2e-2, the worst measured is 8.7e-4, so the bar sits at about 3x that to
+    catch a lost term), <= 1e-3 for F16, <= 1e-4 for F32; the 32-layer chain's
+    accumulated error is held to the contract's 2e-2.
 """
 import numpy as np
 import pytest
@@ -14,7 +17,8 @@ from conftest import max_rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = {0: 1e-4, 1: 1e-3, 8: 2e-2, 12: 2e-2}
+TOL = {0: 1e-4, 1: 1e-3, 8: 3e-3, 12: 3e-3}
+TOL_CHAIN = 2e-2
 ROUTE_KEYS = ("logits", "probs", "bmax", "thr", "allowed", "idx", "weights", "counts",
               "offsets", "perm", "use_block_routing")
 
@@ -164,6 +168,132 @@ def test_route_logits_ties_and_slack(ctx, O):
         dr = O.route(hp, logits, bias)
         _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
         assert dg["allowed"].sum(1).min() >= 8
+
+
+def _slack_bias(E, cap):
+    """Selection-score bias that puts, with all logits 0 (probs 0.5), cap
+    experts at block max 0.6, one expert just inside the 1e-6 slack below
+    the threshold (admitted), one exactly at fl(thr - 1e-6) (rejected: the
+    test is strict, src/diffuse-moe-graph.cpp:241-242) and one just outside
+    the slack; the rest far below.  Same construction as the oracle's
+    slack test."""
+    bias = np.full(E, -0.2, np.float32)
+    bias[:cap] = 0.1
+    tp = np.float32(np.float32(0.6) + np.float32(-1e-6))
+    bias[cap] = np.float32(np.float32(0.6) - np.float32(4e-7)) - np.float32(0.5)
+    bias[cap + 1] = tp - np.float32(0.5)
+    bias[cap + 2] = np.float32(0.6 - 3e-6) - np.float32(0.5)
+    return bias
+
+
+@pytest.mark.parametrize("E,K,cap,N", [(16, 2, 4, 32), (256, 8, 48, 64), (256, 8, 48, 32)],
+                         ids=["E16_one_block", "flash_two_blocks", "flash_one_block"])
+def test_route_logits_slack_boundary(ctx, O, E, K, cap, N):
+    """The capacity test admits a block max inside fl(thr - 1e-6) and rejects
+    one exactly at it: the allowed set holds cap + 1 experts, bit for bit
+    with the oracle (one-group and many-group routing kernels)."""
+    import dmoe
+    _say(f"case: routing slack boundary E={E} K={K} cap={cap} N={N}")
+    hp = dmoe.hparams_of(4096 if E == 256 else 256, E, K, cap, 32)
+    logits = np.zeros((N, E), np.float32)
+    bias = _slack_bias(E, cap)
+    dg = ctx.route_logits(hp, logits, bias)
+    dr = O.route(hp, logits, bias)
+    assert np.all(dr["thr"] == np.float32(0.6))
+    al = dg["allowed"].astype(bool)
+    assert al[:, :cap].all() and al[:, cap].all()
+    assert not al[:, cap + 1].any() and not al[:, cap + 2].any()
+    assert (al.sum(1) == cap + 1).all()
+    _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
+
+
+@pytest.mark.parametrize("cap", [256, 300], ids=["cap_eq_E", "cap_gt_E"])
+def test_route_logits_capacity_at_least_experts(ctx, O, cap):
+    """capacity >= n_experts switches block routing off (plain top-k over all
+    experts, src/diffuse-moe-graph.cpp:215-216)."""
+    import dmoe
+    _say(f"case: routing with capacity {cap} >= 256 experts")
+    rng = np.random.default_rng(cap)
+    hp = dmoe.hparams_of(4096, 256, 8, cap, 32)
+    N = 64
+    logits = (rng.standard_normal((N, 256)) * 1.28).astype(np.float32)
+    bias = rng.uniform(-0.1, 0.1, 256).astype(np.float32)
+    dg = ctx.route_logits(hp, logits, bias)
+    dr = O.route(hp, logits, bias)
+    assert not dg["use_block_routing"] and not dr["use_block_routing"]
+    _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
+
+
+@pytest.mark.parametrize("E,blk,K,cap,N", [(256, 64, 8, 48, 128), (512, 32, 8, 48, 64),
+                                           (64, 64, 20, 40, 128)],
+                         ids=["blk64_E256", "E512", "blk64_K20"])
+def test_route_logits_general_kernel(ctx, O, E, blk, K, cap, N):
+    """Routing groups too large for the LDS kernels (block_size x E above 8192
+    scores, or top_k x block above 1024 pairs) take k_route_general and
+    k_dispatch_general: bit-exact with the oracle, including the slack
+    boundary on the first group."""
+    import dmoe
+    _say(f"case: general routing kernel E={E} blk={blk} K={K} cap={cap} N={N}")
+    rng = np.random.default_rng(E + blk + K)
+    hp = dmoe.hparams_of(4096, E, K, cap, blk)
+    logits = (rng.standard_normal((N, E)) * 1.28).astype(np.float32)
+    bias = rng.uniform(-0.1, 0.1, E).astype(np.float32)
+    dg = ctx.route_logits(hp, logits, bias)
+    dr = O.route(hp, logits, bias)
+    assert dg["use_block_routing"]
+    _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
+    logits[:blk] = 0.0
+    bias = _slack_bias(E, cap)
+    dg = ctx.route_logits(hp, logits, bias)
+    dr = O.route(hp, logits, bias)
+    assert dg["allowed"][0].sum() == cap + 1
+    _check_routing(dg, dr, [k for k in ROUTE_KEYS if k != "logits"])
+
+
+# Layers whose types or widths the MFMA kernels do not take run the GEMV
+# kernels (k_gemv.hip); each case reaches one of its quantised instantiations.
+_GEMV_CASES = {
+    # n_embd 768: not a whole number of 512-row down items
+    "q4k_h768": (768, 256, 256, 12, 12),
+    # shared expert twice as wide as the routed ones
+    "q4k_wide_shared": (512, 256, 512, 12, 12),
+    # Q4_K routed experts with a Q8_0 shared expert
+    "q4k_q80_shared": (512, 256, 256, 12, 8),
+    # moe_ff 96: not a whole number of 256-value steps
+    "q80_ff96": (512, 96, 96, 8, 8),
+    # F16 routed experts with an F32 shared expert
+    "f16_f32_shared": (512, 256, 256, 1, 0),
+}
+
+
+@pytest.mark.parametrize("case", list(_GEMV_CASES))
+def test_gemv_path_layer(ctx, O, case):
+    from dmoe import synth
+    H, FF, SF, wt, st = _GEMV_CASES[case]
+    N = 64
+    _say(f"case: GEMV path {case}: H={H} moe_ff={FF} shared_ff={SF} types {wt}/{st}, N={N}")
+    cfg = synth.LayerConfig(case, H, 32, FF, 8, 4, 32, SF, wt, st, N, -0.05, 0.05)
+    w = synth.host_layer(cfg, 41, O.quantize_rows)
+    x = synth.make_x(cfg, 41, N)
+    layer = ctx.upload(w)
+    assert layer.kernel_path() == "gemv"
+    y, dg = ctx.forward(layer, x, debug=True)
+    yr, dr = O.layer_forward(w, x, debug=True)
+    _check_routing(dg, dr)
+    err = max_rel_err(y, yr)
+    _say(f"  max rel err {err:.3e}")
+    assert err <= max(TOL[wt], TOL[st])
+
+
+def test_mfma_paths_selected(ctx, O):
+    """The shapes of the flash layer take the MFMA kernels for each type."""
+    from dmoe import synth
+    _say("case: kernel path of the small layers")
+    for wt, name in ((12, "q4k_mfma"), (8, "q80_mfma"), (1, "f16_gemm"), (0, "gemv")):
+        cfg = _small(None, synth, wt, 32)
+        layer = ctx.upload(synth.host_layer(cfg, 2, O.quantize_rows))
+        assert layer.kernel_path() == name, (wt, layer.kernel_path())
+        layer.free()
 
 
 def test_sigmoid_sweep(ctx, O):
@@ -368,4 +498,4 @@ def test_stack32_chain(ctx, O):
     _say(f"  per-layer max rel err {worst:.3e}; final hidden state {final:.3e}; "
          f"independent CPU chain: first routing difference at layer {split_at}, "
          f"final difference {indep:.3e}")
-    assert final <= TOL[cfg.wtype]
+    assert final <= TOL_CHAIN

@@ -93,6 +93,7 @@ def test_null_context_is_rejected():
     assert lib.dmoe_last_error(None) == b"null context"
     lib.dmoe_destroy(None)
     lib.dmoe_layer_free(None)
+    assert lib.dmoe_layer_kernel_path(None) == -1
     names = [lib.dmoe_stage_name(i).decode() for i in range(dmoe.N_STAGES)]
     assert names[0] == "front" and "gateup_routed" in names
     assert lib.dmoe_stage_name(99) == b""
