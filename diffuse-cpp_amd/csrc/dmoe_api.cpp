@@ -14,6 +14,7 @@
 #include <cstring>
 #include <algorithm>
 #include <functional>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -25,6 +26,8 @@ using namespace dmoe;
 struct dmoe_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    // device address of this GPU's `scratch` array (the allocation-free forward)
+    uint8_t *scratch = nullptr;
     std::string err;
     // workspace, grown on demand
     void *ws = nullptr;
@@ -49,7 +52,32 @@ struct dmoe_layer {
     std::vector<void *> owned;
 };
 
+// Workspace of dmoe_layer_forward_device_noalloc: a fixed array in device
+// memory.  Every GPU the library runs on holds its own copy, at its own
+// address, until the process ends.  In host code `scratch` is only a handle
+// for hipGetSymbolAddress; kernels and copies take the per-device address.
+static __device__ __align__(256) uint8_t scratch[DMOE_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 256;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_addr[kMaxDevices];   // device address of `scratch`, per HIP device
+
+// Resolves this GPU's address of `scratch` once per device; the device must
+// be current.  Returns the hipGetSymbolAddress status.
+hipError_t scratch_address(int device, uint8_t **out)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_addr[device] = (uint8_t *)p;
+    }
+    *out = g_scratch_addr[device];
+    return hipSuccess;
+}
 
 int set_err(dmoe_ctx *ctx, int code, const char *fmt, ...)
 {
@@ -468,9 +496,9 @@ hipEvent_t take_event(dmoe_ctx *ctx)
 
 // Runs one stage; with profiling on, brackets it with an event pair.
 template <class F>
-hipError_t stage(dmoe_ctx *ctx, int id, hipStream_t s, F &&launch)
+hipError_t stage(dmoe_ctx *ctx, bool prof, int id, hipStream_t s, F &&launch)
 {
-    if (!ctx->prof) return launch();
+    if (!prof) return launch();
     hipEvent_t a = take_event(ctx), b = take_event(ctx);
     if (!a || !b) return hipErrorOutOfMemory;
     hipError_t e = hipEventRecord(a, s);
@@ -487,8 +515,10 @@ hipError_t stage(dmoe_ctx *ctx, int id, hipStream_t s, F &&launch)
             return set_err((ctx), DMOE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));           \
     } while (0)
 
+// prof: bracket the stages with timing events (which may create events; the
+// allocation-free forward passes false).
 int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, const float *x,
-                    int N, float *y, hipStream_t s)
+                    int N, float *y, hipStream_t s, bool prof)
 {
     const dmoe_hparams &hp = L->hp;
     const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
@@ -502,7 +532,7 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
     auto expert = [&](int phase, const MoeJob &j) {
         return q8 ? launch_expert_q80(phase, j, s) : launch_expert_q4k(phase, j, s);
     };
-#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, id, s, [&] { return call; }))
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
     // router logits, sigmoid, selection scores (+ x in the MFMA operand layout)
     PrepJob xj[2];
     int nxj = 0;
@@ -757,7 +787,8 @@ int dmoe_create(int hip_device, dmoe_ctx **out)
     dmoe_ctx *ctx = new (std::nothrow) dmoe_ctx();
     if (!ctx) return DMOE_ERR_OOM;
     ctx->device = hip_device;
-    if (hipSetDevice(hip_device) != hipSuccess ||
+    if (hip_device >= kMaxDevices || hipSetDevice(hip_device) != hipSuccess ||
+        scratch_address(hip_device, &ctx->scratch) != hipSuccess ||
         hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return DMOE_ERR_HIP;
@@ -914,7 +945,7 @@ int dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *x, int32
     if (rc) return rc;
     hipStream_t s = ctx->stream;
     HIP_TRY(ctx, hipMemcpyAsync(w.x, x, (size_t)n_tokens * H * 4, hipMemcpyHostToDevice, s));
-    if ((rc = enqueue_forward(ctx, L, w, w.x, n_tokens, w.y, s))) return rc;
+    if ((rc = enqueue_forward(ctx, L, w, w.x, n_tokens, w.y, s, ctx->prof))) return rc;
     HIP_TRY(ctx, hipMemcpyAsync(y, w.y, (size_t)n_tokens * H * 4, hipMemcpyDeviceToHost, s));
     if ((rc = copy_debug(ctx, L->hp, w, n_tokens, dbg, s))) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(s));
@@ -933,7 +964,35 @@ int dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *x
     Workspace w;
     int rc = ensure_workspace(ctx, L, n_tokens, false, &w);
     if (rc) return rc;
-    return enqueue_forward(ctx, L, w, x_dev, n_tokens, y_dev, (hipStream_t)stream);
+    return enqueue_forward(ctx, L, w, x_dev, n_tokens, y_dev, (hipStream_t)stream, ctx->prof);
+}
+
+int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const float *x_dev,
+                                      int32_t n_tokens, float *y_dev, void *stream)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!L || !x_dev || !y_dev || n_tokens <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
+    if ((uintptr_t)x_dev % 16)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "x_dev must be 16-byte aligned");
+    if (L->device != ctx->device)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer lives on device %d, context on %d",
+                       L->device, ctx->device);
+    if (!ctx->scratch)
+        return set_err(ctx, DMOE_ERR_HIP, "scratch address of device %d not resolved", ctx->device);
+    const size_t need =
+        plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens, false, nullptr, nullptr);
+    if (need > DMOE_NOALLOC_SCRATCH_BYTES)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG,
+                       "n_tokens = %d needs %zu bytes of workspace, above the %zu-byte scratch of "
+                       "the allocation-free forward (use dmoe_layer_forward_device)",
+                       n_tokens, need, (size_t)DMOE_NOALLOC_SCRATCH_BYTES);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    // Every workspace buffer is written by the forward before it is read, so
+    // what a previous call left in the scratch needs no clearing.
+    Workspace w;
+    plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens, false, ctx->scratch, &w);
+    return enqueue_forward(ctx, L, w, x_dev, n_tokens, y_dev, (hipStream_t)stream, false);
 }
 
 int dmoe_route_logits(dmoe_ctx *ctx, const dmoe_hparams *hp, const float *bias,

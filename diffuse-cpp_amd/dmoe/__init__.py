@@ -30,7 +30,9 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_layer_wrap_device", "dmoe_layer_free", "dmoe_layer_forward",
            "dmoe_layer_forward_device", "dmoe_route_logits", "dmoe_row_size",
            "dmoe_quantize_device", "dmoe_residual_rmsnorm", "dmoe_profile_enable",
-           "dmoe_profile_read", "dmoe_stage_name", "dmoe_layer_kernel_path")
+           "dmoe_profile_read", "dmoe_stage_name", "dmoe_layer_kernel_path",
+           "dmoe_layer_forward_device_noalloc")
+NOALLOC_SCRATCH_BYTES = 64 << 20
 N_STAGES = 10
 PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}
 
@@ -74,6 +76,7 @@ def load() -> C.CDLL:
     lib.dmoe_layer_kernel_path.argtypes = [P]
     lib.dmoe_layer_forward.argtypes = [P, P, P, C.c_int32, P, C.POINTER(Debug)]
     lib.dmoe_layer_forward_device.argtypes = [P, P, P, C.c_int32, P, P]
+    lib.dmoe_layer_forward_device_noalloc.argtypes = [P, P, P, C.c_int32, P, P]
     lib.dmoe_route_logits.argtypes = [P, C.POINTER(HParams), P, P, C.c_int32, C.POINTER(Debug)]
     lib.dmoe_row_size.argtypes = [C.c_int32, C.c_int64]
     lib.dmoe_row_size.restype = C.c_size_t
@@ -313,6 +316,14 @@ class Context:
         s = 0 if stream is None else int(stream)
         self._check(load().dmoe_layer_forward_device(self.handle, layer.handle, _ptr(x_dev),
                                                      n_tokens, _ptr(y_dev), s or None))
+
+    def forward_device_noalloc(self, layer: Layer, x_dev, n_tokens: int, y_dev, stream=None):
+        """dmoe_layer_forward_device_noalloc: the same forward on the GPU's
+        fixed scratch array, without any device allocation."""
+        s = 0 if stream is None else int(stream)
+        self._check(load().dmoe_layer_forward_device_noalloc(self.handle, layer.handle,
+                                                             _ptr(x_dev), n_tokens, _ptr(y_dev),
+                                                             s or None))
 
     def route_logits(self, hp: HParams, logits: np.ndarray, bias: Optional[np.ndarray]):
         logits = np.ascontiguousarray(logits, dtype=np.float32)

@@ -183,6 +183,23 @@ int  dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *layer,
                                const float *x_dev, int32_t n_tokens,
                                float *y_dev, void *stream);
 
+/* The device-pointer forward without any device allocation: no hipMalloc,
+ * hipFree or allocating library call, and no profiling events.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it).  Its workspace is a fixed array of DMOE_NOALLOC_SCRATCH_BYTES in
+ * device memory, one per GPU, held until the process ends; a forward whose
+ * workspace would exceed it (the LLaDA2-flash Q4_K layer takes up to 380
+ * tokens, eleven 32-token blocks) is rejected with DMOE_ERR_INVALID_ARG
+ * before anything is queued.  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams, other contexts, other threads) race, so the
+ * caller serialises them.  Results are identical to
+ * dmoe_layer_forward_device. */
+#define DMOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int  dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *layer,
+                                       const float *x_dev, int32_t n_tokens,
+                                       float *y_dev, void *stream);
+
 /* Routing only, from caller-supplied router logits [N][E] (host).  Runs the
  * GPU router stages that follow the logits product (diffuse-moe-graph.cpp:
  * 204-262) plus the dispatch grouping; outputs go to `dbg` (logits is

@@ -1,0 +1,80 @@
+"""GPU: the allocation-free forward (dmoe_layer_forward_device_noalloc)
+against the allocating device forward (dmoe_layer_forward_device), through
+the C ABI.  Both run the same kernels on the same inputs, so the outputs are
+compared bit for bit (stricter than the layer tolerance); two calls in a row,
+the second with fewer tokens, so the second runs on what the first left in
+the GPU's scratch array.  A forward whose workspace exceeds the scratch is
+rejected before anything is queued."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _run_pair(ctx, layer, x_host, n_tokens, stream):
+    import torch
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(np.ascontiguousarray(x_host[:n_tokens])).to(dev)
+    y_ref = torch.full_like(x, float("nan"))
+    y_new = torch.full_like(x, float("nan"))
+    ctx.forward_device(layer, x, n_tokens, y_ref, stream)
+    ctx.forward_device_noalloc(layer, x, n_tokens, y_new, stream)
+    torch.cuda.synchronize(dev)
+    return y_ref.cpu().numpy(), y_new.cpu().numpy()
+
+
+@pytest.mark.parametrize("case", ["flash_q4k", "small_f16", "small_q8_0"])
+def test_noalloc_matches_forward_device(ctx, O, case):
+    import torch
+    from dmoe import synth
+    if case == "flash_q4k":
+        cfg = synth.CONFIGS["flash_q4k"]
+        w = synth.device_layer(cfg, 3, ctx)
+        layer = ctx.wrap_device(w)
+        sizes = (256, 32)
+    else:
+        wt = 1 if case == "small_f16" else 8
+        cfg = synth.LayerConfig(case, 512, 32, 256, 8, 4, 32, 256, wt, wt, 96, -0.05, 0.05)
+        w = synth.host_layer(cfg, 3, O.quantize_rows)
+        layer = ctx.upload(w)
+        sizes = (96, 40)            # the second without block routing
+    x_host = synth.make_x(cfg, 3, max(sizes))
+    stream = torch.cuda.current_stream().cuda_stream
+    for n in sizes:
+        _say(f"case: allocation-free forward, {case}, N={n}")
+        y_ref, y_new = _run_pair(ctx, layer, x_host, n, stream)
+        assert np.isfinite(y_ref).all()
+        assert np.array_equal(y_new.view(np.uint32), y_ref.view(np.uint32)), (case, n)
+    layer.free()
+    del w
+    torch.cuda.empty_cache()
+
+
+def test_noalloc_rejects_oversize(ctx, O):
+    """The flash Q4_K layer at 4096 tokens needs far more than the scratch:
+    rejected with DMOE_ERR_INVALID_ARG and a message naming the limit; the
+    output buffer is left untouched."""
+    import torch
+    import dmoe
+    from dmoe import synth
+    _say("case: allocation-free forward above the scratch size")
+    cfg = synth.CONFIGS["flash_q4k"]
+    w = synth.device_layer(cfg, 4, ctx)
+    layer = ctx.wrap_device(w)
+    n = 4096
+    dev = torch.device("cuda:0")
+    x = torch.zeros((n, cfg.n_embd), dtype=torch.float32, device=dev)
+    y = torch.full_like(x, 7.0)
+    with pytest.raises(dmoe.DmoeError) as ei:
+        ctx.forward_device_noalloc(layer, x, n, y, torch.cuda.current_stream().cuda_stream)
+    assert ei.value.code == dmoe._abi.ERR_INVALID_ARG
+    assert "scratch" in str(ei.value)
+    torch.cuda.synchronize(dev)
+    assert bool((y == 7.0).all())
+    layer.free()
+    del w
+    torch.cuda.empty_cache()
