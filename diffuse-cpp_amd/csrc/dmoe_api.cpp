@@ -309,6 +309,14 @@ bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
     return true;
 }
 
+// Few tokens of Q4_K experts: the down products and the combine run as one
+// launch over 16-row tiles of every expert (k_down_rows.hip).
+bool use_down_rows(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N)
+{
+    return use_mfma_path(hp, wtype, stype, shared) &&
+           down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff);
+}
+
 // Q8_0 experts (and a Q8_0 shared expert of the same width) run on the int8
 // MFMA kernels of k_expert_q80.hip.
 bool use_q80_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared)
@@ -430,8 +438,11 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         t.hq.bsums = (int16_t *)take((size_t)P * (FF / 16 + 1) * 2);
         t.hs = (float *)take((size_t)N * (SF > 0 ? SF : 1) * 4);
     }
-    t.ye = (float *)take((size_t)P * H * 4);
-    t.ys = (float *)take((size_t)N * H * 4);
+    if (!use_down_rows(hp, wtype, stype, shared, N)) {
+        // per-pair and shared down results, folded by the combine launch
+        t.ye = (float *)take((size_t)P * H * 4);
+        t.ys = (float *)take((size_t)N * H * 4);
+    }
     if (w) *w = t;
     return off;
 }
@@ -573,6 +584,29 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.ys = w.ys;
         // the gate/up launch converts h to the down products' layout itself
         STAGE(ST_GATEUP, expert(0, job));
+        if (use_down_rows(hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+            // down products and the combine in one launch
+            DownRowsJob dj{};
+            dj.ed = L->ed;
+            dj.sd = L->sd;
+            dj.has_shared = L->has_shared;
+            dj.N = N;
+            dj.K = K;
+            dj.E = E;
+            dj.H = H;
+            dj.FF = FF;
+            dj.perm = w.rb.perm;
+            dj.offsets = w.rb.offsets;
+            dj.counts = w.rb.counts;
+            dj.wl = w.wl;
+            dj.ec_cap = E + N * K / EXPERT_CHUNK + 1;
+            dj.ah = w.ah;
+            dj.ahs = w.ahs;
+            dj.weights = w.rb.weights;
+            dj.y = y;
+            STAGE(ST_DOWN, launch_down_rows(dj, s));
+            return DMOE_OK;
+        }
         STAGE(ST_DOWN, expert(1, job));
         STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
                                          K, H, y, s));

@@ -184,6 +184,24 @@ hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s);
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
 constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
 hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s);
+// Down products of the Q4_K experts and the weighted combine in one launch
+// for few tokens (k_down_rows.hip): one workgroup per 16 output rows, every
+// touched expert's 16-row tile, results folded in slot order in LDS.
+constexpr int DR_MAX_PAIRS = 1024;      // (token, slot) pairs of one launch
+constexpr int DR_MAX_TOKENS = 128;
+struct DownRowsJob {
+    WTensor ed, sd;                 // tiled Q4_K down weights (routed, shared)
+    int32_t has_shared;
+    int32_t N, K, E, H, FF;         // tokens, top_k, experts, n_embd, moe_ff (== shared_ff)
+    const int32_t *perm, *offsets, *counts;
+    WorkList wl;                    // chunk == EXPERT_CHUNK
+    int32_t ec_cap;                 // allocated work-list length
+    ActI8 ah, ahs;                  // h in the int8 layout (routed pairs; shared digit rows)
+    const float *weights;           // [N][K] gate weights
+    float *y;                       // [N][H] segment output
+};
+bool down_rows_ok(int N, int K, int E, int H, int FF);
+hipError_t launch_down_rows(const DownRowsJob &job, hipStream_t s);
 // The same products for Q8_0 experts (k_expert_q80.hip): activations in the
 // ActI8 layout with ACT_Q80 / ACT_SPLIT32 scales, weights in the Q8_0 tiled
 // layout of launch_tile_q80.

@@ -62,6 +62,12 @@ __device__ __forceinline__ void q8_lds_load16(const void *src, uint32_t lds)
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                  : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
+// the same for weight runs, streamed once per forward: non-temporal hint
+__device__ __forceinline__ void q8_lds_load16_nt(const void *src, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
 __device__ __forceinline__ void q8_lds_load4(const void *src, uint32_t lds)
 {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
@@ -237,7 +243,7 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
             for (int jd = 0; jd < Q8_WDMA; jd++) {
                 const int p = min(64 * jd + lane, pmax);
                 if (64 * (jd + 1) <= Q8_WPIECES || 64 * jd + lane < Q8_WPIECES)
-                    q8_lds_load16(run + p * 16, wst + 1024 * jd);
+                    q8_lds_load16_nt(run + p * 16, wst + 1024 * jd);
             }
             const uint32_t ast = act_base + (uint32_t)(stg * Q8_ABYTES);
             if (aq_on) q8_lds_load16(aq + sb * 256, ast + 1024 * wave);

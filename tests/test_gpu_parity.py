@@ -57,7 +57,7 @@ def test_tiny_layer(ctx, O):
 
 
 @pytest.mark.parametrize("wtype", [12, 8, 1], ids=["Q4_K", "Q8_0", "F16"])
-@pytest.mark.parametrize("n_tokens", [32, 96, 40], ids=["N32", "N96", "N40_noblock"])
+@pytest.mark.parametrize("n_tokens", [32, 96, 40, 128], ids=["N32", "N96", "N40_noblock", "N128"])
 def test_small_layer(ctx, O, wtype, n_tokens):
     import dmoe
     from dmoe import synth
