@@ -49,6 +49,9 @@ struct dmoe_layer {
     WTensor eg{}, eu{}, ed{};
     WTensor sg{}, su{}, sd{};
     bool has_shared = false;
+    // a dense SwiGLU MLP (first_k_dense layers): the three tensors sit in the
+    // shared-expert slots (sg, su, sd), hp.n_embd / hp.shared_ff give its shape
+    bool dense = false;
     std::vector<void *> owned;
 };
 
@@ -806,6 +809,198 @@ int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmo
     return DMOE_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Dense MLP (src/diffuse-moe-graph.cpp:181-187): the shared expert's kernels
+// with an empty routed work list; the down launch writes y directly.
+enum DensePath { DP_GEMV = 0, DP_Q4K, DP_Q80, DP_F16 };
+
+int dense_path(int32_t type, int H, int FF)
+{
+    if (H % 256 == 0 && FF % 256 == 0) {
+        if (type == DMOE_TYPE_Q4_K && FF % expert_rows_per_item(0) == 0 && H % expert_rows_per_item(1) == 0)
+            return DP_Q4K;
+        if (type == DMOE_TYPE_Q8_0 && FF % expert_q80_rows_per_item(0) == 0 &&
+            H % expert_q80_rows_per_item(1) == 0)
+            return DP_Q80;
+    }
+    if (type == DMOE_TYPE_F16 && gemm_shapes_ok(H, FF, FF, true)) return DP_F16;
+    return DP_GEMV;
+}
+
+int dense_validate(dmoe_ctx *ctx, int H, int FF, const dmoe_tensor *g, const dmoe_tensor *u,
+                   const dmoe_tensor *d, bool device_mode)
+{
+    if (!g || !u || !d) return set_err(ctx, DMOE_ERR_INVALID_ARG, "dense: NULL tensor");
+    if (H <= 0 || H % 256) return set_err(ctx, DMOE_ERR_SHAPE, "dense: n_embd = %d must be a positive multiple of 256", H);
+    if (FF <= 0) return set_err(ctx, DMOE_ERR_SHAPE, "dense: n_ff = %d", FF);
+    int rc;
+    if ((rc = check_tensor(ctx, "ffn_gate", *g, H, FF, 0, device_mode))) return rc;
+    if ((rc = check_tensor(ctx, "ffn_up", *u, H, FF, 0, device_mode))) return rc;
+    if ((rc = check_tensor(ctx, "ffn_down", *d, FF, H, 0, device_mode))) return rc;
+    if (u->type != g->type || d->type != g->type)
+        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "dense: ffn tensors differ in type");
+    return DMOE_OK;
+}
+
+// hparams of a dense layer: the MLP as a lone shared expert
+dmoe_hparams dense_hparams(int H, int FF)
+{
+    dmoe_hparams hp{};
+    hp.n_embd = H;
+    hp.moe_ff = FF;
+    hp.shared_ff = FF;
+    hp.n_shared = 1;
+    return hp;
+}
+
+int dense_finish(dmoe_ctx *ctx, dmoe_layer *L)
+{
+    const int H = L->hp.n_embd, FF = L->hp.shared_ff;
+    int rc;
+    switch (dense_path(L->sg.type, H, FF)) {
+    case DP_Q4K:
+        if ((rc = tile_tensor(ctx, L, L->sg, FF, H, 1))) return rc;
+        if ((rc = tile_tensor(ctx, L, L->su, FF, H, 1))) return rc;
+        return tile_tensor(ctx, L, L->sd, H, FF, 1);
+    case DP_Q80:
+        if ((rc = tile_tensor_q80(ctx, L, L->sg, FF, H, 1))) return rc;
+        if ((rc = tile_tensor_q80(ctx, L, L->su, FF, H, 1))) return rc;
+        return tile_tensor_q80(ctx, L, L->sd, H, FF, 1);
+    case DP_F16:
+        if ((rc = tile_tensor_f16(ctx, L, L->sg, FF, H, 1))) return rc;
+        if ((rc = tile_tensor_f16(ctx, L, L->su, FF, H, 1))) return rc;
+        return tile_tensor_f16(ctx, L, L->sd, H, FF, 1);
+    default:
+        return DMOE_OK;
+    }
+}
+
+struct DenseWs {
+    float *x, *y;
+    int32_t *n_ec;                       // an empty routed work list
+    ActI8 axs, ahs;                      // split x and h (int8 paths)
+    uint16_t *xs16, *hs16;               // hi / lo f16 pairs (F16 path)
+    float *hs;                           // f32 h (GEMV path)
+};
+
+size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, DenseWs *w)
+{
+    const int H = L->hp.n_embd, FF = L->hp.shared_ff;
+    size_t off = 0;
+    std::function<uint8_t *(size_t)> take = [&](size_t bytes) -> uint8_t * {
+        uint8_t *p = base ? base + off : nullptr;
+        off += align_up(bytes > 0 ? bytes : 1);
+        return p;
+    };
+    DenseWs t{};
+    if (host_io) {
+        t.x = (float *)take((size_t)N * H * 4);
+        t.y = (float *)take((size_t)N * H * 4);
+    }
+    t.n_ec = (int32_t *)take(4);
+    switch (dense_path(L->sg.type, H, FF)) {
+    case DP_Q4K:
+        t.axs = take_act(take, N, H, true);
+        t.ahs = take_act(take, N, FF, true);
+        break;
+    case DP_Q80:
+        t.axs = take_act(take, N, H, true, true);
+        t.ahs = take_act(take, N, FF, true, true);
+        break;
+    case DP_F16:
+        t.xs16 = (uint16_t *)take((size_t)2 * N * H * 2);
+        t.hs16 = (uint16_t *)take((size_t)2 * N * FF * 2);
+        break;
+    default:
+        t.hs = (float *)take((size_t)N * FF * 4);
+        break;
+    }
+    if (w) *w = t;
+    return off;
+}
+
+int ensure_dense_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, DenseWs *w)
+{
+    const size_t need = plan_dense(L, N, host_io, nullptr, nullptr);
+    if (need > ctx->ws_bytes) {
+        if (ctx->ws) {
+            HIP_TRY(ctx, hipDeviceSynchronize());
+            HIP_TRY(ctx, hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        if (getenv("DMOE_FAIL_ALLOC"))
+            return set_err(ctx, DMOE_ERR_OOM, "workspace allocation of %zu bytes refused (DMOE_FAIL_ALLOC)", need);
+        HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
+        ctx->ws_bytes = need;
+    }
+    plan_dense(L, N, host_io, (uint8_t *)ctx->ws, w);
+    return DMOE_OK;
+}
+
+int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const float *x, int N,
+                  float *y, hipStream_t s, bool prof)
+{
+    const int H = L->hp.n_embd, FF = L->hp.shared_ff;
+    const int path = dense_path(L->sg.type, H, FF);
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
+    if (path == DP_GEMV) {
+        STAGE(ST_SH_GATEUP, launch_gateup_shared(L->sg, L->su, x, N, H, FF, w.hs, s));
+        STAGE(ST_SH_DOWN, launch_down_shared(L->sd, w.hs, N, FF, H, y, s));
+        return DMOE_OK;
+    }
+    // the expert kernels read an empty routed work list
+    LAUNCH_TRY(ctx, launch_fill_i32(w.n_ec, 0, 1, s));
+    WorkList wl{};
+    wl.n_ec = w.n_ec;
+    if (path == DP_F16) {
+        wl.chunk = GM;
+        GemmJob job{};
+        job.sg = L->sg;
+        job.su = L->su;
+        job.sd = L->sd;
+        job.has_shared = 1;
+        job.H = H;
+        job.FF = FF;
+        job.SF = FF;
+        job.n_tokens = N;
+        job.top_k = 1;
+        job.wl = wl;
+        job.xs16 = w.xs16;
+        job.x16 = w.xs16;
+        job.hs16 = w.hs16;
+        job.ys = y;
+        STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 1, w.xs16, s));
+        STAGE(ST_SH_GATEUP, launch_gemm_f16(0, job, s));
+        STAGE(ST_SH_DOWN, launch_gemm_f16(1, job, s));
+        return DMOE_OK;
+    }
+    const bool q8 = path == DP_Q80;
+    wl.chunk = EXPERT_CHUNK;
+    MoeJob job{};
+    job.sg = L->sg;
+    job.su = L->su;
+    job.sd = L->sd;
+    job.has_shared = 1;
+    job.H = H;
+    job.FF = FF;
+    job.SF = FF;
+    job.n_tokens = N;
+    job.top_k = 1;
+    job.wl = wl;
+    job.ax.K = H;                        // no routed activations
+    job.ah.K = FF;
+    job.axs = w.axs;
+    job.ahs = w.ahs;
+    job.ys = y;                          // the shared expert's down output is the MLP's
+    PrepJob pj{x, N, H, q8 ? ACT_SPLIT32 : ACT_SPLIT, w.axs};
+    STAGE(ST_ACTQ_X, launch_prep(&pj, 1, s));
+    STAGE(ST_SH_GATEUP, q8 ? launch_expert_q80(0, job, s) : launch_expert_q4k(0, job, s));
+    STAGE(ST_SH_DOWN, q8 ? launch_expert_q80(1, job, s) : launch_expert_q4k(1, job, s));
+#undef STAGE
+    return DMOE_OK;
+}
+
 } // namespace
 
 // ===========================================================================
@@ -944,6 +1139,52 @@ int dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp, const dmoe_lay
     return DMOE_OK;
 }
 
+static int dense_create(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff, const dmoe_tensor *gate,
+                        const dmoe_tensor *up, const dmoe_tensor *down, bool device_mode,
+                        dmoe_layer **out)
+{
+    if (!ctx || !out) return DMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = dense_validate(ctx, n_embd, n_ff, gate, up, down, device_mode);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    dmoe_layer *L = new (std::nothrow) dmoe_layer();
+    if (!L) return set_err(ctx, DMOE_ERR_OOM, "host allocation failed");
+    L->ctx = ctx;
+    L->device = ctx->device;
+    L->dense = true;
+    L->has_shared = true;
+    L->hp = dense_hparams(n_embd, n_ff);
+    if (device_mode) {
+        L->sg = wrap_tensor(*gate);
+        L->su = wrap_tensor(*up);
+        L->sd = wrap_tensor(*down);
+    } else if ((rc = upload_tensor(ctx, L, *gate, n_ff, 1, L->sg)) ||
+               (rc = upload_tensor(ctx, L, *up, n_ff, 1, L->su)) ||
+               (rc = upload_tensor(ctx, L, *down, n_embd, 1, L->sd))) {
+        dmoe_layer_free(L);
+        return rc;
+    }
+    if ((rc = dense_finish(ctx, L))) {
+        dmoe_layer_free(L);
+        return rc;
+    }
+    *out = L;
+    return DMOE_OK;
+}
+
+int dmoe_dense_upload(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff, const dmoe_tensor *gate,
+                      const dmoe_tensor *up, const dmoe_tensor *down, dmoe_layer **out)
+{
+    return dense_create(ctx, n_embd, n_ff, gate, up, down, false, out);
+}
+
+int dmoe_dense_wrap_device(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff, const dmoe_tensor *gate,
+                           const dmoe_tensor *up, const dmoe_tensor *down, dmoe_layer **out)
+{
+    return dense_create(ctx, n_embd, n_ff, gate, up, down, true, out);
+}
+
 void dmoe_layer_free(dmoe_layer *L)
 {
     if (!L) return;
@@ -957,6 +1198,10 @@ void dmoe_layer_free(dmoe_layer *L)
 int dmoe_layer_kernel_path(const dmoe_layer *L)
 {
     if (!L) return -1;
+    if (L->dense) {
+        static const int kmap[] = {DMOE_PATH_GEMV, DMOE_PATH_Q4K_MFMA, DMOE_PATH_Q80_MFMA, DMOE_PATH_F16_GEMM};
+        return kmap[dense_path(L->sg.type, L->hp.n_embd, L->hp.shared_ff)];
+    }
     if (use_mfma_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q4K_MFMA;
     if (use_q80_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q80_MFMA;
     if (use_gemm_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_F16_GEMM;
@@ -974,6 +1219,18 @@ int dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *x, int32
         if (!std::isfinite(x[i]))
             return set_err(ctx, DMOE_ERR_NONFINITE, "x[%zu] = %g is not finite", i, (double)x[i]);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (L->dense) {
+        DenseWs dw;
+        int rc = ensure_dense_workspace(ctx, L, n_tokens, true, &dw);
+        if (rc) return rc;
+        hipStream_t s = ctx->stream;
+        HIP_TRY(ctx, hipMemcpyAsync(dw.x, x, (size_t)n_tokens * H * 4, hipMemcpyHostToDevice, s));
+        if ((rc = enqueue_dense(ctx, L, dw, dw.x, n_tokens, dw.y, s, ctx->prof))) return rc;
+        HIP_TRY(ctx, hipMemcpyAsync(y, dw.y, (size_t)n_tokens * H * 4, hipMemcpyDeviceToHost, s));
+        if (dbg && dbg->use_block_routing) *dbg->use_block_routing = 0;
+        HIP_TRY(ctx, hipStreamSynchronize(s));
+        return DMOE_OK;
+    }
     Workspace w;
     int rc = ensure_workspace(ctx, L, n_tokens, true, &w);
     if (rc) return rc;
@@ -995,6 +1252,12 @@ int dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *x
     if ((uintptr_t)x_dev % 16)
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "x_dev must be 16-byte aligned");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (L->dense) {
+        DenseWs dw;
+        int rc = ensure_dense_workspace(ctx, L, n_tokens, false, &dw);
+        if (rc) return rc;
+        return enqueue_dense(ctx, L, dw, x_dev, n_tokens, y_dev, (hipStream_t)stream, ctx->prof);
+    }
     Workspace w;
     int rc = ensure_workspace(ctx, L, n_tokens, false, &w);
     if (rc) return rc;
@@ -1014,8 +1277,9 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
                        L->device, ctx->device);
     if (!ctx->scratch)
         return set_err(ctx, DMOE_ERR_HIP, "scratch address of device %d not resolved", ctx->device);
-    const size_t need =
-        plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens, false, nullptr, nullptr);
+    const size_t need = L->dense ? plan_dense(L, n_tokens, false, nullptr, nullptr)
+                                 : plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens,
+                                                  false, nullptr, nullptr);
     if (need > DMOE_NOALLOC_SCRATCH_BYTES)
         return set_err(ctx, DMOE_ERR_INVALID_ARG,
                        "n_tokens = %d needs %zu bytes of workspace, above the %zu-byte scratch of "
@@ -1024,6 +1288,11 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     // Every workspace buffer is written by the forward before it is read, so
     // what a previous call left in the scratch needs no clearing.
+    if (L->dense) {
+        DenseWs dw;
+        plan_dense(L, n_tokens, false, ctx->scratch, &dw);
+        return enqueue_dense(ctx, L, dw, x_dev, n_tokens, y_dev, (hipStream_t)stream, false);
+    }
     Workspace w;
     plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens, false, ctx->scratch, &w);
     return enqueue_forward(ctx, L, w, x_dev, n_tokens, y_dev, (hipStream_t)stream, false);

@@ -179,6 +179,8 @@ hipError_t launch_scores(const float *logits, const float *bias, int N, int E,
                          const RouteBufs &rb, hipStream_t s);
 // Up to two activation conversions in one launch.
 hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s);
+// p[0 .. n) = v
+hipError_t launch_fill_i32(int32_t *p, int32_t v, int n, hipStream_t s);
 // Grouped Q4_K expert products on MFMA (k_expert.hip).  phase 0: h = silu(gate x)
 // * (up x); phase 1: y = down h.
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item

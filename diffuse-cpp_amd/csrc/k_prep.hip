@@ -416,6 +416,21 @@ hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s)
     return hipGetLastError();
 }
 
+// p[0 .. n) = v (a kernel, not a memset, so that a caller's graph capture
+// records no memset node)
+__global__ __launch_bounds__(256) void k_fill_i32(int32_t *__restrict__ p, int32_t v, int n)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+hipError_t launch_fill_i32(int32_t *p, int32_t v, int n, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_i32, dim3((n + 255) / 256), dim3(256), 0, s, p, v, n);
+    return hipGetLastError();
+}
+
 // probs and sel from given logits
 __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ logits,
                                                 const float *__restrict__ bias, int N, int E,

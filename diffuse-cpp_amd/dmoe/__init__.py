@@ -31,7 +31,7 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_layer_forward_device", "dmoe_route_logits", "dmoe_row_size",
            "dmoe_quantize_device", "dmoe_residual_rmsnorm", "dmoe_profile_enable",
            "dmoe_profile_read", "dmoe_stage_name", "dmoe_layer_kernel_path",
-           "dmoe_layer_forward_device_noalloc")
+           "dmoe_layer_forward_device_noalloc", "dmoe_dense_upload", "dmoe_dense_wrap_device")
 NOALLOC_SCRATCH_BYTES = 64 << 20
 N_STAGES = 10
 PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}
@@ -74,6 +74,9 @@ def load() -> C.CDLL:
     lib.dmoe_layer_free.argtypes = [P]
     lib.dmoe_layer_free.restype = None
     lib.dmoe_layer_kernel_path.argtypes = [P]
+    lib.dmoe_dense_upload.argtypes = [P, C.c_int32, C.c_int32, C.POINTER(Tensor), C.POINTER(Tensor),
+                                      C.POINTER(Tensor), C.POINTER(P)]
+    lib.dmoe_dense_wrap_device.argtypes = lib.dmoe_dense_upload.argtypes
     lib.dmoe_layer_forward.argtypes = [P, P, P, C.c_int32, P, C.POINTER(Debug)]
     lib.dmoe_layer_forward_device.argtypes = [P, P, P, C.c_int32, P, P]
     lib.dmoe_layer_forward_device_noalloc.argtypes = [P, P, P, C.c_int32, P, P]
@@ -186,6 +189,29 @@ class LayerWeights:
             return 0
         return (2 * self.shared_ff * row_size(self.stype, self.n_embd)
                 + self.n_embd * row_size(self.stype, self.shared_ff))
+
+
+@dataclass
+class DenseWeights:
+    """The dense SwiGLU MLP of a first_k_dense layer (ffn_gate, ffn_up,
+    ffn_down of diffuse_moe_layer, src/diffuse-common.h:67-70) as GGUF block
+    bytes, numpy (host) or torch (device):
+      gate, up  u8 [n_ff, row_size(T, n_embd)]   (ne [n_embd, n_ff])
+      down      u8 [n_embd, row_size(T, n_ff)]   (ne [n_ff, n_embd])"""
+    n_embd: int
+    n_ff: int
+    wtype: int
+    gate: object
+    up: object
+    down: object
+
+    def views(self):
+        return (tensor_view(self.wtype, self.gate, [self.n_embd, self.n_ff]),
+                tensor_view(self.wtype, self.up, [self.n_embd, self.n_ff]),
+                tensor_view(self.wtype, self.down, [self.n_ff, self.n_embd]))
+
+    def nbytes(self) -> int:
+        return 2 * self.n_ff * row_size(self.wtype, self.n_embd) + self.n_embd * row_size(self.wtype, self.n_ff)
 
 
 def hparams_of(n_embd, n_experts, top_k, capacity, block_size, moe_ff=1, n_shared=0,
@@ -302,6 +328,24 @@ class Context:
                                                   C.byref(out)))
         return Layer(self, out.value, w)
 
+    def _dense(self, fn, w: DenseWeights) -> Layer:
+        g, u, d = w.views()
+        out = C.c_void_p()
+        self._check(fn(self.handle, w.n_embd, w.n_ff, C.byref(g), C.byref(u), C.byref(d),
+                       C.byref(out)))
+        lw = LayerWeights(n_embd=w.n_embd, n_experts=0, top_k=0, capacity=0, block_size=0,
+                          moe_ff=w.n_ff, wtype=w.wtype, gate_w=None, exp_gate=None, exp_up=None,
+                          exp_down=None)
+        return Layer(self, out.value, lw)
+
+    def dense_upload(self, w: DenseWeights) -> Layer:
+        """Copy a dense MLP (host arrays) into HBM (dmoe_dense_upload)."""
+        return self._dense(load().dmoe_dense_upload, w)
+
+    def dense_wrap_device(self, w: DenseWeights) -> Layer:
+        """A dense MLP whose tensors already live on the GPU (dmoe_dense_wrap_device)."""
+        return self._dense(load().dmoe_dense_wrap_device, w)
+
     def forward(self, layer: Layer, x: np.ndarray, debug: bool = False):
         x = np.ascontiguousarray(x, dtype=np.float32)
         N = x.shape[0]
@@ -365,6 +409,6 @@ class Context:
                                                 nrows, n_per_row, s or None))
 
 
-__all__ = ["Context", "Layer", "LayerWeights", "DmoeError", "load", "tensor_view", "hparams_of",
+__all__ = ["Context", "Layer", "LayerWeights", "DenseWeights", "DmoeError", "load", "tensor_view", "hparams_of",
            "use_block_routing", "row_size", "TYPE_F32", "TYPE_F16", "TYPE_Q8_0", "TYPE_Q4_K",
            "TYPE_Q8_K", "TYPE_NAMES", "TYPE_BY_NAME", "EXPORTS", "LIB_PATH"]

@@ -17,7 +17,7 @@ from dataclasses import dataclass, replace
 
 import numpy as np
 
-from . import (LayerWeights, TYPE_F16, TYPE_F32, TYPE_Q4_K, TYPE_Q8_0, row_size)
+from . import (DenseWeights, LayerWeights, TYPE_F16, TYPE_F32, TYPE_Q4_K, TYPE_Q8_0, row_size)
 
 _M1 = np.uint64(0x9E3779B97F4A7C15)
 _M2 = np.uint64(0xBF58476D1CE4E5B9)
@@ -54,6 +54,7 @@ def normal(seed: int, stream: int, n: int, std: float = 1.0) -> np.ndarray:
 
 # tensor stream ids
 S_X, S_GATE_W, S_BIAS, S_EG, S_EU, S_ED, S_SG, S_SU, S_SD = range(1, 10)
+S_FG, S_FU, S_FD = range(20, 23)        # dense MLP (ffn_gate, ffn_up, ffn_down)
 
 
 @dataclass(frozen=True)
@@ -207,3 +208,42 @@ def to_host(w: LayerWeights) -> LayerWeights:
     return replace(w, gate_w=h(w.gate_w), gate_bias=h(w.gate_bias), exp_gate=h(w.exp_gate),
                    exp_up=h(w.exp_up), exp_down=h(w.exp_down), sh_gate=h(w.sh_gate),
                    sh_up=h(w.sh_up), sh_down=h(w.sh_down))
+
+
+# The dense MLP of layer 0 at the LLaDA2-flash shape: hidden 4096, n_ff 9216
+# (first_k_dense = 1; the intermediate size the published Q4_K_S file size
+# implies for that layer).
+DENSE_FLASH = (4096, 9216)
+
+
+def host_dense(n_embd: int, n_ff: int, wtype: int, seed: int, quantize_rows,
+               w_std: float = 0.02) -> DenseWeights:
+    """A DenseWeights in host memory, N(0, w_std) weights quantised by quantize_rows."""
+    def q(stream, rows, n):
+        f = normal(seed, stream, rows * n, w_std).reshape(rows, n)
+        return np.ascontiguousarray(quantize_rows(wtype, f)).view(np.uint8).reshape(rows, row_size(wtype, n))
+    return DenseWeights(n_embd=n_embd, n_ff=n_ff, wtype=wtype, gate=q(S_FG, n_ff, n_embd),
+                        up=q(S_FU, n_ff, n_embd), down=q(S_FD, n_embd, n_ff))
+
+
+def device_dense(n_embd: int, n_ff: int, wtype: int, seed: int, ctx, w_std: float = 0.02) -> DenseWeights:
+    """A DenseWeights on the GPU: torch's seeded generator, dmoe_quantize_device."""
+    import torch
+    dev = torch.device(f"cuda:{ctx.device}")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed * 7919 + 31)
+
+    def q(rows, n):
+        out = torch.empty((rows, row_size(wtype, n)), dtype=torch.uint8, device=dev)
+        f = torch.randn((rows, n), generator=g, device=dev, dtype=torch.float32).mul_(w_std)
+        ctx.quantize_device(wtype, f, out, rows, n)
+        torch.cuda.synchronize(dev)
+        return out
+    return DenseWeights(n_embd=n_embd, n_ff=n_ff, wtype=wtype, gate=q(n_ff, n_embd),
+                        up=q(n_ff, n_embd), down=q(n_embd, n_ff))
+
+
+def dense_to_host(w: DenseWeights) -> DenseWeights:
+    def h(a):
+        return a.detach().cpu().numpy() if hasattr(a, "detach") else a
+    return replace(w, gate=h(w.gate), up=h(w.up), down=h(w.down))

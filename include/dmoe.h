@@ -147,6 +147,24 @@ int  dmoe_layer_upload(dmoe_ctx *ctx, const dmoe_hparams *hp,
 int  dmoe_layer_wrap_device(dmoe_ctx *ctx, const dmoe_hparams *hp,
                             const dmoe_layer_desc *desc, dmoe_layer **out);
 
+/* The dense SwiGLU MLP of the first_k_dense layers, y = W_down (silu(W_gate x)
+ * * (W_up x)) (src/diffuse-moe-graph.cpp:181-187, the ffn_gate / ffn_up /
+ * ffn_down tensors of diffuse_moe_layer, src/diffuse-common.h:67-70; loaded at
+ * src/diffuse-model.cpp:183-185), with the weights' F32 semantics of
+ * ensure_f32_moe (:8-12):
+ *   gate, up  T [n_embd, n_ff]     down  T [n_ff, n_embd]     T in the list above
+ * The result is a dmoe_layer run by dmoe_layer_forward / _forward_device /
+ * _forward_device_noalloc (no routing: a dmoe_debug gets use_block_routing 0
+ * and nothing else).  _upload copies host tensors into HBM; _wrap_device takes
+ * device tensors (Q4_K, Q8_0 and F16 ones are rewritten into a library-owned
+ * tiled copy, others referenced). */
+int  dmoe_dense_upload(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff,
+                       const dmoe_tensor *gate, const dmoe_tensor *up,
+                       const dmoe_tensor *down, dmoe_layer **out);
+int  dmoe_dense_wrap_device(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff,
+                            const dmoe_tensor *gate, const dmoe_tensor *up,
+                            const dmoe_tensor *down, dmoe_layer **out);
+
 /* Release a layer's device buffers.  The layer records its own device, so it
  * may be freed before or after the context that created it. */
 void dmoe_layer_free(dmoe_layer *layer);

@@ -669,6 +669,66 @@ static void matvec_rows(const dmoe_tensor *t, int64_t mat, int64_t r0, int64_t r
     }
 }
 
+/* y = W_down (silu(W_gate x) * (W_up x)) with every weight cast to F32
+ * (ensure_f32_moe, src/diffuse-moe-graph.cpp:8-12) and F32 activations: the
+ * shared expert (:280-286) and the dense MLP (:181-187) build the same ops. */
+static void swiglu_f32(int H, int FF, const dmoe_tensor *gate, const dmoe_tensor *up,
+                       const dmoe_tensor *down, const float *x, int N, float *y)
+{
+    float *sg = (float *)malloc((size_t)N * FF * 4);
+    float *su = (float *)malloc((size_t)N * FF * 4);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int r = 0; r < FF; r++) {
+        float *wg = (float *)malloc((size_t)H * 4);
+        float *wu = (float *)malloc((size_t)H * 4);
+        dmo_dequant_row(gate->type, tensor_row(gate, r, 0), wg, H);
+        dmo_dequant_row(up->type, tensor_row(up, r, 0), wu, H);
+        for (int t = 0; t < N; t++) {
+            float gv = dot_f32(H, wg, x + (size_t)t * H);
+            float uv = dot_f32(H, wu, x + (size_t)t * H);
+            sg[(size_t)t * FF + r] = silu_f32(gv);        /* ggml_silu(g) */
+            su[(size_t)t * FF + r] = uv;
+        }
+        free(wg);
+        free(wu);
+    }
+    for (size_t i = 0; i < (size_t)N * FF; i++) sg[i] = sg[i] * su[i];   /* ggml_mul(g, u) */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int r = 0; r < H; r++) {
+        float *wd = (float *)malloc((size_t)FF * 4);
+        dmo_dequant_row(down->type, tensor_row(down, r, 0), wd, FF);
+        for (int t = 0; t < N; t++)
+            y[(size_t)t * H + r] = dot_f32(FF, wd, sg + (size_t)t * FF);
+        free(wd);
+    }
+    free(sg);
+    free(su);
+}
+
+int dmo_dense_forward(int n_embd, int n_ff, const dmoe_tensor *gate, const dmoe_tensor *up,
+                      const dmoe_tensor *down, const float *x, int n_tokens, float *y,
+                      int n_threads)
+{
+    if (n_embd <= 0 || n_ff <= 0 || n_tokens <= 0 || !gate || !up || !down) return -1;
+#ifdef _OPENMP
+    if (n_threads <= 0) n_threads = omp_get_max_threads();
+    int saved_threads = omp_get_max_threads();
+    omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+    /* :181-187 g = silu(W_gate cur); u = W_up cur; cur = W_down (g * u) */
+    swiglu_f32(n_embd, n_ff, gate, up, down, x, n_tokens, y);
+#ifdef _OPENMP
+    omp_set_num_threads(saved_threads);
+#endif
+    return 0;
+}
+
 int dmo_layer_forward(const dmoe_hparams *hp, const dmoe_layer_desc *desc,
                       const float *x, int n_tokens, float *y,
                       dmoe_debug *dbg, int n_threads)
@@ -797,41 +857,11 @@ int dmo_layer_forward(const dmoe_hparams *hp, const dmoe_layer_desc *desc,
 
     if (hp->n_shared > 0 && desc->sh_gate.data) {
         /* :280-286 shared expert on the MoE input with weights cast to F32
-         * (ensure_f32_moe) and F32 activations */
-        const int SF = hp->shared_ff;
-        float *sg = (float *)malloc((size_t)N * SF * 4);
-        float *su = (float *)malloc((size_t)N * SF * 4);
+         * (ensure_f32_moe) and F32 activations, added to the routed sum */
         float *sd = (float *)malloc((size_t)N * H * 4);
-#ifdef _OPENMP
-#pragma omp parallel for schedule(dynamic)
-#endif
-        for (int r = 0; r < SF; r++) {
-            float *wg = (float *)malloc((size_t)H * 4);
-            float *wu = (float *)malloc((size_t)H * 4);
-            dmo_dequant_row(desc->sh_gate.type, tensor_row(&desc->sh_gate, r, 0), wg, H);
-            dmo_dequant_row(desc->sh_up.type, tensor_row(&desc->sh_up, r, 0), wu, H);
-            for (int t = 0; t < N; t++) {
-                float gv = dot_f32(H, wg, x + (size_t)t * H);
-                float uv = dot_f32(H, wu, x + (size_t)t * H);
-                sg[(size_t)t * SF + r] = silu_f32(gv);
-                su[(size_t)t * SF + r] = uv;
-            }
-            free(wg);
-            free(wu);
-        }
-        for (size_t i = 0; i < (size_t)N * SF; i++) sg[i] = sg[i] * su[i];
-#ifdef _OPENMP
-#pragma omp parallel for schedule(dynamic)
-#endif
-        for (int r = 0; r < H; r++) {
-            float *wd = (float *)malloc((size_t)SF * 4);
-            dmo_dequant_row(desc->sh_down.type, tensor_row(&desc->sh_down, r, 0), wd, SF);
-            for (int t = 0; t < N; t++)
-                sd[(size_t)t * H + r] = dot_f32(SF, wd, sg + (size_t)t * SF);
-            free(wd);
-        }
+        swiglu_f32(H, hp->shared_ff, &desc->sh_gate, &desc->sh_up, &desc->sh_down, x, N, sd);
         for (size_t i = 0; i < (size_t)N * H; i++) y[i] = y[i] + sd[i];
-        free(sg); free(su); free(sd);
+        free(sd);
     }
 
     if (dbg) {

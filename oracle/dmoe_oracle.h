@@ -32,6 +32,8 @@
  *                                    invariants
  *   dmo_layer_forward                pinned: float64 numpy layer on dequantised
  *                                    weights within an analytic error budget
+ *   dmo_dense_forward                pinned: float64 numpy SwiGLU on dequantised
+ *                                    weights within the same error budget
  */
 #ifndef DMOE_ORACLE_H
 #define DMOE_ORACLE_H
@@ -104,6 +106,13 @@ void dmo_dispatch(const int32_t *idx, int n_tokens, int top_k, int n_experts,
 int  dmo_layer_forward(const dmoe_hparams *hp, const dmoe_layer_desc *desc,
                        const float *x, int n_tokens, float *y,
                        dmoe_debug *dbg, int n_threads);
+
+/* Dense SwiGLU MLP of the first_k_dense layers (src/diffuse-moe-graph.cpp:
+ * 181-187): y = W_down (silu(W_gate x) * (W_up x)), weights cast to F32,
+ * F32 activations.  gate, up [n_embd, n_ff]; down [n_ff, n_embd]. */
+int  dmo_dense_forward(int n_embd, int n_ff, const dmoe_tensor *gate, const dmoe_tensor *up,
+                       const dmoe_tensor *down, const float *x, int n_tokens, float *y,
+                       int n_threads);
 
 #ifdef __cplusplus
 }

@@ -22,7 +22,7 @@ LIB_PATH = ORACLE_DIR / "libdmoe_oracle.so"
 sys.path.insert(0, str(ROOT / "diffuse-cpp_amd"))
 
 from dmoe import _abi  # noqa: E402  (struct layouts of include/dmoe.h)
-from dmoe._abi import Debug, HParams, LayerDesc  # noqa: E402
+from dmoe._abi import Debug, HParams, LayerDesc, Tensor  # noqa: E402
 
 TYPE_Q8_K = _abi.TYPE_Q8_K
 
@@ -74,6 +74,8 @@ def load() -> C.CDLL:
     lib.dmo_dispatch.restype = None
     lib.dmo_layer_forward.argtypes = [C.POINTER(HParams), C.POINTER(LayerDesc), P, C.c_int, P,
                                       C.POINTER(Debug), C.c_int]
+    lib.dmo_dense_forward.argtypes = [C.c_int, C.c_int, C.POINTER(Tensor), C.POINTER(Tensor),
+                                      C.POINTER(Tensor), P, C.c_int, P, C.c_int]
     _lib = lib
     return lib
 
@@ -219,6 +221,19 @@ def layer_forward(w, x: np.ndarray, debug: bool = False, n_threads: int = 0):
     if rc:
         raise ValueError("oracle layer forward failed")
     return (y, dbg.as_dict()) if debug else y
+
+
+def dense_forward(w, x: np.ndarray, n_threads: int = 0) -> np.ndarray:
+    """w: dmoe.DenseWeights with numpy arrays (src/diffuse-moe-graph.cpp:181-187)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    N = x.shape[0]
+    g, u, d = w.views()
+    y = np.empty_like(x)
+    rc = load().dmo_dense_forward(w.n_embd, w.n_ff, C.byref(g), C.byref(u), C.byref(d), _p(x), N,
+                                  _p(y), n_threads)
+    if rc:
+        raise ValueError("oracle dense forward failed")
+    return y
 
 
 def n_threads_default() -> int:

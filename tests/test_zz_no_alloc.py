@@ -54,6 +54,23 @@ def test_noalloc_matches_forward_device(ctx, O, case):
     torch.cuda.empty_cache()
 
 
+def test_noalloc_dense(ctx, O):
+    """The dense MLP through the allocation-free forward: bit for bit with
+    the allocating one, 32 then 24 tokens."""
+    import torch
+    from dmoe import synth
+    w = synth.host_dense(512, 768, 12, 5, O.quantize_rows)
+    layer = ctx.dense_upload(w)
+    x_host = synth.normal(5, synth.S_X, 32 * 512).reshape(32, 512)
+    stream = torch.cuda.current_stream().cuda_stream
+    for n in (32, 24):
+        _say(f"case: allocation-free forward, dense MLP, N={n}")
+        y_ref, y_new = _run_pair(ctx, layer, x_host, n, stream)
+        assert np.isfinite(y_ref).all()
+        assert np.array_equal(y_new.view(np.uint32), y_ref.view(np.uint32))
+    layer.free()
+
+
 def test_noalloc_rejects_oversize(ctx, O):
     """The flash Q4_K layer at 4096 tokens needs far more than the scratch:
     rejected with DMOE_ERR_INVALID_ARG and a message naming the limit; the
