@@ -31,7 +31,10 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_layer_forward_device", "dmoe_route_logits", "dmoe_row_size",
            "dmoe_quantize_device", "dmoe_residual_rmsnorm", "dmoe_profile_enable",
            "dmoe_profile_read", "dmoe_stage_name", "dmoe_layer_kernel_path",
-           "dmoe_layer_forward_device_noalloc", "dmoe_dense_upload", "dmoe_dense_wrap_device")
+           "dmoe_layer_forward_device_noalloc", "dmoe_dense_upload", "dmoe_dense_wrap_device",
+           "dmoe_gguf_open", "dmoe_gguf_close", "dmoe_gguf_get_u32", "dmoe_gguf_get_f32",
+           "dmoe_gguf_find_tensor", "dmoe_gguf_tensor_count", "dmoe_gguf_tensor_name",
+           "dmoe_gguf_moe_hparams", "dmoe_gguf_layer_desc", "dmoe_gguf_dense_desc")
 NOALLOC_SCRATCH_BYTES = 64 << 20
 N_STAGES = 10
 PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}

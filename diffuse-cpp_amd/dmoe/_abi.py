@@ -18,6 +18,8 @@ ERR_SHAPE = 3
 ERR_HIP = 4
 ERR_OOM = 5
 ERR_NONFINITE = 6
+ERR_FORMAT = 7
+ERR_NOT_FOUND = 8
 
 
 class Tensor(C.Structure):

@@ -45,7 +45,9 @@ typedef enum dmoe_status {
     DMOE_ERR_SHAPE            = 3, /* ne/nb inconsistent with the hparams    */
     DMOE_ERR_HIP              = 4, /* a HIP runtime call failed              */
     DMOE_ERR_OOM              = 5, /* device allocation failed               */
-    DMOE_ERR_NONFINITE        = 6  /* NaN / Inf in the host input activations */
+    DMOE_ERR_NONFINITE        = 6, /* NaN / Inf in the host input activations */
+    DMOE_ERR_FORMAT           = 7, /* malformed GGUF file or key of the wrong type */
+    DMOE_ERR_NOT_FOUND        = 8  /* GGUF file, key or tensor not present    */
 } dmoe_status;
 
 /* A view of one ggml tensor (ggml_tensor's type/data/ne/nb).  `data` points at
@@ -249,6 +251,51 @@ int  dmoe_quantize_device(dmoe_ctx *ctx, int32_t type, const float *src_dev,
 int  dmoe_residual_rmsnorm(dmoe_ctx *ctx, float *h_dev, const float *y_dev,
                            const float *gain_dev, float *x_dev, int32_t n_rows,
                            int32_t n_embd, float eps, void *stream);
+
+/* ---- GGUF ingestion ------------------------------------------------------
+ * A read-only memory map of a GGUF file (v2/v3, the container
+ * tools/quantize_streaming.py:13-88 parses) with the MoE hyper-parameters and
+ * tensors the reference's loader binds (src/diffuse-model.cpp:143-198).  The
+ * dmoe_tensor views point into the mapping (host memory), so a layer goes to
+ * HBM with dmoe_layer_upload / dmoe_dense_upload straight from the file; they
+ * stay valid until dmoe_gguf_close.  Replaces gguf_init_from_file and the key
+ * helpers of src/diffuse-model.cpp:5-73 for these tensors; where the
+ * reference dies (DIFFUSE_DIE) on a missing key or tensor these return
+ * DMOE_ERR_NOT_FOUND, on a malformed file DMOE_ERR_FORMAT. */
+typedef struct dmoe_gguf dmoe_gguf;
+
+/* Open and parse `path`; err (may be NULL) receives a message on failure. */
+int  dmoe_gguf_open(const char *path, dmoe_gguf **out, char *err, size_t errlen);
+void dmoe_gguf_close(dmoe_gguf *g);
+
+/* Key lookup with the reference's prefix search: "diffuse.<suffix>", then
+ * "qwen2.", "llama." (get_u32_multi / get_f32_multi, src/diffuse-model.cpp:
+ * 21-45).  Integer keys of any integer type convert when the value fits. */
+int  dmoe_gguf_get_u32(const dmoe_gguf *g, const char *suffix, uint32_t *val);
+int  dmoe_gguf_get_f32(const dmoe_gguf *g, const char *suffix, float *val);
+
+/* Any tensor by name (ggml_get_tensor): type, data, ne and ggml strides. */
+int  dmoe_gguf_find_tensor(const dmoe_gguf *g, const char *name, dmoe_tensor *out);
+int  dmoe_gguf_tensor_count(const dmoe_gguf *g);
+const char *dmoe_gguf_tensor_name(const dmoe_gguf *g, int i);
+
+/* The MoE hyper-parameters with the reference's defaults
+ * (src/diffuse-model.cpp:143-158: capacity 48, moe_block_size = block_length
+ * or 32, norm_topk_prob 1, routed_scaling 1.0); n_embd and n_layer
+ * (embedding_length, block_count) are required; shared_ff is ne[1] of the
+ * first moe_shared_gate tensor.  n_layer / first_k_dense may be NULL. */
+int  dmoe_gguf_moe_hparams(const dmoe_gguf *g, dmoe_hparams *hp, int32_t *n_layer,
+                           int32_t *first_k_dense);
+
+/* The MoE tensors of layer il (blk.<il>.moe_gate, moe_gate_bias (optional),
+ * moe_experts_gate/up/down, moe_shared_gate/up/down when expert_shared_count
+ * > 0), src/diffuse-model.cpp:187-196. */
+int  dmoe_gguf_layer_desc(const dmoe_gguf *g, int32_t il, dmoe_layer_desc *desc);
+
+/* The dense MLP of layer il (blk.<il>.ffn_gate/up/down, :183-185); n_ff may
+ * be NULL. */
+int  dmoe_gguf_dense_desc(const dmoe_gguf *g, int32_t il, dmoe_tensor *gate,
+                          dmoe_tensor *up, dmoe_tensor *down, int32_t *n_ff);
 
 /* Per-stage timing.  While enabled, every forward records a HIP event pair
  * around each pipeline stage on the stream it runs on; dmoe_profile_read

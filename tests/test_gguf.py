@@ -1,0 +1,180 @@
+"""CPU: the GGUF reader of libdmoe (dmoe_gguf_*, the loader mechanics of
+src/diffuse-model.cpp:5-73,143-198 for the MoE tensors).
+
+Pinned three ways: a known-answer file assembled byte by byte here from the
+container layout (not by the test writer), a round trip through the writer in
+tests/gguf_writer.py with every tensor compared byte for byte, and malformed
+files (every truncation of a small file, bad magic / version / alignment,
+data past the end) that must be refused without reading past the mapping."""
+import ctypes as C
+import struct
+
+import numpy as np
+import pytest
+
+from gguf_writer import ARR, F32, GGUFWriter, STR, U32, U8, add_dense_layer, add_moe_layer, moe_keys
+
+
+def _s(x: str) -> bytes:
+    b = x.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def _kat_bytes():
+    """GGUF v3: 5 key/values (u32, f32, string, array of u8, i64), two tensors
+    (F32 [4] at offset 0, F16 [8, 2] at offset 32), alignment 32."""
+    kv = [
+        _s("diffuse.expert_count") + struct.pack("<II", 4, 16),
+        _s("qwen2.routed_scaling_factor") + struct.pack("<If", 6, 2.5),
+        _s("general.name") + struct.pack("<I", 8) + _s("kat"),
+        _s("general.blob") + struct.pack("<IIQ", 9, 0, 3) + bytes([7, 8, 9]),
+        _s("llama.expert_capacity") + struct.pack("<Iq", 11, 12),
+    ]
+    ti = [
+        _s("a.weight") + struct.pack("<IQIQ", 1, 4, 0, 0),
+        _s("b.weight") + struct.pack("<IQQIQ", 2, 8, 2, 1, 32),
+    ]
+    head = b"GGUF" + struct.pack("<IQQ", 3, 2, len(kv)) + b"".join(kv) + b"".join(ti)
+    head += b"\0" * ((-len(head)) % 32)
+    a = np.array([1.0, -2.0, 3.5, 0.25], np.float32).tobytes()
+    b = np.arange(16, dtype=np.float16).tobytes()
+    return head + a + b"\0" * (32 - len(a)) + b, len(head)
+
+
+def test_known_answer_file(tmp_path):
+    from dmoe.gguf import GGUF
+    raw, data_start = _kat_bytes()
+    p = tmp_path / "kat.gguf"
+    p.write_bytes(raw)
+    with GGUF(p) as g:
+        assert g.get_u32("expert_count") == 16                     # diffuse. prefix
+        assert g.get_f32("routed_scaling_factor") == 2.5            # qwen2. prefix
+        assert g.get_u32("expert_capacity") == 12                   # llama. prefix, an i64 value
+        assert g.get_u32("expert_used_count") is None
+        assert g.tensor_names() == ["a.weight", "b.weight"]
+        a = g.tensor("a.weight")
+        assert (a.type, list(a.ne), list(a.nb)) == (0, [4, 1, 1, 1], [4, 16, 16, 16])
+        assert C.string_at(a.data, 16) == raw[data_start:data_start + 16]
+        b = g.tensor("b.weight")
+        assert (b.type, list(b.ne), list(b.nb)) == (1, [8, 2, 1, 1], [2, 16, 32, 32])
+        assert np.array_equal(np.frombuffer(C.string_at(b.data, 32), np.float16), np.arange(16))
+
+
+def _tiny_file(tmp_path, O, prefix="diffuse"):
+    from dmoe import synth
+    cfg = synth.CONFIGS["tiny"]
+    w = synth.host_layer(cfg, 3, O.quantize_rows)
+    d = synth.host_dense(256, 512, 12, 4, O.quantize_rows)
+    wr = GGUFWriter()
+    for k, t, v in moe_keys(w, n_layer=2, first_k_dense=1, prefix=prefix):
+        wr.add(k, t, v)
+    wr.add("general.architecture", STR, prefix)
+    wr.add("tokenizer.ggml.tokens", ARR, (STR, ["a", "bb", "ccc"]))
+    add_dense_layer(wr, 0, d)
+    add_moe_layer(wr, 1, w)
+    p = tmp_path / "tiny.gguf"
+    wr.write(p)
+    return p, w, d
+
+
+@pytest.mark.parametrize("prefix", ["diffuse", "qwen2", "llama"])
+def test_round_trip_tiny_layer(tmp_path, O, prefix):
+    from dmoe.gguf import GGUF
+    p, w, d = _tiny_file(tmp_path, O, prefix)
+    with GGUF(p) as g:
+        hp, n_layer, fk = g.moe_hparams()
+        assert (n_layer, fk) == (2, 1)
+        ref = w.hparams()
+        for f in ("n_embd", "n_experts", "top_k", "capacity", "block_size", "moe_ff", "n_shared",
+                  "shared_ff", "norm_topk_prob"):
+            assert getattr(hp, f) == getattr(ref, f), f
+        assert hp.routed_scaling == np.float32(2.5)
+        lw = g.layer_weights(1)
+        for f in ("gate_w", "gate_bias", "exp_gate", "exp_up", "exp_down", "sh_gate", "sh_up", "sh_down"):
+            assert np.array_equal(np.asarray(getattr(lw, f)).view(np.uint8).reshape(-1),
+                                  np.asarray(getattr(w, f)).view(np.uint8).reshape(-1)), f
+        # the oracle on the mapped tensors equals the oracle on the originals
+        x = np.random.default_rng(0).standard_normal((32, 256)).astype(np.float32)
+        assert np.array_equal(O.layer_forward(lw, x), O.layer_forward(w, x))
+        dw = g.dense_weights(0)
+        assert (dw.n_embd, dw.n_ff, dw.wtype) == (256, 512, 12)
+        for f in ("gate", "up", "down"):
+            assert np.array_equal(getattr(dw, f), getattr(d, f)), f
+        desc = g.layer_desc(1)
+        assert desc.exp_gate.nb[1] == 256 * 4 and desc.exp_gate.nb[2] == 256 * 4 * 128
+
+
+def test_defaults_and_missing(tmp_path):
+    """Missing optional keys take the reference's defaults (capacity 48,
+    moe_block_size = block_length or 32, norm_topk_prob 1, routed_scaling 1);
+    a missing required key or tensor is DMOE_ERR_NOT_FOUND."""
+    import dmoe
+    from dmoe.gguf import GGUF
+    wr = GGUFWriter()
+    wr.add("diffuse.block_count", U32, 1)
+    wr.add("diffuse.embedding_length", U32, 256)
+    wr.add("diffuse.block_length", U32, 64)
+    p = tmp_path / "d.gguf"
+    wr.write(p)
+    with GGUF(p) as g:
+        hp, nl, fk = g.moe_hparams()
+        assert (hp.capacity, hp.block_size, hp.norm_topk_prob, hp.routed_scaling, nl, fk) == (48, 64, 1, 1.0, 1, 0)
+        with pytest.raises(dmoe.DmoeError) as ei:
+            g.layer_desc(0)
+        assert ei.value.code == dmoe._abi.ERR_NOT_FOUND
+    wr = GGUFWriter()
+    wr.add("diffuse.block_count", U32, 1)
+    wr.write(p)
+    with GGUF(p) as g:
+        with pytest.raises(dmoe.DmoeError) as ei:
+            g.moe_hparams()                                       # embedding_length missing
+        assert ei.value.code == dmoe._abi.ERR_NOT_FOUND
+
+
+def test_malformed_files_are_refused(tmp_path):
+    import dmoe
+    from dmoe.gguf import GGUF
+    raw, _ = _kat_bytes()
+    p = tmp_path / "m.gguf"
+
+    def code(data):
+        p.write_bytes(data)
+        try:
+            GGUF(p).close()
+            return 0
+        except dmoe.DmoeError as e:
+            return e.code
+
+    assert code(raw) == 0
+    # every truncation: refused (the last tensor's data runs past the end), never a crash
+    for n in range(len(raw)):
+        assert code(raw[:n]) == dmoe._abi.ERR_FORMAT, n
+    assert code(b"GGUX" + raw[4:]) == dmoe._abi.ERR_FORMAT                       # magic
+    assert code(raw[:4] + struct.pack("<I", 9) + raw[8:]) == dmoe._abi.ERR_FORMAT  # version
+    huge = raw[:8] + struct.pack("<Q", 1 << 40) + raw[16:]                        # tensor count
+    assert code(huge) == dmoe._abi.ERR_FORMAT
+    wr = GGUFWriter()
+    wr.add("general.alignment", U32, 24)                                         # not a power of two
+    wr.write(p)
+    with pytest.raises(dmoe.DmoeError) as ei:
+        GGUF(p)
+    assert ei.value.code == dmoe._abi.ERR_FORMAT
+    with pytest.raises(dmoe.DmoeError) as ei:
+        GGUF(tmp_path / "absent.gguf")
+    assert ei.value.code == dmoe._abi.ERR_NOT_FOUND
+
+
+def test_alignment_key_and_u8_values(tmp_path):
+    from dmoe.gguf import GGUF
+    wr = GGUFWriter(alignment=64)
+    wr.add("general.alignment", U32, 64)
+    wr.add("diffuse.expert_count", U8, 200)
+    wr.add_tensor("t.weight", 0, [3], np.array([1, 2, 3], np.float32))
+    wr.add_tensor("u.weight", 0, [2], np.array([4, 5], np.float32))
+    p = tmp_path / "a.gguf"
+    wr.write(p)
+    with GGUF(p) as g:
+        assert g.get_u32("expert_count") == 200
+        t, u = g.tensor("t.weight"), g.tensor("u.weight")
+        assert t.data % 64 == 0 and u.data - t.data == 64
+        assert np.frombuffer(C.string_at(u.data, 8), np.float32).tolist() == [4.0, 5.0]

@@ -16,7 +16,7 @@ HEADER = ROOT / "include" / "dmoe.h"
 def _declared():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(dmoe_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(dmoe_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_exports_match_header():
@@ -29,7 +29,7 @@ def test_exports_match_header():
     assert sorted(dmoe.EXPORTS) == names
     out = subprocess.run(["nm", "-D", "--defined-only", str(dmoe.LIB_PATH)], capture_output=True,
                          text=True, check=True).stdout
-    exported = sorted(set(re.findall(r" T (dmoe_[a-z_]+)$", out, flags=re.M)))
+    exported = sorted(set(re.findall(r" T (dmoe_[a-z0-9_]+)$", out, flags=re.M)))
     assert exported == names
 
 
@@ -94,6 +94,15 @@ def test_null_context_is_rejected():
     lib.dmoe_destroy(None)
     lib.dmoe_layer_free(None)
     assert lib.dmoe_layer_kernel_path(None) == -1
+    from dmoe import gguf
+    gguf._bind(lib)
+    assert lib.dmoe_gguf_open(None, C.byref(out), None, 0) == E
+    lib.dmoe_gguf_close(None)
+    assert lib.dmoe_gguf_get_u32(None, b"expert_count", None) == E
+    assert lib.dmoe_gguf_tensor_count(None) == -1
+    assert lib.dmoe_gguf_tensor_name(None, 0) is None
+    assert lib.dmoe_gguf_layer_desc(None, 0, None) == E
+    assert lib.dmoe_dense_upload(None, 256, 256, None, None, None, C.byref(out)) == E
     names = [lib.dmoe_stage_name(i).decode() for i in range(dmoe.N_STAGES)]
     assert names[0] == "front" and "gateup_routed" in names
     assert lib.dmoe_stage_name(99) == b""
