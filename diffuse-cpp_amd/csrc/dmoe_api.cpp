@@ -52,6 +52,10 @@ struct dmoe_layer {
     // a dense SwiGLU MLP (first_k_dense layers): the three tensors sit in the
     // shared-expert slots (sg, su, sd), hp.n_embd / hp.shared_ff give its shape
     bool dense = false;
+    // the step tail: final norm weight in gate_w (f32 [n_embd]), the output
+    // (LM head) weight in sd as a shared down matrix of n_vocab rows
+    bool head = false;
+    int32_t n_vocab = 0;
     std::vector<void *> owned;
 };
 
@@ -1001,6 +1005,136 @@ int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const fl
     return DMOE_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Step tail (src/diffuse-moe-graph.cpp:295-300 and the temperature-0 sampler,
+// src/diffuse-sampler.cpp:29-49): rms_norm * output_norm, the LM head as a
+// shared expert's down product of n_vocab rows (F32 weight semantics, as
+// ensure_f32_moe gives the reference), then argmax and confidence per row.
+int head_path(int32_t type, int V, int H)
+{
+    if (H % 256 == 0) {
+        if (type == DMOE_TYPE_Q4_K && V % expert_rows_per_item(1) == 0 && V % 256 == 0) return DP_Q4K;
+        if (type == DMOE_TYPE_Q8_0 && V % expert_q80_rows_per_item(1) == 0 && V % 256 == 0) return DP_Q80;
+    }
+    if (type == DMOE_TYPE_F16 && gemm_shapes_ok(V, H, H, true)) return DP_F16;
+    return DP_GEMV;
+}
+
+struct HeadWs {
+    float *h;                            // host input copy
+    int32_t *tokens;                     // host output staging
+    float *probs;
+    float *xn;                           // rms_norm(h) * output_norm
+    float *logits;                       // [N][V] (unless the caller's)
+    int32_t *n_ec;
+    ActI8 ahs;                           // split xn (int8 paths)
+    uint16_t *hs16;                      // hi / lo f16 xn (F16 path)
+};
+
+size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint8_t *base, HeadWs *w)
+{
+    const int H = L->hp.n_embd, V = L->n_vocab;
+    size_t off = 0;
+    std::function<uint8_t *(size_t)> take = [&](size_t bytes) -> uint8_t * {
+        uint8_t *p = base ? base + off : nullptr;
+        off += align_up(bytes > 0 ? bytes : 1);
+        return p;
+    };
+    HeadWs t{};
+    if (host_io) {
+        t.h = (float *)take((size_t)N * H * 4);
+        t.tokens = (int32_t *)take((size_t)N * 4);
+        t.probs = (float *)take((size_t)N * 4);
+    }
+    t.xn = (float *)take((size_t)N * H * 4);
+    if (own_logits) t.logits = (float *)take((size_t)N * V * 4);
+    t.n_ec = (int32_t *)take(4);
+    switch (head_path(L->sd.type, V, H)) {
+    case DP_Q4K: t.ahs = take_act(take, N, H, true); break;
+    case DP_Q80: t.ahs = take_act(take, N, H, true, true); break;
+    case DP_F16: t.hs16 = (uint16_t *)take((size_t)2 * N * H * 2); break;
+    default: break;
+    }
+    if (w) *w = t;
+    return off;
+}
+
+int ensure_head_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, bool own_logits,
+                          HeadWs *w)
+{
+    const size_t need = plan_head(L, N, host_io, own_logits, nullptr, nullptr);
+    if (need > ctx->ws_bytes) {
+        if (ctx->ws) {
+            HIP_TRY(ctx, hipDeviceSynchronize());
+            HIP_TRY(ctx, hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        if (getenv("DMOE_FAIL_ALLOC"))
+            return set_err(ctx, DMOE_ERR_OOM, "workspace allocation of %zu bytes refused (DMOE_FAIL_ALLOC)", need);
+        HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
+        ctx->ws_bytes = need;
+    }
+    plan_head(L, N, host_io, own_logits, (uint8_t *)ctx->ws, w);
+    return DMOE_OK;
+}
+
+int enqueue_head(dmoe_ctx *ctx, const dmoe_layer *L, const HeadWs &w, const float *h, int N, float eps,
+                 int32_t *tokens, float *probs, float *logits, hipStream_t s)
+{
+    const int H = L->hp.n_embd, V = L->n_vocab;
+    const bool prof = ctx->prof;
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
+    // :296-297 rms_norm(cur) * output_norm (h is only read: no residual add)
+    STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->gate_w, w.xn, N, H, eps, s));
+    const int path = head_path(L->sd.type, V, H);
+    if (path == DP_GEMV) {
+        STAGE(ST_SH_DOWN, launch_down_shared(L->sd, w.xn, N, H, V, logits, s));
+    } else {
+        LAUNCH_TRY(ctx, launch_fill_i32(w.n_ec, 0, 1, s));
+        WorkList wl{};
+        wl.n_ec = w.n_ec;
+        if (path == DP_F16) {
+            wl.chunk = GM;
+            GemmJob job{};
+            job.sd = L->sd;
+            job.has_shared = 1;
+            job.H = V;
+            job.FF = H;
+            job.SF = H;
+            job.n_tokens = N;
+            job.top_k = 1;
+            job.wl = wl;
+            job.hs16 = w.hs16;
+            job.ys = logits;
+            STAGE(ST_ACTQ_H, launch_cvt_f16(w.xn, N, H, 1, w.hs16, s));
+            STAGE(ST_SH_DOWN, launch_gemm_f16(1, job, s));
+        } else {
+            const bool q8 = path == DP_Q80;
+            wl.chunk = EXPERT_CHUNK;
+            MoeJob job{};
+            job.sd = L->sd;
+            job.has_shared = 1;
+            job.H = V;                       // output rows
+            job.FF = H;                      // reduction length
+            job.SF = H;
+            job.n_tokens = N;
+            job.top_k = 1;
+            job.wl = wl;
+            job.ax.K = V;
+            job.ah.K = H;
+            job.ahs = w.ahs;
+            job.ys = logits;
+            PrepJob pj{w.xn, N, H, q8 ? ACT_SPLIT32 : ACT_SPLIT, w.ahs};
+            STAGE(ST_ACTQ_H, launch_prep(&pj, 1, s));
+            STAGE(ST_SH_DOWN, q8 ? launch_expert_q80(1, job, s) : launch_expert_q4k(1, job, s));
+        }
+    }
+    STAGE(ST_COMBINE, launch_argmax_prob(logits, N, V, tokens, probs, s));
+#undef STAGE
+    return DMOE_OK;
+}
+
 } // namespace
 
 // ===========================================================================
@@ -1173,6 +1307,121 @@ static int dense_create(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff, const dmoe_
     return DMOE_OK;
 }
 
+static int head_create(dmoe_ctx *ctx, int32_t n_embd, int32_t n_vocab, const dmoe_tensor *norm,
+                       const dmoe_tensor *output, bool device_mode, dmoe_layer **out)
+{
+    if (!ctx || !out) return DMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    if (!norm || !output || !norm->data) return set_err(ctx, DMOE_ERR_INVALID_ARG, "head: NULL tensor");
+    const int H = n_embd, V = n_vocab;
+    if (H <= 0 || H % 256) return set_err(ctx, DMOE_ERR_SHAPE, "head: n_embd = %d must be a positive multiple of 256", H);
+    if (V <= 0) return set_err(ctx, DMOE_ERR_SHAPE, "head: n_vocab = %d", V);
+    if (norm->ne[0] != H || norm->ne[1] > 1)
+        return set_err(ctx, DMOE_ERR_SHAPE, "output_norm: ne0 = %lld, expected %d", (long long)norm->ne[0], H);
+    if (norm->type != DMOE_TYPE_F32 && !(norm->type == DMOE_TYPE_F16 && !device_mode))
+        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "output_norm: type %d", norm->type);
+    if (device_mode && (uintptr_t)norm->data % 16)
+        return set_err(ctx, DMOE_ERR_SHAPE, "output_norm: device data not 16-byte aligned");
+    int rc;
+    if ((rc = check_tensor(ctx, "output", *output, H, V, 0, device_mode))) return rc;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    dmoe_layer *L = new (std::nothrow) dmoe_layer();
+    if (!L) return set_err(ctx, DMOE_ERR_OOM, "host allocation failed");
+    L->ctx = ctx;
+    L->device = ctx->device;
+    L->head = true;
+    L->n_vocab = V;
+    L->hp.n_embd = H;
+    auto fail = [&](int code) {
+        dmoe_layer_free(L);
+        return code;
+    };
+    if (device_mode) {
+        L->gate_w = (float *)norm->data;
+        L->sd = wrap_tensor(*output);
+    } else {
+        std::vector<float> w((size_t)H);
+        for (int k = 0; k < H; k++)
+            w[k] = norm->type == DMOE_TYPE_F32 ? ((const float *)norm->data)[k]
+                                               : f16_to_f32_host(((const uint16_t *)norm->data)[k]);
+        void *dev = nullptr;
+        hipError_t he = hipMalloc(&dev, (size_t)H * 4);
+        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_OOM, "hipMalloc output_norm: %s", hipGetErrorString(he)));
+        L->owned.push_back(dev);
+        he = hipMemcpy(dev, w.data(), (size_t)H * 4, hipMemcpyHostToDevice);
+        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_HIP, "output_norm copy: %s", hipGetErrorString(he)));
+        L->gate_w = (float *)dev;
+        if ((rc = upload_tensor(ctx, L, *output, V, 1, L->sd))) return fail(rc);
+    }
+    switch (head_path(L->sd.type, V, H)) {
+    case DP_Q4K: rc = tile_tensor(ctx, L, L->sd, V, H, 1); break;
+    case DP_Q80: rc = tile_tensor_q80(ctx, L, L->sd, V, H, 1); break;
+    case DP_F16: rc = tile_tensor_f16(ctx, L, L->sd, V, H, 1); break;
+    default: rc = DMOE_OK; break;
+    }
+    if (rc) return fail(rc);
+    *out = L;
+    return DMOE_OK;
+}
+
+int dmoe_head_upload(dmoe_ctx *ctx, int32_t n_embd, int32_t n_vocab, const dmoe_tensor *output_norm,
+                     const dmoe_tensor *output, dmoe_layer **out)
+{
+    return head_create(ctx, n_embd, n_vocab, output_norm, output, false, out);
+}
+
+int dmoe_head_wrap_device(dmoe_ctx *ctx, int32_t n_embd, int32_t n_vocab, const dmoe_tensor *output_norm,
+                          const dmoe_tensor *output, dmoe_layer **out)
+{
+    return head_create(ctx, n_embd, n_vocab, output_norm, output, true, out);
+}
+
+static int head_args(dmoe_ctx *ctx, const dmoe_layer *L, const void *h, int32_t n_tokens, const void *tokens,
+                     const void *probs, float eps)
+{
+    if (!L || !L->head) return set_err(ctx, DMOE_ERR_INVALID_ARG, "not a head layer (dmoe_head_upload)");
+    if (!h || !tokens || !probs || n_tokens <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "h/tokens/probs NULL or n_tokens = %d", n_tokens);
+    if (!(eps >= 0.0f) || eps > 1.0f) return set_err(ctx, DMOE_ERR_INVALID_ARG, "eps = %g outside [0, 1]", (double)eps);
+    return DMOE_OK;
+}
+
+int dmoe_head_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *h, int32_t n_tokens, float eps,
+                      int32_t *tokens, float *probs, float *logits)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    int rc = head_args(ctx, L, h, n_tokens, tokens, probs, eps);
+    if (rc) return rc;
+    const int H = L->hp.n_embd, V = L->n_vocab;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    HeadWs w;
+    if ((rc = ensure_head_workspace(ctx, L, n_tokens, true, true, &w))) return rc;
+    hipStream_t s = ctx->stream;
+    HIP_TRY(ctx, hipMemcpyAsync(w.h, h, (size_t)n_tokens * H * 4, hipMemcpyHostToDevice, s));
+    if ((rc = enqueue_head(ctx, L, w, w.h, n_tokens, eps, w.tokens, w.probs, w.logits, s))) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(tokens, w.tokens, (size_t)n_tokens * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipMemcpyAsync(probs, w.probs, (size_t)n_tokens * 4, hipMemcpyDeviceToHost, s));
+    if (logits)
+        HIP_TRY(ctx, hipMemcpyAsync(logits, w.logits, (size_t)n_tokens * V * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return DMOE_OK;
+}
+
+int dmoe_head_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *h_dev, int32_t n_tokens,
+                             float eps, int32_t *tokens_dev, float *probs_dev, float *logits_dev,
+                             void *stream)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    int rc = head_args(ctx, L, h_dev, n_tokens, tokens_dev, probs_dev, eps);
+    if (rc) return rc;
+    if ((uintptr_t)h_dev % 16) return set_err(ctx, DMOE_ERR_INVALID_ARG, "h_dev must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    HeadWs w;
+    if ((rc = ensure_head_workspace(ctx, L, n_tokens, false, logits_dev == nullptr, &w))) return rc;
+    return enqueue_head(ctx, L, w, h_dev, n_tokens, eps, tokens_dev, probs_dev,
+                        logits_dev ? logits_dev : w.logits, (hipStream_t)stream);
+}
+
 int dmoe_dense_upload(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff, const dmoe_tensor *gate,
                       const dmoe_tensor *up, const dmoe_tensor *down, dmoe_layer **out)
 {
@@ -1198,10 +1447,9 @@ void dmoe_layer_free(dmoe_layer *L)
 int dmoe_layer_kernel_path(const dmoe_layer *L)
 {
     if (!L) return -1;
-    if (L->dense) {
-        static const int kmap[] = {DMOE_PATH_GEMV, DMOE_PATH_Q4K_MFMA, DMOE_PATH_Q80_MFMA, DMOE_PATH_F16_GEMM};
-        return kmap[dense_path(L->sg.type, L->hp.n_embd, L->hp.shared_ff)];
-    }
+    static const int kmap[] = {DMOE_PATH_GEMV, DMOE_PATH_Q4K_MFMA, DMOE_PATH_Q80_MFMA, DMOE_PATH_F16_GEMM};
+    if (L->dense) return kmap[dense_path(L->sg.type, L->hp.n_embd, L->hp.shared_ff)];
+    if (L->head) return kmap[head_path(L->sd.type, L->n_vocab, L->hp.n_embd)];
     if (use_mfma_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q4K_MFMA;
     if (use_q80_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q80_MFMA;
     if (use_gemm_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_F16_GEMM;
@@ -1212,6 +1460,7 @@ int dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *x, int32
                        float *y, dmoe_debug *dbg)
 {
     if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (L && L->head) return set_err(ctx, DMOE_ERR_INVALID_ARG, "a step-tail layer: use dmoe_head_forward");
     if (!L || !x || !y || n_tokens <= 0)
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
     const int H = L->hp.n_embd;
@@ -1247,6 +1496,7 @@ int dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *x
                               int32_t n_tokens, float *y_dev, void *stream)
 {
     if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (L && L->head) return set_err(ctx, DMOE_ERR_INVALID_ARG, "a step-tail layer: use dmoe_head_forward");
     if (!L || !x_dev || !y_dev || n_tokens <= 0)
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
     if ((uintptr_t)x_dev % 16)
@@ -1268,6 +1518,7 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
                                       int32_t n_tokens, float *y_dev, void *stream)
 {
     if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (L && L->head) return set_err(ctx, DMOE_ERR_INVALID_ARG, "a step-tail layer: use dmoe_head_forward");
     if (!L || !x_dev || !y_dev || n_tokens <= 0)
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
     if ((uintptr_t)x_dev % 16)

@@ -181,6 +181,10 @@ hipError_t launch_scores(const float *logits, const float *bias, int N, int E,
 hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s);
 // p[0 .. n) = v
 hipError_t launch_fill_i32(int32_t *p, int32_t v, int n, hipStream_t s);
+// Per row of V logits: the argmax (first index of the largest) and its
+// softmax probability 1 / sum exp(l - max) (k_head.hip).
+hipError_t launch_argmax_prob(const float *logits, int N, int V, int32_t *tokens, float *probs,
+                              hipStream_t s);
 // Grouped Q4_K expert products on MFMA (k_expert.hip).  phase 0: h = silu(gate x)
 // * (up x); phase 1: y = down h.
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item

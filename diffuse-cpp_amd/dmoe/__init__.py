@@ -34,7 +34,8 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_layer_forward_device_noalloc", "dmoe_dense_upload", "dmoe_dense_wrap_device",
            "dmoe_gguf_open", "dmoe_gguf_close", "dmoe_gguf_get_u32", "dmoe_gguf_get_f32",
            "dmoe_gguf_find_tensor", "dmoe_gguf_tensor_count", "dmoe_gguf_tensor_name",
-           "dmoe_gguf_moe_hparams", "dmoe_gguf_layer_desc", "dmoe_gguf_dense_desc")
+           "dmoe_gguf_moe_hparams", "dmoe_gguf_layer_desc", "dmoe_gguf_dense_desc",
+           "dmoe_head_upload", "dmoe_head_wrap_device", "dmoe_head_forward", "dmoe_head_forward_device")
 NOALLOC_SCRATCH_BYTES = 64 << 20
 N_STAGES = 10
 PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}
@@ -80,6 +81,11 @@ def load() -> C.CDLL:
     lib.dmoe_dense_upload.argtypes = [P, C.c_int32, C.c_int32, C.POINTER(Tensor), C.POINTER(Tensor),
                                       C.POINTER(Tensor), C.POINTER(P)]
     lib.dmoe_dense_wrap_device.argtypes = lib.dmoe_dense_upload.argtypes
+    lib.dmoe_head_upload.argtypes = [P, C.c_int32, C.c_int32, C.POINTER(Tensor), C.POINTER(Tensor),
+                                     C.POINTER(P)]
+    lib.dmoe_head_wrap_device.argtypes = lib.dmoe_head_upload.argtypes
+    lib.dmoe_head_forward.argtypes = [P, P, P, C.c_int32, C.c_float, P, P, P]
+    lib.dmoe_head_forward_device.argtypes = [P, P, P, C.c_int32, C.c_float, P, P, P, P]
     lib.dmoe_layer_forward.argtypes = [P, P, P, C.c_int32, P, C.POINTER(Debug)]
     lib.dmoe_layer_forward_device.argtypes = [P, P, P, C.c_int32, P, P]
     lib.dmoe_layer_forward_device_noalloc.argtypes = [P, P, P, C.c_int32, P, P]
@@ -217,6 +223,24 @@ class DenseWeights:
         return 2 * self.n_ff * row_size(self.wtype, self.n_embd) + self.n_embd * row_size(self.wtype, self.n_ff)
 
 
+@dataclass
+class HeadWeights:
+    """The step tail's tensors (diffuse_model's output_norm and output,
+    src/diffuse-common.h:94-96): norm f32 [n_embd] (numpy or torch), output
+    GGUF block bytes u8 [n_vocab, row_size(T, n_embd)] (ne [n_embd, n_vocab])."""
+    n_embd: int
+    n_vocab: int
+    wtype: int
+    norm: object
+    output: object
+
+    def output_view(self) -> Tensor:
+        return tensor_view(self.wtype, self.output, [self.n_embd, self.n_vocab])
+
+    def norm_view(self) -> Tensor:
+        return tensor_view(TYPE_F32, self.norm, [self.n_embd])
+
+
 def hparams_of(n_embd, n_experts, top_k, capacity, block_size, moe_ff=1, n_shared=0,
                shared_ff=0, norm_topk_prob=1, routed_scaling=2.5) -> HParams:
     hp = HParams()
@@ -349,6 +373,44 @@ class Context:
         """A dense MLP whose tensors already live on the GPU (dmoe_dense_wrap_device)."""
         return self._dense(load().dmoe_dense_wrap_device, w)
 
+    def _head(self, fn, w: "HeadWeights") -> Layer:
+        nv, ov = w.norm_view(), w.output_view()
+        out = C.c_void_p()
+        self._check(fn(self.handle, w.n_embd, w.n_vocab, C.byref(nv), C.byref(ov), C.byref(out)))
+        lw = LayerWeights(n_embd=w.n_embd, n_experts=0, top_k=0, capacity=0, block_size=0,
+                          moe_ff=0, wtype=w.wtype, gate_w=None, exp_gate=None, exp_up=None,
+                          exp_down=None)
+        layer = Layer(self, out.value, lw)
+        layer.n_vocab = w.n_vocab
+        return layer
+
+    def head_upload(self, w: "HeadWeights") -> Layer:
+        """The step tail (final norm + LM head) from host arrays (dmoe_head_upload)."""
+        return self._head(load().dmoe_head_upload, w)
+
+    def head_wrap_device(self, w: "HeadWeights") -> Layer:
+        return self._head(load().dmoe_head_wrap_device, w)
+
+    def head_forward(self, layer: Layer, h: np.ndarray, eps: float, logits: bool = False):
+        """(tokens i32 [N], probs f32 [N][, logits f32 [N][V]]) for h [N][n_embd]."""
+        h = np.ascontiguousarray(h, dtype=np.float32)
+        N = h.shape[0]
+        tok = np.zeros(N, np.int32)
+        prob = np.zeros(N, np.float32)
+        lg = np.zeros((N, layer.n_vocab), np.float32) if logits else None
+        self._check(load().dmoe_head_forward(self.handle, layer.handle, h.ctypes.data, N, float(eps),
+                                             tok.ctypes.data, prob.ctypes.data,
+                                             lg.ctypes.data if logits else None))
+        return (tok, prob, lg) if logits else (tok, prob)
+
+    def head_forward_device(self, layer: Layer, h_dev, n_tokens: int, eps: float, tokens_dev, probs_dev,
+                            logits_dev=None, stream=None):
+        s = 0 if stream is None else int(stream)
+        self._check(load().dmoe_head_forward_device(self.handle, layer.handle, _ptr(h_dev), n_tokens,
+                                                    float(eps), _ptr(tokens_dev), _ptr(probs_dev),
+                                                    _ptr(logits_dev) if logits_dev is not None else None,
+                                                    s or None))
+
     def forward(self, layer: Layer, x: np.ndarray, debug: bool = False):
         x = np.ascontiguousarray(x, dtype=np.float32)
         N = x.shape[0]
@@ -412,6 +474,6 @@ class Context:
                                                 nrows, n_per_row, s or None))
 
 
-__all__ = ["Context", "Layer", "LayerWeights", "DenseWeights", "DmoeError", "load", "tensor_view", "hparams_of",
+__all__ = ["Context", "Layer", "LayerWeights", "DenseWeights", "HeadWeights", "DmoeError", "load", "tensor_view", "hparams_of",
            "use_block_routing", "row_size", "TYPE_F32", "TYPE_F16", "TYPE_Q8_0", "TYPE_Q4_K",
            "TYPE_Q8_K", "TYPE_NAMES", "TYPE_BY_NAME", "EXPORTS", "LIB_PATH"]

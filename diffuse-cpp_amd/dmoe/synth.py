@@ -17,7 +17,7 @@ from dataclasses import dataclass, replace
 
 import numpy as np
 
-from . import (DenseWeights, LayerWeights, TYPE_F16, TYPE_F32, TYPE_Q4_K, TYPE_Q8_0, row_size)
+from . import (DenseWeights, HeadWeights, LayerWeights, TYPE_F16, TYPE_F32, TYPE_Q4_K, TYPE_Q8_0, row_size)
 
 _M1 = np.uint64(0x9E3779B97F4A7C15)
 _M2 = np.uint64(0xBF58476D1CE4E5B9)
@@ -55,6 +55,7 @@ def normal(seed: int, stream: int, n: int, std: float = 1.0) -> np.ndarray:
 # tensor stream ids
 S_X, S_GATE_W, S_BIAS, S_EG, S_EU, S_ED, S_SG, S_SU, S_SD = range(1, 10)
 S_FG, S_FU, S_FD = range(20, 23)        # dense MLP (ffn_gate, ffn_up, ffn_down)
+S_ONORM, S_OUT = 30, 31                 # step tail (output_norm, output)
 
 
 @dataclass(frozen=True)
@@ -247,3 +248,39 @@ def dense_to_host(w: DenseWeights) -> DenseWeights:
     def h(a):
         return a.detach().cpu().numpy() if hasattr(a, "detach") else a
     return replace(w, gate=h(w.gate), up=h(w.up), down=h(w.down))
+
+
+# The step tail of LLaDA2-flash: hidden 4096, vocabulary 157184.
+HEAD_FLASH = (4096, 157184)
+
+
+def host_head(n_embd: int, n_vocab: int, wtype: int, seed: int, quantize_rows,
+              w_std: float = 0.02) -> HeadWeights:
+    """output_norm ~ U(0.5, 1.5), output N(0, w_std) quantised by quantize_rows."""
+    f = normal(seed, S_OUT, n_vocab * n_embd, w_std).reshape(n_vocab, n_embd)
+    out = np.ascontiguousarray(quantize_rows(wtype, f)).view(np.uint8).reshape(n_vocab, row_size(wtype, n_embd))
+    return HeadWeights(n_embd=n_embd, n_vocab=n_vocab, wtype=wtype,
+                       norm=uniform(seed, S_ONORM, n_embd, 0.5, 1.5), output=out)
+
+
+def device_head(n_embd: int, n_vocab: int, wtype: int, seed: int, ctx, w_std: float = 0.02,
+                chunk_rows: int = 32768) -> HeadWeights:
+    import torch
+    dev = torch.device(f"cuda:{ctx.device}")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed * 7919 + 131)
+    out = torch.empty((n_vocab, row_size(wtype, n_embd)), dtype=torch.uint8, device=dev)
+    for r0 in range(0, n_vocab, chunk_rows):
+        r1 = min(n_vocab, r0 + chunk_rows)
+        f = torch.randn((r1 - r0, n_embd), generator=g, device=dev, dtype=torch.float32).mul_(w_std)
+        ctx.quantize_device(wtype, f, out[r0:r1], r1 - r0, n_embd)
+        torch.cuda.synchronize(dev)
+        del f
+    norm = torch.from_numpy(uniform(seed, S_ONORM, n_embd, 0.5, 1.5)).to(dev)
+    return HeadWeights(n_embd=n_embd, n_vocab=n_vocab, wtype=wtype, norm=norm, output=out)
+
+
+def head_to_host(w: HeadWeights) -> HeadWeights:
+    def h(a):
+        return a.detach().cpu().numpy() if hasattr(a, "detach") else a
+    return replace(w, norm=h(w.norm), output=h(w.output))

@@ -167,6 +167,33 @@ int  dmoe_dense_wrap_device(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff,
                             const dmoe_tensor *gate, const dmoe_tensor *up,
                             const dmoe_tensor *down, dmoe_layer **out);
 
+/* The step tail: the final norm and LM head (src/diffuse-moe-graph.cpp:
+ * 295-300) and the temperature-0 sampling of every position
+ * (sample_token, src/diffuse-sampler.cpp:29-49), without the logits leaving
+ * the GPU:
+ *   x = rms_norm(h, eps) * output_norm        output_norm F32 [n_embd] (F16 too for _upload)
+ *   logits = output x                         output T [n_embd, n_vocab], F32 weight semantics
+ *   tokens[t] = first index of the largest logit, probs[t] = 1 / sum exp(l - max)
+ * (output_norm / output of diffuse_model, src/diffuse-common.h:95-96).  The
+ * result is a dmoe_layer for dmoe_head_forward / _forward_device only. */
+int  dmoe_head_upload(dmoe_ctx *ctx, int32_t n_embd, int32_t n_vocab,
+                      const dmoe_tensor *output_norm, const dmoe_tensor *output,
+                      dmoe_layer **out);
+int  dmoe_head_wrap_device(dmoe_ctx *ctx, int32_t n_embd, int32_t n_vocab,
+                           const dmoe_tensor *output_norm, const dmoe_tensor *output,
+                           dmoe_layer **out);
+/* h [n_tokens][n_embd] f32 (the residual stream after the last layer);
+ * tokens, probs [n_tokens]; logits [n_tokens][n_vocab] may be NULL (the
+ * reference copies all of them out, src/diffuse-moe-graph.cpp:331-332).
+ * Host buffers, synchronous. */
+int  dmoe_head_forward(dmoe_ctx *ctx, const dmoe_layer *head, const float *h,
+                       int32_t n_tokens, float eps, int32_t *tokens, float *probs,
+                       float *logits);
+/* Device buffers, queued on `stream` without synchronising. */
+int  dmoe_head_forward_device(dmoe_ctx *ctx, const dmoe_layer *head, const float *h_dev,
+                              int32_t n_tokens, float eps, int32_t *tokens_dev,
+                              float *probs_dev, float *logits_dev, void *stream);
+
 /* Release a layer's device buffers.  The layer records its own device, so it
  * may be freed before or after the context that created it. */
 void dmoe_layer_free(dmoe_layer *layer);

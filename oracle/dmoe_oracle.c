@@ -729,6 +729,76 @@ int dmo_dense_forward(int n_embd, int n_ff, const dmoe_tensor *gate, const dmoe_
     return 0;
 }
 
+/* ggml_rms_norm (CPU definition): the f32 squares summed in binary64
+ * sequentially, mean = (float)(sum / n), scale = 1 / sqrtf(mean + eps),
+ * out = x * scale; then ggml_mul by the norm weight. */
+void dmo_rms_norm(const float *x, const float *w, int n, float eps, float *out)
+{
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) sum += (double)(x[i] * x[i]);
+    const float mean = (float)(sum / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < n; i++) {
+        const float v = x[i] * scale;
+        out[i] = w ? v * w[i] : v;
+    }
+}
+
+/* The temperature-0 branch of sample_token (src/diffuse-sampler.cpp:29-49):
+ * the first index of the largest logit (strict >, so a NaN never wins and a
+ * NaN logits[0] stays the answer), prob = 1 / sum of expf(l - max) added
+ * sequentially in float. */
+void dmo_argmax_prob(const float *logits, int n_vocab, int32_t *token, float *prob)
+{
+    int best = 0;
+    float best_val = logits[0];
+    for (int v = 1; v < n_vocab; v++)
+        if (logits[v] > best_val) {
+            best_val = logits[v];
+            best = v;
+        }
+    float sum = 0.0f;
+    for (int v = 0; v < n_vocab; v++) sum += dmo_expf(logits[v] - best_val);
+    *token = best;
+    *prob = 1.0f / sum;
+}
+
+int dmo_head_forward(int n_embd, int n_vocab, const float *norm_w, const dmoe_tensor *output,
+                     const float *h, int n_tokens, float eps, int32_t *tokens, float *probs,
+                     float *logits_out, int n_threads)
+{
+    const int H = n_embd, V = n_vocab, N = n_tokens;
+    if (H <= 0 || V <= 0 || N <= 0 || !output || !h || !tokens || !probs) return -1;
+#ifdef _OPENMP
+    if (n_threads <= 0) n_threads = omp_get_max_threads();
+    int saved_threads = omp_get_max_threads();
+    omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+    /* :296-297 cur = rms_norm(cur) * output_norm */
+    float *xn = (float *)malloc((size_t)N * H * 4);
+    float *logits = logits_out ? logits_out : (float *)malloc((size_t)N * V * 4);
+    for (int t = 0; t < N; t++) dmo_rms_norm(h + (size_t)t * H, norm_w, H, eps, xn + (size_t)t * H);
+    /* :299 logits = output x, the output weight cast to F32 (ensure_f32_moe) */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 64)
+#endif
+    for (int v = 0; v < V; v++) {
+        float *wrow = (float *)malloc((size_t)H * 4);
+        dmo_dequant_row(output->type, tensor_row(output, v, 0), wrow, H);
+        for (int t = 0; t < N; t++) logits[(size_t)t * V + v] = dot_f32(H, wrow, xn + (size_t)t * H);
+        free(wrow);
+    }
+    for (int t = 0; t < N; t++) dmo_argmax_prob(logits + (size_t)t * V, V, tokens + t, probs + t);
+    free(xn);
+    if (!logits_out) free(logits);
+#ifdef _OPENMP
+    omp_set_num_threads(saved_threads);
+#endif
+    return 0;
+}
+
 int dmo_layer_forward(const dmoe_hparams *hp, const dmoe_layer_desc *desc,
                       const float *x, int n_tokens, float *y,
                       dmoe_debug *dbg, int n_threads)

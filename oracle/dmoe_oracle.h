@@ -34,6 +34,13 @@
  *                                    weights within an analytic error budget
  *   dmo_dense_forward                pinned: float64 numpy SwiGLU on dequantised
  *                                    weights within the same error budget
+ *   dmo_rms_norm                     pinned: float64 numpy on random rows, an
+ *                                    all-equal row (closed form)
+ *   dmo_argmax_prob                  pinned: known answers (ties to the first
+ *                                    index, NaN first element, one-hot and
+ *                                    uniform rows) and float64 softmax
+ *   dmo_head_forward                 pinned: float64 numpy logits on the
+ *                                    dequantised output weight
  */
 #ifndef DMOE_ORACLE_H
 #define DMOE_ORACLE_H
@@ -113,6 +120,19 @@ int  dmo_layer_forward(const dmoe_hparams *hp, const dmoe_layer_desc *desc,
 int  dmo_dense_forward(int n_embd, int n_ff, const dmoe_tensor *gate, const dmoe_tensor *up,
                        const dmoe_tensor *down, const float *x, int n_tokens, float *y,
                        int n_threads);
+
+/* ---- step tail ------------------------------------------------------------
+ * ggml_rms_norm (binary64 sum of the f32 squares) times w (may be NULL). */
+void dmo_rms_norm(const float *x, const float *w, int n, float eps, float *out);
+/* sample_token at temperature 0 (src/diffuse-sampler.cpp:29-49). */
+void dmo_argmax_prob(const float *logits, int n_vocab, int32_t *token, float *prob);
+/* src/diffuse-moe-graph.cpp:295-300 then the sampler's argmax and confidence:
+ * x = rms_norm(h, eps) * norm_w, logits = output x (output [n_embd, n_vocab]
+ * cast to F32), per token the argmax and its softmax probability.
+ * logits_out [N][V] may be NULL. */
+int  dmo_head_forward(int n_embd, int n_vocab, const float *norm_w, const dmoe_tensor *output,
+                      const float *h, int n_tokens, float eps, int32_t *tokens, float *probs,
+                      float *logits_out, int n_threads);
 
 #ifdef __cplusplus
 }

@@ -76,6 +76,12 @@ def load() -> C.CDLL:
                                       C.POINTER(Debug), C.c_int]
     lib.dmo_dense_forward.argtypes = [C.c_int, C.c_int, C.POINTER(Tensor), C.POINTER(Tensor),
                                       C.POINTER(Tensor), P, C.c_int, P, C.c_int]
+    lib.dmo_rms_norm.argtypes = [P, P, C.c_int, C.c_float, P]
+    lib.dmo_rms_norm.restype = None
+    lib.dmo_argmax_prob.argtypes = [P, C.c_int, P, P]
+    lib.dmo_argmax_prob.restype = None
+    lib.dmo_head_forward.argtypes = [C.c_int, C.c_int, P, C.POINTER(Tensor), P, C.c_int, C.c_float,
+                                     P, P, P, C.c_int]
     _lib = lib
     return lib
 
@@ -234,6 +240,43 @@ def dense_forward(w, x: np.ndarray, n_threads: int = 0) -> np.ndarray:
     if rc:
         raise ValueError("oracle dense forward failed")
     return y
+
+
+def rms_norm(x: np.ndarray, w=None, eps: float = 1e-6) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    wp = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    for i in range(x.shape[0]):
+        load().dmo_rms_norm(_p(x[i]), _p(wp), x.shape[1], eps, _p(out[i]))
+    return out
+
+
+def argmax_prob(logits: np.ndarray):
+    """(tokens i32 [N], probs f32 [N]) of logits [N][V]."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    N, V = logits.shape
+    tok = np.zeros(N, np.int32)
+    prob = np.zeros(N, np.float32)
+    for i in range(N):
+        load().dmo_argmax_prob(_p(logits[i]), V, _p(tok[i:i + 1]), _p(prob[i:i + 1]))
+    return tok, prob
+
+
+def head_forward(w, h: np.ndarray, eps: float = 1e-6, n_threads: int = 0):
+    """w: dmoe.HeadWeights (numpy).  Returns (tokens, probs, logits)."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    N = h.shape[0]
+    V = w.n_vocab
+    tok = np.zeros(N, np.int32)
+    prob = np.zeros(N, np.float32)
+    logits = np.zeros((N, V), np.float32)
+    norm = np.ascontiguousarray(w.norm, dtype=np.float32)
+    ov = w.output_view()
+    rc = load().dmo_head_forward(w.n_embd, V, _p(norm), C.byref(ov), _p(h), N, eps, _p(tok), _p(prob),
+                                 _p(logits), n_threads)
+    if rc:
+        raise ValueError("oracle head forward failed")
+    return tok, prob, logits
 
 
 def n_threads_default() -> int:
