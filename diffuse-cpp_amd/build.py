@@ -37,7 +37,7 @@ CFLAGS = [
 ]
 
 SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "k_expert_q80.hip",
-           "k_gemm.hip", "k_norm.hip", "k_down_rows.hip", "k_head.hip", "dmoe_api.cpp", "dmoe_gguf.cpp"]
+           "k_gemm.hip", "k_norm.hip", "k_down_rows.hip", "k_head.hip", "k_attn.hip", "dmoe_api.cpp", "dmoe_gguf.cpp"]
 HEADERS = ["dmoe_internal.h", "dmoe_device.h", "dmoe_prep.h"]
 
 

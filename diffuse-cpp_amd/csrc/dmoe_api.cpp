@@ -56,6 +56,13 @@ struct dmoe_layer {
     // (LM head) weight in sd as a shared down matrix of n_vocab rows
     bool head = false;
     int32_t n_vocab = 0;
+    // the attention half of the layer: its projections as shared down
+    // matrices (aqkv: (nh + 2 nkv) hd rows of n_embd; awo: n_embd rows of
+    // nh hd), its norms f32
+    bool attn = false;
+    dmoe_attn_hparams ahp{};
+    WTensor aqkv{}, awo{};
+    float *attn_norm = nullptr, *post_norm = nullptr, *qn = nullptr, *kn = nullptr;
     std::vector<void *> owned;
 };
 
@@ -1020,22 +1027,122 @@ int head_path(int32_t type, int V, int H)
     return DP_GEMV;
 }
 
+// One projection y [N][rows] = W x with W's F32 semantics (x [N][K] f32):
+// the shared-down product of the expert kernels (Q4_K / Q8_0 on int8 digits,
+// F16 on hi / lo pairs) or the GEMV kernel.
+struct ProjWs {
+    int32_t *n_ec;                       // an empty routed work list
+    ActI8 act;                           // split x (int8 paths)
+    uint16_t *x16;                       // hi / lo f16 x (F16 path)
+};
+
+template <class Take>
+ProjWs plan_proj(int path, int N, int K, Take &&take)
+{
+    ProjWs p{};
+    p.n_ec = (int32_t *)take(4);
+    switch (path) {
+    case DP_Q4K: p.act = take_act(take, N, K, true); break;
+    case DP_Q80: p.act = take_act(take, N, K, true, true); break;
+    case DP_F16: p.x16 = (uint16_t *)take((size_t)2 * N * K * 2); break;
+    default: break;
+    }
+    return p;
+}
+
+int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTensor &W, int rows, int K,
+                 const float *x, int N, float *y, const ProjWs &p, hipStream_t s)
+{
+    const int path = head_path(W.type, rows, K);
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
+    if (path == DP_GEMV) {
+        STAGE(st_prod, launch_down_shared(W, x, N, K, rows, y, s));
+        return DMOE_OK;
+    }
+    LAUNCH_TRY(ctx, launch_fill_i32(p.n_ec, 0, 1, s));
+    WorkList wl{};
+    wl.n_ec = p.n_ec;
+    if (path == DP_F16) {
+        wl.chunk = GM;
+        GemmJob job{};
+        job.sd = W;
+        job.has_shared = 1;
+        job.H = rows;
+        job.FF = K;
+        job.SF = K;
+        job.n_tokens = N;
+        job.top_k = 1;
+        job.wl = wl;
+        job.hs16 = p.x16;
+        job.ys = y;
+        STAGE(st_conv, launch_cvt_f16(x, N, K, 1, p.x16, s));
+        STAGE(st_prod, launch_gemm_f16(1, job, s));
+        return DMOE_OK;
+    }
+    const bool q8 = path == DP_Q80;
+    wl.chunk = EXPERT_CHUNK;
+    MoeJob job{};
+    job.sd = W;
+    job.has_shared = 1;
+    job.H = rows;                        // output rows
+    job.FF = K;                          // reduction length
+    job.SF = K;
+    job.n_tokens = N;
+    job.top_k = 1;
+    job.wl = wl;
+    job.ax.K = rows;
+    job.ah.K = K;
+    job.ahs = p.act;
+    job.ys = y;
+    PrepJob pj{x, N, K, q8 ? ACT_SPLIT32 : ACT_SPLIT, p.act};
+    STAGE(st_conv, launch_prep(&pj, 1, s));
+    STAGE(st_prod, q8 ? launch_expert_q80(1, job, s) : launch_expert_q4k(1, job, s));
+#undef STAGE
+    return DMOE_OK;
+}
+
+// Tiles a projection weight for its path (library-owned copy).
+int tile_proj(dmoe_ctx *ctx, dmoe_layer *L, WTensor &W, int rows, int K)
+{
+    switch (head_path(W.type, rows, K)) {
+    case DP_Q4K: return tile_tensor(ctx, L, W, rows, K, 1);
+    case DP_Q80: return tile_tensor_q80(ctx, L, W, rows, K, 1);
+    case DP_F16: return tile_tensor_f16(ctx, L, W, rows, K, 1);
+    default: return DMOE_OK;
+    }
+}
+
+// Grows the context workspace to `need` bytes (synchronising before a free).
+int grow_workspace(dmoe_ctx *ctx, size_t need)
+{
+    if (need <= ctx->ws_bytes) return DMOE_OK;
+    if (ctx->ws) {
+        HIP_TRY(ctx, hipDeviceSynchronize());
+        HIP_TRY(ctx, hipFree(ctx->ws));
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    if (getenv("DMOE_FAIL_ALLOC"))
+        return set_err(ctx, DMOE_ERR_OOM, "workspace allocation of %zu bytes refused (DMOE_FAIL_ALLOC)", need);
+    HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
+    ctx->ws_bytes = need;
+    return DMOE_OK;
+}
+
 struct HeadWs {
     float *h;                            // host input copy
     int32_t *tokens;                     // host output staging
     float *probs;
     float *xn;                           // rms_norm(h) * output_norm
     float *logits;                       // [N][V] (unless the caller's)
-    int32_t *n_ec;
-    ActI8 ahs;                           // split xn (int8 paths)
-    uint16_t *hs16;                      // hi / lo f16 xn (F16 path)
+    ProjWs proj;
 };
 
 size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint8_t *base, HeadWs *w)
 {
     const int H = L->hp.n_embd, V = L->n_vocab;
     size_t off = 0;
-    std::function<uint8_t *(size_t)> take = [&](size_t bytes) -> uint8_t * {
+    auto take = [&](size_t bytes) -> uint8_t * {
         uint8_t *p = base ? base + off : nullptr;
         off += align_up(bytes > 0 ? bytes : 1);
         return p;
@@ -1048,13 +1155,7 @@ size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint
     }
     t.xn = (float *)take((size_t)N * H * 4);
     if (own_logits) t.logits = (float *)take((size_t)N * V * 4);
-    t.n_ec = (int32_t *)take(4);
-    switch (head_path(L->sd.type, V, H)) {
-    case DP_Q4K: t.ahs = take_act(take, N, H, true); break;
-    case DP_Q80: t.ahs = take_act(take, N, H, true, true); break;
-    case DP_F16: t.hs16 = (uint16_t *)take((size_t)2 * N * H * 2); break;
-    default: break;
-    }
+    t.proj = plan_proj(head_path(L->sd.type, V, H), N, H, take);
     if (w) *w = t;
     return off;
 }
@@ -1062,19 +1163,8 @@ size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint
 int ensure_head_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, bool own_logits,
                           HeadWs *w)
 {
-    const size_t need = plan_head(L, N, host_io, own_logits, nullptr, nullptr);
-    if (need > ctx->ws_bytes) {
-        if (ctx->ws) {
-            HIP_TRY(ctx, hipDeviceSynchronize());
-            HIP_TRY(ctx, hipFree(ctx->ws));
-            ctx->ws = nullptr;
-            ctx->ws_bytes = 0;
-        }
-        if (getenv("DMOE_FAIL_ALLOC"))
-            return set_err(ctx, DMOE_ERR_OOM, "workspace allocation of %zu bytes refused (DMOE_FAIL_ALLOC)", need);
-        HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
-        ctx->ws_bytes = need;
-    }
+    int rc = grow_workspace(ctx, plan_head(L, N, host_io, own_logits, nullptr, nullptr));
+    if (rc) return rc;
     plan_head(L, N, host_io, own_logits, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
 }
@@ -1087,50 +1177,90 @@ int enqueue_head(dmoe_ctx *ctx, const dmoe_layer *L, const HeadWs &w, const floa
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
     // :296-297 rms_norm(cur) * output_norm (h is only read: no residual add)
     STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->gate_w, w.xn, N, H, eps, s));
-    const int path = head_path(L->sd.type, V, H);
-    if (path == DP_GEMV) {
-        STAGE(ST_SH_DOWN, launch_down_shared(L->sd, w.xn, N, H, V, logits, s));
-    } else {
-        LAUNCH_TRY(ctx, launch_fill_i32(w.n_ec, 0, 1, s));
-        WorkList wl{};
-        wl.n_ec = w.n_ec;
-        if (path == DP_F16) {
-            wl.chunk = GM;
-            GemmJob job{};
-            job.sd = L->sd;
-            job.has_shared = 1;
-            job.H = V;
-            job.FF = H;
-            job.SF = H;
-            job.n_tokens = N;
-            job.top_k = 1;
-            job.wl = wl;
-            job.hs16 = w.hs16;
-            job.ys = logits;
-            STAGE(ST_ACTQ_H, launch_cvt_f16(w.xn, N, H, 1, w.hs16, s));
-            STAGE(ST_SH_DOWN, launch_gemm_f16(1, job, s));
-        } else {
-            const bool q8 = path == DP_Q80;
-            wl.chunk = EXPERT_CHUNK;
-            MoeJob job{};
-            job.sd = L->sd;
-            job.has_shared = 1;
-            job.H = V;                       // output rows
-            job.FF = H;                      // reduction length
-            job.SF = H;
-            job.n_tokens = N;
-            job.top_k = 1;
-            job.wl = wl;
-            job.ax.K = V;
-            job.ah.K = H;
-            job.ahs = w.ahs;
-            job.ys = logits;
-            PrepJob pj{w.xn, N, H, q8 ? ACT_SPLIT32 : ACT_SPLIT, w.ahs};
-            STAGE(ST_ACTQ_H, launch_prep(&pj, 1, s));
-            STAGE(ST_SH_DOWN, q8 ? launch_expert_q80(1, job, s) : launch_expert_q4k(1, job, s));
-        }
-    }
+    int rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->sd, V, H, w.xn, N, logits, w.proj, s);
+    if (rc) return rc;
     STAGE(ST_COMBINE, launch_argmax_prob(logits, N, V, tokens, probs, s));
+#undef STAGE
+    return DMOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Attention half of the layer (src/diffuse-moe-graph.cpp:116-178).
+struct AttnWs {
+    float *h, *h_out, *moe_in;           // host io copies
+    float *xn;                           // rms_norm(h) * attn_norm       [N][H]
+    float *qkv;                          // fused projection              [N][QKV]
+    float *Qh, *Kh, *Vh;                 // head-major after norm / RoPE
+    float *att;                          // attention output              [N][nh hd]
+    float *proj;                         // output projection             [N][H]
+    float *scratch;                      // post-norm output when not wanted [N][H]
+    ProjWs pq, po;
+};
+
+size_t plan_attn(const dmoe_layer *L, int N, bool host_io, uint8_t *base, AttnWs *w)
+{
+    const dmoe_attn_hparams &a = L->ahp;
+    const int H = a.n_embd, QD = a.n_head * a.head_dim, KD = a.n_head_kv * a.head_dim, QKV = QD + 2 * KD;
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> uint8_t * {
+        uint8_t *p = base ? base + off : nullptr;
+        off += align_up(bytes > 0 ? bytes : 1);
+        return p;
+    };
+    AttnWs t{};
+    if (host_io) {
+        t.h = (float *)take((size_t)N * H * 4);
+        t.h_out = (float *)take((size_t)N * H * 4);
+        t.moe_in = (float *)take((size_t)N * H * 4);
+    }
+    t.xn = (float *)take((size_t)N * H * 4);
+    t.qkv = (float *)take((size_t)N * QKV * 4);
+    t.Qh = (float *)take((size_t)N * QD * 4);
+    t.Kh = (float *)take((size_t)N * KD * 4);
+    t.Vh = (float *)take((size_t)N * KD * 4);
+    t.att = (float *)take((size_t)N * QD * 4);
+    t.proj = (float *)take((size_t)N * H * 4);
+    t.scratch = (float *)take((size_t)N * H * 4);
+    t.pq = plan_proj(head_path(L->aqkv.type, QKV, H), N, H, take);
+    t.po = plan_proj(head_path(L->awo.type, H, QD), N, QD, take);
+    if (w) *w = t;
+    return off;
+}
+
+int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const float *h, int N, float *h_out,
+                 float *moe_in, hipStream_t s)
+{
+    const dmoe_attn_hparams &a = L->ahp;
+    const int H = a.n_embd, QD = a.n_head * a.head_dim, KD = a.n_head_kv * a.head_dim, QKV = QD + 2 * KD;
+    const bool prof = ctx->prof;
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
+    // :120-121 input layernorm
+    STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->attn_norm, w.xn, N, H,
+                                            a.rms_eps, s));
+    // :124 fused QKV
+    int rc = enqueue_proj(ctx, prof, ST_ACTQ_X, ST_SH_GATEUP, L->aqkv, QKV, H, w.xn, N, w.qkv, w.pq, s);
+    if (rc) return rc;
+    AttnDims d{};
+    d.n = N;
+    d.nh = a.n_head;
+    d.nkv = a.n_head_kv;
+    d.hd = a.head_dim;
+    d.rd = a.rotary_dim;
+    d.qk_norm = a.use_qk_norm;
+    d.block = a.block_length;
+    d.eps = a.rms_eps;
+    // the rope cache's angle step, as ggml computes it on the host
+    d.theta_scale = a.rotary_dim > 0 ? powf(a.rope_base, -2.0f / (float)a.rotary_dim) : 1.0f;
+    d.scale = 1.0f / sqrtf((float)a.head_dim);
+    STAGE(ST_ROUTE, launch_qk_rope(w.qkv, L->qn, L->kn, d, w.Qh, w.Kh, w.Vh, s));
+    STAGE(ST_SCORES, launch_attn(w.Qh, w.Kh, w.Vh, d, w.att, s));
+    // :172 output projection
+    if ((rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->awo, H, QD, w.att, N, w.proj, w.po, s)))
+        return rc;
+    // :175-178 residual, then the post-attention layernorm (the MoE input)
+    if (h_out != h) HIP_TRY(ctx, hipMemcpyAsync(h_out, h, (size_t)N * H * 4, hipMemcpyDeviceToDevice, s));
+    STAGE(ST_COMBINE, launch_residual_rmsnorm(h_out, w.proj, L->post_norm, moe_in ? moe_in : w.scratch, N, H,
+                                              a.rms_eps, s));
 #undef STAGE
     return DMOE_OK;
 }
@@ -1307,21 +1437,41 @@ static int dense_create(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff, const dmoe_
     return DMOE_OK;
 }
 
+static int f32_vector(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_tensor &t, int n, bool device_mode,
+                      const char *name, float **out)
+{
+    if (!t.data) return set_err(ctx, DMOE_ERR_INVALID_ARG, "%s: data is NULL", name);
+    if (t.ne[0] != n || t.ne[1] > 1)
+        return set_err(ctx, DMOE_ERR_SHAPE, "%s: ne0 = %lld, expected %d", name, (long long)t.ne[0], n);
+    if (t.type != DMOE_TYPE_F32 && !(t.type == DMOE_TYPE_F16 && !device_mode))
+        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "%s: type %d", name, t.type);
+    if (device_mode) {
+        if ((uintptr_t)t.data % 16) return set_err(ctx, DMOE_ERR_SHAPE, "%s: device data not 16-byte aligned", name);
+        *out = (float *)t.data;
+        return DMOE_OK;
+    }
+    std::vector<float> w((size_t)n);
+    for (int k = 0; k < n; k++)
+        w[k] = t.type == DMOE_TYPE_F32 ? ((const float *)t.data)[k] : f16_to_f32_host(((const uint16_t *)t.data)[k]);
+    void *dev = nullptr;
+    hipError_t he = hipMalloc(&dev, (size_t)n * 4);
+    if (he != hipSuccess) return set_err(ctx, DMOE_ERR_OOM, "hipMalloc %s: %s", name, hipGetErrorString(he));
+    L->owned.push_back(dev);
+    he = hipMemcpy(dev, w.data(), (size_t)n * 4, hipMemcpyHostToDevice);
+    if (he != hipSuccess) return set_err(ctx, DMOE_ERR_HIP, "%s copy: %s", name, hipGetErrorString(he));
+    *out = (float *)dev;
+    return DMOE_OK;
+}
+
 static int head_create(dmoe_ctx *ctx, int32_t n_embd, int32_t n_vocab, const dmoe_tensor *norm,
                        const dmoe_tensor *output, bool device_mode, dmoe_layer **out)
 {
     if (!ctx || !out) return DMOE_ERR_INVALID_ARG;
     *out = nullptr;
-    if (!norm || !output || !norm->data) return set_err(ctx, DMOE_ERR_INVALID_ARG, "head: NULL tensor");
+    if (!norm || !output) return set_err(ctx, DMOE_ERR_INVALID_ARG, "head: NULL tensor");
     const int H = n_embd, V = n_vocab;
     if (H <= 0 || H % 256) return set_err(ctx, DMOE_ERR_SHAPE, "head: n_embd = %d must be a positive multiple of 256", H);
     if (V <= 0) return set_err(ctx, DMOE_ERR_SHAPE, "head: n_vocab = %d", V);
-    if (norm->ne[0] != H || norm->ne[1] > 1)
-        return set_err(ctx, DMOE_ERR_SHAPE, "output_norm: ne0 = %lld, expected %d", (long long)norm->ne[0], H);
-    if (norm->type != DMOE_TYPE_F32 && !(norm->type == DMOE_TYPE_F16 && !device_mode))
-        return set_err(ctx, DMOE_ERR_UNSUPPORTED_TYPE, "output_norm: type %d", norm->type);
-    if (device_mode && (uintptr_t)norm->data % 16)
-        return set_err(ctx, DMOE_ERR_SHAPE, "output_norm: device data not 16-byte aligned");
     int rc;
     if ((rc = check_tensor(ctx, "output", *output, H, V, 0, device_mode))) return rc;
     HIP_TRY(ctx, hipSetDevice(ctx->device));
@@ -1336,30 +1486,12 @@ static int head_create(dmoe_ctx *ctx, int32_t n_embd, int32_t n_vocab, const dmo
         dmoe_layer_free(L);
         return code;
     };
-    if (device_mode) {
-        L->gate_w = (float *)norm->data;
+    if ((rc = f32_vector(ctx, L, *norm, H, device_mode, "output_norm", &L->gate_w))) return fail(rc);
+    if (device_mode)
         L->sd = wrap_tensor(*output);
-    } else {
-        std::vector<float> w((size_t)H);
-        for (int k = 0; k < H; k++)
-            w[k] = norm->type == DMOE_TYPE_F32 ? ((const float *)norm->data)[k]
-                                               : f16_to_f32_host(((const uint16_t *)norm->data)[k]);
-        void *dev = nullptr;
-        hipError_t he = hipMalloc(&dev, (size_t)H * 4);
-        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_OOM, "hipMalloc output_norm: %s", hipGetErrorString(he)));
-        L->owned.push_back(dev);
-        he = hipMemcpy(dev, w.data(), (size_t)H * 4, hipMemcpyHostToDevice);
-        if (he != hipSuccess) return fail(set_err(ctx, DMOE_ERR_HIP, "output_norm copy: %s", hipGetErrorString(he)));
-        L->gate_w = (float *)dev;
-        if ((rc = upload_tensor(ctx, L, *output, V, 1, L->sd))) return fail(rc);
-    }
-    switch (head_path(L->sd.type, V, H)) {
-    case DP_Q4K: rc = tile_tensor(ctx, L, L->sd, V, H, 1); break;
-    case DP_Q80: rc = tile_tensor_q80(ctx, L, L->sd, V, H, 1); break;
-    case DP_F16: rc = tile_tensor_f16(ctx, L, L->sd, V, H, 1); break;
-    default: rc = DMOE_OK; break;
-    }
-    if (rc) return fail(rc);
+    else if ((rc = upload_tensor(ctx, L, *output, V, 1, L->sd)))
+        return fail(rc);
+    if ((rc = tile_proj(ctx, L, L->sd, V, H))) return fail(rc);
     *out = L;
     return DMOE_OK;
 }
@@ -1422,6 +1554,110 @@ int dmoe_head_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *h_
                         logits_dev ? logits_dev : w.logits, (hipStream_t)stream);
 }
 
+static int attn_create(dmoe_ctx *ctx, const dmoe_attn_hparams *ap, const dmoe_attn_desc *d, bool device_mode,
+                       dmoe_layer **out)
+{
+    if (!ctx || !out) return DMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    if (!ap || !d) return set_err(ctx, DMOE_ERR_INVALID_ARG, "attn: hparams / desc is NULL");
+    const dmoe_attn_hparams a = *ap;
+    if (a.n_embd <= 0 || a.n_embd % 256) return set_err(ctx, DMOE_ERR_SHAPE, "attn: n_embd = %d must be a positive multiple of 256", a.n_embd);
+    if (a.n_head <= 0 || a.n_head_kv <= 0 || a.n_head % a.n_head_kv)
+        return set_err(ctx, DMOE_ERR_SHAPE, "attn: n_head = %d, n_head_kv = %d", a.n_head, a.n_head_kv);
+    if (a.head_dim != 64 && a.head_dim != 128)
+        return set_err(ctx, DMOE_ERR_SHAPE, "attn: head_dim = %d (64 or 128 supported)", a.head_dim);
+    if (a.rotary_dim < 0 || a.rotary_dim > a.head_dim || a.rotary_dim % 2)
+        return set_err(ctx, DMOE_ERR_SHAPE, "attn: rotary_dim = %d", a.rotary_dim);
+    if (!(a.rms_eps >= 0.0f) || !(a.rope_base > 0.0f))
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "attn: rms_eps / rope_base out of range");
+    const int H = a.n_embd, QD = a.n_head * a.head_dim, QKV = QD + 2 * a.n_head_kv * a.head_dim;
+    if (QD % 256) return set_err(ctx, DMOE_ERR_SHAPE, "attn: n_head * head_dim = %d not a multiple of 256", QD);
+    int rc;
+    if ((rc = check_tensor(ctx, "attn_qkv", d->qkv, H, QKV, 0, device_mode))) return rc;
+    if ((rc = check_tensor(ctx, "attn_output", d->wo, QD, H, 0, device_mode))) return rc;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    dmoe_layer *L = new (std::nothrow) dmoe_layer();
+    if (!L) return set_err(ctx, DMOE_ERR_OOM, "host allocation failed");
+    L->ctx = ctx;
+    L->device = ctx->device;
+    L->attn = true;
+    L->ahp = a;
+    L->hp.n_embd = H;
+    auto fail = [&](int code) {
+        dmoe_layer_free(L);
+        return code;
+    };
+    if ((rc = f32_vector(ctx, L, d->attn_norm, H, device_mode, "attn_norm", &L->attn_norm))) return fail(rc);
+    if (d->post_attn_norm.data &&
+        (rc = f32_vector(ctx, L, d->post_attn_norm, H, device_mode, "post_attn_norm", &L->post_norm)))
+        return fail(rc);
+    if (a.use_qk_norm) {
+        if ((rc = f32_vector(ctx, L, d->q_norm, a.head_dim, device_mode, "attn_q_norm", &L->qn))) return fail(rc);
+        if ((rc = f32_vector(ctx, L, d->k_norm, a.head_dim, device_mode, "attn_k_norm", &L->kn))) return fail(rc);
+    }
+    if (device_mode) {
+        L->aqkv = wrap_tensor(d->qkv);
+        L->awo = wrap_tensor(d->wo);
+    } else if ((rc = upload_tensor(ctx, L, d->qkv, QKV, 1, L->aqkv)) ||
+               (rc = upload_tensor(ctx, L, d->wo, H, 1, L->awo))) {
+        return fail(rc);
+    }
+    if ((rc = tile_proj(ctx, L, L->aqkv, QKV, H)) || (rc = tile_proj(ctx, L, L->awo, H, QD))) return fail(rc);
+    *out = L;
+    return DMOE_OK;
+}
+
+int dmoe_attn_upload(dmoe_ctx *ctx, const dmoe_attn_hparams *ap, const dmoe_attn_desc *desc, dmoe_layer **out)
+{
+    return attn_create(ctx, ap, desc, false, out);
+}
+
+int dmoe_attn_wrap_device(dmoe_ctx *ctx, const dmoe_attn_hparams *ap, const dmoe_attn_desc *desc,
+                          dmoe_layer **out)
+{
+    return attn_create(ctx, ap, desc, true, out);
+}
+
+int dmoe_attn_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *h, int32_t n_tokens, float *h_out,
+                      float *moe_in)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!L || !L->attn) return set_err(ctx, DMOE_ERR_INVALID_ARG, "not an attention layer (dmoe_attn_upload)");
+    if (!h || !h_out || n_tokens <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "h/h_out NULL or n_tokens = %d", n_tokens);
+    const int H = L->ahp.n_embd;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int rc = grow_workspace(ctx, plan_attn(L, n_tokens, true, nullptr, nullptr));
+    if (rc) return rc;
+    AttnWs w;
+    plan_attn(L, n_tokens, true, (uint8_t *)ctx->ws, &w);
+    hipStream_t s = ctx->stream;
+    HIP_TRY(ctx, hipMemcpyAsync(w.h, h, (size_t)n_tokens * H * 4, hipMemcpyHostToDevice, s));
+    if ((rc = enqueue_attn(ctx, L, w, w.h, n_tokens, w.h_out, moe_in ? w.moe_in : nullptr, s))) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(h_out, w.h_out, (size_t)n_tokens * H * 4, hipMemcpyDeviceToHost, s));
+    if (moe_in) HIP_TRY(ctx, hipMemcpyAsync(moe_in, w.moe_in, (size_t)n_tokens * H * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return DMOE_OK;
+}
+
+int dmoe_attn_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *h_dev, int32_t n_tokens,
+                             float *h_out_dev, float *moe_in_dev, void *stream)
+{
+    if (!ctx) return DMOE_ERR_INVALID_ARG;
+    if (!L || !L->attn) return set_err(ctx, DMOE_ERR_INVALID_ARG, "not an attention layer (dmoe_attn_upload)");
+    if (!h_dev || !h_out_dev || n_tokens <= 0)
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "h/h_out NULL or n_tokens = %d", n_tokens);
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(h_dev) || !al16(h_out_dev) || (moe_in_dev && !al16(moe_in_dev)))
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "device buffers must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int rc = grow_workspace(ctx, plan_attn(L, n_tokens, false, nullptr, nullptr));
+    if (rc) return rc;
+    AttnWs w;
+    plan_attn(L, n_tokens, false, (uint8_t *)ctx->ws, &w);
+    return enqueue_attn(ctx, L, w, h_dev, n_tokens, h_out_dev, moe_in_dev, (hipStream_t)stream);
+}
+
 int dmoe_dense_upload(dmoe_ctx *ctx, int32_t n_embd, int32_t n_ff, const dmoe_tensor *gate,
                       const dmoe_tensor *up, const dmoe_tensor *down, dmoe_layer **out)
 {
@@ -1450,6 +1686,10 @@ int dmoe_layer_kernel_path(const dmoe_layer *L)
     static const int kmap[] = {DMOE_PATH_GEMV, DMOE_PATH_Q4K_MFMA, DMOE_PATH_Q80_MFMA, DMOE_PATH_F16_GEMM};
     if (L->dense) return kmap[dense_path(L->sg.type, L->hp.n_embd, L->hp.shared_ff)];
     if (L->head) return kmap[head_path(L->sd.type, L->n_vocab, L->hp.n_embd)];
+    if (L->attn) {
+        const int QD = L->ahp.n_head * L->ahp.head_dim, QKV = QD + 2 * L->ahp.n_head_kv * L->ahp.head_dim;
+        return kmap[head_path(L->aqkv.type, QKV, L->ahp.n_embd)];
+    }
     if (use_mfma_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q4K_MFMA;
     if (use_q80_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_Q80_MFMA;
     if (use_gemm_path(L->hp, L->eg.type, L->sg.type, L->has_shared)) return DMOE_PATH_F16_GEMM;
@@ -1460,7 +1700,8 @@ int dmoe_layer_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *x, int32
                        float *y, dmoe_debug *dbg)
 {
     if (!ctx) return DMOE_ERR_INVALID_ARG;
-    if (L && L->head) return set_err(ctx, DMOE_ERR_INVALID_ARG, "a step-tail layer: use dmoe_head_forward");
+    if (L && (L->head || L->attn))
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "not a MoE / dense layer (a step-tail or attention layer)");
     if (!L || !x || !y || n_tokens <= 0)
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
     const int H = L->hp.n_embd;
@@ -1496,7 +1737,8 @@ int dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *x
                               int32_t n_tokens, float *y_dev, void *stream)
 {
     if (!ctx) return DMOE_ERR_INVALID_ARG;
-    if (L && L->head) return set_err(ctx, DMOE_ERR_INVALID_ARG, "a step-tail layer: use dmoe_head_forward");
+    if (L && (L->head || L->attn))
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "not a MoE / dense layer (a step-tail or attention layer)");
     if (!L || !x_dev || !y_dev || n_tokens <= 0)
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
     if ((uintptr_t)x_dev % 16)
@@ -1518,7 +1760,8 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
                                       int32_t n_tokens, float *y_dev, void *stream)
 {
     if (!ctx) return DMOE_ERR_INVALID_ARG;
-    if (L && L->head) return set_err(ctx, DMOE_ERR_INVALID_ARG, "a step-tail layer: use dmoe_head_forward");
+    if (L && (L->head || L->attn))
+        return set_err(ctx, DMOE_ERR_INVALID_ARG, "not a MoE / dense layer (a step-tail or attention layer)");
     if (!L || !x_dev || !y_dev || n_tokens <= 0)
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "layer/x/y NULL or n_tokens = %d", n_tokens);
     if ((uintptr_t)x_dev % 16)

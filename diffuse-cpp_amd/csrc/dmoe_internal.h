@@ -181,6 +181,19 @@ hipError_t launch_scores(const float *logits, const float *bias, int N, int E,
 hipError_t launch_prep(const PrepJob *jobs, int njobs, hipStream_t s);
 // p[0 .. n) = v
 hipError_t launch_fill_i32(int32_t *p, int32_t v, int n, hipStream_t s);
+// The attention half of the layer (k_attn.hip).
+struct AttnDims {
+    int32_t n, nh, nkv, hd, rd;          // tokens, heads, kv heads, head_dim, rotary_dim
+    int32_t qk_norm, block;              // use_qk_norm, block_length (0: bidirectional)
+    float eps, theta_scale, scale;       // rms eps, powf(base, -2/rd), 1/sqrt(hd)
+};
+// fused QKV rows [N][(nh + 2 nkv) hd] -> QK RMSNorm, partial NEOX RoPE ->
+// head-major Q [nh][N][hd], K, V [nkv][N][hd]
+hipError_t launch_qk_rope(const float *qkv, const float *qn, const float *kn, const AttnDims &a, float *Qh,
+                          float *Kh, float *Vh, hipStream_t s);
+// block-causal GQA attention -> out [N][nh hd]
+hipError_t launch_attn(const float *Qh, const float *Kh, const float *Vh, const AttnDims &a, float *out,
+                       hipStream_t s);
 // Per row of V logits: the argmax (first index of the largest) and its
 // softmax probability 1 / sum exp(l - max) (k_head.hip).
 hipError_t launch_argmax_prob(const float *logits, int N, int V, int32_t *tokens, float *probs,

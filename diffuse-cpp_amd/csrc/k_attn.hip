@@ -1,0 +1,238 @@
+// k_attn.hip — the attention half of the LLaDA2 layer on gfx950
+// (src/diffuse-moe-graph.cpp:116-178), between the fused QKV projection and
+// the output projection (both run on the expert kernels' shared-down path).
+//
+// k_qk_rope: per (token, head) one wavefront: the head's slice of the fused
+//   QKV row (Q heads, then K heads, then V heads, :132-134), the QK RMSNorm
+//   over head_dim times q_norm / k_norm (:141-146; binary64 sum of the f32
+//   squares, as ggml_rms_norm), the partial NEOX RoPE of the first rotary_dim
+//   dims at position t (:154-155): pair ic = (x[ic], x[ic + rd/2]) rotated by
+//   theta = t * theta_scale^ic, the angle formed by repeated f32
+//   multiplication as ggml's rope cache does (theta_scale = powf(base,
+//   -2/rd), computed on the host); V heads are copied.  Output head-major:
+//   Q [n_head][N][hd], K and V [n_head_kv][N][hd].
+//
+// k_attn: flash attention with the block-causal mask of :19-55 (query i sees
+//   key j iff j / B <= i / B; every key when B <= 0), scale 1/sqrt(hd), GQA
+//   query head h on kv head h / (n_head / n_head_kv) (:158-167).  One
+//   workgroup per (64 queries, head), four wavefronts of 16 queries each;
+//   64-key tiles of K and V staged in LDS; S = Q K^T and O += P V on
+//   v_mfma_f32_16x16x4f32 (fp32 operands and accumulation), online softmax
+//   per query row in registers.  Keys past the last block a query tile can
+//   see are not visited.
+#include "dmoe_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace dmoe {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int QR_THREADS = 256;
+
+__global__ __launch_bounds__(QR_THREADS) void k_qk_rope(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                        const float *__restrict__ kn, AttnDims a,
+                                                        float *__restrict__ Qh, float *__restrict__ Kh,
+                                                        float *__restrict__ Vh)
+{
+    __shared__ float s_x[QR_THREADS / 64][256];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int heads = a.nh + 2 * a.nkv;
+    const int item = blockIdx.x * (QR_THREADS / 64) + w;
+    if (item >= a.n * heads) return;
+    const int t = item / heads, hh = item % heads;
+    const int HD = a.hd, QKV = (a.nh + 2 * a.nkv) * HD;
+    const float *src = qkv + (size_t)t * QKV + (size_t)hh * HD;
+    float *x = s_x[w];
+    for (int d = lane; d < HD; d += 64) x[d] = src[d];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (hh < a.nh + a.nkv) {
+        if (a.qk_norm) {
+            double acc = 0.0;
+            for (int d = lane; d < HD; d += 64) acc += (double)(x[d] * x[d]);
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+            const float mean = (float)(acc / (double)HD);
+            const float scale = 1.0f / sqrtf(mean + a.eps);
+            const float *nw = hh < a.nh ? qn : kn;
+            for (int d = lane; d < HD; d += 64) x[d] = (x[d] * scale) * nw[d];
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        }
+        const int half = a.rd / 2;
+        if (lane < half) {
+            float theta = (float)t;
+            for (int i = 0; i < lane; i++) theta *= a.theta_scale;
+            const float c = cosf(theta), sn = sinf(theta);
+            const float x0 = x[lane], x1 = x[lane + half];
+            x[lane] = x0 * c - x1 * sn;
+            x[lane + half] = x0 * sn + x1 * c;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+    float *dst;
+    if (hh < a.nh)
+        dst = Qh + ((size_t)hh * a.n + t) * HD;
+    else if (hh < a.nh + a.nkv)
+        dst = Kh + ((size_t)(hh - a.nh) * a.n + t) * HD;
+    else
+        dst = Vh + ((size_t)(hh - a.nh - a.nkv) * a.n + t) * HD;
+    for (int d = lane; d < HD; d += 64) dst[d] = x[d];
+}
+
+hipError_t launch_qk_rope(const float *qkv, const float *qn, const float *kn, const AttnDims &a, float *Qh,
+                          float *Kh, float *Vh, hipStream_t s)
+{
+    if (a.hd <= 0 || a.hd > 256 || a.rd > a.hd || a.rd % 2 || a.rd / 2 > 64) return hipErrorInvalidValue;
+    const int items = a.n * (a.nh + 2 * a.nkv);
+    hipLaunchKernelGGL(k_qk_rope, dim3((items + 3) / 4), dim3(QR_THREADS), 0, s, qkv, qn, kn, a, Qh, Kh, Vh);
+    return hipGetLastError();
+}
+
+constexpr int AT_Q = 64;              // queries per workgroup (16 per wavefront)
+constexpr int AT_K = 64;              // keys per tile
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, const float *__restrict__ Kh,
+                                              const float *__restrict__ Vh, AttnDims a, float *__restrict__ out)
+{
+    constexpr int LD = HD + 1;                         // padded LDS rows
+    __shared__ float sQ[AT_Q * LD];
+    __shared__ float sK[AT_K * LD];
+    __shared__ float sV[AT_K * LD];
+    __shared__ float sP[4][16 * (AT_K + 1)];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int N = a.n, h = blockIdx.y, kvh = h / (a.nh / a.nkv);
+    const int q_wg = blockIdx.x * AT_Q;
+    const float *Q = Qh + (size_t)h * N * HD, *K = Kh + (size_t)kvh * N * HD, *V = Vh + (size_t)kvh * N * HD;
+    // queries of the workgroup (rows past N: zero)
+    for (int i = tid; i < AT_Q * HD; i += 256) {
+        const int r = i / HD, d = i % HD;
+        sQ[r * LD + d] = q_wg + r < N ? Q[(size_t)(q_wg + r) * HD + d] : 0.0f;
+    }
+    // keys the workgroup's last query can see
+    const int q_last = min(N, q_wg + AT_Q) - 1;
+    const int k_end = a.block > 0 ? min(N, (q_last / a.block + 1) * a.block) : N;
+    const float scale = a.scale;
+    const int q0 = q_wg + 16 * w;                      // this wavefront's first query
+    float m[4], l[4];
+    f4v o[HD / 16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        m[i] = -__builtin_inff();
+        l[i] = 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < HD / 16; b++) o[b] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < k_end; k0 += AT_K) {
+        __syncthreads();
+        for (int i = tid; i < AT_K * HD; i += 256) {
+            const int r = i / HD, d = i % HD;
+            const bool in = k0 + r < N;
+            sK[r * LD + d] = in ? K[(size_t)(k0 + r) * HD + d] : 0.0f;
+            sV[r * LD + d] = in ? V[(size_t)(k0 + r) * HD + d] : 0.0f;
+        }
+        __syncthreads();
+        // S[16 q][64 k]: lane holds rows 4g + i of key block kb, key kb*16 + r16
+        f4v sacc[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) sacc[kb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        const float *qrow = sQ + (16 * w + r16) * LD;
+#pragma unroll 4
+        for (int s = 0; s < HD / 4; s++) {
+            const float av = qrow[4 * s + g];
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const float bv = sK[(kb * 16 + r16) * LD + 4 * s + g];
+                sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, sacc[kb], 0, 0, 0);
+            }
+        }
+        // scale, mask, online softmax per query row (rows 4g + i of the wave)
+        float mt[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = q0 + 4 * g + i;
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const int k = k0 + kb * 16 + r16;
+                const bool ok = k < N && (a.block <= 0 || k / a.block <= q / a.block);
+                const float v = ok ? sacc[kb][i] * scale : -__builtin_inff();
+                sacc[kb][i] = v;
+                mx = fmaxf(mx, v);
+            }
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, 16));
+            mt[i] = mx;
+        }
+        float corr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float mn = fmaxf(m[i], mt[i]);
+            // a row with no visible key yet keeps m = -inf and contributes 0
+            corr[i] = mn == -__builtin_inff() ? 1.0f : expf(m[i] - mn);
+            float rs = 0.0f;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const float p = mn == -__builtin_inff() ? 0.0f : expf(sacc[kb][i] - mn);
+                sacc[kb][i] = p;
+                rs += p;
+            }
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) rs += __shfl_xor(rs, sh, 16);
+            l[i] = l[i] * corr[i] + rs;
+            m[i] = mn;
+        }
+#pragma unroll
+        for (int b = 0; b < HD / 16; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[b][i] *= corr[i];
+        // P to LDS in the layout of the next product's A operand
+        float *pw = sP[w];
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) pw[(4 * g + i) * (AT_K + 1) + kb * 16 + r16] = sacc[kb][i];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // O[16 q][HD] += P[16 q][64 k] V[64 k][HD]
+#pragma unroll 4
+        for (int s = 0; s < AT_K / 4; s++) {
+            const float av = pw[r16 * (AT_K + 1) + 4 * s + g];
+            const float *vrow = sV + (4 * s + g) * LD;
+#pragma unroll
+            for (int b = 0; b < HD / 16; b++)
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, vrow[b * 16 + r16], o[b], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+    // out[t][h*HD + d] = O / l (lane: rows 4g + i, column b*16 + r16)
+    const int QD = a.nh * HD;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = q0 + 4 * g + i;
+        if (q >= N) continue;
+        const float inv = l[i];
+#pragma unroll
+        for (int b = 0; b < HD / 16; b++) out[(size_t)q * QD + (size_t)h * HD + b * 16 + r16] = o[b][i] / inv;
+    }
+}
+
+hipError_t launch_attn(const float *Qh, const float *Kh, const float *Vh, const AttnDims &a, float *out,
+                       hipStream_t s)
+{
+    if (a.nkv <= 0 || a.nh % a.nkv) return hipErrorInvalidValue;
+    const dim3 grid((a.n + AT_Q - 1) / AT_Q, a.nh);
+    switch (a.hd) {
+    case 64: hipLaunchKernelGGL(k_attn<64>, grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
+    case 128: hipLaunchKernelGGL(k_attn<128>, grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+} // namespace dmoe

@@ -18,7 +18,7 @@ from typing import Optional
 
 import numpy as np
 
-from ._abi import (Debug, HParams, LayerDesc, Tensor, TYPE_F16, TYPE_F32, TYPE_Q4_K,
+from ._abi import (AttnDesc, AttnHParams, Debug, HParams, LayerDesc, Tensor, TYPE_F16, TYPE_F32, TYPE_Q4_K,
                    TYPE_Q8_0, TYPE_Q8_K, TYPE_NAMES, TYPE_BY_NAME, row_size, block_elems,
                    block_bytes)
 from . import _abi
@@ -35,7 +35,8 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_gguf_open", "dmoe_gguf_close", "dmoe_gguf_get_u32", "dmoe_gguf_get_f32",
            "dmoe_gguf_find_tensor", "dmoe_gguf_tensor_count", "dmoe_gguf_tensor_name",
            "dmoe_gguf_moe_hparams", "dmoe_gguf_layer_desc", "dmoe_gguf_dense_desc",
-           "dmoe_head_upload", "dmoe_head_wrap_device", "dmoe_head_forward", "dmoe_head_forward_device")
+           "dmoe_head_upload", "dmoe_head_wrap_device", "dmoe_head_forward", "dmoe_head_forward_device",
+           "dmoe_attn_upload", "dmoe_attn_wrap_device", "dmoe_attn_forward", "dmoe_attn_forward_device")
 NOALLOC_SCRATCH_BYTES = 64 << 20
 N_STAGES = 10
 PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}
@@ -86,6 +87,10 @@ def load() -> C.CDLL:
     lib.dmoe_head_wrap_device.argtypes = lib.dmoe_head_upload.argtypes
     lib.dmoe_head_forward.argtypes = [P, P, P, C.c_int32, C.c_float, P, P, P]
     lib.dmoe_head_forward_device.argtypes = [P, P, P, C.c_int32, C.c_float, P, P, P, P]
+    lib.dmoe_attn_upload.argtypes = [P, C.POINTER(AttnHParams), C.POINTER(AttnDesc), C.POINTER(P)]
+    lib.dmoe_attn_wrap_device.argtypes = lib.dmoe_attn_upload.argtypes
+    lib.dmoe_attn_forward.argtypes = [P, P, P, C.c_int32, P, P]
+    lib.dmoe_attn_forward_device.argtypes = [P, P, P, C.c_int32, P, P, P]
     lib.dmoe_layer_forward.argtypes = [P, P, P, C.c_int32, P, C.POINTER(Debug)]
     lib.dmoe_layer_forward_device.argtypes = [P, P, P, C.c_int32, P, P]
     lib.dmoe_layer_forward_device_noalloc.argtypes = [P, P, P, C.c_int32, P, P]
@@ -239,6 +244,59 @@ class HeadWeights:
 
     def norm_view(self) -> Tensor:
         return tensor_view(TYPE_F32, self.norm, [self.n_embd])
+
+
+@dataclass
+class AttnWeights:
+    """The attention half of a layer (diffuse_moe_layer's attn_norm, wqkv,
+    attn_q_norm, attn_k_norm, wo, attn_post_norm, src/diffuse-common.h:60-65)
+    and its hyper-parameters.  Norms f32 (numpy or torch); qkv u8
+    [(n_head + 2 n_head_kv) head_dim, row_size(T, n_embd)] (ne [n_embd,
+    QKV]: rows Q then K then V); wo u8 [n_embd, row_size(T, n_head head_dim)]
+    (ne [n_head head_dim, n_embd]).  q_norm / k_norm f32 [head_dim] or None."""
+    n_embd: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    rotary_dim: int
+    block_length: int
+    rope_base: float
+    rms_eps: float
+    wtype: int
+    attn_norm: object
+    qkv: object
+    wo: object
+    post_norm: object
+    q_norm: object = None
+    k_norm: object = None
+
+    @property
+    def q_dim(self) -> int:
+        return self.n_head * self.head_dim
+
+    @property
+    def qkv_dim(self) -> int:
+        return (self.n_head + 2 * self.n_head_kv) * self.head_dim
+
+    def hparams(self) -> "AttnHParams":
+        a = AttnHParams()
+        a.n_embd, a.n_head, a.n_head_kv = self.n_embd, self.n_head, self.n_head_kv
+        a.head_dim, a.rotary_dim = self.head_dim, self.rotary_dim
+        a.use_qk_norm = int(self.q_norm is not None)
+        a.block_length, a.rope_base, a.rms_eps = self.block_length, self.rope_base, self.rms_eps
+        return a
+
+    def desc(self) -> "AttnDesc":
+        d = AttnDesc()
+        d.attn_norm = tensor_view(TYPE_F32, self.attn_norm, [self.n_embd])
+        d.qkv = tensor_view(self.wtype, self.qkv, [self.n_embd, self.qkv_dim])
+        d.wo = tensor_view(self.wtype, self.wo, [self.q_dim, self.n_embd])
+        if self.post_norm is not None:
+            d.post_attn_norm = tensor_view(TYPE_F32, self.post_norm, [self.n_embd])
+        if self.q_norm is not None:
+            d.q_norm = tensor_view(TYPE_F32, self.q_norm, [self.head_dim])
+            d.k_norm = tensor_view(TYPE_F32, self.k_norm, [self.head_dim])
+        return d
 
 
 def hparams_of(n_embd, n_experts, top_k, capacity, block_size, moe_ff=1, n_shared=0,
@@ -411,6 +469,42 @@ class Context:
                                                     _ptr(logits_dev) if logits_dev is not None else None,
                                                     s or None))
 
+    def _attn(self, fn, w: AttnWeights) -> Layer:
+        a, d = w.hparams(), w.desc()
+        out = C.c_void_p()
+        self._check(fn(self.handle, C.byref(a), C.byref(d), C.byref(out)))
+        lw = LayerWeights(n_embd=w.n_embd, n_experts=0, top_k=0, capacity=0, block_size=0,
+                          moe_ff=0, wtype=w.wtype, gate_w=None, exp_gate=None, exp_up=None,
+                          exp_down=None)
+        layer = Layer(self, out.value, lw)
+        layer.attn = w
+        return layer
+
+    def attn_upload(self, w: AttnWeights) -> Layer:
+        """The attention half of a layer from host arrays (dmoe_attn_upload)."""
+        return self._attn(load().dmoe_attn_upload, w)
+
+    def attn_wrap_device(self, w: AttnWeights) -> Layer:
+        return self._attn(load().dmoe_attn_wrap_device, w)
+
+    def attn_forward(self, layer: Layer, h: np.ndarray):
+        """(h + attention(h), post-attention norm of it) for h [N][n_embd]."""
+        h = np.ascontiguousarray(h, dtype=np.float32)
+        N = h.shape[0]
+        h_out = np.empty_like(h)
+        moe_in = np.empty_like(h)
+        self._check(load().dmoe_attn_forward(self.handle, layer.handle, h.ctypes.data, N,
+                                             h_out.ctypes.data, moe_in.ctypes.data))
+        return h_out, moe_in
+
+    def attn_forward_device(self, layer: Layer, h_dev, n_tokens: int, h_out_dev, moe_in_dev=None,
+                            stream=None):
+        s = 0 if stream is None else int(stream)
+        self._check(load().dmoe_attn_forward_device(self.handle, layer.handle, _ptr(h_dev), n_tokens,
+                                                    _ptr(h_out_dev),
+                                                    _ptr(moe_in_dev) if moe_in_dev is not None else None,
+                                                    s or None))
+
     def forward(self, layer: Layer, x: np.ndarray, debug: bool = False):
         x = np.ascontiguousarray(x, dtype=np.float32)
         N = x.shape[0]
@@ -474,6 +568,6 @@ class Context:
                                                 nrows, n_per_row, s or None))
 
 
-__all__ = ["Context", "Layer", "LayerWeights", "DenseWeights", "HeadWeights", "DmoeError", "load", "tensor_view", "hparams_of",
+__all__ = ["Context", "Layer", "LayerWeights", "DenseWeights", "HeadWeights", "AttnWeights", "DmoeError", "load", "tensor_view", "hparams_of",
            "use_block_routing", "row_size", "TYPE_F32", "TYPE_F16", "TYPE_Q8_0", "TYPE_Q4_K",
            "TYPE_Q8_K", "TYPE_NAMES", "TYPE_BY_NAME", "EXPORTS", "LIB_PATH"]

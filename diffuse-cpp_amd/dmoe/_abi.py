@@ -39,6 +39,16 @@ class LayerDesc(C.Structure):
                                       "sh_gate", "sh_up", "sh_down")]
 
 
+class AttnHParams(C.Structure):
+    _fields_ = [("n_embd", C.c_int32), ("n_head", C.c_int32), ("n_head_kv", C.c_int32),
+                ("head_dim", C.c_int32), ("rotary_dim", C.c_int32), ("use_qk_norm", C.c_int32),
+                ("block_length", C.c_int32), ("rope_base", C.c_float), ("rms_eps", C.c_float)]
+
+
+class AttnDesc(C.Structure):
+    _fields_ = [(n, Tensor) for n in ("attn_norm", "qkv", "q_norm", "k_norm", "wo", "post_attn_norm")]
+
+
 class Debug(C.Structure):
     _fields_ = [("logits", C.c_void_p), ("probs", C.c_void_p), ("bmax", C.c_void_p),
                 ("thr", C.c_void_p), ("allowed", C.c_void_p), ("idx", C.c_void_p),

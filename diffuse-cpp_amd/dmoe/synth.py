@@ -17,7 +17,7 @@ from dataclasses import dataclass, replace
 
 import numpy as np
 
-from . import (DenseWeights, HeadWeights, LayerWeights, TYPE_F16, TYPE_F32, TYPE_Q4_K, TYPE_Q8_0, row_size)
+from . import (AttnWeights, DenseWeights, HeadWeights, LayerWeights, TYPE_F16, TYPE_F32, TYPE_Q4_K, TYPE_Q8_0, row_size)
 
 _M1 = np.uint64(0x9E3779B97F4A7C15)
 _M2 = np.uint64(0xBF58476D1CE4E5B9)
@@ -56,6 +56,7 @@ def normal(seed: int, stream: int, n: int, std: float = 1.0) -> np.ndarray:
 S_X, S_GATE_W, S_BIAS, S_EG, S_EU, S_ED, S_SG, S_SU, S_SD = range(1, 10)
 S_FG, S_FU, S_FD = range(20, 23)        # dense MLP (ffn_gate, ffn_up, ffn_down)
 S_ONORM, S_OUT = 30, 31                 # step tail (output_norm, output)
+S_ANORM, S_QKV, S_QN, S_KN, S_WO, S_PNORM = range(40, 46)   # attention half
 
 
 @dataclass(frozen=True)
@@ -284,3 +285,37 @@ def head_to_host(w: HeadWeights) -> HeadWeights:
     def h(a):
         return a.detach().cpu().numpy() if hasattr(a, "detach") else a
     return replace(w, norm=h(w.norm), output=h(w.output))
+
+
+# LLaDA2.0-flash attention: GQA 32 / 4, head_dim 128, NEOX RoPE over the first
+# 64 dims with base 3e6, QK RMSNorm, 32-token blocks.
+ATTN_FLASH = dict(n_embd=4096, n_head=32, n_head_kv=4, head_dim=128, rotary_dim=64, block_length=32,
+                  rope_base=3e6, rms_eps=1e-6)
+
+
+def host_attn(wtype: int, seed: int, quantize_rows, n_embd: int, n_head: int, n_head_kv: int, head_dim: int,
+              rotary_dim: int, block_length: int = 32, rope_base: float = 3e6, rms_eps: float = 1e-6,
+              qk_norm: bool = True, w_std: float = 0.02) -> AttnWeights:
+    """Norm gains ~ U(0.5, 1.5); wqkv and wo N(0, w_std) quantised by quantize_rows."""
+    QD, QKV = n_head * head_dim, (n_head + 2 * n_head_kv) * head_dim
+
+    def q(stream, rows, n):
+        f = normal(seed, stream, rows * n, w_std).reshape(rows, n)
+        return np.ascontiguousarray(quantize_rows(wtype, f)).view(np.uint8).reshape(rows, row_size(wtype, n))
+
+    return AttnWeights(n_embd=n_embd, n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim,
+                       rotary_dim=rotary_dim, block_length=block_length, rope_base=rope_base, rms_eps=rms_eps,
+                       wtype=wtype, attn_norm=uniform(seed, S_ANORM, n_embd, 0.5, 1.5),
+                       qkv=q(S_QKV, QKV, n_embd), wo=q(S_WO, n_embd, QD),
+                       post_norm=uniform(seed, S_PNORM, n_embd, 0.5, 1.5),
+                       q_norm=uniform(seed, S_QN, head_dim, 0.5, 1.5) if qk_norm else None,
+                       k_norm=uniform(seed, S_KN, head_dim, 0.5, 1.5) if qk_norm else None)
+
+
+def attn_to_device(w: AttnWeights, device) -> AttnWeights:
+    import torch
+
+    def d(a):
+        return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    return replace(w, attn_norm=d(w.attn_norm), qkv=d(w.qkv), wo=d(w.wo), post_norm=d(w.post_norm),
+                   q_norm=d(w.q_norm), k_norm=d(w.k_norm))

@@ -194,6 +194,51 @@ int  dmoe_head_forward_device(dmoe_ctx *ctx, const dmoe_layer *head, const float
                               int32_t n_tokens, float eps, int32_t *tokens_dev,
                               float *probs_dev, float *logits_dev, void *stream);
 
+/* ---- attention half of the layer (src/diffuse-moe-graph.cpp:116-178) ----
+ * h_out = h + wo attn(rms_norm(h) * attn_norm) and moe_in =
+ * rms_norm(h_out) * post_attn_norm (the MoE segment's input; no gain when
+ * post_attn_norm.data is NULL):
+ *   qkv = W_qkv x (fused [Q heads; K heads; V heads], :124-134), QK RMSNorm
+ *   over head_dim times q_norm / k_norm (:141-146), partial NEOX RoPE of the
+ *   first rotary_dim dims at position t (:154-155), flash attention with the
+ *   block-causal mask of :19-55 (query i sees key j iff j / block_length <=
+ *   i / block_length; every key when block_length <= 0), GQA query head h on
+ *   kv head h / (n_head / n_head_kv), scale 1 / sqrt(head_dim) (:165-167),
+ *   output projection and residual (:172-175), post-attention RMSNorm
+ *   (:177-178).  Projection weights have F32 semantics (ensure_f32_moe).
+ * Limits: n_embd and n_head * head_dim multiples of 256, head_dim 64 or 128,
+ * rotary_dim even and <= head_dim, n_head a multiple of n_head_kv; other
+ * shapes are refused with DMOE_ERR_SHAPE. */
+typedef struct dmoe_attn_hparams {
+    int32_t n_embd, n_head, n_head_kv, head_dim, rotary_dim;
+    int32_t use_qk_norm;     /* model.use_qk_norm                           */
+    int32_t block_length;    /* hparams.block_length (0: bidirectional)     */
+    float   rope_base;       /* hparams.rope_theta (rope.freq_base)         */
+    float   rms_eps;         /* hparams.rms_norm_eps                        */
+} dmoe_attn_hparams;
+
+/* diffuse_moe_layer's attention tensors (src/diffuse-common.h:60-65):
+ *   attn_norm, post_attn_norm F32 [n_embd] (post_attn_norm data may be NULL)
+ *   qkv  T [n_embd, (n_head + 2 n_head_kv) head_dim]
+ *   q_norm, k_norm F32 [head_dim] (ignored unless use_qk_norm)
+ *   wo   T [n_head head_dim, n_embd] */
+typedef struct dmoe_attn_desc {
+    dmoe_tensor attn_norm, qkv, q_norm, k_norm, wo, post_attn_norm;
+} dmoe_attn_desc;
+
+int  dmoe_attn_upload(dmoe_ctx *ctx, const dmoe_attn_hparams *ap, const dmoe_attn_desc *desc,
+                      dmoe_layer **out);
+int  dmoe_attn_wrap_device(dmoe_ctx *ctx, const dmoe_attn_hparams *ap,
+                           const dmoe_attn_desc *desc, dmoe_layer **out);
+/* h, h_out [n_tokens][n_embd] (h_out may be h); moe_in may be NULL.  Host
+ * buffers, synchronous. */
+int  dmoe_attn_forward(dmoe_ctx *ctx, const dmoe_layer *attn, const float *h, int32_t n_tokens,
+                       float *h_out, float *moe_in);
+/* Device buffers (16-byte aligned), queued on `stream` without synchronising. */
+int  dmoe_attn_forward_device(dmoe_ctx *ctx, const dmoe_layer *attn, const float *h_dev,
+                              int32_t n_tokens, float *h_out_dev, float *moe_in_dev,
+                              void *stream);
+
 /* Release a layer's device buffers.  The layer records its own device, so it
  * may be freed before or after the context that created it. */
 void dmoe_layer_free(dmoe_layer *layer);

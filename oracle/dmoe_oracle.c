@@ -799,6 +799,140 @@ int dmo_head_forward(int n_embd, int n_vocab, const float *norm_w, const dmoe_te
     return 0;
 }
 
+/* ggml_rope_ext in NEOX mode with n_dims = rotary_dim (freq_scale 1,
+ * ext_factor 0, attn_factor 1, no frequency factors), ggml's CPU algorithm:
+ * theta_scale = powf(base, -2/n_dims); per position p the angle of pair ic is
+ * p * theta_scale^ic formed by repeated float multiplication (theta *=
+ * theta_scale); x0 = x[ic], x1 = x[ic + n_dims/2] ->
+ * (x0 cos - x1 sin, x0 sin + x1 cos); dims from n_dims on are copied. */
+void dmo_rope_neox(float *x, int head_dim, int n_dims, int pos, float base)
+{
+    const float theta_scale = powf(base, -2.0f / (float)n_dims);
+    float theta = (float)pos;
+    for (int i0 = 0; i0 < n_dims; i0 += 2) {
+        const float c = cosf(theta), sn = sinf(theta);
+        const int ic = i0 / 2;
+        const float x0 = x[ic], x1 = x[ic + n_dims / 2];
+        x[ic] = x0 * c - x1 * sn;
+        x[ic + n_dims / 2] = x0 * sn + x1 * c;
+        theta *= theta_scale;
+    }
+    (void)head_dim;
+}
+
+/* ggml_flash_attn_ext on the CPU for one query row, F32 K and V: keys in
+ * order, s = (q . k) * scale + mask (mask 0 or -inf; -inf keys skipped),
+ * online softmax (running max M and sum S, the accumulator rescaled by
+ * expf(M_old - M_new) when the max grows), result VKQ / S. */
+static void attn_row(const float *q, const float *K, const float *V, size_t kstride, int n_keys,
+                     const uint8_t *allowed, int hd, float scale, float *out)
+{
+    float M = -INFINITY, S = 0.0f;
+    float *acc = (float *)calloc((size_t)hd, 4);
+    for (int j = 0; j < n_keys; j++) {
+        if (!allowed[j]) continue;
+        const float *k = K + (size_t)j * kstride, *v = V + (size_t)j * kstride;
+        const float s = dot_f32(hd, q, k) * scale;
+        float ms = 1.0f, vs = 1.0f;
+        if (s > M) {
+            ms = dmo_expf(M - s);
+            M = s;
+            for (int d = 0; d < hd; d++) acc[d] = acc[d] * ms;
+        } else {
+            vs = dmo_expf(s - M);
+        }
+        for (int d = 0; d < hd; d++) acc[d] = acc[d] + v[d] * vs;
+        S = S * ms + vs;
+    }
+    for (int d = 0; d < hd; d++) out[d] = acc[d] / S;
+    free(acc);
+}
+
+int dmo_attn_forward(const dmoe_attn_hparams *ap, const dmoe_attn_desc *desc, const float *h,
+                     int n_tokens, float *h_out, float *moe_in, int n_threads)
+{
+    const int N = n_tokens, H = ap->n_embd, NH = ap->n_head, NKV = ap->n_head_kv;
+    const int HD = ap->head_dim, RD = ap->rotary_dim;
+    const int QD = NH * HD, KD = NKV * HD, QKV = QD + 2 * KD;
+    if (N <= 0 || H <= 0 || NH <= 0 || NKV <= 0 || NH % NKV || HD <= 0 || RD > HD || RD % 2) return -1;
+#ifdef _OPENMP
+    if (n_threads <= 0) n_threads = omp_get_max_threads();
+    int saved_threads = omp_get_max_threads();
+    omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+    const float eps = ap->rms_eps;
+    float *xn = (float *)malloc((size_t)N * H * 4);
+    float *qkv = (float *)malloc((size_t)N * QKV * 4);
+    float *att = (float *)malloc((size_t)N * QD * 4);
+    float *proj = (float *)malloc((size_t)N * H * 4);
+    /* :120-121 input layernorm */
+    for (int t = 0; t < N; t++)
+        dmo_rms_norm(h + (size_t)t * H, (const float *)desc->attn_norm.data, H, eps, xn + (size_t)t * H);
+    /* :124 fused QKV, the weight cast to F32 */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+    for (int r = 0; r < QKV; r++) {
+        float *w = (float *)malloc((size_t)H * 4);
+        dmo_dequant_row(desc->qkv.type, tensor_row(&desc->qkv, r, 0), w, H);
+        for (int t = 0; t < N; t++) qkv[(size_t)t * QKV + r] = dot_f32(H, w, xn + (size_t)t * H);
+        free(w);
+    }
+    /* :141-146 QK norm (RMSNorm over head_dim, times q_norm / k_norm), then
+     * :154-155 partial NEOX RoPE at position t (inp_pos = 0..N-1, :93-99) */
+    for (int t = 0; t < N; t++) {
+        float *row = qkv + (size_t)t * QKV;
+        for (int hh = 0; hh < NH + NKV; hh++) {
+            float *x = row + (size_t)hh * HD;
+            if (ap->use_qk_norm) {
+                const float *w = (const float *)(hh < NH ? desc->q_norm.data : desc->k_norm.data);
+                dmo_rms_norm(x, w, HD, eps, x);
+            }
+            dmo_rope_neox(x, HD, RD, t, ap->rope_base);
+        }
+    }
+    /* :165-167 flash attention with the block-causal mask (:19-55): query i
+     * sees key j iff j / B <= i / B (all keys when B <= 0); query head hh
+     * reads kv head hh / (NH / NKV); scale 1 / sqrt(head_dim) */
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int B = ap->block_length;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int i = 0; i < N * NH; i++) {
+        const int t = i / NH, hh = i % NH, g = hh / (NH / NKV);
+        uint8_t *allowed = (uint8_t *)malloc((size_t)N);
+        for (int j = 0; j < N; j++) allowed[j] = B <= 0 || j / B <= t / B;
+        attn_row(qkv + (size_t)t * QKV + (size_t)hh * HD, qkv + QD + (size_t)g * HD,
+                 qkv + QD + KD + (size_t)g * HD, (size_t)QKV, N, allowed, HD, scale,
+                 att + (size_t)t * QD + (size_t)hh * HD);
+        free(allowed);
+    }
+    /* :172 output projection (cast to F32), :175 residual */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+    for (int r = 0; r < H; r++) {
+        float *w = (float *)malloc((size_t)QD * 4);
+        dmo_dequant_row(desc->wo.type, tensor_row(&desc->wo, r, 0), w, QD);
+        for (int t = 0; t < N; t++) proj[(size_t)t * H + r] = dot_f32(QD, w, att + (size_t)t * QD);
+        free(w);
+    }
+    for (size_t i = 0; i < (size_t)N * H; i++) h_out[i] = proj[i] + h[i];
+    /* :177-178 post-attention layernorm: the MoE segment's input */
+    if (moe_in)
+        for (int t = 0; t < N; t++)
+            dmo_rms_norm(h_out + (size_t)t * H, (const float *)desc->post_attn_norm.data, H, eps,
+                         moe_in + (size_t)t * H);
+    free(xn); free(qkv); free(att); free(proj);
+#ifdef _OPENMP
+    omp_set_num_threads(saved_threads);
+#endif
+    return 0;
+}
+
 int dmo_layer_forward(const dmoe_hparams *hp, const dmoe_layer_desc *desc,
                       const float *x, int n_tokens, float *y,
                       dmoe_debug *dbg, int n_threads)

@@ -41,6 +41,11 @@
  *                                    uniform rows) and float64 softmax
  *   dmo_head_forward                 pinned: float64 numpy logits on the
  *                                    dequantised output weight
+ *   dmo_rope_neox                    pinned: float64 rotation with the same
+ *                                    angle chain (and the closed-form angle
+ *                                    within the chain's rounding); norm kept
+ *   dmo_attn_forward                 pinned: float64 numpy attention (mask,
+ *                                    GQA head map, RoPE, QK norm, residual)
  */
 #ifndef DMOE_ORACLE_H
 #define DMOE_ORACLE_H
@@ -133,6 +138,14 @@ void dmo_argmax_prob(const float *logits, int n_vocab, int32_t *token, float *pr
 int  dmo_head_forward(int n_embd, int n_vocab, const float *norm_w, const dmoe_tensor *output,
                       const float *h, int n_tokens, float eps, int32_t *tokens, float *probs,
                       float *logits_out, int n_threads);
+
+/* ---- attention half of the layer -----------------------------------------
+ * ggml_rope_ext, NEOX mode, n_dims rotated of head_dim, at position pos. */
+void dmo_rope_neox(float *x, int head_dim, int n_dims, int pos, float base);
+/* src/diffuse-moe-graph.cpp:116-178: h_out = h + wo attn(h), moe_in =
+ * rms_norm(h_out) * post_attn_norm (may be NULL). */
+int  dmo_attn_forward(const dmoe_attn_hparams *ap, const dmoe_attn_desc *desc, const float *h,
+                      int n_tokens, float *h_out, float *moe_in, int n_threads);
 
 #ifdef __cplusplus
 }

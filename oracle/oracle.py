@@ -22,7 +22,7 @@ LIB_PATH = ORACLE_DIR / "libdmoe_oracle.so"
 sys.path.insert(0, str(ROOT / "diffuse-cpp_amd"))
 
 from dmoe import _abi  # noqa: E402  (struct layouts of include/dmoe.h)
-from dmoe._abi import Debug, HParams, LayerDesc, Tensor  # noqa: E402
+from dmoe._abi import AttnDesc, AttnHParams, Debug, HParams, LayerDesc, Tensor  # noqa: E402
 
 TYPE_Q8_K = _abi.TYPE_Q8_K
 
@@ -80,6 +80,9 @@ def load() -> C.CDLL:
     lib.dmo_rms_norm.restype = None
     lib.dmo_argmax_prob.argtypes = [P, C.c_int, P, P]
     lib.dmo_argmax_prob.restype = None
+    lib.dmo_rope_neox.argtypes = [P, C.c_int, C.c_int, C.c_int, C.c_float]
+    lib.dmo_rope_neox.restype = None
+    lib.dmo_attn_forward.argtypes = [C.POINTER(AttnHParams), C.POINTER(AttnDesc), P, C.c_int, P, P, C.c_int]
     lib.dmo_head_forward.argtypes = [C.c_int, C.c_int, P, C.POINTER(Tensor), P, C.c_int, C.c_float,
                                      P, P, P, C.c_int]
     _lib = lib
@@ -277,6 +280,25 @@ def head_forward(w, h: np.ndarray, eps: float = 1e-6, n_threads: int = 0):
     if rc:
         raise ValueError("oracle head forward failed")
     return tok, prob, logits
+
+
+def rope_neox(x: np.ndarray, n_dims: int, pos: int, base: float) -> np.ndarray:
+    """A rotated copy of one head vector x (NEOX pairs (i, i + n_dims/2))."""
+    y = np.array(x, dtype=np.float32, copy=True)
+    load().dmo_rope_neox(_p(y), y.shape[0], n_dims, pos, base)
+    return y
+
+
+def attn_forward(w, h: np.ndarray, n_threads: int = 0):
+    """w: dmoe.AttnWeights (numpy).  Returns (h_out, moe_in)."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    N = h.shape[0]
+    a, d = w.hparams(), w.desc()
+    h_out = np.empty_like(h)
+    moe_in = np.empty_like(h)
+    if load().dmo_attn_forward(C.byref(a), C.byref(d), _p(h), N, _p(h_out), _p(moe_in), n_threads):
+        raise ValueError("oracle attention forward failed")
+    return h_out, moe_in
 
 
 def n_threads_default() -> int:
