@@ -7,8 +7,10 @@ weights and activations already resident in HBM.  Default workload: the
 LLaDA2-flash-shaped layer with Q4_K experts over one 32-token block.
 
 Prints one JSON line with tokens/s, the roofline of the dominant kernel
-(timed live with HIP events on the launch stream) and the CPU baseline
-(the oracle, timed on this host over a bounded sample).
+(timed live with HIP events on the launch stream), the realised routing
+(touched experts, tokens per expert), the CPU baseline (the oracle, timed on
+this host over a bounded sample) and, under "prefill", the same record for
+the 2048-token F16 prefill layer (its dominant kernel MFMA-bound).
 
     python bench.py [--steps K] [--warmup W] [--config flash_q4k]
 """
@@ -39,6 +41,9 @@ def parse():
                     help="weight copies rotated per step so the 256 MB MALL cannot serve repeats")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-steps", type=int, default=10,
+                    help="steps of the 2048-token F16 prefill layer measured after the headline "
+                         "(0: skip)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the bench, run 5 plain device copies of this many MiB "
@@ -57,30 +62,59 @@ def traffic_from_profile(kernel, workload):
     return None
 
 
-def main():
-    a = parse()
-    if a.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
-                          "n_gpus": a.gpus}))
-        sys.exit(2)
+def cpu_info():
+    """CPU model and physical core count of this host (/proc/cpuinfo)."""
+    model, cores = None, set()
+    phys = core = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model is None:
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    flags = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("flags"):
+                flags = line
+                break
+    except OSError:
+        pass
+    isa = [f for f in ("avx2", "avx512f", "avx512_vnni", "avx_vnni", "amx_int8") if f" {f}" in flags]
+    return {"model": model, "physical_cores": len(cores) or None, "logical_cpus": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "isa": isa}
 
+
+def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
+    """One MoE layer of config cfg: tokens/s, per-stage times, the dominant
+    kernel's roofline, realised routing and (cpu_seconds > 0) the oracle's
+    rate on this host."""
     import numpy as np
     import torch
     import dmoe
     from dmoe import synth
 
-    cfg = synth.CONFIGS[a.config]
-    if cfg.n_layers != 1:
-        return bench_stack(a, cfg)
     N, H, FF, E, K = cfg.n_tokens, cfg.n_embd, cfg.moe_ff, cfg.n_experts, cfg.top_k
     ctx = dmoe.Context(0)
     dev = torch.device("cuda:0")
 
     t0 = time.time()
     weights = [synth.device_layer(cfg, a.seed, ctx, weight_seed=a.seed + 17 * i)
-               for i in range(a.copies)]
+               for i in range(copies)]
     layers = [ctx.wrap_device(w) for w in weights]
-    print(f"# built {a.copies} weight copies in {time.time() - t0:.1f}s", file=sys.stderr,
+    print(f"# {cfg.name}: built {copies} weight copies in {time.time() - t0:.1f}s", file=sys.stderr,
           flush=True)
     x_host = synth.make_x(cfg, a.seed)
     x = torch.from_numpy(x_host).to(dev)
@@ -92,27 +126,28 @@ def main():
     _, dbg = ctx.forward(layers[0], x_host, debug=True)
     counts = dbg["counts"]
     touched = int((counts > 0).sum())
+    routing = synth.routing_stats(dbg["idx"].reshape(N, K), E, cfg.block_size)
     eb = weights[0].expert_bytes()
     sb = weights[0].shared_bytes()
 
     def step(i):
-        ctx.forward_device(layers[i % a.copies], x, N, y, sp)
+        ctx.forward_device(layers[i % copies], x, N, y, sp)
 
-    for i in range(a.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
-    for i in range(a.steps):
+    for i in range(steps):
         step(i)
     ev1.record(stream)
     torch.cuda.synchronize(dev)
-    ms_step = ev0.elapsed_time(ev1) / a.steps
+    ms_step = ev0.elapsed_time(ev1) / steps
 
     # per-stage durations, HIP events around each launch on the same stream
     ctx.profile(True)
-    for i in range(a.steps):
+    for i in range(steps):
         step(i)
     torch.cuda.synchronize(dev)
     prof = ctx.profile_read()
@@ -133,6 +168,7 @@ def main():
     P = N * K
     dom_stage = "gateup_routed"
     dom_us = stages.get(dom_stage)
+    flops = 2.0 * N * (K * 3 * H * FF + 3 * H * SF + H * E)
     if cfg.wtype == dmoe.TYPE_F16:
         dom_kernel = "dmoe::k_gemm_f16<0>"
         dom_flops = 2.0 * (P * 2 * H * FF + N * 2 * H * SF)
@@ -170,23 +206,14 @@ def main():
 
     # layer-level: every weight byte the layer must read
     layer_bytes = touched * eb + sb + E * H * 4 + E * 4 + 2 * N * H * 4
-    flops = 2.0 * N * (K * 3 * H * FF + 3 * H * cfg.shared_ff + H * E)
-
-    tokens_s = N / (ms_step * 1e-3)
-    out = {
-        "metric": METRIC,
-        "value": round(tokens_s, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
+    sec = ms_step * 1e-3
+    rec = {
+        "value": round(N / sec, 1),
         "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "steps": steps,
+        "warmup": warmup,
         "dtype": {dmoe.TYPE_Q4_K: "i8", dmoe.TYPE_Q8_0: "i8", dmoe.TYPE_F16: "f16",
                   dmoe.TYPE_F32: "f32"}[cfg.wtype],
-        "data": "synthetic: random-init weights N(0,0.02) quantised on the GPU, x ~ N(0,1)",
         "config": {
             "workload": (f"{cfg.name}: LLaDA2 MoE layer, hidden {H}, {E} experts, moe_ff {FF}, "
                          f"top-{K} within capacity {cfg.capacity} per {cfg.block_size}-token block, "
@@ -194,23 +221,25 @@ def main():
                          f"{N} tokens"),
             "n_tokens": N,
             "expert_type": dmoe.TYPE_NAMES[cfg.wtype],
-            "touched_experts": touched,
-            "max_tokens_per_expert": int(counts.max()),
-            "weight_copies_rotated": a.copies,
+            "router_bias": (f"{cfg.bias_mode} U({cfg.bias_lo}, {cfg.bias_hi})"
+                            + (f" + {cfg.hot_delta} on a hot quarter" if cfg.bias_mode == "hot" else "")),
+            "weight_copies_rotated": copies,
+            **routing,
         },
         "roofline": roofline,
         "layer": {
             "bytes": layer_bytes,
             "touched_expert_bytes": touched * eb,
-            "GB_s": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
-            "hbm_frac": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "touched_expert_frac": round(touched * eb / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
+            "GB_s": round(layer_bytes / sec / 1e9, 1),
+            "hbm_frac": round(layer_bytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "touched_expert_frac": round(touched * eb / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / sec / 1e12, 2),
+            "mfma_frac": round(flops / sec / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
             "stage_us": stages,
         },
     }
 
-    if not a.no_cpu:
+    if cpu_seconds > 0:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as O
         wh = synth.to_host(weights[0])
@@ -221,22 +250,75 @@ def main():
             O.layer_forward(wh, x_host, n_threads=threads)
             reps += 1
             el = time.time() - t_start
-            if el >= a.cpu_seconds or reps >= 1000:
+            if el >= cpu_seconds or reps >= 1000:
                 break
-        out["cpu_baseline"] = {
+        info = cpu_info()
+        rec["cpu_baseline"] = {
             "value": round(N * reps / el, 2),
             "unit": "tokens/s",
             "cores": threads,
             "kind": "port",
-            "sample": f"{reps} forwards of the same {N}-token layer ({el:.1f} s), oracle with "
-                      f"{threads} OpenMP threads",
+            "sample": f"{reps} forwards of the same {N}-token layer ({el:.1f} s), oracle (scalar C, "
+                      f"gcc -O2, OpenMP over rows) with {threads} threads",
+            "cpu_model": info["model"],
+            "physical_cores": info["physical_cores"],
+            "logical_cpus": info["logical_cpus"],
+            "affinity_cpus": info["affinity_cpus"],
+            "isa": info["isa"],
         }
         ctx.forward_device(layers[0], x, N, y, sp)
         torch.cuda.synchronize(dev)
         err = float(np.abs(y.cpu().numpy() - yr).max() / np.abs(yr).max())
-        out["check_max_rel_err_vs_oracle"] = err
+        rec["check_max_rel_err_vs_oracle"] = err
+
+    del layers, weights, x, y
+    ctx.close()
+    torch.cuda.empty_cache()
+    return rec
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+
+    import torch
+    from dmoe import synth
+
+    cfg = synth.CONFIGS[a.config]
+    if cfg.n_layers != 1:
+        return bench_stack(a, cfg)
+    rec = bench_layer(a, cfg, a.steps, a.warmup, a.copies, 0 if a.no_cpu else a.cpu_seconds)
+    out = {
+        "metric": METRIC,
+        "value": rec.pop("value"),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": rec.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": rec.pop("dtype"),
+        "data": "synthetic: random-init weights N(0,0.02) quantised on the GPU, x ~ N(0,1)",
+    }
+    rec.pop("steps")
+    rec.pop("warmup")
+    out.update(rec)
+
+    # the metric's second half: the 2048-token prefill layer (F16 experts,
+    # MFMA-bound), measured in the same run
+    if a.prefill_steps > 0 and cfg.n_tokens <= 256:
+        pcfg = synth.CONFIGS["prefill_f16"]
+        pre = bench_layer(a, pcfg, a.prefill_steps, max(1, a.prefill_steps // 4), 1, 0)
+        pre["unit"] = "tokens/s"
+        out["prefill"] = pre
 
     if a.copy_probe_mib:
+        dev = torch.device("cuda:0")
         n = a.copy_probe_mib * (1 << 20) // 4
         src = torch.randn(n, device=dev)
         dst = torch.empty_like(src)
