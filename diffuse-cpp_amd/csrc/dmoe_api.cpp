@@ -323,12 +323,30 @@ bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
     return true;
 }
 
+// Activation column blocks of 16 pairs per routed Q4_K work item, by the
+// tokens per expert the forward brings: pairs per expert averaged over all
+// experts (N k / E) of 64 or more take 4 blocks, of 32 or more 2, else 1.  A
+// weight tile read from HBM then serves up to 64 pairs instead of 16 (the
+// prefill-sized windows); few tokens per expert keep the 16-pair items, whose
+// finer work division fills the chip.  DMOE_Q4K_COLUMN_BLOCKS (1, 2, 4)
+// overrides the choice.
+int q4k_column_blocks(const dmoe_hparams &hp, int N)
+{
+    if (const char *ov = getenv("DMOE_Q4K_COLUMN_BLOCKS")) {
+        const int v = atoi(ov);
+        if (v == 1 || v == 2 || v == 4) return v;
+    }
+    const long avg = (long)N * hp.top_k / (hp.n_experts > 0 ? hp.n_experts : 1);
+    return avg >= 64 ? 4 : avg >= 32 ? 2 : 1;
+}
+
 // Few tokens of Q4_K experts: the down products and the combine run as one
-// launch over 16-row tiles of every expert (k_down_rows.hip).
+// launch over 16-row tiles of every expert (k_down_rows.hip); it takes the
+// 16-pair work list.
 bool use_down_rows(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N)
 {
     return use_mfma_path(hp, wtype, stype, shared) &&
-           down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff);
+           down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff) && q4k_column_blocks(hp, N) == 1;
 }
 
 // Q8_0 experts (and a Q8_0 shared expert of the same width) run on the int8
@@ -404,7 +422,8 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
     const bool gemm = use_gemm_path(hp, wtype, stype, shared);
     const bool gemv = !gemm && !use_mfma_path(hp, wtype, stype, shared) &&
                       !use_q80_path(hp, wtype, stype, shared);
-    t.wl.chunk = gemm ? GM : EXPERT_CHUNK;
+    t.wl.chunk = gemm ? GM
+                      : EXPERT_CHUNK * (use_mfma_path(hp, wtype, stype, shared) ? q4k_column_blocks(hp, N) : 1);
     t.wl.n_ec = (int32_t *)take(4);
     t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
     t.wl.ec_chunk = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
@@ -554,8 +573,9 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
     const bool gemm = use_gemm_path(hp, L->eg.type, L->sg.type, L->has_shared);
     // activation layouts of the int8 MFMA kernels (routed, shared expert)
     const int mode_r = q8 ? ACT_Q80 : ACT_Q8K, mode_s = q8 ? ACT_SPLIT32 : ACT_SPLIT;
+    const int nc = q4 ? q4k_column_blocks(hp, N) : 1;
     auto expert = [&](int phase, const MoeJob &j) {
-        return q8 ? launch_expert_q80(phase, j, s) : launch_expert_q4k(phase, j, s);
+        return q8 ? launch_expert_q80(phase, j, s) : launch_expert_q4k(phase, j, s, nc);
     };
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
     // router logits, sigmoid, selection scores (+ x in the MFMA operand layout)

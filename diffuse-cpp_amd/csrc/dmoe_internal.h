@@ -202,7 +202,9 @@ hipError_t launch_argmax_prob(const float *logits, int N, int V, int32_t *tokens
 // * (up x); phase 1: y = down h.
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
 constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
-hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s);
+// nc: activation column blocks of 16 pairs per routed item (1, 2 or 4; the
+// work list's chunk is 16 nc): each weight tile read serves 16 nc pairs.
+hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc = 1);
 // Down products of the Q4_K experts and the weighted combine in one launch
 // for few tokens (k_down_rows.hip): one workgroup per 16 output rows, every
 // touched expert's 16-row tile, results folded in slot order in LDS.

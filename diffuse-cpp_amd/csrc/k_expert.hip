@@ -211,26 +211,39 @@ __device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[RT], const uint8
 }
 
 // Work items of phase 0: routed (work-list entry ec, group of GROWS_GU rows),
-// then shared (chunk of 8 tokens, group of GROWS_GU rows); phase 1 the same
-// with groups of GROWS_DN rows.  A routed item's 16 activation rows are the
-// pairs of its entry (one expert, up to 16 consecutive pairs of it); a shared
-// item's are the a1 / a0 digit rows of its 8 tokens interleaved (t a1, t a0,
-// ...), so that each lane's four outputs are (t, a1), (t, a0), (t+1, a1),
-// (t+1, a0) and the two digits' products are summed in-lane.
+// then shared (chunk of 8 NC tokens, group of GROWS_GU rows); phase 1 the
+// same with groups of GROWS_DN rows.  A routed item's activation rows are the
+// pairs of its entry (one expert, up to 16 NC consecutive pairs of it, in NC
+// column blocks of 16); a shared item's are the a1 / a0 digit rows of its
+// tokens interleaved (t a1, t a0, ...; 8 tokens per column block), so that
+// each lane's four outputs are (t, a1), (t, a0), (t+1, a1), (t+1, a0) and the
+// two digits' products are summed in-lane.  NC > 1 (many tokens per expert)
+// multiplies every weight tile read from HBM by NC activation blocks: the
+// weights stream once per 16 NC pairs instead of once per 16.
 //
 // Step s of an item is super-block s % nsb of row pass s / nsb.  Its weights
-// (each wavefront's own tiles) and its activations (the workgroup's 16 rows,
-// loaded by wavefronts 0..5) go to ring stage s % WSTAGES with LDS-direct
-// loads issued WSTAGES - 1 steps ahead; one barrier per step makes the
+// (each wavefront's own tiles) and its activations (the workgroup's 16 NC
+// rows, loaded by wavefronts 0..5) go to ring stage s % WST with LDS-direct
+// loads issued WST - 1 steps ahead; one barrier per step makes the
 // activations visible to all wavefronts and frees the stage for refilling.
-template <int PHASE>
+template <int PHASE, int NC>
 __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
 {
     constexpr bool DOWN = PHASE == 1;
-    constexpr int IT = DOWN ? DN_IT : GU_IT;         // row passes per item
-    constexpr int GROWS = DOWN ? GROWS_DN : GROWS_GU;
-    __shared__ __align__(16) uint8_t s_act[WSTAGES][ASTEP_BYTES];
-    __shared__ __align__(16) uint8_t s_w[WAVES][WSTAGES][WSTEP_BYTES];
+    // row passes per item (a down item of 4 column blocks takes one, which
+    // keeps its accumulators and two items' pointers in registers)
+    constexpr int IT = DOWN ? (NC >= 4 ? 1 : DN_IT) : GU_IT;
+    constexpr int GROWS = DOWN ? WAVES * 16 * RT * IT : GROWS_GU;
+    // ring depth: a step of NC blocks computes NC times as long, so fewer
+    // stages keep the stream busy (and the LDS budget holds NC activation
+    // blocks per stage)
+    constexpr int WST = NC == 1 ? WSTAGES : 2;
+    constexpr int CH = EXPERT_CHUNK * NC;            // pairs of a routed item
+    constexpr int SCH = SHARED_CHUNK * NC;           // tokens of a shared item
+    __shared__ __align__(16) uint8_t s_act[WST][NC * ASTEP_BYTES];
+    __shared__ __align__(16) uint8_t s_w[WAVES][WST][WSTEP_BYTES];
+    static_assert(NC * 16 * 256 * 4 <= WAVES * WST * WSTEP_BYTES, "h of a gate/up item fits the weight ring");
+    static_assert(WAVES * 256 * 4 <= WST * NC * ASTEP_BYTES, "conversion scratch fits the activation ring");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -238,7 +251,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     const int N = job.n_tokens, K = job.top_k;
     const int H = job.H, FF = job.FF, SF = job.SF;
     const int n_ec = job.wl.n_ec[0];
-    const int nch = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
+    const int nch = job.has_shared ? (N + SCH - 1) / SCH : 0;
     const int rg = (DOWN ? H : FF) / GROWS, rg_sh = (DOWN ? H : SF) / GROWS;
     const int routed_items = n_ec * rg;
     const int total = routed_items + nch * rg_sh;
@@ -249,7 +262,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     // lanes below TPIECES - 128) from the tile's step run, to slot 64 j + lane
     // of the tile's place in the stage
     const uint32_t loff = lane * 16;
-    // activation load of this wavefront (wavefronts 0..5): which item row
+    // activation load of this wavefront (wavefronts 0..5): which block row
     // (ar) and piece; 0..3: q units of rows 4w .. 4w+3, 4: bs halves, 5: d
     const int ar = wave < 4 ? 4 * wave + (lane >> 4) : (wave == 4 ? (lane >> 1) & 15 : lane & 15);
     const int aunit = (lane & 15) ^ (ar & 11);       // q: logical unit of this lane's slot
@@ -258,10 +271,10 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     // The pointers of one work item.
     struct ItemPtrs {
         const uint8_t *tb[IT][RT];   // this wave's weight tiles of pass it
-        const int8_t *aq;            // the lane's activation load sources
-        const uint16_t *abs_;
-        const float *ad;
-        int t_first, nt, rbase;
+        const int8_t *aq[NC];        // the lane's activation load sources, per block
+        const uint16_t *abs_[NC];
+        const float *ad[NC];
+        int t_first, nt, rbase, nblk;
         bool shared;
     };
     auto setup = [&](int item, ItemPtrs &P) {
@@ -273,12 +286,12 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         int t_first, nt, e = 0;
         if (!shared) {
             e = job.wl.ec_expert[unit];
-            const int c0 = job.wl.ec_chunk[unit] * EXPERT_CHUNK;
+            const int c0 = job.wl.ec_chunk[unit] * CH;
             t_first = job.offsets[e] + c0;
-            nt = min(EXPERT_CHUNK, job.counts[e] - c0);
+            nt = min(CH, job.counts[e] - c0);
         } else {
-            t_first = unit * SHARED_CHUNK;
-            nt = min(SHARED_CHUNK, N - t_first);
+            t_first = unit * SCH;
+            nt = min(SCH, N - t_first);
         }
         if (!DOWN) {
             const WTensor &a = shared ? job.sg : job.eg;
@@ -299,22 +312,29 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
                     P.tb[it][r] = a.data + (size_t)e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
                 }
         }
-        // the activation row of item row ar: tokens in phase 0, pairs in phase
-        // 1; shared rows interleave the a1 and a0 digit rows (a0 rows start at N)
+        // the activation row of block row ar of each block: tokens in phase
+        // 0, pairs in phase 1; shared rows interleave the a1 and a0 digit
+        // rows (a0 rows start at N).  Rows past the item's last repeat it (a
+        // block past it loads the last row again and is not computed).
         const ActI8 &act = DOWN ? (shared ? job.ahs : job.ah) : (shared ? job.axs : job.ax);
-        int arow;
-        if (shared) {
-            arow = t_first + min(ar >> 1, nt - 1) + (ar & 1) * N;
-        } else {
-            const int p = job.perm[t_first + min(ar, nt - 1)];
-            arow = DOWN ? p : p / K;
+        const int per = shared ? SHARED_CHUNK : EXPERT_CHUNK;   // items of a block
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            int arow;
+            if (shared) {
+                arow = t_first + min(per * c + (ar >> 1), nt - 1) + (ar & 1) * N;
+            } else {
+                const int p = job.perm[t_first + min(per * c + ar, nt - 1)];
+                arow = DOWN ? p : p / K;
+            }
+            P.aq[c] = act.q + (size_t)arow * Kin + aunit * 16;
+            P.abs_[c] = act.bs + (size_t)arow * (Kin / 16) + (lane & 1) * 8;
+            P.ad[c] = act.d + (size_t)arow * nsb;
         }
-        P.aq = act.q + (size_t)arow * Kin + aunit * 16;
-        P.abs_ = act.bs + (size_t)arow * (Kin / 16) + (lane & 1) * 8;
-        P.ad = act.d + (size_t)arow * nsb;
         P.t_first = t_first;
         P.nt = nt;
         P.rbase = rbase;
+        P.nblk = (nt + per - 1) / per;
         P.shared = shared;
     };
 
@@ -325,11 +345,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         for (int q = 1; q < IT; q++) it += s >= q * nsb ? 1 : 0;
         return it;
     };
-    // step s of item P to ring stage gstep % WSTAGES
+    // step s of item P to ring stage gstep % WST
     auto issue = [&](const ItemPtrs &P, int s, int gstep) {
         if (s >= steps) return;
         const int it = pass_of(s), sb = s - it * nsb;
-        const int stg = gstep % WSTAGES;
+        const int stg = gstep % WST;
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const uint8_t *t = P.tb[0][r];
@@ -342,22 +362,26 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             lds_load16_sa(t, loff + 1024, d + 1024);
             if (lane < TPIECES - 128) lds_load16_sa(t, loff + 2048, d + 2048);
         }
-        if (wave < 4)
-            lds_load16(P.aq + sb * 256, &s_act[stg][1024 * wave]);
-        else if (wave == 4 && aload)
-            lds_load16(P.abs_ + sb * 16, &s_act[stg][ABS_OFF]);
-        else if (wave == 5 && aload)
-            lds_load4(P.ad + sb, &s_act[stg][AD_OFF]);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            uint8_t *st = &s_act[stg][c * ASTEP_BYTES];
+            if (wave < 4)
+                lds_load16(P.aq[c] + sb * 256, st + 1024 * wave);
+            else if (wave == 4 && aload)
+                lds_load16(P.abs_[c] + sb * 16, st + ABS_OFF);
+            else if (wave == 5 && aload)
+                lds_load4(P.ad[c] + sb, st + AD_OFF);
+        }
     };
 
     // Down items end with global stores only, so the rings run on from one
     // item of this workgroup to its next: the last steps of an item issue
-    // the next item's first WSTAGES - 1 steps (ring positions continue), and
+    // the next item's first WST - 1 steps (ring positions continue), and
     // the next item starts without draining.  Gate/up items convert h through
     // the rings after their last step, so each starts from drained rings.
     constexpr bool XPF = DOWN;
     ItemPtrs cur, nx;
-    bool primed = false;             // cur's first WSTAGES - 1 steps are issued
+    bool primed = false;             // cur's first WST - 1 steps are issued
     int g0 = 0;                      // ring position of cur's step 0
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
         if (primed)
@@ -365,10 +389,10 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         else
             setup(item, cur);
         const int nitem = item + gridDim.x;
-        const bool has_next = XPF && steps >= WSTAGES - 1 && nitem < total;
+        const bool has_next = XPF && steps >= WST - 1 && nitem < total;
         if (has_next) setup(nitem, nx);
         const bool shared = cur.shared;
-        const int t_first = cur.t_first, nt = cur.nt, rbase = cur.rbase;
+        const int t_first = cur.t_first, nt = cur.nt, rbase = cur.rbase, nblk = cur.nblk;
 
         if (!primed) {
             // the previous item's reads of the rings are done in every wavefront
@@ -377,47 +401,52 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
 #pragma unroll
-            for (int s = 0; s < WSTAGES - 1; s++) issue(cur, s, s);
+            for (int s = 0; s < WST - 1; s++) issue(cur, s, s);
         }
 
-        float acc[IT][RT][4];
+        float acc[IT][NC][RT][4];
 #pragma unroll
         for (int it = 0; it < IT; it++)
 #pragma unroll
-            for (int r = 0; r < RT; r++)
+            for (int c = 0; c < NC; c++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[it][r][i] = 0.0f;
+                for (int r = 0; r < RT; r++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[it][c][r][i] = 0.0f;
         for (int s = 0; s < steps; s++) {
-            // step s's loads have landed once the WSTAGES - 2 later steps' are
+            // step s's loads have landed once the WST - 2 later steps' are
             // all that may be in flight (a wavefront issues WLOADS loads per step,
-            // plus one when it loads activations; the previous item's output
+            // plus NC when it loads activations; the previous item's output
             // stores, when they follow, only make this stricter); when fewer
             // later steps were issued (the item's last steps, no next item
             // primed): wait for all.  The barrier makes that true of every
             // wavefront and frees the stage read in the step before.
-            if (s + WSTAGES - 2 < steps || has_next) {
+            if (WST > 2 && (s + WST - 2 < steps || has_next)) {
                 if (wave < ADMA_WAVES)
-                    EXPERT_WAIT_VM((WLOADS + 1) * (WSTAGES - 2));
+                    EXPERT_WAIT_VM((WLOADS + NC) * (WST - 2));
                 else
-                    EXPERT_WAIT_VM(WLOADS * (WSTAGES - 2));
+                    EXPERT_WAIT_VM(WLOADS * (WST - 2));
             } else {
                 EXPERT_WAIT_VM(0);
             }
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            const int sn = s + WSTAGES - 1;
+            const int sn = s + WST - 1;
             if (sn < steps)
                 issue(cur, sn, g0 + sn);
             else if (has_next)
                 issue(nx, sn - steps, g0 + sn);
             const int it = pass_of(s);
-            const int stg = (g0 + s) % WSTAGES;
+            const int stg = (g0 + s) % WST;
             Q4KTile cur_t[RT];
 #pragma unroll
             for (int r = 0; r < RT; r++) read_tile(cur_t[r], &s_w[wave][stg][r * TILE_BYTES], r16, g);
 #pragma unroll
-            for (int q = 0; q < IT; q++)
-                if (it == q) compute_sb(cur_t, s_act[stg], r16, g, acc[q]);
+            for (int c = 0; c < NC; c++)
+                if (c < nblk)
+#pragma unroll
+                    for (int q = 0; q < IT; q++)
+                        if (it == q) compute_sb(cur_t, &s_act[stg][c * ASTEP_BYTES], r16, g, acc[q][c]);
         }
         primed = has_next;
         g0 += steps;
@@ -430,20 +459,26 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             // (no loads in flight after the last step): h goes through the
             // weight-ring LDS, the conversion scratch through the activation
             // ring's.
-            float *s_h = reinterpret_cast<float *>(&s_w[0][0][0]);      // [16][256]
+            float *s_h = reinterpret_cast<float *>(&s_w[0][0][0]);      // [16 NC][256]
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
 #pragma unroll
             for (int it = 0; it < IT; it++) {
                 const int col = it * (WAVES * 16) + wave * 16 + r16;
-                if (!shared) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) s_h[(4 * g + i) * 256 + col] = silu(acc[it][0][i]) * acc[it][1][i];
-                } else {
+                for (int c = 0; c < NC; c++) {
+                    if (c >= nblk) continue;
+                    if (!shared) {
 #pragma unroll
-                    for (int i = 0; i < 4; i += 2)
-                        s_h[(2 * g + (i >> 1)) * 256 + col] =
-                            silu(acc[it][0][i] + acc[it][0][i + 1]) * (acc[it][1][i] + acc[it][1][i + 1]);
+                        for (int i = 0; i < 4; i++)
+                            s_h[(16 * c + 4 * g + i) * 256 + col] = silu(acc[it][c][0][i]) * acc[it][c][1][i];
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i += 2)
+                            s_h[(8 * c + 2 * g + (i >> 1)) * 256 + col] =
+                                silu(acc[it][c][0][i] + acc[it][c][0][i + 1]) *
+                                (acc[it][c][1][i] + acc[it][c][1][i + 1]);
+                    }
                 }
             }
             __syncthreads();
@@ -466,21 +501,27 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int row0 = rbase + it * (WAVES * 32) + wave * 32;
-            if (!shared) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    if (4 * g + i >= nt) continue;
-                    float *o = out + (size_t)job.perm[t_first + 4 * g + i] * H + row0 + r16;
+            for (int c = 0; c < NC; c++) {
+                if (c >= nblk) continue;
+                if (!shared) {
 #pragma unroll
-                    for (int r = 0; r < RT; r++) o[16 * r] = acc[it][r][i];
-                }
-            } else {
+                    for (int i = 0; i < 4; i++) {
+                        const int q = 16 * c + 4 * g + i;
+                        if (q >= nt) continue;
+                        float *o = out + (size_t)job.perm[t_first + q] * H + row0 + r16;
 #pragma unroll
-                for (int i = 0; i < 4; i += 2) {
-                    if (2 * g + (i >> 1) >= nt) continue;
-                    float *o = out + (size_t)(t_first + 2 * g + (i >> 1)) * H + row0 + r16;
+                        for (int r = 0; r < RT; r++) o[16 * r] = acc[it][c][r][i];
+                    }
+                } else {
 #pragma unroll
-                    for (int r = 0; r < RT; r++) o[16 * r] = acc[it][r][i] + acc[it][r][i + 1];
+                    for (int i = 0; i < 4; i += 2) {
+                        const int q = 8 * c + 2 * g + (i >> 1);
+                        if (q >= nt) continue;
+                        float *o = out + (size_t)(t_first + q) * H + row0 + r16;
+#pragma unroll
+                        for (int r = 0; r < RT; r++) o[16 * r] = acc[it][c][r][i] + acc[it][c][r][i + 1];
+                    }
                 }
             }
         }
@@ -491,31 +532,42 @@ int expert_rows_per_item(int phase) { return phase == 0 ? GROWS_GU : GROWS_DN; }
 
 bool expert_k_ok(int K) { return K % 256 == 0; }
 
-hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s)
+template <int PHASE>
+static hipError_t launch_phase(int nc, const MoeJob &job, dim3 grid, hipStream_t s)
+{
+    switch (nc) {
+    case 1: hipLaunchKernelGGL((k_expert_q4k<PHASE, 1>), grid, dim3(WAVES * 64), 0, s, job); break;
+    case 2: hipLaunchKernelGGL((k_expert_q4k<PHASE, 2>), grid, dim3(WAVES * 64), 0, s, job); break;
+    case 4: hipLaunchKernelGGL((k_expert_q4k<PHASE, 4>), grid, dim3(WAVES * 64), 0, s, job); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc)
 {
     if (job.FF % GROWS_GU || job.FF % 256 || job.H % GROWS_DN || job.H % 256 ||
         job.ax.K != job.H || job.ah.K != job.FF ||
         (job.has_shared && (job.SF != job.FF || job.ahs.K != job.SF)))
         return hipErrorInvalidValue;
-    if (phase == 0) {
-        hipLaunchKernelGGL(k_expert_q4k<0>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
-    } else {
-        // one workgroup per compute unit (one fits at a time), so that each
-        // runs its items back to back with the rings running on between them
-        static int n_cu[64] = {0};
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
+    // routed work-list entries hold 16 nc pairs
+    if ((nc != 1 && nc != 2 && nc != 4) || (job.wl.n_ec && job.wl.chunk != EXPERT_CHUNK * nc))
+        return hipErrorInvalidValue;
+    if (phase == 0) return launch_phase<0>(nc, job, dim3(DMOE_X_BLOCKS), s);
+    // one workgroup per compute unit (one fits at a time), so that each
+    // runs its items back to back with the rings running on between them
+    static int n_cu[64] = {0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (n_cu[dev] <= 0) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
-        if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-        if (n_cu[dev] <= 0) {
-            int n = 0;
-            e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-            if (e != hipSuccess) return e;
-            n_cu[dev] = n > 0 ? n : DMOE_X_BLOCKS;
-        }
-        hipLaunchKernelGGL(k_expert_q4k<1>, dim3(n_cu[dev]), dim3(WAVES * 64), 0, s, job);
+        n_cu[dev] = n > 0 ? n : DMOE_X_BLOCKS;
     }
-    return hipGetLastError();
+    return launch_phase<1>(nc, job, dim3(n_cu[dev]), s);
 }
 
 } // namespace dmoe

@@ -93,6 +93,16 @@ CONFIGS = {
     # 8 independent 32-token blocks
     "flash_q4k_n256": LayerConfig("flash_q4k_n256", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
                                   TYPE_Q4_K, 256, -0.1, 0.1),
+    # the sampler's growing window (N = 32 (blk + 1)): 16, 32 and 64 blocks
+    "flash_q4k_n512": LayerConfig("flash_q4k_n512", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
+                                  TYPE_Q4_K, 512, -0.1, 0.1),
+    "flash_q4k_n1024": LayerConfig("flash_q4k_n1024", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
+                                   TYPE_Q4_K, 1024, -0.1, 0.1),
+    "flash_q4k_n2048": LayerConfig("flash_q4k_n2048", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
+                                   TYPE_Q4_K, 2048, -0.1, 0.1),
+    # F16 experts on one 32-token block (few tokens per expert on the GEMM path)
+    "flash_f16": LayerConfig("flash_f16", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_F16, TYPE_F16, 32,
+                             -0.1, 0.1),
     # prompt prefill: F16 experts, 64 blocks; bias ~U(-0.05, 0.05) plus 0.05 on
     # a hot quarter of the experts, so that about 60% of each block's routed
     # pairs go to the layer's 48 most-used experts (routing_stats'

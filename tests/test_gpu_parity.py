@@ -98,11 +98,13 @@ def test_small_layer_many_items(ctx, O, wtype):
     assert err <= TOL[wtype]
 
 
-@pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "prefill_f16"])
+@pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "flash_q4k_n1024",
+                                  "flash_q4k_n2048", "prefill_f16"])
 def test_flash_layer(ctx, O, name):
     """Flash-shaped layers: one 32-token block (Q4_K, Q8_0), eight blocks
-    (Q4_K, 256 tokens, each block its own allowed set) and the 2048-token F16
-    prefill with a hot expert set."""
+    (Q4_K, 256 tokens, each block its own allowed set), the sampler's 1024-
+    and 2048-token windows (Q4_K items of 2 and 4 column blocks) and the
+    2048-token F16 prefill."""
     import torch
     import dmoe
     from dmoe import synth
@@ -123,6 +125,31 @@ def test_flash_layer(ctx, O, name):
     assert err <= TOL[cfg.wtype]
     del layer, wd
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("name", ["flash_q4k_n1024", "small_q4k_n2048"])
+def test_q4k_column_blocks_bit_exact(ctx, name, monkeypatch):
+    """Q4_K work items of 1, 2 and 4 column blocks (16, 32, 64 pairs of an
+    expert per weight-tile read) compute every product in the same order:
+    the layer outputs are identical bit for bit."""
+    import dmoe
+    from dmoe import synth
+    if name.startswith("small"):
+        cfg = _small(dmoe, synth, 12, 2048)
+    else:
+        cfg = synth.CONFIGS[name]
+    _say(f"case: Q4_K column blocks 1 / 2 / 4, {name}")
+    wd = synth.device_layer(cfg, 23, ctx)
+    layer = ctx.wrap_device(wd)
+    x = synth.make_x(cfg, 23, cfg.n_tokens)
+    ys = []
+    for nc in ("1", "2", "4"):
+        monkeypatch.setenv("DMOE_Q4K_COLUMN_BLOCKS", nc)
+        ys.append(ctx.forward(layer, x))
+    monkeypatch.delenv("DMOE_Q4K_COLUMN_BLOCKS")
+    ys.append(ctx.forward(layer, x))                      # the automatic choice
+    for y in ys[1:]:
+        assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32))
 
 
 def test_route_logits_flash_shape(ctx, O):
