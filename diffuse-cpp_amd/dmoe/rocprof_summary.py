@@ -4,6 +4,13 @@ Two reports:
 
 * ``kernels``: the per-kernel table of a ``--kernel-trace --stats`` run
   (calls, average and total duration, share of GPU time).
+* ``counters``: per-dispatch means of the SQ / GRBM counters of one
+  ``--pmc`` run for chosen kernels, with the utilisations they imply:
+  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (G x SIMDs), VALU busy =
+  4 SQ_ACTIVE_INST_VALU / (G x SIMDs) (a wave64 VALU instruction occupies a
+  SIMD four cycles), G = GRBM_GUI_ACTIVE / XCDs (the counter sums the busy
+  cycles of every XCD: G matches the kernel's duration at the shader clock),
+  LDS bank-conflict share = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.
 * ``traffic``: HBM bytes per launch of one kernel from two ``--pmc`` runs,
   ``FETCH_SIZE`` then ``WRITE_SIZE`` (both in KiB per dispatch).  Each counter
   is scaled by what it reads for a plain device copy of known size run in the
@@ -14,6 +21,8 @@ Two reports:
   bench.py reads.
 
     python -m dmoe.rocprof_summary kernels --dir D --cmd "..." --out F
+    python -m dmoe.rocprof_summary counters --dir D --kernel "k_gemm_f16<0>" \\
+        --cmd "..." --out F
     python -m dmoe.rocprof_summary traffic --fetch D1 --write D2 \\
         --kernel "k_expert_q4k<0>" --copy-bytes B --cmd-fetch "..." \\
         --cmd-write "..." --algorithmic-bytes A --out F
@@ -94,6 +103,44 @@ def report_kernels(a):
     print("\n".join(lines))
 
 
+def report_counters(a):
+    rows = _rows(a.dir, "counter_collection.csv")
+    per = {}
+    for r in rows:
+        d = per.setdefault(r["Kernel_Name"], {}).setdefault(r["Dispatch_Id"], {})
+        d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    simds = a.simds
+    lines = [f"# SQ counters: {a.title}", "", "Command:", "", "```", a.cmd, "```", "",
+             f"Per-dispatch means over the kernel's dispatches; {simds} SIMDs, {a.xcds} XCDs.", "",
+             "| kernel | dispatches | counter | mean per dispatch |", "|---|---:|---|---:|"]
+    derived = ["", "| kernel | MFMA busy | VALU busy | VALU instr / wave | LDS bank-conflict share |",
+               "|---|---:|---:|---:|---:|"]
+    for pat in a.kernel:
+        hits = {k: v for k, v in per.items() if pat in k}
+        if not hits:
+            raise SystemExit(f"no kernel matching {pat!r}")
+        for kname, disp in hits.items():
+            names = sorted({c for d in disp.values() for c in d})
+            mean = {c: statistics.mean(d.get(c, 0.0) for d in disp.values()) for c in names}
+            for c in names:
+                lines.append(f"| `{_short(kname)}` | {len(disp)} | {c} | {mean[c]:.1f} |")
+            gui = mean.get("GRBM_GUI_ACTIVE", 0.0) / a.xcds
+            mf = mean.get("SQ_VALU_MFMA_BUSY_CYCLES")
+            va = mean.get("SQ_ACTIVE_INST_VALU")
+            waves = mean.get("SQ_WAVES")
+            lds = mean.get("SQ_LDS_IDX_ACTIVE")
+            cells = [
+                f"{mf / (gui * simds):.3f}" if mf is not None and gui else "-",
+                f"{4 * va / (gui * simds):.3f}" if va is not None and gui else "-",
+                f"{mean['SQ_INSTS_VALU'] / waves:.0f}" if waves and "SQ_INSTS_VALU" in mean else "-",
+                f"{mean['SQ_LDS_BANK_CONFLICT'] / lds:.3f}" if lds and "SQ_LDS_BANK_CONFLICT" in mean else "-",
+            ]
+            derived.append(f"| `{_short(kname)}` | " + " | ".join(cells) + " |")
+    out = lines + derived
+    Path(a.out).write_text("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def report_traffic(a):
     fetch = counter_values(a.fetch, "FETCH_SIZE")
     write = counter_values(a.write, "WRITE_SIZE")
@@ -157,8 +204,16 @@ def main():
     t.add_argument("--algorithmic-bytes", type=int, default=0)
     t.add_argument("--title", default="")
     t.add_argument("--out", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("--dir", required=True)
+    c.add_argument("--kernel", action="append", required=True, help="name pattern (repeatable)")
+    c.add_argument("--simds", type=int, default=1024, help="SIMDs of the GPU (MI355X: 256 CUs x 4)")
+    c.add_argument("--xcds", type=int, default=8, help="XCDs whose busy cycles GRBM_GUI_ACTIVE sums")
+    c.add_argument("--cmd", required=True)
+    c.add_argument("--title", default="")
+    c.add_argument("--out", required=True)
     a = ap.parse_args()
-    (report_kernels if a.what == "kernels" else report_traffic)(a)
+    {"kernels": report_kernels, "traffic": report_traffic, "counters": report_counters}[a.what](a)
 
 
 if __name__ == "__main__":
