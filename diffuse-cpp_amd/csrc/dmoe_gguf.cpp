@@ -461,4 +461,51 @@ int dmoe_gguf_dense_desc(const dmoe_gguf *g, int32_t il, dmoe_tensor *gate, dmoe
     return DMOE_OK;
 }
 
+int dmoe_gguf_attn_hparams(const dmoe_gguf *g, dmoe_attn_hparams *ap)
+{
+    if (!g || !ap) return DMOE_ERR_INVALID_ARG;
+    dmoe_attn_hparams a{};
+    uint32_t v = 0;
+    int rc;
+    // required (:83-85)
+    if ((rc = find_u32(g, "embedding_length", &v))) return rc;
+    a.n_embd = (int32_t)v;
+    if ((rc = find_u32(g, "attention.head_count", &v))) return rc;
+    a.n_head = (int32_t)v;
+    if ((rc = find_u32(g, "attention.head_count_kv", &v))) return rc;
+    a.n_head_kv = (int32_t)v;
+    if (a.n_head <= 0) return DMOE_ERR_FORMAT;
+    // defaults as the reference's loader (:90-93, :148-150)
+    a.head_dim = (int32_t)u32_or(g, "head_dim", (uint32_t)(a.n_embd / a.n_head));
+    a.rotary_dim = (int32_t)u32_or(g, "rotary_dim", (uint32_t)a.head_dim);
+    a.use_qk_norm = u32_or(g, "use_qk_norm", 0) != 0;
+    a.block_length = (int32_t)u32_or(g, "block_length", 0);
+    a.rope_base = 1000000.0f;
+    if ((rc = find_f32(g, "rope.freq_base", &a.rope_base)) && rc != DMOE_ERR_NOT_FOUND) return rc;
+    a.rms_eps = 1e-6f;
+    if ((rc = find_f32(g, "attention.layer_norm_rms_epsilon", &a.rms_eps)) && rc != DMOE_ERR_NOT_FOUND)
+        return rc;
+    *ap = a;
+    return DMOE_OK;
+}
+
+int dmoe_gguf_attn_desc(const dmoe_gguf *g, int32_t il, int32_t use_qk_norm, dmoe_attn_desc *desc)
+{
+    if (!g || !desc || il < 0) return DMOE_ERR_INVALID_ARG;
+    dmoe_attn_desc d{};
+    int rc;
+    // :171-174
+    if ((rc = tensor_view(g, layer_name("blk.%d.attn_norm.weight", il), &d.attn_norm))) return rc;
+    if ((rc = tensor_view(g, layer_name("blk.%d.post_attn_norm.weight", il), &d.post_attn_norm))) return rc;
+    if ((rc = tensor_view(g, layer_name("blk.%d.attn_qkv.weight", il), &d.qkv))) return rc;
+    if ((rc = tensor_view(g, layer_name("blk.%d.attn_output.weight", il), &d.wo))) return rc;
+    // :176-179, when the model uses QK norm
+    if (use_qk_norm) {
+        if ((rc = tensor_view(g, layer_name("blk.%d.attn_q_norm.weight", il), &d.q_norm))) return rc;
+        if ((rc = tensor_view(g, layer_name("blk.%d.attn_k_norm.weight", il), &d.k_norm))) return rc;
+    }
+    *desc = d;
+    return DMOE_OK;
+}
+
 } // extern "C"

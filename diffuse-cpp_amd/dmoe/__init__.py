@@ -36,7 +36,8 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_gguf_find_tensor", "dmoe_gguf_tensor_count", "dmoe_gguf_tensor_name",
            "dmoe_gguf_moe_hparams", "dmoe_gguf_layer_desc", "dmoe_gguf_dense_desc",
            "dmoe_head_upload", "dmoe_head_wrap_device", "dmoe_head_forward", "dmoe_head_forward_device",
-           "dmoe_attn_upload", "dmoe_attn_wrap_device", "dmoe_attn_forward", "dmoe_attn_forward_device")
+           "dmoe_attn_upload", "dmoe_attn_wrap_device", "dmoe_attn_forward", "dmoe_attn_forward_device",
+           "dmoe_gguf_attn_hparams", "dmoe_gguf_attn_desc")
 NOALLOC_SCRATCH_BYTES = 64 << 20
 N_STAGES = 10
 PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}

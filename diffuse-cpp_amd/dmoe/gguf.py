@@ -14,8 +14,8 @@ import ctypes as C
 
 import numpy as np
 
-from . import DenseWeights, DmoeError, LayerWeights, load
-from ._abi import HParams, LayerDesc, Tensor, row_size
+from . import AttnWeights, DenseWeights, DmoeError, LayerWeights, load
+from ._abi import AttnDesc, AttnHParams, HParams, LayerDesc, Tensor, row_size
 
 
 def _bind(lib):
@@ -36,6 +36,8 @@ def _bind(lib):
     lib.dmoe_gguf_layer_desc.argtypes = [P, C.c_int32, C.POINTER(LayerDesc)]
     lib.dmoe_gguf_dense_desc.argtypes = [P, C.c_int32, C.POINTER(Tensor), C.POINTER(Tensor),
                                          C.POINTER(Tensor), C.POINTER(C.c_int32)]
+    lib.dmoe_gguf_attn_hparams.argtypes = [P, C.POINTER(AttnHParams)]
+    lib.dmoe_gguf_attn_desc.argtypes = [P, C.c_int32, C.c_int32, C.POINTER(AttnDesc)]
     lib._gguf_bound = True
     return lib
 
@@ -144,3 +146,32 @@ class GGUF:
         H, FF = int(g.ne[0]), nff.value
         return DenseWeights(n_embd=H, n_ff=FF, wtype=g.type, gate=_bytes_view(g, FF),
                             up=_bytes_view(u, FF), down=_bytes_view(dn, H))
+
+    def attn_hparams(self) -> AttnHParams:
+        a = AttnHParams()
+        self._check(self.lib.dmoe_gguf_attn_hparams(self.handle, C.byref(a)), "attention hparams")
+        return a
+
+    def attn_desc(self, il: int, use_qk_norm: bool) -> AttnDesc:
+        d = AttnDesc()
+        self._check(self.lib.dmoe_gguf_attn_desc(self.handle, il, int(use_qk_norm), C.byref(d)),
+                    f"attention layer {il}")
+        return d
+
+    def attn_weights(self, il: int) -> AttnWeights:
+        """The attention tensors of layer il as an AttnWeights of views onto the file."""
+        a = self.attn_hparams()
+        d = self.attn_desc(il, bool(a.use_qk_norm))
+        QD, QKV = a.n_head * a.head_dim, (a.n_head + 2 * a.n_head_kv) * a.head_dim
+
+        def f32(t, n):
+            if t.type != 0:
+                raise DmoeError(2, "norm weight of type %d (F32 expected here)" % t.type)
+            return np.frombuffer((C.c_uint8 * (4 * n)).from_address(t.data), np.float32)
+        return AttnWeights(n_embd=a.n_embd, n_head=a.n_head, n_head_kv=a.n_head_kv, head_dim=a.head_dim,
+                           rotary_dim=a.rotary_dim, block_length=a.block_length, rope_base=a.rope_base,
+                           rms_eps=a.rms_eps, wtype=d.qkv.type, attn_norm=f32(d.attn_norm, a.n_embd),
+                           qkv=_bytes_view(d.qkv, QKV), wo=_bytes_view(d.wo, a.n_embd),
+                           post_norm=f32(d.post_attn_norm, a.n_embd),
+                           q_norm=f32(d.q_norm, a.head_dim) if a.use_qk_norm else None,
+                           k_norm=f32(d.k_norm, a.head_dim) if a.use_qk_norm else None)

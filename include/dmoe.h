@@ -369,6 +369,19 @@ int  dmoe_gguf_layer_desc(const dmoe_gguf *g, int32_t il, dmoe_layer_desc *desc)
 int  dmoe_gguf_dense_desc(const dmoe_gguf *g, int32_t il, dmoe_tensor *gate,
                           dmoe_tensor *up, dmoe_tensor *down, int32_t *n_ff);
 
+/* The attention hyper-parameters (src/diffuse-model.cpp:83-93, :148-150):
+ * embedding_length, attention.head_count and attention.head_count_kv are
+ * required; head_dim defaults to n_embd / n_head, rotary_dim to head_dim,
+ * use_qk_norm and block_length to 0, rope.freq_base to 1e6,
+ * attention.layer_norm_rms_epsilon to 1e-6. */
+int  dmoe_gguf_attn_hparams(const dmoe_gguf *g, dmoe_attn_hparams *ap);
+
+/* The attention tensors of layer il (blk.<il>.attn_norm, post_attn_norm,
+ * attn_qkv, attn_output; attn_q_norm / attn_k_norm when use_qk_norm),
+ * src/diffuse-model.cpp:171-179. */
+int  dmoe_gguf_attn_desc(const dmoe_gguf *g, int32_t il, int32_t use_qk_norm,
+                         dmoe_attn_desc *desc);
+
 /* Per-stage timing.  While enabled, every forward records a HIP event pair
  * around each pipeline stage on the stream it runs on; dmoe_profile_read
  * waits for the recorded work, adds each stage's elapsed milliseconds and

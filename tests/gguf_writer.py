@@ -111,3 +111,28 @@ def add_dense_layer(wr: GGUFWriter, il: int, d):
     wr.add_tensor(f"blk.{il}.ffn_gate.weight", d.wtype, [d.n_embd, d.n_ff], d.gate)
     wr.add_tensor(f"blk.{il}.ffn_up.weight", d.wtype, [d.n_embd, d.n_ff], d.up)
     wr.add_tensor(f"blk.{il}.ffn_down.weight", d.wtype, [d.n_ff, d.n_embd], d.down)
+
+
+def attn_keys(a, prefix: str = "diffuse"):
+    """The attention hyper-parameter keys of an AttnWeights, as the
+    reference's converter writes them (tools/convert-llada2-fast.py:125-144)."""
+    return [(f"{prefix}.attention.head_count", U32, a.n_head),
+            (f"{prefix}.attention.head_count_kv", U32, a.n_head_kv),
+            (f"{prefix}.head_dim", U32, a.head_dim),
+            (f"{prefix}.rotary_dim", U32, a.rotary_dim),
+            (f"{prefix}.use_qk_norm", U32, 1 if a.q_norm is not None else 0),
+            (f"{prefix}.block_length", U32, a.block_length),
+            (f"{prefix}.rope.freq_base", F32, a.rope_base),
+            (f"{prefix}.attention.layer_norm_rms_epsilon", F32, a.rms_eps)]
+
+
+def add_attn_layer(wr: GGUFWriter, il: int, a):
+    """blk.<il>.attn_* tensors of an AttnWeights (numpy)."""
+    H, QD, QKV = a.n_embd, a.n_head * a.head_dim, (a.n_head + 2 * a.n_head_kv) * a.head_dim
+    wr.add_tensor(f"blk.{il}.attn_norm.weight", 0, [H], np.ascontiguousarray(a.attn_norm, np.float32))
+    wr.add_tensor(f"blk.{il}.post_attn_norm.weight", 0, [H], np.ascontiguousarray(a.post_norm, np.float32))
+    wr.add_tensor(f"blk.{il}.attn_qkv.weight", a.wtype, [H, QKV], a.qkv)
+    wr.add_tensor(f"blk.{il}.attn_output.weight", a.wtype, [QD, H], a.wo)
+    if a.q_norm is not None:
+        wr.add_tensor(f"blk.{il}.attn_q_norm.weight", 0, [a.head_dim], np.ascontiguousarray(a.q_norm, np.float32))
+        wr.add_tensor(f"blk.{il}.attn_k_norm.weight", 0, [a.head_dim], np.ascontiguousarray(a.k_norm, np.float32))

@@ -12,7 +12,8 @@ import struct
 import numpy as np
 import pytest
 
-from gguf_writer import ARR, F32, GGUFWriter, STR, U32, U8, add_dense_layer, add_moe_layer, moe_keys
+from gguf_writer import (ARR, F32, GGUFWriter, STR, U32, U8, add_attn_layer, add_dense_layer, add_moe_layer,
+                         attn_keys, moe_keys)
 
 
 def _s(x: str) -> bytes:
@@ -128,6 +129,71 @@ def test_defaults_and_missing(tmp_path):
     with GGUF(p) as g:
         with pytest.raises(dmoe.DmoeError) as ei:
             g.moe_hparams()                                       # embedding_length missing
+        assert ei.value.code == dmoe._abi.ERR_NOT_FOUND
+
+
+@pytest.mark.parametrize("qk_norm", [True, False])
+def test_attention_round_trip(tmp_path, O, qk_norm):
+    """The attention keys and blk.N.attn_* tensors written by the converter's
+    layout come back as the AttnWeights they were written from; the oracle
+    on the mapped tensors equals the oracle on the originals."""
+    from dmoe import synth
+    from dmoe.gguf import GGUF
+    a = synth.host_attn(12, 3, O.quantize_rows, 256, 4, 2, 64, 32, block_length=16, rope_base=5e5,
+                        rms_eps=1e-5, qk_norm=qk_norm)
+    wr = GGUFWriter()
+    wr.add("diffuse.block_count", U32, 2)
+    wr.add("diffuse.embedding_length", U32, 256)
+    for k, t, v in attn_keys(a):
+        wr.add(k, t, v)
+    add_attn_layer(wr, 1, a)
+    p = tmp_path / "attn.gguf"
+    wr.write(p)
+    with GGUF(p) as g:
+        ap = g.attn_hparams()
+        assert (ap.n_embd, ap.n_head, ap.n_head_kv, ap.head_dim, ap.rotary_dim, ap.use_qk_norm,
+                ap.block_length) == (256, 4, 2, 64, 32, int(qk_norm), 16)
+        assert ap.rope_base == np.float32(5e5) and ap.rms_eps == np.float32(1e-5)
+        aw = g.attn_weights(1)
+        for f in ("attn_norm", "qkv", "wo", "post_norm", "q_norm", "k_norm"):
+            x, y = getattr(aw, f), getattr(a, f)
+            if y is None:
+                assert x is None, f
+            else:
+                assert np.array_equal(np.asarray(x).view(np.uint8).reshape(-1),
+                                      np.asarray(y).view(np.uint8).reshape(-1)), f
+        h = synth.normal(4, 1, 24 * 256).reshape(24, 256)
+        r0, r1 = O.attn_forward(aw, h), O.attn_forward(a, h)
+        assert np.array_equal(r0[0], r1[0]) and np.array_equal(r0[1], r1[1])
+        import dmoe
+        with pytest.raises(dmoe.DmoeError) as ei:
+            g.attn_desc(0, qk_norm)                             # layer 0 has no attention tensors
+        assert ei.value.code == dmoe._abi.ERR_NOT_FOUND
+
+
+def test_attention_defaults(tmp_path):
+    """head_dim = n_embd / n_head, rotary_dim = head_dim, no QK norm, block
+    length 0, rope base 1e6, eps 1e-6 when the keys are absent; head counts
+    are required."""
+    import dmoe
+    from dmoe.gguf import GGUF
+    wr = GGUFWriter()
+    wr.add("llama.embedding_length", U32, 512)
+    wr.add("llama.attention.head_count", U32, 8)
+    wr.add("llama.attention.head_count_kv", U32, 2)
+    p = tmp_path / "a.gguf"
+    wr.write(p)
+    with GGUF(p) as g:
+        ap = g.attn_hparams()
+        assert (ap.head_dim, ap.rotary_dim, ap.use_qk_norm, ap.block_length) == (64, 64, 0, 0)
+        assert ap.rope_base == np.float32(1e6) and ap.rms_eps == np.float32(1e-6)
+    wr = GGUFWriter()
+    wr.add("diffuse.embedding_length", U32, 512)
+    wr.add("diffuse.attention.head_count", U32, 8)
+    wr.write(p)
+    with GGUF(p) as g:
+        with pytest.raises(dmoe.DmoeError) as ei:
+            g.attn_hparams()                                      # head_count_kv missing
         assert ei.value.code == dmoe._abi.ERR_NOT_FOUND
 
 

@@ -62,3 +62,33 @@ def test_flash_layer_from_gguf(ctx, O, tmp_path):
         assert err <= 5e-4
         dl.free()
     torch.cuda.empty_cache()
+
+
+def test_attention_from_gguf(ctx, O, tmp_path):
+    """The flash-shaped attention half (32 / 4 heads of 128, RoPE over 64
+    dims, QK norm, Q4_K projections) loaded through dmoe_gguf_attn_hparams /
+    dmoe_gguf_attn_desc and dmoe_attn_upload from the mapping, against the
+    oracle on the same mapped bytes (bar 1e-4, as tests/test_gpu_attn.py)."""
+    from dmoe import synth
+    from dmoe.gguf import GGUF
+    from gguf_writer import U32, add_attn_layer, attn_keys
+    _say("case: flash attention half through a GGUF file")
+    a = synth.host_attn(12, 17, O.quantize_rows, **synth.ATTN_FLASH)
+    wr = GGUFWriter()
+    wr.add("diffuse.block_count", U32, 1)
+    wr.add("diffuse.embedding_length", U32, a.n_embd)
+    for k, t, v in attn_keys(a):
+        wr.add(k, t, v)
+    add_attn_layer(wr, 0, a)
+    path = tmp_path / "attn.gguf"
+    wr.write(path)
+    with GGUF(path) as g:
+        aw = g.attn_weights(0)
+        layer = ctx.attn_upload(aw)
+        h = (synth.normal(18, synth.S_X, 32 * a.n_embd).reshape(32, a.n_embd) * 2).astype(np.float32)
+        h_out, moe_in = ctx.attn_forward(layer, h)
+        r_out, r_in = O.attn_forward(aw, h)
+        e1, e2 = max_rel_err(h_out, r_out), max_rel_err(moe_in, r_in)
+        _say(f"  h_out err {e1:.3e}  moe_in err {e2:.3e}")
+        assert e1 <= 1e-4 and e2 <= 1e-4
+        layer.free()
