@@ -210,6 +210,87 @@ __device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[RT], const uint8
     }
 }
 
+// The same products for NC column blocks that share the step's weight tiles,
+// with the sub-block scales folded into the weight operand: sc_j = 8 sh_j +
+// sl_j (sh_j, sl_j < 8), so sh_j q and sl_j q (q < 16) are int8 values below
+// 106 and
+//   sum_j sc_j S_j = 8 sum_k (sh q)_k a_k + sum_k (sl q)_k a_k,
+// two int32 sums over the whole super-block, each from four
+// v_mfma_i32_16x16x64_i8 (sub-blocks 2c and 2c+1 side by side in one 16-byte
+// operand: the activation bytes 64g + 16c .. +15 as they lie in LDS, and the
+// weight dwords of chunk c).  The integers equal the per-sub-block sums of
+// compute_sb exactly, so the results are bit-identical; the tile's operands
+// are formed once for all NC blocks instead of 32 scale multiply-adds per
+// tile and block.
+struct Q4KFolded {
+    v4i bh[4], bl[4];   // (sh q), (sl q) operands of chunks 0..3
+    h4 bm;              // min-term operand
+    float d, dmin;
+};
+
+__device__ __forceinline__ void fold_tile(const Q4KTile &t, int g, Q4KFolded &f)
+{
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    // scale j: 6 bits at 6j of dword y (j < 5), at 6 (j - 5) of dword z
+    uint32_t sh[8], sl[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t src = j < 5 ? t.h.y : t.h.z;
+        const uint32_t off = j < 5 ? 6u * j : 6u * (j - 5);
+        sl[j] = bfe(src, off, 3);
+        sh[j] = bfe(src, off + 3, 3);
+    }
+    const uint32_t w[8] = {t.q0.x, t.q0.y, t.q0.z, t.q0.w, t.q1.x, t.q1.y, t.q1.z, t.q1.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t l0 = w[2 * c] & 0x0F0F0F0Fu, l1 = w[2 * c + 1] & 0x0F0F0F0Fu;
+        const uint32_t h0 = (w[2 * c] >> 4) & 0x0F0F0F0Fu, h1 = (w[2 * c + 1] >> 4) & 0x0F0F0F0Fu;
+        // byte-wise products by a scale below 8: each byte stays below 128, so
+        // a 16-bit lane product carries nothing across its two bytes
+        auto mul = [](uint32_t v, uint32_t s) -> int {
+            const u16x2 a = __builtin_bit_cast(u16x2, v);
+            const u16x2 b = {(unsigned short)s, (unsigned short)s};
+            return __builtin_bit_cast(int, (u16x2)(a * b));
+        };
+        f.bh[c] = (v4i){mul(l0, sh[2 * c]), mul(l1, sh[2 * c]), mul(h0, sh[2 * c + 1]), mul(h1, sh[2 * c + 1])};
+        f.bl[c] = (v4i){mul(l0, sl[2 * c]), mul(l1, sl[2 * c]), mul(h0, sl[2 * c + 1]), mul(h1, sl[2 * c + 1])};
+    }
+    const uint32_t msrc = g == 0 ? t.h.z : t.h.w;
+    const uint32_t moff = g == 0 ? 18u : 12u * (uint32_t)g - 12u;
+    const uint32_t m7 = (t.h.y >> 30) | ((t.h.z >> 30) << 2) | ((t.h.w >> 30) << 4);
+    const uint32_t ma = bfe(msrc, moff, 6);
+    const uint32_t mb = g == 3 ? m7 : bfe(msrc, moff + 6, 6);
+    const _Float16 fa = (_Float16)(float)ma, fb = (_Float16)(float)mb;
+    f.bm = (h4){fa, fa, fb, fb};
+    f.d = h16f(t.h.x & 0xffffu);
+    f.dmin = h16f(t.h.x >> 16);
+}
+
+// One folded tile against one column block's activations of the step.
+__device__ __forceinline__ void compute_folded(const Q4KFolded &f, const uint8_t *ast, int r16, int g, float (&acc)[4])
+{
+    const uint4 *ap = reinterpret_cast<const uint4 *>(ast + r16 * 256);
+    v4i a[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) a[c] = __builtin_bit_cast(v4i, ap[(4 * g + c) ^ (r16 & 11)]);
+    const h4 ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(ast + ABS_OFF + r16 * 32 + 8 * g));
+    const float4 dxv = *reinterpret_cast<const float4 *>(ast + AD_OFF + 16 * g);
+    const float dx[4] = {dxv.x, dxv.y, dxv.z, dxv.w};
+    v4i sh = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[c], f.bh[c], sh, 0, 0, 0);
+        sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[c], f.bl[c], sl, 0, 0, 0);
+    }
+    f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, f.bm, s2, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int isum = 8 * sh[i] + sl[i];
+        acc[i] += dx[i] * (f.d * (float)isum - f.dmin * s2[i]);
+    }
+}
+
 // Work items of phase 0: routed (work-list entry ec, group of GROWS_GU rows),
 // then shared (chunk of 8 NC tokens, group of GROWS_GU rows); phase 1 the
 // same with groups of GROWS_DN rows.  A routed item's activation rows are the
@@ -234,16 +315,20 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     // keeps its accumulators and two items' pointers in registers)
     constexpr int IT = DOWN ? (NC >= 4 ? 1 : DN_IT) : GU_IT;
     constexpr int GROWS = DOWN ? WAVES * 16 * RT * IT : GROWS_GU;
-    // ring depth: a step of NC blocks computes NC times as long, so fewer
-    // stages keep the stream busy (and the LDS budget holds NC activation
-    // blocks per stage)
-    constexpr int WST = NC == 1 ? WSTAGES : 2;
+    // ring depths: one column block runs both rings WSTAGES deep, loads of
+    // a step issued together WSTAGES - 1 steps ahead; NC > 1 blocks keep the
+    // weight ring three deep (two steps of HBM loads in flight) and the
+    // activation ring two deep (its loads come from L2, one step ahead), which
+    // is what the LDS holds next to NC activation blocks per stage
+    constexpr int WST = NC == 1 ? WSTAGES : 3;           // weight ring
+    constexpr int AST = NC == 1 ? WSTAGES : 2;           // activation ring
     constexpr int CH = EXPERT_CHUNK * NC;            // pairs of a routed item
     constexpr int SCH = SHARED_CHUNK * NC;           // tokens of a shared item
-    __shared__ __align__(16) uint8_t s_act[WST][NC * ASTEP_BYTES];
+    __shared__ __align__(16) uint8_t s_act[AST][NC * ASTEP_BYTES];
     __shared__ __align__(16) uint8_t s_w[WAVES][WST][WSTEP_BYTES];
     static_assert(NC * 16 * 256 * 4 <= WAVES * WST * WSTEP_BYTES, "h of a gate/up item fits the weight ring");
-    static_assert(WAVES * 256 * 4 <= WST * NC * ASTEP_BYTES, "conversion scratch fits the activation ring");
+    static_assert(WAVES * 256 * 4 <= AST * NC * ASTEP_BYTES, "conversion scratch fits the activation ring");
+    static_assert(NC == 1 || (WST == 3 && AST == 2), "the NC > 1 issue order below assumes these depths");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -345,8 +430,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         for (int q = 1; q < IT; q++) it += s >= q * nsb ? 1 : 0;
         return it;
     };
-    // step s of item P to ring stage gstep % WST
-    auto issue = [&](const ItemPtrs &P, int s, int gstep) {
+    // weights of step s of item P to weight stage gstep % WST
+    auto issue_w = [&](const ItemPtrs &P, int s, int gstep) {
         if (s >= steps) return;
         const int it = pass_of(s), sb = s - it * nsb;
         const int stg = gstep % WST;
@@ -362,6 +447,12 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             lds_load16_sa(t, loff + 1024, d + 1024);
             if (lane < TPIECES - 128) lds_load16_sa(t, loff + 2048, d + 2048);
         }
+    };
+    // activations of step s of item P to activation stage gstep % AST
+    auto issue_a = [&](const ItemPtrs &P, int s, int gstep) {
+        if (s >= steps) return;
+        const int it = pass_of(s), sb = s - it * nsb;
+        const int stg = gstep % AST;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             uint8_t *st = &s_act[stg][c * ASTEP_BYTES];
@@ -372,6 +463,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             else if (wave == 5 && aload)
                 lds_load4(P.ad[c] + sb, st + AD_OFF);
         }
+    };
+    // both parts of step s (the one-block order: weights, then activations)
+    auto issue = [&](const ItemPtrs &P, int s, int gstep) {
+        issue_w(P, s, gstep);
+        issue_a(P, s, gstep);
     };
 
     // Down items end with global stores only, so the rings run on from one
@@ -389,7 +485,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
         else
             setup(item, cur);
         const int nitem = item + gridDim.x;
-        const bool has_next = XPF && steps >= WST - 1 && nitem < total;
+        const bool has_next = XPF && steps >= 2 && nitem < total;
         if (has_next) setup(nitem, nx);
         const bool shared = cur.shared;
         const int t_first = cur.t_first, nt = cur.nt, rbase = cur.rbase, nblk = cur.nblk;
@@ -400,8 +496,15 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             EXPERT_WAIT_VM(0);
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
+            if constexpr (NC == 1) {
 #pragma unroll
-            for (int s = 0; s < WST - 1; s++) issue(cur, s, s);
+                for (int s = 0; s < WST - 1; s++) issue(cur, s, s);
+            } else {
+                // W(0), A(0), W(1): step 0 waits with only W(1) in flight
+                issue_w(cur, 0, 0);
+                issue_a(cur, 0, 0);
+                issue_w(cur, 1, 1);
+            }
         }
 
         float acc[IT][NC][RT][4];
@@ -421,32 +524,68 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             // later steps were issued (the item's last steps, no next item
             // primed): wait for all.  The barrier makes that true of every
             // wavefront and frees the stage read in the step before.
-            if (WST > 2 && (s + WST - 2 < steps || has_next)) {
-                if (wave < ADMA_WAVES)
-                    EXPERT_WAIT_VM((WLOADS + NC) * (WST - 2));
-                else
-                    EXPERT_WAIT_VM(WLOADS * (WST - 2));
+            if constexpr (NC == 1) {
+                if (s + WST - 2 < steps || has_next) {
+                    if (wave < ADMA_WAVES)
+                        EXPERT_WAIT_VM((WLOADS + 1) * (WST - 2));
+                    else
+                        EXPERT_WAIT_VM(WLOADS * (WST - 2));
+                } else {
+                    EXPERT_WAIT_VM(0);
+                }
             } else {
-                EXPERT_WAIT_VM(0);
+                // issue order per step: A(s + 1), then W(s + 2); so when
+                // step s runs only W(s + 1) may still be in flight (every
+                // earlier load, A(s) included, was issued before it)
+                if (s + 1 < steps || has_next)
+                    EXPERT_WAIT_VM(WLOADS);
+                else
+                    EXPERT_WAIT_VM(0);
             }
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            const int sn = s + WST - 1;
-            if (sn < steps)
-                issue(cur, sn, g0 + sn);
-            else if (has_next)
-                issue(nx, sn - steps, g0 + sn);
+            if constexpr (NC == 1) {
+                const int sn = s + WST - 1;
+                if (sn < steps)
+                    issue(cur, sn, g0 + sn);
+                else if (has_next)
+                    issue(nx, sn - steps, g0 + sn);
+            } else {
+                const int sa = s + 1, sw = s + 2;
+                if (sa < steps)
+                    issue_a(cur, sa, g0 + sa);
+                else if (has_next)
+                    issue_a(nx, sa - steps, g0 + sa);
+                if (sw < steps)
+                    issue_w(cur, sw, g0 + sw);
+                else if (has_next)
+                    issue_w(nx, sw - steps, g0 + sw);
+            }
             const int it = pass_of(s);
-            const int stg = (g0 + s) % WST;
-            Q4KTile cur_t[RT];
+            const int stg = (g0 + s) % WST, astg = (g0 + s) % AST;
+            if constexpr (NC == 1) {
+                Q4KTile cur_t[RT];
 #pragma unroll
-            for (int r = 0; r < RT; r++) read_tile(cur_t[r], &s_w[wave][stg][r * TILE_BYTES], r16, g);
+                for (int r = 0; r < RT; r++) read_tile(cur_t[r], &s_w[wave][stg][r * TILE_BYTES], r16, g);
 #pragma unroll
-            for (int c = 0; c < NC; c++)
-                if (c < nblk)
+                for (int q = 0; q < IT; q++)
+                    if (it == q) compute_sb(cur_t, s_act[astg], r16, g, acc[q][0]);
+            } else {
+                // each tile's operands formed once, then every column block
 #pragma unroll
-                    for (int q = 0; q < IT; q++)
-                        if (it == q) compute_sb(cur_t, &s_act[stg][c * ASTEP_BYTES], r16, g, acc[q][c]);
+                for (int r = 0; r < RT; r++) {
+                    Q4KTile t;
+                    read_tile(t, &s_w[wave][stg][r * TILE_BYTES], r16, g);
+                    Q4KFolded f;
+                    fold_tile(t, g, f);
+#pragma unroll
+                    for (int c = 0; c < NC; c++)
+                        if (c < nblk)
+#pragma unroll
+                            for (int q = 0; q < IT; q++)
+                                if (it == q) compute_folded(f, &s_act[astg][c * ASTEP_BYTES], r16, g, acc[q][c][r]);
+                }
+            }
         }
         primed = has_next;
         g0 += steps;
