@@ -244,6 +244,9 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
         import oracle as O
         wh = synth.to_host(weights[0])
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        # the quantised dots through AVX-512 VNNI where the host has it (the
+        # same results bit for bit as the scalar dots)
+        simd = O.set_simd(True)
         yr = O.layer_forward(wh, x_host, n_threads=threads)     # warm-up
         reps, t_start = 0, time.time()
         while True:
@@ -258,14 +261,17 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
             "unit": "tokens/s",
             "cores": threads,
             "kind": "port",
-            "sample": f"{reps} forwards of the same {N}-token layer ({el:.1f} s), oracle (scalar C, "
-                      f"gcc -O2, OpenMP over rows) with {threads} threads",
+            "sample": f"{reps} forwards of the same {N}-token layer ({el:.1f} s), oracle (C, gcc -O2, "
+                      f"OpenMP over rows; quantised dots "
+                      f"{'AVX-512 VNNI' if simd else 'scalar'}, F32 dots scalar binary64) "
+                      f"with {threads} threads",
             "cpu_model": info["model"],
             "physical_cores": info["physical_cores"],
             "logical_cpus": info["logical_cpus"],
             "affinity_cpus": info["affinity_cpus"],
             "isa": info["isa"],
         }
+        O.set_simd(False)
         ctx.forward_device(layers[0], x, N, y, sp)
         torch.cuda.synchronize(dev)
         err = float(np.abs(y.cpu().numpy() - yr).max() / np.abs(yr).max())

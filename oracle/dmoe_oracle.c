@@ -446,8 +446,24 @@ static float dot_q4K(int64_t n, const dmo_block_q4_K *w, const dmo_block_q8_K *x
     return s;
 }
 
+/* The AVX-512 VNNI dots of dmoe_cpu_simd.c (bit-identical results), used
+ * for the quantised types once dmo_set_simd(1) has found them supported. */
+static int g_simd = 0;
+
+int dmo_set_simd(int on)
+{
+    g_simd = on && dmo_simd_available();
+    return g_simd;
+}
+
 float dmo_vec_dot(int32_t wtype, int64_t n, const void *wrow, const void *xrow)
 {
+    if (g_simd) {
+        if (wtype == DMOE_TYPE_Q4_K)
+            return dmo_dot_q4K_simd(n, (const dmo_block_q4_K *)wrow, (const dmo_block_q8_K *)xrow);
+        if (wtype == DMOE_TYPE_Q8_0)
+            return dmo_dot_q8_0_simd(n, (const dmo_block_q8_0 *)wrow, (const dmo_block_q8_0 *)xrow);
+    }
     switch (wtype) {
     case DMOE_TYPE_F32:  return dot_f32(n, (const float *)wrow, (const float *)xrow);
     case DMOE_TYPE_F16:  return dot_f16(n, (const uint16_t *)wrow, (const uint16_t *)xrow);
@@ -661,6 +677,12 @@ static void matvec_rows(const dmoe_tensor *t, int64_t mat, int64_t r0, int64_t r
                         int64_t n, const uint8_t *act, size_t act_stride,
                         const int32_t *rows_in, int n_in, float *out, size_t out_stride)
 {
+    if (g_simd && t->type == DMOE_TYPE_Q4_K) {
+        for (int64_t r = r0; r < r1; r++)
+            dmo_rows_q4K_simd(n, (const dmo_block_q4_K *)tensor_row(t, r, mat), act, act_stride, rows_in, n_in,
+                              out + r, out_stride);
+        return;
+    }
     for (int64_t r = r0; r < r1; r++) {
         const void *w = tensor_row(t, r, mat);
         for (int i = 0; i < n_in; i++)

@@ -72,6 +72,17 @@ uint16_t dmo_f32_to_f16(float f);
 void     dmo_f16_to_f32_n(const uint16_t *h, float *f, int64_t n);
 void     dmo_f32_to_f16_n(const float *f, uint16_t *h, int64_t n);
 
+/* AVX-512 VNNI versions of the Q4_K x Q8_K and Q8_0 x Q8_0 dots
+ * (dmoe_cpu_simd.c; bit-identical to the scalar dots, for the timed CPU
+ * baseline).  dmo_set_simd(1) routes dmo_vec_dot through them when the CPU
+ * has AVX-512 F / BW and VNNI; returns whether it does. */
+int      dmo_simd_available(void);
+int      dmo_set_simd(int on);
+float    dmo_dot_q4K_simd(int64_t n, const dmo_block_q4_K *w, const dmo_block_q8_K *x);
+float    dmo_dot_q8_0_simd(int64_t n, const dmo_block_q8_0 *w, const dmo_block_q8_0 *x);
+void     dmo_rows_q4K_simd(int64_t n, const dmo_block_q4_K *w, const uint8_t *act, size_t act_stride,
+                           const int32_t *rows_in, int n_in, float *out, size_t out_stride);
+
 float    dmo_expf(float x);
 void     dmo_expf_n(const float *x, float *y, int64_t n);
 float    dmo_sigmoid(float x);

@@ -30,7 +30,8 @@ _lib = None
 
 
 def build(force: bool = False) -> Path:
-    srcs = [ORACLE_DIR / "dmoe_oracle.c", ORACLE_DIR / "dmoe_oracle.h", ROOT / "include" / "dmoe.h"]
+    srcs = [ORACLE_DIR / "dmoe_oracle.c", ORACLE_DIR / "dmoe_cpu_simd.c", ORACLE_DIR / "dmoe_oracle.h",
+            ROOT / "include" / "dmoe.h"]
     if force or not LIB_PATH.exists() or any(s.stat().st_mtime > LIB_PATH.stat().st_mtime for s in srcs):
         subprocess.run(["make", "-s", "-C", str(ORACLE_DIR), "-B" if force else "all"], check=True)
     return LIB_PATH
@@ -80,6 +81,12 @@ def load() -> C.CDLL:
     lib.dmo_rms_norm.restype = None
     lib.dmo_argmax_prob.argtypes = [P, C.c_int, P, P]
     lib.dmo_argmax_prob.restype = None
+    lib.dmo_simd_available.argtypes = []
+    lib.dmo_set_simd.argtypes = [C.c_int]
+    lib.dmo_dot_q4K_simd.argtypes = [C.c_int64, P, P]
+    lib.dmo_dot_q4K_simd.restype = C.c_float
+    lib.dmo_dot_q8_0_simd.argtypes = [C.c_int64, P, P]
+    lib.dmo_dot_q8_0_simd.restype = C.c_float
     lib.dmo_rope_neox.argtypes = [P, C.c_int, C.c_int, C.c_int, C.c_float]
     lib.dmo_rope_neox.restype = None
     lib.dmo_attn_forward.argtypes = [C.POINTER(AttnHParams), C.POINTER(AttnDesc), P, C.c_int, P, P, C.c_int]
@@ -280,6 +287,21 @@ def head_forward(w, h: np.ndarray, eps: float = 1e-6, n_threads: int = 0):
     if rc:
         raise ValueError("oracle head forward failed")
     return tok, prob, logits
+
+
+def simd_available() -> bool:
+    return bool(load().dmo_simd_available())
+
+
+def set_simd(on: bool) -> bool:
+    """Route the quantised dots through the AVX-512 VNNI versions (bit-identical
+    results; the CPU baseline's fast path).  Returns whether they are in use."""
+    return bool(load().dmo_set_simd(1 if on else 0))
+
+
+def vec_dot_simd(wt: int, n: int, wrow: np.ndarray, xrow: np.ndarray) -> float:
+    f = load().dmo_dot_q4K_simd if wt == 12 else load().dmo_dot_q8_0_simd
+    return float(f(n, _p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(xrow))))
 
 
 def rope_neox(x: np.ndarray, n_dims: int, pos: int, base: float) -> np.ndarray:
