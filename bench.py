@@ -41,6 +41,9 @@ def parse():
                     help="weight copies rotated per step so the 256 MB MALL cannot serve repeats")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--rows-steps", type=int, default=20,
+                    help="calls of each row next to the segment (attention, dense MLP, step tail) "
+                         "timed after the layer records (0: skip)")
     ap.add_argument("--prefill-steps", type=int, default=10,
                     help="steps of the 2048-token F16 prefill layer measured after the headline "
                          "(0: skip)")
@@ -283,6 +286,110 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
     return rec
 
 
+def bench_rows(a):
+    """The rows next to the MoE segment at their flash shapes, each timed over
+    a.rows_steps calls with HIP events on the launch stream, weights resident
+    in HBM (copies rotated past the 256 MB memory-side cache): the attention
+    half of a layer (32 and 256 tokens), the dense layer-0 MLP (32 tokens) and
+    the step tail (final norm, 157,184-row LM head, argmax and confidence;
+    32 tokens).  All three stream weights: the roofline is HBM, the
+    algorithmic bytes are stated per record."""
+    import torch
+    import dmoe
+    from dmoe import synth
+
+    ctx = dmoe.Context(0)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    H = 4096
+    rs = dmoe.row_size(dmoe.TYPE_Q4_K, H)
+    out = {}
+
+    def timed(fn, copies):
+        for i in range(3):
+            fn(i % copies)
+        torch.cuda.synchronize(dev)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(a.rows_steps):
+            fn(i % copies)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) / a.rows_steps * 1e3          # us per call
+
+    def rec(workload, us, nbytes, what):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"workload": workload, "us_per_call": round(us, 2), "algorithmic_bytes": int(nbytes),
+                "bytes_are": what, "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    # attention half: 16 copies of the 20.2 MB of projections
+    A = synth.ATTN_FLASH
+    copies = 16
+    layers, keep = [], []
+    for i in range(copies):
+        w = synth.device_attn(dmoe.TYPE_Q4_K, a.seed + i, ctx, **A)
+        layers.append(ctx.attn_wrap_device(w))
+        keep.append(w)
+    QKV = (A["n_head"] + 2 * A["n_head_kv"]) * A["head_dim"]
+    QD = A["n_head"] * A["head_dim"]
+    wbytes = (QKV + H) * rs                                       # wqkv and wo, Q4_K
+    recs = {}
+    for N in (32, 256):
+        h = torch.randn((N, H), device=dev)
+        ho = torch.empty_like(h)
+        mi = torch.empty_like(h)
+        us = timed(lambda i: ctx.attn_forward_device(layers[i], h, N, ho, mi, stream=sp), copies)
+        # weights, h read, h_out and moe_in written, the f32 qkv / attention
+        # rows written and read once
+        act = N * H * 4 * 3 + N * (QKV + QD) * 4 * 2
+        recs[f"n{N}"] = rec(f"attention half, flash shape (32 / 4 heads of 128, RoPE 64, Q4_K projections), "
+                            f"{N} tokens", us, wbytes + act, "wqkv + wo weights, h in, h_out and moe_in out, "
+                            "qkv and attention rows written and read")
+    out["attention"] = recs
+    del layers, keep
+    torch.cuda.empty_cache()
+
+    # dense layer-0 MLP: 5 copies of 63.7 MB
+    Hd, FF = synth.DENSE_FLASH
+    copies = 5
+    dl, keep = [], []
+    for i in range(copies):
+        w = synth.device_dense(Hd, FF, dmoe.TYPE_Q4_K, a.seed + i, ctx)
+        dl.append(ctx.dense_wrap_device(w))
+        keep.append(w)
+    N = 32
+    x = torch.randn((N, Hd), device=dev)
+    y = torch.empty_like(x)
+    us = timed(lambda i: ctx.forward_device(dl[i], x, N, y, sp), copies)
+    wb = 2 * FF * dmoe.row_size(dmoe.TYPE_Q4_K, Hd) + Hd * dmoe.row_size(dmoe.TYPE_Q4_K, FF)
+    out["dense_mlp"] = rec(f"dense layer-0 MLP {Hd} x {FF}, Q4_K (F32 weight semantics), {N} tokens", us,
+                           wb + 2 * N * Hd * 4, "gate, up and down weights, x in, y out")
+    del dl, keep
+    torch.cuda.empty_cache()
+
+    # step tail: 2 copies of the 362 MB LM head
+    Hh, V = synth.HEAD_FLASH
+    copies = 2
+    hl, keep = [], []
+    for i in range(copies):
+        w = synth.device_head(Hh, V, dmoe.TYPE_Q4_K, a.seed + i, ctx)
+        hl.append(ctx.head_wrap_device(w))
+        keep.append(w)
+    h = torch.randn((N, Hh), device=dev)
+    tok = torch.empty(N, dtype=torch.int32, device=dev)
+    prob = torch.empty(N, dtype=torch.float32, device=dev)
+    us = timed(lambda i: ctx.head_forward_device(hl[i], h, N, 1e-6, tok, prob, None, sp), copies)
+    wb = V * dmoe.row_size(dmoe.TYPE_Q4_K, Hh)
+    out["step_tail"] = rec(f"step tail: RMSNorm, LM head {Hh} x {V} Q4_K, argmax + confidence, {N} tokens", us,
+                           wb + 2 * N * V * 4 + N * Hh * 4, "output weights, logits written and read once, h in")
+    del hl, keep
+    ctx.close()
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -322,6 +429,9 @@ def main():
         pre = bench_layer(a, pcfg, a.prefill_steps, max(1, a.prefill_steps // 4), 1, 0)
         pre["unit"] = "tokens/s"
         out["prefill"] = pre
+
+    if a.rows_steps > 0 and cfg.n_tokens <= 256:
+        out["rows"] = bench_rows(a)
 
     if a.copy_probe_mib:
         dev = torch.device("cuda:0")

@@ -1047,6 +1047,10 @@ int head_path(int32_t type, int V, int H)
     return DP_GEMV;
 }
 
+// Output rows up to which a few-token Q4_K projection runs one workgroup per
+// 16 rows (k_down_rows); above it (the LM head) the expert kernel's items.
+constexpr int PROJ_ROWS_MAX = 32768;
+
 // One projection y [N][rows] = W x with W's F32 semantics (x [N][K] f32):
 // the shared-down product of the expert kernels (Q4_K / Q8_0 on int8 digits,
 // F16 on hi / lo pairs) or the GEMV kernel.
@@ -1100,7 +1104,33 @@ int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTens
         return DMOE_OK;
     }
     const bool q8 = path == DP_Q80;
-    wl.chunk = EXPERT_CHUNK;
+    if (!q8 && N <= DR_MAX_TOKENS && rows <= PROJ_ROWS_MAX) {
+        // few tokens, up to a few thousand rows: one workgroup per 16 output
+        // rows over every token (k_down_rows with the shared slot only), so
+        // the weights stream once from as many compute units as there are
+        // 16-row tiles
+        DownRowsJob dj{};
+        dj.sd = W;
+        dj.has_shared = 1;
+        dj.N = N;
+        dj.K = 0;
+        dj.E = 0;
+        dj.H = rows;
+        dj.FF = K;
+        dj.wl = wl;
+        dj.wl.chunk = EXPERT_CHUNK;
+        dj.ec_cap = 0;
+        dj.ahs = p.act;
+        dj.y = y;
+        PrepJob pj{x, N, K, ACT_SPLIT, p.act};
+        STAGE(st_conv, launch_prep(&pj, 1, s));
+        STAGE(st_prod, launch_down_rows(dj, s));
+        return DMOE_OK;
+    }
+    // more rows or tokens: items of up to 32 tokens (4 column blocks of 8
+    // tokens' two digit rows) per weight-tile read
+    const int nc = q8 ? 1 : (N >= 32 ? 4 : N >= 16 ? 2 : 1);
+    wl.chunk = EXPERT_CHUNK * nc;
     MoeJob job{};
     job.sd = W;
     job.has_shared = 1;
@@ -1116,7 +1146,7 @@ int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTens
     job.ys = y;
     PrepJob pj{x, N, K, q8 ? ACT_SPLIT32 : ACT_SPLIT, p.act};
     STAGE(st_conv, launch_prep(&pj, 1, s));
-    STAGE(st_prod, q8 ? launch_expert_q80(1, job, s) : launch_expert_q4k(1, job, s));
+    STAGE(st_prod, q8 ? launch_expert_q80(1, job, s) : launch_expert_q4k(1, job, s, nc));
 #undef STAGE
     return DMOE_OK;
 }
@@ -1155,6 +1185,7 @@ struct HeadWs {
     float *probs;
     float *xn;                           // rms_norm(h) * output_norm
     float *logits;                       // [N][V] (unless the caller's)
+    ArgmaxPart *part;                    // per-chunk argmax / exp-sum partials
     ProjWs proj;
 };
 
@@ -1175,6 +1206,7 @@ size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint
     }
     t.xn = (float *)take((size_t)N * H * 4);
     if (own_logits) t.logits = (float *)take((size_t)N * V * 4);
+    t.part = (ArgmaxPart *)take(argmax_partials_bytes(N, V));
     t.proj = plan_proj(head_path(L->sd.type, V, H), N, H, take);
     if (w) *w = t;
     return off;
@@ -1199,7 +1231,7 @@ int enqueue_head(dmoe_ctx *ctx, const dmoe_layer *L, const HeadWs &w, const floa
     STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->gate_w, w.xn, N, H, eps, s));
     int rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->sd, V, H, w.xn, N, logits, w.proj, s);
     if (rc) return rc;
-    STAGE(ST_COMBINE, launch_argmax_prob(logits, N, V, tokens, probs, s));
+    STAGE(ST_COMBINE, launch_argmax_prob(logits, N, V, w.part, tokens, probs, s));
 #undef STAGE
     return DMOE_OK;
 }

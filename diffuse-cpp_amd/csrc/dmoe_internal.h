@@ -195,9 +195,16 @@ hipError_t launch_qk_rope(const float *qkv, const float *qn, const float *kn, co
 hipError_t launch_attn(const float *Qh, const float *Kh, const float *Vh, const AttnDims &a, float *out,
                        hipStream_t s);
 // Per row of V logits: the argmax (first index of the largest) and its
-// softmax probability 1 / sum exp(l - max) (k_head.hip).
-hipError_t launch_argmax_prob(const float *logits, int N, int V, int32_t *tokens, float *probs,
-                              hipStream_t s);
+// softmax probability 1 / sum exp(l - max) (k_head.hip), through per-chunk
+// partials (argmax_partials_bytes of workspace).
+struct ArgmaxPart {
+    float m;                             // the chunk's largest logit
+    int idx;                             // its first index (V: none above -inf)
+    double sum;                          // sum of exp(l - m) over the chunk
+};
+size_t argmax_partials_bytes(int N, int V);
+hipError_t launch_argmax_prob(const float *logits, int N, int V, ArgmaxPart *part, int32_t *tokens,
+                              float *probs, hipStream_t s);
 // Grouped Q4_K expert products on MFMA (k_expert.hip).  phase 0: h = silu(gate x)
 // * (up x); phase 1: y = down h.
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item

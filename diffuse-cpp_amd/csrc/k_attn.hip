@@ -108,11 +108,30 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     const int N = a.n, h = blockIdx.y, kvh = h / (a.nh / a.nkv);
     const int q_wg = blockIdx.x * AT_Q;
     const float *Q = Qh + (size_t)h * N * HD, *K = Kh + (size_t)kvh * N * HD, *V = Vh + (size_t)kvh * N * HD;
+    // 16-byte pieces of a 64-row tile of HD floats: every thread's pieces are
+    // loaded before any is stored, so the loads overlap
+    constexpr int PPT = AT_K * HD / 4 / 256;          // pieces per thread (8 or 4)
+    static_assert(PPT * 256 * 4 == AT_K * HD, "whole pieces per thread");
+    auto stage_tile = [&](const float *src, int row0, float *dst) {
+        float4 v[PPT];
+#pragma unroll
+        for (int j = 0; j < PPT; j++) {
+            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
+            v[j] = row0 + r < N ? *reinterpret_cast<const float4 *>(src + (size_t)(row0 + r) * HD + 4 * c)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int j = 0; j < PPT; j++) {
+            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
+            float *o = dst + r * LD + 4 * c;
+            o[0] = v[j].x;
+            o[1] = v[j].y;
+            o[2] = v[j].z;
+            o[3] = v[j].w;
+        }
+    };
     // queries of the workgroup (rows past N: zero)
-    for (int i = tid; i < AT_Q * HD; i += 256) {
-        const int r = i / HD, d = i % HD;
-        sQ[r * LD + d] = q_wg + r < N ? Q[(size_t)(q_wg + r) * HD + d] : 0.0f;
-    }
+    stage_tile(Q, q_wg, sQ);
     // keys the workgroup's last query can see
     const int q_last = min(N, q_wg + AT_Q) - 1;
     const int k_end = a.block > 0 ? min(N, (q_last / a.block + 1) * a.block) : N;
@@ -129,12 +148,8 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     for (int b = 0; b < HD / 16; b++) o[b] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = 0; k0 < k_end; k0 += AT_K) {
         __syncthreads();
-        for (int i = tid; i < AT_K * HD; i += 256) {
-            const int r = i / HD, d = i % HD;
-            const bool in = k0 + r < N;
-            sK[r * LD + d] = in ? K[(size_t)(k0 + r) * HD + d] : 0.0f;
-            sV[r * LD + d] = in ? V[(size_t)(k0 + r) * HD + d] : 0.0f;
-        }
+        stage_tile(K, k0, sK);
+        stage_tile(V, k0, sV);
         __syncthreads();
         // S[16 q][64 k]: lane holds rows 4g + i of key block kb, key kb*16 + r16
         f4v sacc[4];

@@ -165,6 +165,18 @@ __global__ __launch_bounds__(DR_WAVES * 64) void k_down_rows(DownRowsJob job)
     }
     __syncthreads();
 
+    // A projection (K == 0: shared units only, at most N / 8 of them, fewer
+    // than the wavefronts) splits the units' super-blocks instead: wavefront w
+    // takes the contiguous range of (unit, super-block) steps w T / 8 ..
+    // (w + 1) T / 8 - 1 of the T = units x nsb, and leaves the partial sums of
+    // the units it touches in its own slot of LDS (aliasing the routed
+    // products, unused here), added in wavefront order after the barrier.
+    const bool ksplit = K == 0;
+    float *ps = y_s;                                   // [DR_WAVES][N][16] partial sums
+    if (ksplit) {
+        for (int i = tid; i < DR_WAVES * N * 16; i += DR_WAVES * 64) ps[i] = 0.0f;
+        __syncthreads();
+    }
     // Activation row of row j of a unit (rows past the unit's last repeat
     // it), without branches: every load of a step is issued unconditionally,
     // so the vector-memory counter waits stay exact across the step loop.
@@ -211,6 +223,12 @@ __global__ __launch_bounds__(DR_WAVES * 64) void k_down_rows(DownRowsJob job)
     };
     auto store = [&](int u, const float (&acc)[4]) {
         const int np = s_unp[u], p0 = s_up0[u];
+        if (ksplit) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 2)
+                if (2 * g + (i >> 1) < -np) ps[(wave * N + p0 + 2 * g + (i >> 1)) * 16 + r16] = acc[i] + acc[i + 1];
+            return;
+        }
         if (np > 0) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -228,10 +246,21 @@ __global__ __launch_bounds__(DR_WAVES * 64) void k_down_rows(DownRowsJob job)
     // before this step's arithmetic.  Every load is issued in consumption
     // order, so waiting for one step's operands never waits for a later
     // step's (the vector-memory counter completes in issue order).
-    const int nk = wave < nu ? (nu - 1 - wave) / DR_WAVES + 1 : 0;
-    const int S = nk * nsb;
+    const int ustride = ksplit ? 1 : DR_WAVES;
+    int S, u_first, sb_first;
+    if (ksplit) {
+        const int T = nu * nsb, t0 = wave * T / DR_WAVES, t1 = (wave + 1) * T / DR_WAVES;
+        S = t1 - t0;
+        u_first = S > 0 ? t0 / nsb : 0;
+        sb_first = S > 0 ? t0 - u_first * nsb : 0;
+    } else {
+        const int nk = wave < nu ? (nu - 1 - wave) / DR_WAVES + 1 : 0;
+        S = nk * nsb;
+        u_first = wave;
+        sb_first = 0;
+    }
     if (S > 0) {
-        int lu = wave, lsb = 0, ls = 0;          // next step to load (clamped to the last)
+        int lu = u_first, lsb = sb_first, ls = 0;          // next step to load (clamped to the last)
         Cursor lc;
         resolve(lu, lc);
         auto next = [&]() {
@@ -239,7 +268,7 @@ __global__ __launch_bounds__(DR_WAVES * 64) void k_down_rows(DownRowsJob job)
                 ls++;
                 if (++lsb == nsb) {
                     lsb = 0;
-                    lu += DR_WAVES;
+                    lu += ustride;
                     resolve(lu, lc);
                 }
             }
@@ -255,17 +284,19 @@ __global__ __launch_bounds__(DR_WAVES * 64) void k_down_rows(DownRowsJob job)
         load(lc, lsb, o3);
         next();
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        int cu = wave, csb = 0;
+        int cu = u_first, csb = sb_first, cs = 0;
         auto step = [&](DrOps &cur, DrOps &ahead) {
             load(lc, lsb, ahead);
             next();
             dr_compute(cur, g, acc);
-            if (++csb == nsb) {
+            ++cs;
+            if (++csb == nsb || cs == S) {
+                // a unit's last super-block, or (split) the end of the range
                 store(cu, acc);
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[i] = 0.0f;
                 csb = 0;
-                cu += DR_WAVES;
+                cu += ustride;
             }
         };
         for (int s = 0; s < S; s += 5) {
@@ -278,21 +309,31 @@ __global__ __launch_bounds__(DR_WAVES * 64) void k_down_rows(DownRowsJob job)
     }
     __syncthreads();
 
-    // combine: out[t][row] = ((y_0 w_0 + y_1 w_1) + ...) + y_shared
+    // combine: out[t][row] = ((y_0 w_0 + y_1 w_1) + ...) + y_shared; with no
+    // routed pairs (K == 0: a plain projection through the shared slot) the
+    // shared value alone
     float *out = job.y + (size_t)blockIdx.x * 16;
     for (int o = tid; o < N * 16; o += DR_WAVES * 64) {
         const int t = o >> 4, r = o & 15;
-        const float *wt = job.weights + (size_t)t * K;
-        float a = y_s[(t * K) * 16 + r] * wt[0];
-        for (int k = 1; k < K; k++) a = a + y_s[(t * K + k) * 16 + r] * wt[k];
-        if (job.has_shared) a = a + ys_s[t * 16 + r];
+        float a;
+        if (ksplit) {
+            a = ps[t * 16 + r];
+            for (int w = 1; w < DR_WAVES; w++) a = a + ps[(w * N + t) * 16 + r];
+        } else if (K > 0) {
+            const float *wt = job.weights + (size_t)t * K;
+            a = y_s[(t * K) * 16 + r] * wt[0];
+            for (int k = 1; k < K; k++) a = a + y_s[(t * K + k) * 16 + r] * wt[k];
+            if (job.has_shared) a = a + ys_s[t * 16 + r];
+        } else {
+            a = ys_s[t * 16 + r];
+        }
         out[(size_t)t * H + r] = a;
     }
 }
 
 bool down_rows_ok(int N, int K, int E, int H, int FF)
 {
-    return N > 0 && N <= DR_MAX_TOKENS && N * K <= DR_MAX_PAIRS && E <= DR_MAX_E && H % 16 == 0 &&
+    return N > 0 && N <= DR_MAX_TOKENS && K >= 0 && N * K <= DR_MAX_PAIRS && E <= DR_MAX_E && H % 16 == 0 &&
            FF % 256 == 0;
 }
 
@@ -300,7 +341,8 @@ hipError_t launch_down_rows(const DownRowsJob &job, hipStream_t s)
 {
     if (!down_rows_ok(job.N, job.K, job.E, job.H, job.FF) ||
         job.ec_cap + (job.has_shared ? (job.N + 7) / 8 : 0) > DR_MAX_UNITS ||
-        job.wl.chunk != EXPERT_CHUNK || job.ah.K != job.FF || (job.has_shared && job.ahs.K != job.FF))
+        job.wl.chunk != EXPERT_CHUNK || (job.K > 0 && job.ah.K != job.FF) ||
+        (job.has_shared && job.ahs.K != job.FF) || (job.K == 0 && (!job.has_shared || job.ec_cap != 0)))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_down_rows, dim3(job.H / 16), dim3(DR_WAVES * 64), 0, s, job);
     return hipGetLastError();

@@ -355,3 +355,31 @@ def attn_to_device(w: AttnWeights, device) -> AttnWeights:
         return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device)
     return replace(w, attn_norm=d(w.attn_norm), qkv=d(w.qkv), wo=d(w.wo), post_norm=d(w.post_norm),
                    q_norm=d(w.q_norm), k_norm=d(w.k_norm))
+
+
+def device_attn(wtype: int, seed: int, ctx, n_embd: int, n_head: int, n_head_kv: int, head_dim: int,
+                rotary_dim: int, block_length: int = 32, rope_base: float = 3e6, rms_eps: float = 1e-6,
+                qk_norm: bool = True, w_std: float = 0.02) -> AttnWeights:
+    """An AttnWeights on the GPU: projections from torch's seeded generator
+    quantised by dmoe_quantize_device, norm gains ~ U(0.5, 1.5)."""
+    import torch
+    dev = torch.device(f"cuda:{ctx.device}")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed * 7919 + 57)
+    QD, QKV = n_head * head_dim, (n_head + 2 * n_head_kv) * head_dim
+
+    def q(rows, n):
+        out = torch.empty((rows, row_size(wtype, n)), dtype=torch.uint8, device=dev)
+        f = torch.randn((rows, n), generator=g, device=dev, dtype=torch.float32).mul_(w_std)
+        ctx.quantize_device(wtype, f, out, rows, n)
+        torch.cuda.synchronize(dev)
+        return out
+
+    def u(stream, n):
+        return torch.from_numpy(uniform(seed, stream, n, 0.5, 1.5)).to(dev)
+    return AttnWeights(n_embd=n_embd, n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim,
+                       rotary_dim=rotary_dim, block_length=block_length, rope_base=rope_base, rms_eps=rms_eps,
+                       wtype=wtype, attn_norm=u(S_ANORM, n_embd), qkv=q(QKV, n_embd), wo=q(n_embd, QD),
+                       post_norm=u(S_PNORM, n_embd),
+                       q_norm=u(S_QN, head_dim) if qk_norm else None,
+                       k_norm=u(S_KN, head_dim) if qk_norm else None)
