@@ -912,7 +912,15 @@ struct DenseWs {
     ActI8 axs, ahs;                      // split x and h (int8 paths)
     uint16_t *xs16, *hs16;               // hi / lo f16 pairs (F16 path)
     float *hs;                           // f32 h (GEMV path)
+    float *part_gu, *part_d;             // slice sums of the few-token Q4_K projections
 };
+
+// Few tokens of a Q4_K dense MLP: gate and up as one two-matrix projection,
+// h formed and converted from their slice sums, down as a projection.
+bool dense_few(int path, int H, int FF, int N)
+{
+    return path == DP_Q4K && proj_ok(FF, H, N) && proj_ok(H, FF, N) && FF % 256 == 0;
+}
 
 size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, DenseWs *w)
 {
@@ -933,6 +941,10 @@ size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, Dense
     case DP_Q4K:
         t.axs = take_act(take, N, H, true);
         t.ahs = take_act(take, N, FF, true);
+        if (dense_few(DP_Q4K, H, FF, N)) {
+            t.part_gu = (float *)take(proj_partial_floats(FF, H, 2, N) * 4);
+            if (proj_plan(H, FF, 1, N).KS > 1) t.part_d = (float *)take(proj_partial_floats(H, FF, 1, N) * 4);
+        }
         break;
     case DP_Q80:
         t.axs = take_act(take, N, H, true, true);
@@ -978,6 +990,38 @@ int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const fl
     if (path == DP_GEMV) {
         STAGE(ST_SH_GATEUP, launch_gateup_shared(L->sg, L->su, x, N, H, FF, w.hs, s));
         STAGE(ST_SH_DOWN, launch_down_shared(L->sd, w.hs, N, FF, H, y, s));
+        return DMOE_OK;
+    }
+    if (dense_few(path, H, FF, N)) {
+        // gate and up: one launch over both matrices, h from their slices
+        ProjJob gu{};
+        gu.w[0] = L->sg.data;
+        gu.w[1] = L->su.data;
+        gu.M = 2;
+        gu.R = FF;
+        gu.K = H;
+        gu.N = N;
+        gu.KS = proj_plan(FF, H, 2, N).KS;
+        gu.x = w.axs;
+        gu.partial = 1;
+        gu.out = w.part_gu;
+        ProjJob dn{};
+        dn.w[0] = L->sd.data;
+        dn.M = 1;
+        dn.R = H;
+        dn.K = FF;
+        dn.N = N;
+        dn.KS = proj_plan(H, FF, 1, N).KS;
+        dn.x = w.ahs;
+        dn.partial = dn.KS > 1;
+        dn.out = dn.partial ? w.part_d : y;
+        dn.ldo = H;
+        PrepJob pj{x, N, H, ACT_SPLIT, w.axs};
+        STAGE(ST_ACTQ_X, launch_prep(&pj, 1, s));
+        STAGE(ST_SH_GATEUP, launch_proj_q4k(gu, s));
+        STAGE(ST_ACTQ_H, launch_proj_swiglu(w.part_gu, gu.KS, N, FF, w.ahs, s));
+        STAGE(ST_SH_DOWN, launch_proj_q4k(dn, s));
+        if (dn.partial) STAGE(ST_COMBINE, launch_proj_reduce(w.part_d, dn.KS, N, H, y, H, s));
         return DMOE_OK;
     }
     // the expert kernels read an empty routed work list
@@ -1058,15 +1102,20 @@ struct ProjWs {
     int32_t *n_ec;                       // an empty routed work list
     ActI8 act;                           // split x (int8 paths)
     uint16_t *x16;                       // hi / lo f16 x (F16 path)
+    float *part;                         // slice sums of the few-token Q4_K projection
 };
 
 template <class Take>
-ProjWs plan_proj(int path, int N, int K, Take &&take)
+ProjWs plan_proj(int path, int N, int K, int rows, Take &&take)
 {
     ProjWs p{};
     p.n_ec = (int32_t *)take(4);
     switch (path) {
-    case DP_Q4K: p.act = take_act(take, N, K, true); break;
+    case DP_Q4K:
+        p.act = take_act(take, N, K, true);
+        if (proj_ok(rows, K, N) && proj_plan(rows, K, 1, N).KS > 1)
+            p.part = (float *)take(proj_partial_floats(rows, K, 1, N) * 4);
+        break;
     case DP_Q80: p.act = take_act(take, N, K, true, true); break;
     case DP_F16: p.x16 = (uint16_t *)take((size_t)2 * N * K * 2); break;
     default: break;
@@ -1081,6 +1130,26 @@ int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTens
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
     if (path == DP_GEMV) {
         STAGE(st_prod, launch_down_shared(W, x, N, K, rows, y, s));
+        return DMOE_OK;
+    }
+    if (path == DP_Q4K && proj_ok(rows, K, N)) {
+        // few tokens: 128-row tiles x reduction slices over every CU, the
+        // slices added in order
+        ProjJob j{};
+        j.w[0] = W.data;
+        j.M = 1;
+        j.R = rows;
+        j.K = K;
+        j.N = N;
+        j.KS = proj_plan(rows, K, 1, N).KS;
+        j.x = p.act;
+        j.partial = j.KS > 1;
+        j.out = j.partial ? p.part : y;
+        j.ldo = rows;
+        PrepJob pj{x, N, K, ACT_SPLIT, p.act};
+        STAGE(st_conv, launch_prep(&pj, 1, s));
+        STAGE(st_prod, launch_proj_q4k(j, s));
+        if (j.partial) STAGE(ST_COMBINE, launch_proj_reduce(p.part, j.KS, N, rows, y, rows, s));
         return DMOE_OK;
     }
     LAUNCH_TRY(ctx, launch_fill_i32(p.n_ec, 0, 1, s));
@@ -1207,7 +1276,7 @@ size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint
     t.xn = (float *)take((size_t)N * H * 4);
     if (own_logits) t.logits = (float *)take((size_t)N * V * 4);
     t.part = (ArgmaxPart *)take(argmax_partials_bytes(N, V));
-    t.proj = plan_proj(head_path(L->sd.type, V, H), N, H, take);
+    t.proj = plan_proj(head_path(L->sd.type, V, H), N, H, V, take);
     if (w) *w = t;
     return off;
 }
@@ -1273,8 +1342,8 @@ size_t plan_attn(const dmoe_layer *L, int N, bool host_io, uint8_t *base, AttnWs
     t.att = (float *)take((size_t)N * QD * 4);
     t.proj = (float *)take((size_t)N * H * 4);
     t.scratch = (float *)take((size_t)N * H * 4);
-    t.pq = plan_proj(head_path(L->aqkv.type, QKV, H), N, H, take);
-    t.po = plan_proj(head_path(L->awo.type, H, QD), N, QD, take);
+    t.pq = plan_proj(head_path(L->aqkv.type, QKV, H), N, H, QKV, take);
+    t.po = plan_proj(head_path(L->awo.type, H, QD), N, QD, H, take);
     if (w) *w = t;
     return off;
 }

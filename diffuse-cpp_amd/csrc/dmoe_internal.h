@@ -205,6 +205,30 @@ struct ArgmaxPart {
 size_t argmax_partials_bytes(int N, int V);
 hipError_t launch_argmax_prob(const float *logits, int N, int V, ArgmaxPart *part, int32_t *tokens,
                               float *probs, hipStream_t s);
+// Q4_K projections of few tokens with F32 weight semantics (k_proj.hip):
+// matrices w[0..M-1] (tiled Q4_K, R rows, reduction K) against x as two int8
+// digit rows per token (ACT_SPLIT); the reduction runs in KS slices.
+constexpr int PROJ_MAX_TOKENS = 32;
+struct ProjJob {
+    const uint8_t *w[2];
+    int32_t M, R, K, N, KS;
+    ActI8 x;
+    float *out;              // partial: [M][KS][N][R] slice sums; else y [N][ldo] (M = KS = 1)
+    int32_t partial, ldo;
+};
+bool proj_ok(int R, int K, int N);
+struct ProjPlan {
+    int T;                   // 16-row tiles per wavefront
+    int KS;                  // reduction slices
+};
+ProjPlan proj_plan(int R, int K, int M, int N);          // the launch shape for a projection
+size_t proj_partial_floats(int R, int K, int M, int N);  // partial buffer of that KS
+hipError_t launch_proj_q4k(const ProjJob &j, hipStream_t s);
+// y [N][ldy] = the KS slices of part [KS][N][R] added in slice order
+hipError_t launch_proj_reduce(const float *part, int KS, int N, int R, float *y, int ldy, hipStream_t s);
+// h = silu(gate) up from part [2][KS][N][R], to ah (two int8 digit rows per token)
+hipError_t launch_proj_swiglu(const float *part, int KS, int N, int R, const ActI8 &ah, hipStream_t s);
+
 // Grouped Q4_K expert products on MFMA (k_expert.hip).  phase 0: h = silu(gate x)
 // * (up x); phase 1: y = down h.
 constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
