@@ -1123,6 +1123,39 @@ ProjWs plan_proj(int path, int N, int K, int rows, Take &&take)
     return p;
 }
 
+// Few tokens of Q4_K weights: k_proj.hip on x already converted to p.act.
+bool proj_few(int path, int rows, int K, int N) { return path == DP_Q4K && proj_ok(rows, K, N); }
+
+// y [N][rows] = W x from p.act: 128 T-row tiles x reduction slices over every
+// CU.  With ks_out the slices are left for the consumer to add in order
+// (*src_out: the slices, *ks_out of them, N rows apart); else they are added
+// into y here.
+int enqueue_proj_few(dmoe_ctx *ctx, bool prof, int st_prod, const WTensor &W, int rows, int K, int N,
+                     const ProjWs &p, float *y, int *ks_out, const float **src_out, hipStream_t s)
+{
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
+    ProjJob j{};
+    j.w[0] = W.data;
+    j.M = 1;
+    j.R = rows;
+    j.K = K;
+    j.N = N;
+    j.KS = proj_plan(rows, K, 1, N).KS;
+    j.x = p.act;
+    j.partial = j.KS > 1;
+    j.out = j.partial ? p.part : y;
+    j.ldo = rows;
+    STAGE(st_prod, launch_proj_q4k(j, s));
+    if (ks_out) {
+        *ks_out = j.KS;
+        *src_out = j.out;
+    } else if (j.partial) {
+        STAGE(ST_COMBINE, launch_proj_reduce(p.part, j.KS, N, rows, y, rows, s));
+    }
+#undef STAGE
+    return DMOE_OK;
+}
+
 int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTensor &W, int rows, int K,
                  const float *x, int N, float *y, const ProjWs &p, hipStream_t s)
 {
@@ -1132,25 +1165,10 @@ int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTens
         STAGE(st_prod, launch_down_shared(W, x, N, K, rows, y, s));
         return DMOE_OK;
     }
-    if (path == DP_Q4K && proj_ok(rows, K, N)) {
-        // few tokens: 128-row tiles x reduction slices over every CU, the
-        // slices added in order
-        ProjJob j{};
-        j.w[0] = W.data;
-        j.M = 1;
-        j.R = rows;
-        j.K = K;
-        j.N = N;
-        j.KS = proj_plan(rows, K, 1, N).KS;
-        j.x = p.act;
-        j.partial = j.KS > 1;
-        j.out = j.partial ? p.part : y;
-        j.ldo = rows;
+    if (proj_few(path, rows, K, N)) {
         PrepJob pj{x, N, K, ACT_SPLIT, p.act};
         STAGE(st_conv, launch_prep(&pj, 1, s));
-        STAGE(st_prod, launch_proj_q4k(j, s));
-        if (j.partial) STAGE(ST_COMBINE, launch_proj_reduce(p.part, j.KS, N, rows, y, rows, s));
-        return DMOE_OK;
+        return enqueue_proj_few(ctx, prof, st_prod, W, rows, K, N, p, y, nullptr, nullptr, s);
     }
     LAUNCH_TRY(ctx, launch_fill_i32(p.n_ec, 0, 1, s));
     WorkList wl{};
@@ -1296,9 +1314,24 @@ int enqueue_head(dmoe_ctx *ctx, const dmoe_layer *L, const HeadWs &w, const floa
     const int H = L->hp.n_embd, V = L->n_vocab;
     const bool prof = ctx->prof;
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
-    // :296-297 rms_norm(cur) * output_norm (h is only read: no residual add)
-    STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->gate_w, w.xn, N, H, eps, s));
-    int rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->sd, V, H, w.xn, N, logits, w.proj, s);
+    // :296-297 rms_norm(cur) * output_norm (h is only read: no residual add);
+    // :299 the LM head.  Few tokens of Q4_K: the norm hands the head its
+    // int8 digits directly.
+    int rc;
+    if (proj_few(head_path(L->sd.type, V, H), V, H, N) && H <= 8192) {
+        NormArgs na{};
+        na.h_in = h;
+        na.gain = L->gate_w;
+        na.act = w.proj.act;
+        na.rows = N;
+        na.H = H;
+        na.eps = eps;
+        STAGE(ST_FRONT, launch_norm_fused(na, s));
+        rc = enqueue_proj_few(ctx, prof, ST_SH_DOWN, L->sd, V, H, N, w.proj, logits, nullptr, nullptr, s);
+    } else {
+        STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->gate_w, w.xn, N, H, eps, s));
+        rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->sd, V, H, w.xn, N, logits, w.proj, s);
+    }
     if (rc) return rc;
     STAGE(ST_COMBINE, launch_argmax_prob(logits, N, V, w.part, tokens, probs, s));
 #undef STAGE
@@ -1354,13 +1387,32 @@ int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const floa
     const dmoe_attn_hparams &a = L->ahp;
     const int H = a.n_embd, QD = a.n_head * a.head_dim, KD = a.n_head_kv * a.head_dim, QKV = QD + 2 * KD;
     const bool prof = ctx->prof;
+    // few tokens of Q4_K projections: the norms hand them int8 digits and take
+    // their reduction slices directly (k_norm_fused, k_qk_rope)
+    const bool fq = proj_few(head_path(L->aqkv.type, QKV, H), QKV, H, N) && H <= 8192;
+    const bool fo = proj_few(head_path(L->awo.type, H, QD), H, QD, N) && H <= 8192;
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
-    // :120-121 input layernorm
-    STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->attn_norm, w.xn, N, H,
-                                            a.rms_eps, s));
-    // :124 fused QKV
-    int rc = enqueue_proj(ctx, prof, ST_ACTQ_X, ST_SH_GATEUP, L->aqkv, QKV, H, w.xn, N, w.qkv, w.pq, s);
-    if (rc) return rc;
+    // :120-121 input layernorm; :124 fused QKV
+    const float *qkv = w.qkv;
+    int qks = 1;
+    int rc;
+    if (fq) {
+        NormArgs na{};
+        na.h_in = h;
+        na.gain = L->attn_norm;
+        na.act = w.pq.act;
+        na.rows = N;
+        na.H = H;
+        na.eps = a.rms_eps;
+        STAGE(ST_FRONT, launch_norm_fused(na, s));
+        if ((rc = enqueue_proj_few(ctx, prof, ST_SH_GATEUP, L->aqkv, QKV, H, N, w.pq, w.qkv, &qks, &qkv, s)))
+            return rc;
+    } else {
+        STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->attn_norm, w.xn, N, H,
+                                                a.rms_eps, s));
+        if ((rc = enqueue_proj(ctx, prof, ST_ACTQ_X, ST_SH_GATEUP, L->aqkv, QKV, H, w.xn, N, w.qkv, w.pq, s)))
+            return rc;
+    }
     AttnDims d{};
     d.n = N;
     d.nh = a.n_head;
@@ -1373,15 +1425,36 @@ int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const floa
     // the rope cache's angle step, as ggml computes it on the host
     d.theta_scale = a.rotary_dim > 0 ? powf(a.rope_base, -2.0f / (float)a.rotary_dim) : 1.0f;
     d.scale = 1.0f / sqrtf((float)a.head_dim);
-    STAGE(ST_ROUTE, launch_qk_rope(w.qkv, L->qn, L->kn, d, w.Qh, w.Kh, w.Vh, s));
+    STAGE(ST_ROUTE, launch_qk_rope(qkv, qks, (size_t)N * QKV, L->qn, L->kn, d, w.Qh, w.Kh, w.Vh, s));
     STAGE(ST_SCORES, launch_attn(w.Qh, w.Kh, w.Vh, d, w.att, s));
-    // :172 output projection
-    if ((rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->awo, H, QD, w.att, N, w.proj, w.po, s)))
-        return rc;
-    // :175-178 residual, then the post-attention layernorm (the MoE input)
-    if (h_out != h) HIP_TRY(ctx, hipMemcpyAsync(h_out, h, (size_t)N * H * 4, hipMemcpyDeviceToDevice, s));
-    STAGE(ST_COMBINE, launch_residual_rmsnorm(h_out, w.proj, L->post_norm, moe_in ? moe_in : w.scratch, N, H,
-                                              a.rms_eps, s));
+    // :172 output projection; :175-178 residual, then the post-attention
+    // layernorm (the MoE input)
+    if (fo) {
+        PrepJob pj{w.att, N, QD, ACT_SPLIT, w.po.act};
+        STAGE(ST_ACTQ_H, launch_prep(&pj, 1, s));
+        const float *o = w.proj;
+        int oks = 1;
+        if ((rc = enqueue_proj_few(ctx, prof, ST_SH_DOWN, L->awo, H, QD, N, w.po, w.proj, &oks, &o, s)))
+            return rc;
+        NormArgs na{};
+        na.h_in = h;
+        na.h_out = h_out;
+        na.y = o;
+        na.ks = oks;
+        na.kstride = (size_t)N * H;
+        na.gain = L->post_norm;
+        na.x = moe_in;
+        na.rows = N;
+        na.H = H;
+        na.eps = a.rms_eps;
+        STAGE(ST_COMBINE, launch_norm_fused(na, s));
+    } else {
+        if ((rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->awo, H, QD, w.att, N, w.proj, w.po, s)))
+            return rc;
+        if (h_out != h) HIP_TRY(ctx, hipMemcpyAsync(h_out, h, (size_t)N * H * 4, hipMemcpyDeviceToDevice, s));
+        STAGE(ST_COMBINE, launch_residual_rmsnorm(h_out, w.proj, L->post_norm, moe_in ? moe_in : w.scratch, N, H,
+                                                  a.rms_eps, s));
+    }
 #undef STAGE
     return DMOE_OK;
 }

@@ -156,6 +156,22 @@ hipError_t launch_tile_f16(const uint8_t *src, size_t nb1, size_t nb2, int rows,
 // Residual add and RMSNorm of the residual stream (k_norm.hip): per row of H
 // floats (H % 4 == 0, 16-byte aligned rows), h += y (y may be null), then
 // x = rms_norm(h, eps) * gain (gain may be null).
+// rows of h_in (+ the sum of y's ks slices, kstride floats apart, written to
+// h_out when given) -> rms_norm * gain to x (f32, when given) and / or act
+// (two int8 digit rows per row, ACT_SPLIT, when act.q is given); H <= 8192
+struct NormArgs {
+    const float *h_in;
+    float *h_out;
+    const float *y;
+    int32_t ks;
+    size_t kstride;
+    const float *gain;
+    float *x;
+    ActI8 act;
+    int32_t rows, H;
+    float eps;
+};
+hipError_t launch_norm_fused(const NormArgs &a, hipStream_t s);
 hipError_t launch_residual_rmsnorm(float *h, const float *y, const float *gain, float *x, int rows, int H,
                                    float eps, hipStream_t s);
 
@@ -187,10 +203,11 @@ struct AttnDims {
     int32_t qk_norm, block;              // use_qk_norm, block_length (0: bidirectional)
     float eps, theta_scale, scale;       // rms eps, powf(base, -2/rd), 1/sqrt(hd)
 };
-// fused QKV rows [N][(nh + 2 nkv) hd] -> QK RMSNorm, partial NEOX RoPE ->
-// head-major Q [nh][N][hd], K, V [nkv][N][hd]
-hipError_t launch_qk_rope(const float *qkv, const float *qn, const float *kn, const AttnDims &a, float *Qh,
-                          float *Kh, float *Vh, hipStream_t s);
+// fused QKV rows [N][(nh + 2 nkv) hd] (the sum of ks slices kstride floats
+// apart) -> QK RMSNorm, partial NEOX RoPE -> head-major Q [nh][N][hd], K, V
+// [nkv][N][hd]
+hipError_t launch_qk_rope(const float *qkv, int ks, size_t kstride, const float *qn, const float *kn,
+                          const AttnDims &a, float *Qh, float *Kh, float *Vh, hipStream_t s);
 // block-causal GQA attention -> out [N][nh hd]
 hipError_t launch_attn(const float *Qh, const float *Kh, const float *Vh, const AttnDims &a, float *out,
                        hipStream_t s);

@@ -20,6 +20,8 @@
 //   v_mfma_f32_16x16x4f32 (fp32 operands and accumulation), online softmax
 //   per query row in registers.  Keys past the last block a query tile can
 //   see are not visited.
+#include <type_traits>
+
 #include "dmoe_internal.h"
 
 #pragma clang fp contract(off)
@@ -30,7 +32,8 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int QR_THREADS = 256;
 
-__global__ __launch_bounds__(QR_THREADS) void k_qk_rope(const float *__restrict__ qkv, const float *__restrict__ qn,
+__global__ __launch_bounds__(QR_THREADS) void k_qk_rope(const float *__restrict__ qkv, int ks, size_t kstride,
+                                                        const float *__restrict__ qn,
                                                         const float *__restrict__ kn, AttnDims a,
                                                         float *__restrict__ Qh, float *__restrict__ Kh,
                                                         float *__restrict__ Vh)
@@ -44,7 +47,12 @@ __global__ __launch_bounds__(QR_THREADS) void k_qk_rope(const float *__restrict_
     const int HD = a.hd, QKV = (a.nh + 2 * a.nkv) * HD;
     const float *src = qkv + (size_t)t * QKV + (size_t)hh * HD;
     float *x = s_x[w];
-    for (int d = lane; d < HD; d += 64) x[d] = src[d];
+    // the fused projection's row: the sum of its ks reduction slices, in order
+    for (int d = lane; d < HD; d += 64) {
+        float v = src[d];
+        for (int k = 1; k < ks; k++) v = v + src[(size_t)k * kstride + d];
+        x[d] = v;
+    }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     if (hh < a.nh + a.nkv) {
@@ -82,12 +90,13 @@ __global__ __launch_bounds__(QR_THREADS) void k_qk_rope(const float *__restrict_
     for (int d = lane; d < HD; d += 64) dst[d] = x[d];
 }
 
-hipError_t launch_qk_rope(const float *qkv, const float *qn, const float *kn, const AttnDims &a, float *Qh,
-                          float *Kh, float *Vh, hipStream_t s)
+hipError_t launch_qk_rope(const float *qkv, int ks, size_t kstride, const float *qn, const float *kn,
+                          const AttnDims &a, float *Qh, float *Kh, float *Vh, hipStream_t s)
 {
-    if (a.hd <= 0 || a.hd > 256 || a.rd > a.hd || a.rd % 2 || a.rd / 2 > 64) return hipErrorInvalidValue;
+    if (a.hd <= 0 || a.hd > 256 || a.rd > a.hd || a.rd % 2 || a.rd / 2 > 64 || ks < 1) return hipErrorInvalidValue;
     const int items = a.n * (a.nh + 2 * a.nkv);
-    hipLaunchKernelGGL(k_qk_rope, dim3((items + 3) / 4), dim3(QR_THREADS), 0, s, qkv, qn, kn, a, Qh, Kh, Vh);
+    hipLaunchKernelGGL(k_qk_rope, dim3((items + 3) / 4), dim3(QR_THREADS), 0, s, qkv, ks, kstride, qn, kn, a, Qh,
+                       Kh, Vh);
     return hipGetLastError();
 }
 
@@ -151,19 +160,34 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         stage_tile(K, k0, sK);
         stage_tile(V, k0, sV);
         __syncthreads();
+        // a wavefront whose queries are all past N, and key blocks / steps
+        // wholly past the last visible key, have nothing to add (their
+        // probabilities are 0): skipped
+        if (q0 >= N) continue;
+        const int nkb = min(4, (k_end - k0 + 15) / 16);
+        const int nps = min(AT_K / 4, (k_end - k0 + 3) / 4);
         // S[16 q][64 k]: lane holds rows 4g + i of key block kb, key kb*16 + r16
         f4v sacc[4];
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) sacc[kb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
         const float *qrow = sQ + (16 * w + r16) * LD;
+        auto qk = [&](auto nkb_c) {
+            constexpr int NKB = decltype(nkb_c)::value;
 #pragma unroll 4
-        for (int s = 0; s < HD / 4; s++) {
-            const float av = qrow[4 * s + g];
+            for (int s = 0; s < HD / 4; s++) {
+                const float av = qrow[4 * s + g];
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
-                const float bv = sK[(kb * 16 + r16) * LD + 4 * s + g];
-                sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, sacc[kb], 0, 0, 0);
+                for (int kb = 0; kb < NKB; kb++) {
+                    const float bv = sK[(kb * 16 + r16) * LD + 4 * s + g];
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, sacc[kb], 0, 0, 0);
+                }
             }
+        };
+        switch (nkb) {
+        case 1: qk(std::integral_constant<int, 1>{}); break;
+        case 2: qk(std::integral_constant<int, 2>{}); break;
+        case 3: qk(std::integral_constant<int, 3>{}); break;
+        default: qk(std::integral_constant<int, 4>{}); break;
         }
         // scale, mask, online softmax per query row (rows 4g + i of the wave)
         float mt[4];
@@ -214,14 +238,20 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         // O[16 q][HD] += P[16 q][64 k] V[64 k][HD]
+        auto pv = [&](int ns) {
 #pragma unroll 4
-        for (int s = 0; s < AT_K / 4; s++) {
-            const float av = pw[r16 * (AT_K + 1) + 4 * s + g];
-            const float *vrow = sV + (4 * s + g) * LD;
+            for (int s = 0; s < ns; s++) {
+                const float av = pw[r16 * (AT_K + 1) + 4 * s + g];
+                const float *vrow = sV + (4 * s + g) * LD;
 #pragma unroll
-            for (int b = 0; b < HD / 16; b++)
-                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, vrow[b * 16 + r16], o[b], 0, 0, 0);
-        }
+                for (int b = 0; b < HD / 16; b++)
+                    o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, vrow[b * 16 + r16], o[b], 0, 0, 0);
+            }
+        };
+        if (nps == AT_K / 4)
+            pv(AT_K / 4);
+        else
+            pv(nps);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
