@@ -107,11 +107,17 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, const float *__restrict__ Kh,
                                               const float *__restrict__ Vh, AttnDims a, float *__restrict__ out)
 {
-    constexpr int LD = HD + 1;                         // padded LDS rows
-    __shared__ float sQ[AT_Q * LD];
-    __shared__ float sK[AT_K * LD];
-    __shared__ float sV[AT_K * LD];
-    __shared__ float sP[4][16 * (AT_K + 1)];
+    // padded LDS rows, so that the 64 lanes of an operand read hit 64
+    // different banks: Q and K are read at row r16, column 4 s + g (a row
+    // stride of 4 mod 64 words spreads them), V at row 4 s + g, column
+    // 16 b + r16 (16 mod 64), P like Q
+    constexpr int LD = HD + 4;
+    constexpr int LDV = HD + 16;
+    constexpr int LDP = AT_K + 4;
+    __shared__ __align__(16) float sQ[AT_Q * LD];
+    __shared__ __align__(16) float sK[AT_K * LD];
+    __shared__ __align__(16) float sV[AT_K * LDV];
+    __shared__ float sP[4][16 * LDP];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int N = a.n, h = blockIdx.y, kvh = h / (a.nh / a.nkv);
@@ -121,7 +127,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     // loaded before any is stored, so the loads overlap
     constexpr int PPT = AT_K * HD / 4 / 256;          // pieces per thread (8 or 4)
     static_assert(PPT * 256 * 4 == AT_K * HD, "whole pieces per thread");
-    auto stage_tile = [&](const float *src, int row0, float *dst) {
+    auto stage_tile = [&](const float *src, int row0, float *dst, int ld) {
         float4 v[PPT];
 #pragma unroll
         for (int j = 0; j < PPT; j++) {
@@ -132,15 +138,11 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
 #pragma unroll
         for (int j = 0; j < PPT; j++) {
             const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
-            float *o = dst + r * LD + 4 * c;
-            o[0] = v[j].x;
-            o[1] = v[j].y;
-            o[2] = v[j].z;
-            o[3] = v[j].w;
+            *reinterpret_cast<float4 *>(dst + r * ld + 4 * c) = v[j];
         }
     };
     // queries of the workgroup (rows past N: zero)
-    stage_tile(Q, q_wg, sQ);
+    stage_tile(Q, q_wg, sQ, LD);
     // keys the workgroup's last query can see
     const int q_last = min(N, q_wg + AT_Q) - 1;
     const int k_end = a.block > 0 ? min(N, (q_last / a.block + 1) * a.block) : N;
@@ -157,8 +159,8 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     for (int b = 0; b < HD / 16; b++) o[b] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = 0; k0 < k_end; k0 += AT_K) {
         __syncthreads();
-        stage_tile(K, k0, sK);
-        stage_tile(V, k0, sV);
+        stage_tile(K, k0, sK, LD);
+        stage_tile(V, k0, sV, LDV);
         __syncthreads();
         // a wavefront whose queries are all past N, and key blocks / steps
         // wholly past the last visible key, have nothing to add (their
@@ -234,15 +236,15 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
 #pragma unroll
         for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) pw[(4 * g + i) * (AT_K + 1) + kb * 16 + r16] = sacc[kb][i];
+            for (int i = 0; i < 4; i++) pw[(4 * g + i) * LDP + kb * 16 + r16] = sacc[kb][i];
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         // O[16 q][HD] += P[16 q][64 k] V[64 k][HD]
         auto pv = [&](int ns) {
 #pragma unroll 4
             for (int s = 0; s < ns; s++) {
-                const float av = pw[r16 * (AT_K + 1) + 4 * s + g];
-                const float *vrow = sV + (4 * s + g) * LD;
+                const float av = pw[r16 * LDP + 4 * s + g];
+                const float *vrow = sV + (4 * s + g) * LDV;
 #pragma unroll
                 for (int b = 0; b < HD / 16; b++)
                     o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, vrow[b * 16 + r16], o[b], 0, 0, 0);
