@@ -89,8 +89,13 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     // weight ring three deep (two steps of HBM loads in flight) and the
     // activation ring two deep (its loads come from L2, one step ahead), which
     // is what the LDS holds next to NC activation blocks per stage
-    constexpr int WST = NC == 1 ? WSTAGES : 3;           // weight ring
-    constexpr int AST = NC == 1 ? WSTAGES : 2;           // activation ring
+    // Gate/up items of one column block run the weight ring four deep (three
+    // steps of HBM loads in flight) beside a three-deep activation ring whose
+    // loads (from L2) go two steps ahead, issued before the weights of the
+    // step after: 161,472 bytes of LDS.
+    constexpr bool SPLIT = !DOWN && NC == 1;
+    constexpr int WST = SPLIT ? 4 : NC == 1 ? WSTAGES : 3;   // weight ring
+    constexpr int AST = SPLIT ? 3 : NC == 1 ? WSTAGES : 2;   // activation ring
     constexpr int CH = EXPERT_CHUNK * NC;            // pairs of a routed item
     constexpr int SCH = SHARED_CHUNK * NC;           // tokens of a shared item
     __shared__ __align__(16) uint8_t s_act[AST][NC * ASTEP_BYTES];
@@ -265,7 +270,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             EXPERT_WAIT_VM(0);
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if constexpr (NC == 1) {
+            if constexpr (SPLIT) {
+                // W(0), A(0), W(1), A(1), W(2): the steady order A(s + 2), W(s + 3)
+                issue_w(cur, 0, 0);
+                issue_a(cur, 0, 0);
+                issue_w(cur, 1, 1);
+                issue_a(cur, 1, 1);
+                issue_w(cur, 2, 2);
+            } else if constexpr (NC == 1) {
 #pragma unroll
                 for (int s = 0; s < WST - 1; s++) issue(cur, s, s);
             } else {
@@ -293,7 +305,24 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             // later steps were issued (the item's last steps, no next item
             // primed): wait for all.  The barrier makes that true of every
             // wavefront and frees the stage read in the step before.
-            if constexpr (NC == 1) {
+            if constexpr (SPLIT) {
+                // A(s) was issued after W(s); after it: W(s + 1), A(s + 1),
+                // W(s + 2), those of them that exist
+                const int al = wave < ADMA_WAVES ? 1 : 0;
+                if (s + 2 < steps) {
+                    if (al)
+                        EXPERT_WAIT_VM(2 * WLOADS + 1);
+                    else
+                        EXPERT_WAIT_VM(2 * WLOADS);
+                } else if (s + 1 < steps) {
+                    if (al)
+                        EXPERT_WAIT_VM(WLOADS + 1);
+                    else
+                        EXPERT_WAIT_VM(WLOADS);
+                } else {
+                    EXPERT_WAIT_VM(0);
+                }
+            } else if constexpr (NC == 1) {
                 if (s + WST - 2 < steps || has_next) {
                     if (wave < ADMA_WAVES)
                         EXPERT_WAIT_VM((WLOADS + 1) * (WST - 2));
@@ -313,7 +342,10 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
             }
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if constexpr (NC == 1) {
+            if constexpr (SPLIT) {
+                if (s + 2 < steps) issue_a(cur, s + 2, s + 2);
+                if (s + 3 < steps) issue_w(cur, s + 3, s + 3);
+            } else if constexpr (NC == 1) {
                 const int sn = s + WST - 1;
                 if (sn < steps)
                     issue(cur, sn, g0 + sn);
