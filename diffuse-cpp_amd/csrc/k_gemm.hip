@@ -23,6 +23,8 @@
 // weight row l%16, activation rows 4*(l/16)+i).
 #include "dmoe_internal.h"
 
+#include <type_traits>
+
 namespace dmoe {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -218,7 +220,11 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         // reads ahead of each group of four MFMAs.  The scheduling groups fix
         // that interleave; the reads complete during the step and are awaited
         // before the next step's first MFMA.
-        auto step = [&](int st, int c, bool tail, bool next) {
+        // NTI (8, 4 or 0): the wavefront's 16-row activation blocks that hold
+        // pairs of the item; the MFMAs and operand reads of the others are
+        // skipped (an item of fewer than 256 pairs repeats its last row)
+        auto step = [&](auto nti_c, int st, int c, bool tail, bool next) {
+            constexpr int NTI = decltype(nti_c)::value;
             if (!tail)
                 GEMM_WAIT_VM(2 * GP * (GS - 2));
             else
@@ -231,7 +237,7 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
             const uint32_t nb = (uint32_t)(((st + 1) % GS) * 2 * GTILE);
             const uint32_t aoffs = al + nb, boffs = bl + nb + GTILE;
 #pragma unroll
-            for (int ti = 0; ti < 8; ti++) {
+            for (int ti = 0; ti < NTI; ti++) {
                 if (next) {
                     if (ti < 4) rw[c ^ 1][ti] = read_w(boffs, ti);
                     ra[c ^ 1][ti] = read_a(aoffs, ti);
@@ -271,16 +277,26 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         // operand set each.  Steps st with st + GS - 1 < total_steps refill
         // the ring (when a stage is left) and wait for a fixed count; the last
         // ones wait for all loads.
-        int st = 0;
-        for (; st + 1 + GS - 1 < total_steps; st += 2) {
-            step(st, 0, false, true);
-            step(st + 1, 1, false, true);
-        }
-        for (; st < total_steps; st += 2) {
-            // every stage is issued by now
-            step(st, 0, st + GS - 1 >= total_steps, true);
-            step(st + 1, 1, true, st + 2 < total_steps);
-        }
+        auto run = [&](auto nti_c) {
+            int st = 0;
+            for (; st + 1 + GS - 1 < total_steps; st += 2) {
+                step(nti_c, st, 0, false, true);
+                step(nti_c, st + 1, 1, false, true);
+            }
+            for (; st < total_steps; st += 2) {
+                // every stage is issued by now
+                step(nti_c, st, 0, st + GS - 1 >= total_steps, true);
+                step(nti_c, st + 1, 1, true, st + 2 < total_steps);
+            }
+        };
+        // (down only: skipping them in the gate/up launch measured slower)
+        const int wrows = nt - tok0;                     // the wavefront's activation rows with pairs
+        if (!DOWN || wrows > 64)
+            run(std::integral_constant<int, 8>());
+        else if (wrows > 0)
+            run(std::integral_constant<int, 4>());
+        else
+            run(std::integral_constant<int, 0>());
 
         // results: output row of tile tw for lane r16; activation rows 16 ti + 4 g + i
         // (the row base goes through an empty asm so that the compiler does not
