@@ -437,10 +437,24 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
         }
         // :232-236  thr = the cap-th largest bmax (position cap-1 of the
         // descending order, ties to the lower expert id)
-        if (wave == 0) {
-            if (E == 256)
-                find_threshold<4, true>(E, rp.capacity, s_rk, s_bmax, &s_thr);
-            else if (E < 256)
+        if (E == 256) {
+            // rank counting on all 1,024 threads: thread (part q, expert e)
+            // counts the experts of part q (64 of them, read as LDS
+            // broadcasts) whose rank key is above e's; the expert whose four
+            // counts sum to cap - 1 holds the threshold (rank keys are unique)
+            int *s_cnt4 = s_idx;                      // [4][256], free until the top-k
+            const int e = tid & 255, q = tid >> 8;
+            const uint64_t my = s_rk[e];
+            int cnt = 0;
+#pragma unroll 16
+            for (int i = 0; i < 64; i++) cnt += s_rk[64 * q + i] > my ? 1 : 0;
+            s_cnt4[q * 256 + e] = cnt;
+            __syncthreads();
+            if (tid < 256 &&
+                s_cnt4[tid] + s_cnt4[256 + tid] + s_cnt4[512 + tid] + s_cnt4[768 + tid] == rp.capacity - 1)
+                s_thr = s_bmax[tid];
+        } else if (wave == 0) {
+            if (E < 256)
                 find_threshold<4, false>(E, rp.capacity, s_rk, s_bmax, &s_thr);
             else
                 find_threshold<MAX_E / 64, false>(E, rp.capacity, s_rk, s_bmax, &s_thr);
