@@ -349,6 +349,19 @@ bool use_down_rows(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
            down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff) && q4k_column_blocks(hp, N) == 1;
 }
 
+// Of those, the shapes whose down products run by spans of (unit, tile) work
+// (k_down_span.hip) with the combine launch after them: every activation row
+// is read once per workgroup instead of once per 16 output rows (26.8 + 4.1
+// against 36.0 us at the flash shape, 32 tokens).  DMOE_DOWN_FUSED=1 selects
+// the single fused launch (k_down_rows.hip) instead: the same bits.
+bool use_down_span(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N)
+{
+    const char *ov = getenv("DMOE_DOWN_FUSED");
+    if (ov && atoi(ov) == 1) return false;
+    return use_down_rows(hp, wtype, stype, shared, N) &&
+           down_span_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff, shared);
+}
+
 // Q8_0 experts (and a Q8_0 shared expert of the same width) run on the int8
 // MFMA kernels of k_expert_q80.hip.
 bool use_q80_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared)
@@ -471,7 +484,7 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         t.hq.bsums = (int16_t *)take((size_t)P * (FF / 16 + 1) * 2);
         t.hs = (float *)take((size_t)N * (SF > 0 ? SF : 1) * 4);
     }
-    if (!use_down_rows(hp, wtype, stype, shared, N)) {
+    if (!use_down_rows(hp, wtype, stype, shared, N) || use_down_span(hp, wtype, stype, shared, N)) {
         // per-pair and shared down results, folded by the combine launch
         t.ye = (float *)take((size_t)P * H * 4);
         t.ys = (float *)take((size_t)N * H * 4);
@@ -638,6 +651,14 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
             dj.ahs = w.ahs;
             dj.weights = w.rb.weights;
             dj.y = y;
+            if (use_down_span(hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+                dj.ye = w.ye;
+                dj.ys = w.ys;
+                STAGE(ST_DOWN, launch_down_span(dj, s));
+                STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
+                                                 K, H, y, s));
+                return DMOE_OK;
+            }
             STAGE(ST_DOWN, launch_down_rows(dj, s));
             return DMOE_OK;
         }

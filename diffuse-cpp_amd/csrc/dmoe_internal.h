@@ -268,9 +268,16 @@ struct DownRowsJob {
     ActI8 ah, ahs;                  // h in the int8 layout (routed pairs; shared digit rows)
     const float *weights;           // [N][K] gate weights
     float *y;                       // [N][H] segment output
+    float *ye, *ys;                 // k_down_span: per-pair [N K][H] and shared [N][H] products
 };
 bool down_rows_ok(int N, int K, int E, int H, int FF);
 hipError_t launch_down_rows(const DownRowsJob &job, hipStream_t s);
+// The same products by spans of (unit, 16-row tile) work, one workgroup per
+// CU, to ye / ys; launch_combine folds them (k_down_span.hip).
+bool down_span_ok(int N, int K, int E, int H, int FF, int has_shared);
+hipError_t launch_down_span(const DownRowsJob &job, hipStream_t s);
+// Compute units of the current device (k_expert.hip).
+hipError_t device_cu_count(int *out);
 // The same products for Q8_0 experts (k_expert_q80.hip): activations in the
 // ActI8 layout with ACT_Q80 / ACT_SPLIT32 scales, weights in the Q8_0 tiled
 // layout of launch_tile_q80.

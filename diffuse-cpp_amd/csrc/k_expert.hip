@@ -496,6 +496,16 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc
     if (phase == 0) return launch_phase<0>(nc, job, dim3(DMOE_X_BLOCKS), s);
     // one workgroup per compute unit (one fits at a time), so that each
     // runs its items back to back with the rings running on between them
+    int n_cu = 0;
+    const hipError_t e = device_cu_count(&n_cu);
+    if (e != hipSuccess) return e;
+    return launch_phase<1>(nc, job, dim3(n_cu), s);
+}
+
+hipError_t device_cu_count(int *out)
+{
+    // compute units of each device, looked up once (a repeated lookup
+    // stores the same value)
     static int n_cu[64] = {0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -505,9 +515,11 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc
         int n = 0;
         e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
-        n_cu[dev] = n > 0 ? n : DMOE_X_BLOCKS;
+        if (n <= 0) return hipErrorInvalidDevice;
+        n_cu[dev] = n;
     }
-    return launch_phase<1>(nc, job, dim3(n_cu[dev]), s);
+    *out = n_cu[dev];
+    return hipSuccess;
 }
 
 } // namespace dmoe

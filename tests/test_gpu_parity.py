@@ -152,6 +152,33 @@ def test_q4k_column_blocks_bit_exact(ctx, name, monkeypatch):
         assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32))
 
 
+@pytest.mark.parametrize("name", ["flash_q4k", "small_q4k_n40", "small_q4k_n96", "small_q4k_n128"])
+def test_down_span_bit_exact(ctx, name, monkeypatch):
+    """Few-token Q4_K down products by spans of (unit, 16-row tile) work,
+    then the combine launch, against the fused kernel that folds in LDS: the
+    same products in the same order, so the layer outputs are identical bit
+    for bit.  Each span call follows one on other inputs of the same size, so
+    products left in HBM by that call would show if the combine read them."""
+    import dmoe
+    from dmoe import synth
+    if name.startswith("small"):
+        cfg = _small(dmoe, synth, 12, int(name.rsplit("_n", 1)[1]))
+    else:
+        cfg = synth.CONFIGS[name]
+    _say(f"case: down spans vs down rows, {name}")
+    wd = synth.device_layer(cfg, 27, ctx)
+    layer = ctx.wrap_device(wd)
+    x = synth.make_x(cfg, 27, cfg.n_tokens)
+    xo = synth.make_x(cfg, 28, cfg.n_tokens)
+    n2 = cfg.n_tokens // 2 + 3
+    monkeypatch.setenv("DMOE_DOWN_FUSED", "1")
+    ref = [ctx.forward(layer, a) for a in (x, xo, x[:n2], xo[:n2])]
+    monkeypatch.delenv("DMOE_DOWN_FUSED")
+    got = [ctx.forward(layer, a) for a in (xo, x, xo[:n2], x[:n2])]
+    for r, g in zip(ref, (got[1], got[0], got[3], got[2])):
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32))
+
+
 def test_route_logits_flash_shape(ctx, O):
     import dmoe
     _say("case: routing from injected logits, flash shape, 8 blocks")
