@@ -20,9 +20,9 @@
 // Weights go straight to registers, a ring of DS_R sets per wavefront loaded
 // DS_R - 1 steps ahead (the compiler's own loads, so it counts their waits);
 // the activations are in LDS, so the step loop has no barrier.  (Deeper
-// rings measured slower: 27.0, 27.7, 28.5, 30.0, 30.2, 31.8 us for 4, 5, 6,
-// 8, 10, 12 sets at 32 tokens; so did 16 wavefronts and two workgroups per
-// CU.)  Each step's arithmetic is compute_sb's for one
+// rings measured slower: 26.8, 26.8, 27.0, 27.7, 28.5, 30.0, 31.8 us for 2,
+// 3, 4, 5, 6, 8, 12 sets at 32 tokens; so did 16 wavefronts and two
+// workgroups per CU.)  Each step's arithmetic is compute_sb's for one
 // tile (k_expert.hip) with no fused multiply-adds, as k_down_rows computes
 // it, so the products equal that kernel's bit for bit; they go to ye [pair][H] and ys [token][H] (the shared expert's
 // two digits summed in-lane) for the combine launch.  Contraction is off for
@@ -35,7 +35,7 @@
 namespace dmoe {
 
 constexpr int DS_WAVES = 8;
-constexpr int DS_R = 4;            // weight register sets per wavefront (3 steps in flight)
+constexpr int DS_R = 3;            // weight register sets per wavefront (2 steps in flight)
 constexpr int DS_SLOTS = 3;        // units whose activations a workgroup holds
 constexpr int DS_MAX_SB = 4;       // super-blocks of the reduction (moe_ff <= 1024)
 

@@ -33,6 +33,9 @@
 // without holding registers.
 #include "dmoe_q4k.h"
 
+#include <cstdlib>
+#include <type_traits>
+
 namespace dmoe {
 
 
@@ -468,6 +471,210 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Gate/up items of one column block (few tokens) with the weights streamed to
+// registers: the same items, rows and arithmetic as k_expert_q4k<0, 1>, but
+// the item's activations (16 rows of every super-block, 74.75 KB at n_embd
+// 4096) are loaded into LDS once at the item's start and each wavefront
+// streams its gate and up tiles to a ring of GR_R register sets, GR_R - 1
+// steps ahead (the compiler's own loads: its waits are exact), with no
+// barrier in the step loop.  The first steps' weights are issued before the
+// item's pairs and activation rows are looked up.  The h conversion after
+// the last step is k_expert_q4k's, through the activation region.  The
+// stream is bandwidth bound in the steady state: more register sets only
+// lengthen the ramp (kernel trace at 32 tokens: 45.1, 46.1, 47.0, 47.3 us for
+// 2, 3, 4, 5 sets; 171 / 174 us for 2 / 3 sets at 256 tokens).
+constexpr int GR_R = 2;          // weight register sets per wavefront (one step ahead)
+constexpr int GR_MAX_SB = 16;    // super-blocks of the reduction held in LDS (n_embd <= 4096)
+
+template <int J0, int J1, class F>
+__device__ __forceinline__ void gr_unroll(F &&f)
+{
+    if constexpr (J0 < J1) {
+        f(std::integral_constant<int, J0>());
+        gr_unroll<J0 + 1, J1>(f);
+    }
+}
+
+typedef unsigned int gr_u4v __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) gr_u4v *gr_gu4v_ptr;
+
+__device__ __forceinline__ uint4 gr_ld_nt16(const void *p)
+{
+    const gr_u4v v = __builtin_nontemporal_load((gr_gu4v_ptr)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__global__ __launch_bounds__(WAVES * 64) void k_gateup_rr(MoeJob job)
+{
+    __shared__ __align__(16) uint8_t s_act[GR_MAX_SB][ASTEP_BYTES];
+    static_assert(GROWS_GU * 16 * 4 + WAVES * 256 * 4 <= GR_MAX_SB * ASTEP_BYTES, "h and its scratch fit");
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, r16 = lane & 15;
+    const int N = job.n_tokens, K = job.top_k;
+    const int H = job.H, FF = job.FF, SF = job.SF;
+    const int n_ec = job.wl.n_ec[0];
+    const int nch = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
+    const int rg = FF / GROWS_GU, rg_sh = SF / GROWS_GU;
+    const int routed_items = n_ec * rg;
+    const int total = routed_items + nch * rg_sh;
+    const int nsb = H / 256;
+    const int steps = GU_IT * nsb;
+    // activation loads (k_expert_q4k's roles)
+    const int ar = wave < 4 ? 4 * wave + (lane >> 4) : (wave == 4 ? (lane >> 1) & 15 : lane & 15);
+    const int aunit = (lane & 15) ^ (ar & 11);
+    const bool aload = wave < 4 || (wave == 4 && lane < 32) || (wave == 5 && lane < 16);
+
+    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+        const bool shared = item >= routed_items;
+        const int j = shared ? item - routed_items : item;
+        const int rgn = shared ? rg_sh : rg;
+        const int unit = j / rgn;
+        const int rbase = (j - unit * rgn) * GROWS_GU;
+        int t_first, nt, e = 0;
+        if (!shared) {
+            e = job.wl.ec_expert[unit];
+            const int c0 = job.wl.ec_chunk[unit] * EXPERT_CHUNK;
+            t_first = job.offsets[e] + c0;
+            nt = min(EXPERT_CHUNK, job.counts[e] - c0);
+        } else {
+            t_first = unit * SHARED_CHUNK;
+            nt = min(SHARED_CHUNK, N - t_first);
+        }
+        // this wavefront's tiles: gate and up rows rbase + 128 it + 16 wave
+        const WTensor &wa = shared ? job.sg : job.eg;
+        const WTensor &wb = shared ? job.su : job.eu;
+        // (pass it's tiles are WAVES tiles further: no array of pointers,
+        // which would be indexed from private memory)
+        const int t16 = (rbase + wave * 16) / 16;
+        const uint8_t *tg = wa.data + (size_t)e * wa.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+        const uint8_t *tu = wb.data + (size_t)e * wb.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+        const size_t pass_step = (size_t)WAVES * nsb * TILE_BYTES;
+        // the load cursor (pass, super-block) runs GR_R - 1 steps ahead and
+        // stays on the last step once there (loading it again, never used)
+        int l_it = 0, l_sb = 0, lq = 0;
+        auto load = [&](Q4KTile (&o)[2]) __attribute__((always_inline)) {
+            const size_t off = (size_t)l_it * pass_step + (size_t)l_sb * TILE_BYTES;
+            const uint4 *pg = reinterpret_cast<const uint4 *>(tg + off);
+            const uint4 *pu = reinterpret_cast<const uint4 *>(tu + off);
+            o[0].h = gr_ld_nt16(pg + r16);
+            o[0].q0 = gr_ld_nt16(pg + (1 + 2 * g) * 16 + r16);
+            o[0].q1 = gr_ld_nt16(pg + (2 + 2 * g) * 16 + r16);
+            o[1].h = gr_ld_nt16(pu + r16);
+            o[1].q0 = gr_ld_nt16(pu + (1 + 2 * g) * 16 + r16);
+            o[1].q1 = gr_ld_nt16(pu + (2 + 2 * g) * 16 + r16);
+            if (lq + 1 < steps) {
+                lq++;
+                if (++l_sb == nsb) {
+                    l_sb = 0;
+                    l_it++;
+                }
+            }
+        };
+        Q4KTile o[GR_R][2];
+        gr_unroll<0, GR_R - 1>([&](auto jc) { load(o[decltype(jc)::value]); });
+
+        // the previous item's h conversion is done with the activation region
+        __syncthreads();
+        int arow;
+        if (shared) {
+            arow = t_first + min(ar >> 1, nt - 1) + (ar & 1) * N;
+        } else {
+            arow = job.perm[t_first + min(ar, nt - 1)] / K;
+        }
+        const ActI8 &act = shared ? job.axs : job.ax;
+        if (wave < ADMA_WAVES) {
+            for (int sb = 0; sb < nsb; sb++) {
+                uint8_t *st = &s_act[sb][0];
+                if (wave < 4)
+                    lds_load16(act.q + (size_t)arow * H + sb * 256 + aunit * 16, st + 1024 * wave);
+                else if (wave == 4 && aload)
+                    lds_load16(act.bs + (size_t)arow * (H / 16) + sb * 16 + (lane & 1) * 8, st + ABS_OFF);
+                else if (wave == 5 && aload)
+                    lds_load4(act.d + (size_t)arow * nsb + sb, st + AD_OFF);
+            }
+        }
+        // the activation loads (and the weight loads before them) have
+        // landed in every wavefront
+        EXPERT_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+
+        // the current pass's sums, and pass 0's once it is done (a register
+        // copy at the pass boundary: no accumulator chosen by a run-time index)
+        static_assert(GU_IT == 2, "two row passes");
+        float acc[2][4], acc0[2][4];
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[r][i] = acc0[r][i] = 0.0f;
+        int c_sb = 0;
+        bool c_first = true;
+        auto compute = [&](const Q4KTile (&w)[2]) __attribute__((always_inline)) {
+            compute_sb<2>(w, &s_act[c_sb][0], r16, g, acc);
+            if (++c_sb == nsb) {
+                c_sb = 0;
+                if (c_first) {
+#pragma unroll
+                    for (int r = 0; r < 2; r++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            acc0[r][i] = acc[r][i];
+                            acc[r][i] = 0.0f;
+                        }
+                    c_first = false;
+                }
+            }
+        };
+        int s0 = 0;
+        for (; s0 + GR_R <= steps; s0 += GR_R)
+            gr_unroll<0, GR_R>([&](auto jc) {
+                constexpr int jj = decltype(jc)::value;
+                load(o[(jj + GR_R - 1) % GR_R]);
+                compute(o[jj]);
+            });
+        gr_unroll<0, GR_R - 1>([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
+            if (s0 + jj < steps) {
+                load(o[(jj + GR_R - 1) % GR_R]);
+                compute(o[jj]);
+            }
+        });
+
+        // h = silu(gate) * up for the item's rows, then converted to the down
+        // products' operand layout (k_expert_q4k's conversion)
+        float *s_h = reinterpret_cast<float *>(&s_act[0][0]);              // [16][256]
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < GU_IT; it++) {
+            const int col = it * (WAVES * 16) + wave * 16 + r16;
+            const float (&a)[2][4] = it == 0 ? acc0 : acc;
+            if (!shared) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) s_h[(4 * g + i) * 256 + col] = silu(a[0][i]) * a[1][i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i += 2)
+                    s_h[(2 * g + (i >> 1)) * 256 + col] = silu(a[0][i] + a[0][i + 1]) * (a[1][i] + a[1][i + 1]);
+            }
+        }
+        __syncthreads();
+        float *sv = reinterpret_cast<float *>(&s_act[0][0]) + 16 * 256 + wave * 256;
+        const int sbh = rbase / 256, nsb_h = (shared ? SF : FF) / 256;
+        for (int t = wave; t < nt; t += WAVES) {
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) v[c] = s_h[t * 256 + lane + 64 * c];
+            if (!shared)
+                prep_values(v, job.ah, ACT_Q8K, job.perm[t_first + t], N * K, sbh, nsb_h, sv);
+            else
+                prep_values(v, job.ahs, ACT_SPLIT, t_first + t, N, sbh, nsb_h, sv);
+        }
+    }
+}
+
 int expert_rows_per_item(int phase) { return phase == 0 ? GROWS_GU : GROWS_DN; }
 
 bool expert_k_ok(int K) { return K % 256 == 0; }
@@ -493,7 +700,16 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc
     // routed work-list entries hold 16 nc pairs
     if ((nc != 1 && nc != 2 && nc != 4) || (job.wl.n_ec && job.wl.chunk != EXPERT_CHUNK * nc))
         return hipErrorInvalidValue;
-    if (phase == 0) return launch_phase<0>(nc, job, dim3(DMOE_X_BLOCKS), s);
+    if (phase == 0) {
+        // one column block: the register-ring kernel unless DMOE_GATEUP_LDS=1
+        // selects the LDS-ring one (the same bits)
+        const char *ov = getenv("DMOE_GATEUP_LDS");
+        if (nc == 1 && job.H / 256 <= GR_MAX_SB && !(ov && atoi(ov) == 1)) {
+            hipLaunchKernelGGL(k_gateup_rr, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
+            return hipGetLastError();
+        }
+        return launch_phase<0>(nc, job, dim3(DMOE_X_BLOCKS), s);
+    }
     // one workgroup per compute unit (one fits at a time), so that each
     // runs its items back to back with the rings running on between them
     int n_cu = 0;

@@ -179,6 +179,31 @@ def test_down_span_bit_exact(ctx, name, monkeypatch):
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32))
 
 
+@pytest.mark.parametrize("name", ["flash_q4k", "flash_q4k_n256", "small_q4k_n40", "small_q4k_n128"])
+def test_gateup_register_ring_bit_exact(ctx, name, monkeypatch):
+    """Q4_K gate/up items of one column block with the weights streamed to
+    registers and the item's activations in LDS, against the kernel with LDS
+    rings for both: the same products in the same order, so the layer
+    outputs are identical bit for bit."""
+    import dmoe
+    from dmoe import synth
+    if name.startswith("small"):
+        cfg = _small(dmoe, synth, 12, int(name.rsplit("_n", 1)[1]))
+    else:
+        cfg = synth.CONFIGS[name]
+    _say(f"case: gate/up register ring vs LDS rings, {name}")
+    wd = synth.device_layer(cfg, 29, ctx)
+    layer = ctx.wrap_device(wd)
+    x = synth.make_x(cfg, 29, cfg.n_tokens)
+    xo = synth.make_x(cfg, 30, cfg.n_tokens)
+    monkeypatch.setenv("DMOE_GATEUP_LDS", "1")
+    ref = [ctx.forward(layer, a) for a in (x, xo)]
+    monkeypatch.delenv("DMOE_GATEUP_LDS")
+    got = [ctx.forward(layer, a) for a in (xo, x)]
+    assert np.array_equal(got[1].view(np.uint32), ref[0].view(np.uint32))
+    assert np.array_equal(got[0].view(np.uint32), ref[1].view(np.uint32))
+
+
 def test_route_logits_flash_shape(ctx, O):
     import dmoe
     _say("case: routing from injected logits, flash shape, 8 blocks")
