@@ -352,8 +352,9 @@ bool use_down_rows(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
 // Of those, the shapes whose down products run by spans of (unit, tile) work
 // (k_down_span.hip) with the combine launch after them: every activation row
 // is read once per workgroup instead of once per 16 output rows (26.8 + 4.1
-// against 36.0 us at the flash shape, 32 tokens).  DMOE_DOWN_FUSED=1 selects
-// the single fused launch (k_down_rows.hip) instead: the same bits.
+// against 36.0 us at the flash shape, 32 tokens; at 256 tokens the item
+// kernel is faster, 98.6 against 107.2 us).  DMOE_DOWN_FUSED=1 selects the
+// single fused launch (k_down_rows.hip) instead: the same bits.
 bool use_down_span(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N)
 {
     const char *ov = getenv("DMOE_DOWN_FUSED");
@@ -631,7 +632,8 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.ys = w.ys;
         // the gate/up launch converts h to the down products' layout itself
         STAGE(ST_GATEUP, expert(0, job));
-        if (use_down_rows(hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+        const bool span = use_down_span(hp, L->eg.type, L->sg.type, L->has_shared, N);
+        if (span || use_down_rows(hp, L->eg.type, L->sg.type, L->has_shared, N)) {
             // down products and the combine in one launch
             DownRowsJob dj{};
             dj.ed = L->ed;
@@ -651,7 +653,7 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
             dj.ahs = w.ahs;
             dj.weights = w.rb.weights;
             dj.y = y;
-            if (use_down_span(hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+            if (span) {
                 dj.ye = w.ye;
                 dj.ys = w.ys;
                 STAGE(ST_DOWN, launch_down_span(dj, s));
