@@ -187,7 +187,9 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
             if cfg.wtype == dmoe.TYPE_Q4_K:
                 def act_row(n):
                     return n + (n // 16) * 2 + (n // 256) * 4
-                dom_kernel = "dmoe::k_expert_q4k<0>"
+                # items of one column block (fewer than 32 pairs per expert on
+                # average) run on the register-ring kernel
+                dom_kernel = "dmoe::k_gateup_rr" if N * K // E < 32 else "dmoe::k_expert_q4k<0>"
             else:
                 def act_row(n):
                     return n + (n // 32) * 4
