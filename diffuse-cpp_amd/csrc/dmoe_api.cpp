@@ -599,9 +599,13 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         xj[nxj++] = PrepJob{x, N, H, mode_r, w.ax};
         if (L->has_shared) xj[nxj++] = PrepJob{x, N, H, mode_s, w.axs};
     }
-    STAGE(ST_FRONT, launch_front(L->gate_w, L->gate_bias, x, N, H, E, w.rb, xj, nxj, s));
+    // With one routing group the conversions run in the route launch, on the
+    // compute units its one routing workgroup leaves idle, rather than in
+    // the front, whose workgroups would run them before their logit products
+    const bool conv_route = nxj > 0 && route_single(rp);
+    STAGE(ST_FRONT, launch_front(L->gate_w, L->gate_bias, x, N, H, E, w.rb, xj, conv_route ? 0 : nxj, s));
     // block routing, top-k, gate weights and the dispatch
-    STAGE(ST_ROUTE, launch_route(rp, w.rb, w.wl, s));
+    STAGE(ST_ROUTE, launch_route(rp, w.rb, w.wl, s, xj, conv_route ? nxj : 0));
     if (mfma) {
         // Q4_K / Q8_0 experts on int8 MFMA: routed experts and the shared one
         // share a launch

@@ -175,16 +175,21 @@ hipError_t launch_norm_fused(const NormArgs &a, hipStream_t s);
 hipError_t launch_residual_rmsnorm(float *h, const float *y, const float *gain, float *x, int rows, int H,
                                    float eps, hipStream_t s);
 
-// Routing + dispatch (k_router.hip).
-hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl, hipStream_t s);
-bool route_fits_lds(const RouteParams &rp);
-
 // One activation conversion into the MFMA operand layout.
 struct PrepJob {
     const float *src;
     int32_t rows, K, mode;   // K % 256 == 0
     ActI8 out;
 };
+
+// Routing + dispatch (k_router.hip).  When the forward is one routing group
+// (route_single), up to two activation conversions may ride along in the
+// same launch: their workgroups run beside the routing workgroup, on compute
+// units it leaves idle.
+hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl, hipStream_t s,
+                        const PrepJob *jobs = nullptr, int njobs = 0);
+bool route_fits_lds(const RouteParams &rp);
+bool route_single(const RouteParams &rp);
 // Front kernel (k_prep.hip): router logits L = Wg x in one fixed fp32 order,
 // probs = sigmoid(L), sel = probs + bias, plus up to two activation
 // conversions of x, in one launch.

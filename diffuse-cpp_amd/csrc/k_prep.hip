@@ -14,19 +14,6 @@
 
 namespace dmoe {
 
-// One wavefront converts one (row, super-block) of a job.  sv: 256 floats of LDS.
-__device__ void prep_wave(const PrepJob &job, int wid, float *sv)
-{
-    const int lane = threadIdx.x & 63;
-    const int nsb = job.K / 256;
-    const int row = wid / nsb, sb = wid - row * nsb;
-    const float *x = job.src + (size_t)row * job.K + sb * 256;
-    float v[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) v[c] = x[lane + 64 * c];
-    prep_values(v, job.out, job.mode, row, job.rows, sb, nsb, sv);
-}
-
 // ---------------------------------------------------------------------------
 // Router logits.  One wavefront per (LE experts, LT tokens).  For every
 // (token, expert) lane l keeps one partial:  a_l = fma(W[k], x[k], a_l) for

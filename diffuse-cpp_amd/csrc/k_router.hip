@@ -16,7 +16,7 @@
 // Bit-exactness: single IEEE operations in a fixed order (no contraction),
 // order decisions on exact integer keys, counts and ranks without atomics on
 // the results.
-#include "dmoe_device.h"
+#include "dmoe_prep.h"
 
 #pragma clang fp contract(off)
 
@@ -326,10 +326,19 @@ __device__ __forceinline__ int flag_scan256(int flag, int *s_w4, int *total)
     return before + below;
 }
 
+// Activation conversions that ride along with a one-group route: job list
+// and the conversion workgroups after the routing one.
+struct RoutePrep {
+    PrepJob job[2];
+    int njobs;
+};
+
 // SINGLE: the forward is one routing group (the dispatch needs nothing
-// beyond this block; the token probabilities are staged in LDS).
+// beyond this block; the token probabilities are staged in LDS).  Blocks
+// after the first then convert activations (pp), one (row, super-block) per
+// wavefront, and touch nothing of the routing.
 template <bool SINGLE>
-__global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs rb, WorkList wl)
+__global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs rb, WorkList wl, RoutePrep pp)
 {
     __shared__ uint32_t s_key[ROUTE_LDS];         // group scores, then sel' keys
     __shared__ float s_bmax[MAX_E];
@@ -353,6 +362,22 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(RouteParams rp, RouteBufs 
     const int lane = tid & 63, wave = tid >> 6;
     const int words = (G + 31) / 32;
     float *s_sel = reinterpret_cast<float *>(s_key);
+
+    if constexpr (SINGLE) {
+        if (g > 0) {
+            int wid = (g - 1) * RT_WAVES + wave;
+            float *sv = s_sel + wave * 256;
+            for (int j = 0; j < pp.njobs; j++) {
+                const int n = pp.job[j].rows * (pp.job[j].K / 256);
+                if (wid < n) {
+                    prep_wave(pp.job[j], wid, sv);
+                    return;
+                }
+                wid -= n;
+            }
+            return;
+        }
+    }
 
     // one forward = one group: the group's probs go to LDS, loaded with the scores
     constexpr int R = ROUTE_LDS / RT_THREADS;
@@ -755,16 +780,33 @@ bool route_fits_lds(const RouteParams &rp)
            rp.top_k <= MAX_K && rp.n_experts <= RT_THREADS && (size_t)rp.n_tokens * rp.top_k < (1u << 24);
 }
 
-hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl, hipStream_t s)
+bool route_single(const RouteParams &rp)
+{
+    const int G = rp.use_block ? rp.block_size : 32;
+    return route_fits_lds(rp) && (rp.n_tokens + G - 1) / G == 1;
+}
+
+hipError_t launch_route(const RouteParams &rp, const RouteBufs &rb, const WorkList &wl, hipStream_t s,
+                        const PrepJob *jobs, int njobs)
 {
     const int G = rp.use_block ? rp.block_size : 32;
     const int ngroups = (rp.n_tokens + G - 1) / G;
+    RoutePrep pp{};
+    if (njobs < 0 || njobs > 2 || (njobs > 0 && !route_single(rp))) return hipErrorInvalidValue;
+    int ptasks = 0;
+    for (int j = 0; j < njobs; j++) {
+        if (jobs[j].K <= 0 || jobs[j].K % 256 || jobs[j].rows <= 0) return hipErrorInvalidValue;
+        pp.job[j] = jobs[j];
+        ptasks += jobs[j].rows * (jobs[j].K / 256);
+    }
+    pp.njobs = njobs;
     if (route_fits_lds(rp)) {
         if (ngroups == 1) {
-            hipLaunchKernelGGL(k_route<true>, dim3(1), dim3(RT_THREADS), 0, s, rp, rb, wl);
+            const int blocks = 1 + (ptasks + RT_WAVES - 1) / RT_WAVES;
+            hipLaunchKernelGGL(k_route<true>, dim3(blocks), dim3(RT_THREADS), 0, s, rp, rb, wl, pp);
             return hipGetLastError();
         }
-        hipLaunchKernelGGL(k_route<false>, dim3(ngroups), dim3(RT_THREADS), 0, s, rp, rb, wl);
+        hipLaunchKernelGGL(k_route<false>, dim3(ngroups), dim3(RT_THREADS), 0, s, rp, rb, wl, pp);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_dispatch_groups, dim3((ngroups + DISP_GROUPS - 1) / DISP_GROUPS), dim3(RT_THREADS),
