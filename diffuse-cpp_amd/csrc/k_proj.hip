@@ -15,15 +15,21 @@
 // activation layout, two stages) and shared by the eight wavefronts, which
 // each run through their T tiles of that super-block; so the activations are
 // read once per 128 T rows (T = 5 for the 157,184-row LM head: a fifth of the
-// weight bytes).  Each tile step's operands are formed once for all blocks
-// (fold_tile / compute_folded).  Weights go to a per-wavefront LDS ring of
-// PJ_WST stages, PJ_WST - 1 tile steps ahead; a barrier per super-block
-// publishes its activations.  A few thousand rows make too few workgroups of
+// weight bytes).  Each wavefront reads the super-block's activation operands
+// from LDS into registers once for its T tiles; each tile step's weight
+// operands are formed once for all blocks (fold_tile), and a token's two
+// digit rows share one scale epilogue (their scales differ by exactly 256).
+// Weights go to a per-wavefront LDS ring of PJ_WST stages, PJ_WST - 1 tile
+// steps ahead; a barrier per super-block publishes its activations.  The
+// step counts are fixed at compile time (T, the column blocks NB), so every
+// wait on the loads is a constant.  A few thousand rows make too few workgroups of
 // whole reductions, so the reduction may be split into KS slices (proj_plan
 // weighs workgroup rounds, steps and the slices' reduction): the slices' sums go to
 // part [m][s][t][row] and k_proj_reduce (or k_proj_swiglu for the MLP's gate
 // and up) adds them in slice order.
 #include "dmoe_q4k.h"
+
+#include <type_traits>
 
 namespace dmoe {
 
@@ -33,28 +39,97 @@ constexpr int PJ_WST = 5;                         // weight ring stages per wave
 constexpr int PJ_AHEAD = PJ_WST - 1;              // tile steps in flight
 constexpr int PJ_TMAX = 6;                        // tiles per wavefront at most
 
-// s_waitcnt vmcnt(n), lgkmcnt(0) for a wave-uniform n below 32 (the counter
-// field is an immediate: one case per value; vmcnt bits 5:4 at 15:14)
-#define PJ_WAIT_CASE(n)                                                              \
-    case n: __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70); break;
-__device__ __forceinline__ void pj_wait_vm(int n)
+// s_waitcnt vmcnt(n), lgkmcnt(0) for a compile-time n below 64 (vmcnt bits
+// 5:4 at 15:14)
+template <int n>
+__device__ __forceinline__ void pj_wait()
 {
-    switch (n) {
-        PJ_WAIT_CASE(0) PJ_WAIT_CASE(1) PJ_WAIT_CASE(2) PJ_WAIT_CASE(3) PJ_WAIT_CASE(4) PJ_WAIT_CASE(5)
-        PJ_WAIT_CASE(6) PJ_WAIT_CASE(7) PJ_WAIT_CASE(8) PJ_WAIT_CASE(9) PJ_WAIT_CASE(10) PJ_WAIT_CASE(11)
-        PJ_WAIT_CASE(12) PJ_WAIT_CASE(13) PJ_WAIT_CASE(14) PJ_WAIT_CASE(15) PJ_WAIT_CASE(16) PJ_WAIT_CASE(17)
-        PJ_WAIT_CASE(18) PJ_WAIT_CASE(19) PJ_WAIT_CASE(20) PJ_WAIT_CASE(21) PJ_WAIT_CASE(22) PJ_WAIT_CASE(23)
-        PJ_WAIT_CASE(24) PJ_WAIT_CASE(25) PJ_WAIT_CASE(26) PJ_WAIT_CASE(27) PJ_WAIT_CASE(28) PJ_WAIT_CASE(29)
-        PJ_WAIT_CASE(30) PJ_WAIT_CASE(31)
-    default: __builtin_amdgcn_s_waitcnt(0x70); break;
+    static_assert(n >= 0 && n < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x70);
+}
+
+template <int J0, int J1, class F>
+__device__ __forceinline__ void pj_unroll(F &&f)
+{
+    if constexpr (J0 < J1) {
+        f(std::integral_constant<int, J0>());
+        pj_unroll<J0 + 1, J1>(f);
     }
 }
-#undef PJ_WAIT_CASE
 
-template <int T>
+// A column block's operands of one step, read from LDS ahead of use: the
+// four 16-byte activation units, the sums of 16 and the row scales
+// (compute_folded's reads).
+struct PjOps {
+    v4i a[4];
+    h4 ab;
+    float4 dx;
+};
+
+__device__ __forceinline__ void pj_read_ops(PjOps &o, const uint8_t *ast, int r16, int g)
+{
+    const uint4 *ap = reinterpret_cast<const uint4 *>(ast + r16 * 256);
+#pragma unroll
+    for (int c = 0; c < 4; c++) o.a[c] = __builtin_bit_cast(v4i, ap[(4 * g + c) ^ (r16 & 11)]);
+    o.ab = __builtin_bit_cast(h4, *reinterpret_cast<const uint2 *>(ast + ABS_OFF + r16 * 32 + 8 * g));
+    o.dx = *reinterpret_cast<const float4 *>(ast + AD_OFF + 16 * g);
+}
+
+// A block's MFMAs (compute_folded's) and, separately, its scale epilogue,
+// so that a block's epilogue can follow the next block's MFMAs
+struct PjSums {
+    v4i sh, sl;
+    f4 s2;
+    float4 dx;
+};
+
+__device__ __forceinline__ void pj_mfma(const Q4KFolded &f, const PjOps &o, PjSums &r)
+{
+    v4i sh = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[c], f.bh[c], sh, 0, 0, 0);
+        sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[c], f.bl[c], sl, 0, 0, 0);
+    }
+    f4 s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    r.s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(o.ab, f.bm, s2, 0, 0, 0);
+    r.sh = sh;
+    r.sl = sl;
+    r.dx = o.dx;
+}
+
+// Lane (r16, g) holds block rows 4 g .. 4 g + 3 = the a1 and a0 digit rows
+// of tokens 2 g and 2 g + 1 (rows 4 g + 2 u, 4 g + 2 u + 1).  The a0 row's
+// scale is the a1 row's / 256 exactly (ACT_SPLIT), so a token's step is
+//   dx1 (d (S1 + S0 / 256) - dmin (M1 + M0 / 256))
+// with S the integer sums and M the min-term sums of its two rows: one scale
+// epilogue per token instead of one per digit row.
+__device__ __forceinline__ void pj_epilogue(const Q4KFolded &f, const PjSums &r, float (&acc)[2])
+{
+    const float dx1[2] = {r.dx.x, r.dx.z};
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int s1 = 8 * r.sh[2 * u] + r.sl[2 * u];
+        const int s0 = 8 * r.sh[2 * u + 1] + r.sl[2 * u + 1];
+        const float sv = __builtin_fmaf((float)s0, 0.00390625f, (float)s1);
+        const float mv = __builtin_fmaf(r.s2[2 * u + 1], 0.00390625f, r.s2[2 * u]);
+        acc[u] = __builtin_fmaf(dx1[u], f.d * sv - f.dmin * mv, acc[u]);
+    }
+}
+
+// T tiles per wavefront, NB column blocks of 8 tokens (N in 8 NB - 7 .. 8 NB).
+// Every wavefront runs T tiles (tile indices past the matrix clamped to its
+// last tile, their results not stored) and every step count is fixed: the
+// weight loads run PJ_AHEAD steps ahead to the end (the last steps load the
+// last step's tile again, into ring stages no step reads), and every
+// super-block issues an activation step (the last super-block's again at the
+// end, into the stage its predecessor used, which every wavefront has
+// passed).  So each wait below is a compile-time count and the step body has
+// no branch.
+template <int T, int NB>
 __global__ __launch_bounds__(PJ_WAVES * 64) void k_proj_q4k(ProjJob j)
 {
-    __shared__ __align__(16) uint8_t s_act[2][PJ_BLOCKS][ASTEP_BYTES];
+    __shared__ __align__(16) uint8_t s_act[2][NB][ASTEP_BYTES];
     __shared__ __align__(16) uint8_t s_w[PJ_WAVES][PJ_WST][TILE_BYTES];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -64,108 +139,140 @@ __global__ __launch_bounds__(PJ_WAVES * 64) void k_proj_q4k(ProjJob j)
     const int m = blockIdx.z, sl = blockIdx.y;
     const int ntile = R / 16;
     const int tile0 = blockIdx.x * PJ_WAVES * T + wave;      // tile k: tile0 + 8 k
-    // this wavefront's tiles: a prefix k < ntw of the T
-    const int ntw = tile0 >= ntile ? 0 : min(T, (ntile - 1 - tile0) / PJ_WAVES + 1);
-    const int Q = S * ntw;                                   // its tile steps
+    const int Q = S * T;                                     // tile steps of every wavefront
+    const int nbr = (N + 7) / 8;                             // NB
     const int sb0 = sl * S;
-    const int NB = (N + 7) / 8;
     const uint8_t *wm = j.w[m];
     // this lane's activation load (k_expert.hip's roles): block row ar and its
     // 16-byte unit; wavefronts 0..3 load the q rows, 4 the sums of 16, 5 the
-    // scales
+    // scales.  Per block one source pointer at the slice's first super-block
+    // and one stride per super-block, fixed for the launch.
     const int ar = wave < 4 ? 4 * wave + (lane >> 4) : (wave == 4 ? (lane >> 1) & 15 : lane & 15);
     const int aunit = (lane & 15) ^ (ar & 11);
     const bool aload = wave < 4 || (wave == 4 && lane < 32) || (wave == 5 && lane < 16);
     const bool loader = wave < ADMA_WAVES;
     const uint32_t loff = lane * 16;
-
-    // activations of super-block s to stage s % 2 (NB loads in a loader wavefront)
-    auto issue_a = [&](int s) {
-        const int sb = sb0 + s;
+    const int astride = wave < 4 ? 256 : (wave == 4 ? 32 : 4);
+    const int adst = wave < 4 ? 1024 * wave : (wave == 4 ? ABS_OFF : AD_OFF);
+    const uint8_t *asrc[NB];
 #pragma unroll
-        for (int c = 0; c < PJ_BLOCKS; c++) {
-            if (c >= NB) break;
-            // block row ar: token 8 c + ar / 2 (the last one repeated past N), digit ar % 2
-            const int row = min(8 * c + (ar >> 1), N - 1) + (ar & 1) * N;
-            uint8_t *st8 = &s_act[s & 1][c][0];
-            if (wave < 4)
-                lds_load16(j.x.q + (size_t)row * K + sb * 256 + aunit * 16, st8 + 1024 * wave);
-            else if (wave == 4 && aload)
-                lds_load16(j.x.bs + (size_t)row * (K / 16) + sb * 16 + (lane & 1) * 8, st8 + ABS_OFF);
-            else if (wave == 5 && aload)
-                lds_load4(j.x.d + (size_t)row * nsb + sb, st8 + AD_OFF);
+    for (int c = 0; c < NB; c++) {
+        // block row ar: token 8 c + ar / 2 (the last one repeated past N), digit ar % 2
+        const int row = min(8 * c + (ar >> 1), N - 1) + (ar & 1) * N;
+        asrc[c] = wave < 4 ? reinterpret_cast<const uint8_t *>(j.x.q + (size_t)row * K + sb0 * 256 + aunit * 16)
+                : wave == 4 ? reinterpret_cast<const uint8_t *>(j.x.bs + (size_t)row * (K / 16) + sb0 * 16) +
+                                  (lane & 1) * 16
+                            : reinterpret_cast<const uint8_t *>(j.x.d + (size_t)row * nsb + sb0);
+    }
+
+    // activations of super-block s (clamped to the slice) to stage st (NB
+    // loads in a loader wavefront)
+    auto issue_a = [&](int s, int st) __attribute__((always_inline)) {
+        const int off = min(s, S - 1) * astride;
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            const uint8_t *st8 = &s_act[st][c][0] + adst;
+            if (wave < 5) {
+                if (aload) lds_load16(asrc[c] + off, st8);
+            } else if (wave == 5 && aload) {
+                lds_load4(asrc[c] + off, st8);
+            }
         }
     };
-    // weights of tile step q (super-block q / ntw of tile q % ntw) to ring stage q % PJ_WST
-    auto issue_w = [&](int q) {
-        const int s = q / ntw, k = q - s * ntw;
-        const uint8_t *t = wm + ((size_t)(tile0 + PJ_WAVES * k) * nsb + sb0 + s) * TILE_BYTES;
+    // weights of tile step q (clamped to the last) to ring stage q % PJ_WST
+    auto issue_w = [&](int q) __attribute__((always_inline)) {
+        const int qc = min(q, Q - 1);
+        const int s = qc / T, k = qc - s * T;
+        const int tile = min(tile0 + PJ_WAVES * k, ntile - 1);
+        const uint8_t *t = wm + ((size_t)tile * nsb + sb0 + s) * TILE_BYTES;
         const uint8_t *d = &s_w[wave][q % PJ_WST][0];
         lds_load16_sa(t, loff, d);
         lds_load16_sa(t, loff + 1024, d + 1024);
         if (lane < TPIECES - 128) lds_load16_sa(t, loff + 2048, d + 2048);
     };
 
-    float acc[T][PJ_BLOCKS][4];
+    float acc[T][NB][2];
 #pragma unroll
     for (int k = 0; k < T; k++)
 #pragma unroll
-        for (int c = 0; c < PJ_BLOCKS; c++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[k][c][i] = 0.0f;
+        for (int c = 0; c < NB; c++) acc[k][c][0] = acc[k][c][1] = 0.0f;
 
     // Issue order: A(0), W(0 .. PJ_AHEAD - 1); then per super-block s: wait
     // for A(s) (loaders), barrier, A(s + 1), and per tile step q of s: W(q +
     // PJ_AHEAD), wait for W(q), products.  Loads complete in issue order, so
-    // each wait allows exactly the loads issued after the one awaited (3 per
-    // weight step, NB per activation step of a loader).
-    issue_a(0);
-    for (int q = 0; q < min(PJ_AHEAD, Q); q++) issue_w(q);
+    // each wait allows exactly the loads issued after the one awaited: 3 per
+    // weight step (the third, of lanes 0..15, is one instruction of the
+    // wavefront), NB per activation step of a loader.  Before the barrier of
+    // super-block s, A(s) has the weight steps issued since after it: PJ_AHEAD
+    // at s = 0, T after (one per step of s - 1).  W(q) of step k of s has the
+    // PJ_AHEAD weight steps after it and, when k < PJ_AHEAD, A(s + 1), which
+    // was issued at the start of s; activation steps of earlier super-blocks
+    // that may also follow it (T < PJ_AHEAD) are left out of the count, so
+    // the wait is then longer than it need be, never shorter.
+    issue_a(0, 0);
+    for (int q = 0; q < PJ_AHEAD; q++) issue_w(q);
     for (int s = 0; s < S; s++) {
         if (loader) {
-            const int cnt = s == 0 ? min(PJ_AHEAD, Q)
-                                   : max(0, min(Q, s * ntw + PJ_AHEAD) - ((s - 1) * ntw + PJ_AHEAD));
-            pj_wait_vm(3 * cnt);
+            if (s == 0)
+                pj_wait<3 * PJ_AHEAD>();
+            else
+                pj_wait<3 * T>();
         }
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 1 < S) issue_a(s + 1);
+        issue_a(s + 1, (s + 1) & 1);
+        const uint8_t *ast = &s_act[s & 1][0][0];
+        // the super-block's activation operands, read once for its T tiles
+        PjOps o[NB];
+#pragma unroll
+        for (int c = 0; c < NB; c++) pj_read_ops(o[c], ast + c * ASTEP_BYTES, r16, g);
 #pragma unroll
         for (int k = 0; k < T; k++) {
-            if (k >= ntw) break;
-            const int q = s * ntw + k;
-            if (q + PJ_AHEAD < Q) issue_w(q + PJ_AHEAD);
-            // loads issued after W(q): the weight steps ahead of it and the
-            // activation steps issued since (super-blocks past the one W(q)
-            // was issued in)
-            const int iss = q < PJ_AHEAD ? -1 : (q - PJ_AHEAD) / ntw;
-            const int a_lo = max(1, iss + 2), a_hi = min(s + 1, S - 1);
-            const int cnt_a = loader ? max(0, a_hi - a_lo + 1) : 0;
-            pj_wait_vm(3 * min(PJ_AHEAD, Q - 1 - q) + NB * cnt_a);
+            const int q = s * T + k;
+            issue_w(q + PJ_AHEAD);
+            constexpr int nw = 3 * PJ_AHEAD;
+            if (k < PJ_AHEAD && loader)
+                pj_wait<nw + NB>();
+            else
+                pj_wait<nw>();
             asm volatile("" ::: "memory");
+            // block c + 1's MFMAs are issued before block c's epilogue, which
+            // then finds block c's sums ready (two sum sets live at a time)
             Q4KTile t;
             read_tile(t, &s_w[wave][q % PJ_WST][0], r16, g);
+            PjSums r[2];
             Q4KFolded f;
             fold_tile(t, g, f);
+            pj_mfma(f, o[0], r[0]);
 #pragma unroll
-            for (int c = 0; c < PJ_BLOCKS; c++)
-                if (c < NB) compute_folded(f, &s_act[s & 1][c][0], r16, g, acc[k][c]);
+            for (int c = 0; c < NB; c++) {
+                // (nbr == NB; a run-time test keeps each block's work in a
+                // region of its own: merged, the blocks' and steps' products
+                // are interleaved past the register file)
+                if (c < nbr) {
+                    if (c + 1 < NB) pj_mfma(f, o[c + 1], r[(c + 1) & 1]);
+                    pj_epilogue(f, r[c & 1], acc[k][c]);
+                }
+            }
         }
     }
-    // lane (r16, g): outputs of block rows 4 g + i = token 8 c + 2 g + i / 2,
-    // digit i % 2; the token's value is the sum of its two digits' products
+    // the last loads (repeats, never read) have landed before the workgroup
+    // ends
+    pj_wait<0>();
+    // lane (r16, g): outputs of tokens 8 c + 2 g + u (u = 0, 1), weight row
+    // r16 of each tile
 #pragma unroll
     for (int k = 0; k < T; k++) {
-        if (k >= ntw) break;
-        const int row = (tile0 + PJ_WAVES * k) * 16 + r16;
+        const int tile = tile0 + PJ_WAVES * k;
+        if (tile >= ntile) break;
+        const int row = tile * 16 + r16;
 #pragma unroll
-        for (int c = 0; c < PJ_BLOCKS; c++) {
-            if (c >= NB) break;
+        for (int c = 0; c < NB; c++) {
 #pragma unroll
-            for (int i = 0; i < 4; i += 2) {
-                const int t = 8 * c + 2 * g + (i >> 1);
+            for (int u = 0; u < 2; u++) {
+                const int t = 8 * c + 2 * g + u;
                 if (t >= N) continue;
-                const float v = acc[k][c][i] + acc[k][c][i + 1];
+                const float v = acc[k][c][u];
                 if (j.partial)
                     j.out[((size_t)(m * KS + sl) * N + t) * R + row] = v;
                 else
@@ -264,6 +371,29 @@ size_t proj_partial_floats(int R, int K, int M, int N)
     return (size_t)M * proj_plan(R, K, M, N).KS * N * R;
 }
 
+template <int T, int NB>
+static hipError_t proj_launch_nb(int nb, dim3 grid, const ProjJob &j, hipStream_t s)
+{
+    if constexpr (NB > PJ_BLOCKS) {
+        return hipErrorInvalidValue;
+    } else {
+        if (nb != NB) return proj_launch_nb<T, NB + 1>(nb, grid, j, s);
+        hipLaunchKernelGGL((k_proj_q4k<T, NB>), grid, dim3(PJ_WAVES * 64), 0, s, j);
+        return hipGetLastError();
+    }
+}
+
+template <int T>
+static hipError_t proj_launch_t(int t, int nb, dim3 grid, const ProjJob &j, hipStream_t s)
+{
+    if constexpr (T < 1) {
+        return hipErrorInvalidValue;
+    } else {
+        if (t != T) return proj_launch_t<T - 1>(t, nb, grid, j, s);
+        return proj_launch_nb<T, 1>(nb, grid, j, s);
+    }
+}
+
 hipError_t launch_proj_q4k(const ProjJob &j, hipStream_t s)
 {
     const ProjPlan pl = proj_plan(j.R, j.K, j.M, j.N);
@@ -271,15 +401,8 @@ hipError_t launch_proj_q4k(const ProjJob &j, hipStream_t s)
         (!j.partial && (j.M != 1 || j.KS != 1 || j.ldo < j.R)))
         return hipErrorInvalidValue;
     const dim3 grid((j.R / 16 + PJ_WAVES * pl.T - 1) / (PJ_WAVES * pl.T), j.KS, j.M);
-    switch (pl.T) {
-    case 1: hipLaunchKernelGGL(k_proj_q4k<1>, grid, dim3(PJ_WAVES * 64), 0, s, j); break;
-    case 2: hipLaunchKernelGGL(k_proj_q4k<2>, grid, dim3(PJ_WAVES * 64), 0, s, j); break;
-    case 3: hipLaunchKernelGGL(k_proj_q4k<3>, grid, dim3(PJ_WAVES * 64), 0, s, j); break;
-    case 4: hipLaunchKernelGGL(k_proj_q4k<4>, grid, dim3(PJ_WAVES * 64), 0, s, j); break;
-    case 5: hipLaunchKernelGGL(k_proj_q4k<5>, grid, dim3(PJ_WAVES * 64), 0, s, j); break;
-    default: hipLaunchKernelGGL(k_proj_q4k<6>, grid, dim3(PJ_WAVES * 64), 0, s, j); break;
-    }
-    return hipGetLastError();
+    const int nb = (j.N + 7) / 8;
+    return proj_launch_t<PJ_TMAX>(pl.T, nb, grid, j, s);
 }
 
 hipError_t launch_proj_reduce(const float *part, int KS, int N, int R, float *y, int ldy, hipStream_t s)
