@@ -625,6 +625,8 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.perm = w.rb.perm;
         job.offsets = w.rb.offsets;
         job.counts = w.rb.counts;
+        job.E = E;
+        job.ec_cap = E + N * K / EXPERT_CHUNK + 1;
         job.wl = w.wl;
         job.ax = w.ax;
         job.axs = w.axs;

@@ -104,6 +104,7 @@ struct MoeJob {
     int32_t H, FF, SF;       // n_embd, moe_ff, shared_ff
     int32_t n_tokens, top_k;
     const int32_t *perm, *offsets, *counts;
+    int32_t E, ec_cap;       // routed experts (offsets / counts length), work-list length (0: none)
     WorkList wl;
     ActI8 ax, axs;         // x converted: Q8_K (rows: tokens), split (shared)
     float *h, *hs;           // gate/up results [N*K][FF], [N][SF]

@@ -486,6 +486,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void k_expert_q4k(MoeJob job)
 // 2, 3, 4, 5 sets; 171 / 174 us for 2 / 3 sets at 256 tokens).
 constexpr int GR_R = 2;          // weight register sets per wavefront (one step ahead)
 constexpr int GR_MAX_SB = 16;    // super-blocks of the reduction held in LDS (n_embd <= 4096)
+constexpr int GR_TAB_E = 1024;   // routed experts whose offsets and counts are staged in LDS
+constexpr int GR_TAB_P = 2048;   // (token, slot) pairs whose permutation entries are staged
 
 template <int J0, int J1, class F>
 __device__ __forceinline__ void gr_unroll(F &&f)
@@ -505,9 +507,13 @@ __device__ __forceinline__ uint4 gr_ld_nt16(const void *p)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// TABS: the routing's offsets, counts and permutation fit the LDS tables
+// (gr_tabs) and are read from there
+template <bool TABS>
 __global__ __launch_bounds__(WAVES * 64) void k_gateup_rr(MoeJob job)
 {
     __shared__ __align__(16) uint8_t s_act[GR_MAX_SB][ASTEP_BYTES];
+    __shared__ int32_t s_off[GR_TAB_E], s_cnt[GR_TAB_E], s_perm[GR_TAB_P];
     static_assert(GROWS_GU * 16 * 4 + WAVES * 256 * 4 <= GR_MAX_SB * ASTEP_BYTES, "h and its scratch fit");
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -515,9 +521,29 @@ __global__ __launch_bounds__(WAVES * 64) void k_gateup_rr(MoeJob job)
     const int g = lane >> 4, r16 = lane & 15;
     const int N = job.n_tokens, K = job.top_k;
     const int H = job.H, FF = job.FF, SF = job.SF;
-    const int n_ec = job.wl.n_ec[0];
-    const int nch = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
     const int rg = FF / GROWS_GU, rg_sh = SF / GROWS_GU;
+    // The work-list count, the first item's work-list entry (read as if the
+    // item were routed) and the routing's offsets, counts and permutation
+    // (into LDS) are independent loads, issued together: one round trip
+    // before the item's weight and activation addresses are known, where
+    // looking them up in turn (count, entry, offset, pair) takes four.
+    constexpr bool tabs = TABS;
+    const int n_ec = job.wl.n_ec[0];
+    int e_first = 0, c_first = 0;
+    if (job.ec_cap > 0) {
+        const int u = min((int)blockIdx.x / rg, job.ec_cap - 1);
+        e_first = job.wl.ec_expert[u];
+        c_first = job.wl.ec_chunk[u];
+    }
+    if constexpr (tabs) {
+        for (int i = tid; i < job.E; i += WAVES * 64) {
+            s_off[i] = job.offsets[i];
+            s_cnt[i] = job.counts[i];
+        }
+        for (int i = tid; i < N * K; i += WAVES * 64) s_perm[i] = job.perm[i];
+    }
+    __syncthreads();
+    const int nch = job.has_shared ? (N + SHARED_CHUNK - 1) / SHARED_CHUNK : 0;
     const int routed_items = n_ec * rg;
     const int total = routed_items + nch * rg_sh;
     const int nsb = H / 256;
@@ -535,10 +561,16 @@ __global__ __launch_bounds__(WAVES * 64) void k_gateup_rr(MoeJob job)
         const int rbase = (j - unit * rgn) * GROWS_GU;
         int t_first, nt, e = 0;
         if (!shared) {
-            e = job.wl.ec_expert[unit];
-            const int c0 = job.wl.ec_chunk[unit] * EXPERT_CHUNK;
-            t_first = job.offsets[e] + c0;
-            nt = min(EXPERT_CHUNK, job.counts[e] - c0);
+            const bool first = item == (int)blockIdx.x;
+            e = first ? e_first : job.wl.ec_expert[unit];
+            const int c0 = (first ? c_first : job.wl.ec_chunk[unit]) * EXPERT_CHUNK;
+            if constexpr (tabs) {
+                t_first = s_off[e] + c0;
+                nt = min(EXPERT_CHUNK, s_cnt[e] - c0);
+            } else {
+                t_first = job.offsets[e] + c0;
+                nt = min(EXPERT_CHUNK, job.counts[e] - c0);
+            }
         } else {
             t_first = unit * SHARED_CHUNK;
             nt = min(SHARED_CHUNK, N - t_first);
@@ -573,17 +605,24 @@ __global__ __launch_bounds__(WAVES * 64) void k_gateup_rr(MoeJob job)
                 }
             }
         };
+        // this lane's activation row, looked up before the first weight loads
+        // are issued (a global load after them would wait for them too)
+        int arow;
+        if (shared) {
+            arow = t_first + min(ar >> 1, nt - 1) + (ar & 1) * N;
+        } else {
+            const int pi = t_first + min(ar, nt - 1);
+            if constexpr (tabs)
+                arow = s_perm[pi] / K;
+            else
+                arow = job.perm[pi] / K;
+        }
+        asm volatile("" : "+v"(arow));
         Q4KTile o[GR_R][2];
         gr_unroll<0, GR_R - 1>([&](auto jc) { load(o[decltype(jc)::value]); });
 
         // the previous item's h conversion is done with the activation region
         __syncthreads();
-        int arow;
-        if (shared) {
-            arow = t_first + min(ar >> 1, nt - 1) + (ar & 1) * N;
-        } else {
-            arow = job.perm[t_first + min(ar, nt - 1)] / K;
-        }
         const ActI8 &act = shared ? job.axs : job.ax;
         if (wave < ADMA_WAVES) {
             for (int sb = 0; sb < nsb; sb++) {
@@ -668,7 +707,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gateup_rr(MoeJob job)
 #pragma unroll
             for (int c = 0; c < 4; c++) v[c] = s_h[t * 256 + lane + 64 * c];
             if (!shared)
-                prep_values(v, job.ah, ACT_Q8K, job.perm[t_first + t], N * K, sbh, nsb_h, sv);
+                prep_values(v, job.ah, ACT_Q8K, tabs ? (int)s_perm[t_first + t] : (int)job.perm[t_first + t], N * K,
+                            sbh, nsb_h, sv);
             else
                 prep_values(v, job.ahs, ACT_SPLIT, t_first + t, N, sbh, nsb_h, sv);
         }
@@ -705,7 +745,10 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc
         // selects the LDS-ring one (the same bits)
         const char *ov = getenv("DMOE_GATEUP_LDS");
         if (nc == 1 && job.H / 256 <= GR_MAX_SB && !(ov && atoi(ov) == 1)) {
-            hipLaunchKernelGGL(k_gateup_rr, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
+            if (job.E > 0 && job.E <= GR_TAB_E && job.n_tokens * job.top_k <= GR_TAB_P)
+                hipLaunchKernelGGL(k_gateup_rr<true>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
+            else
+                hipLaunchKernelGGL(k_gateup_rr<false>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
             return hipGetLastError();
         }
         return launch_phase<0>(nc, job, dim3(DMOE_X_BLOCKS), s);
