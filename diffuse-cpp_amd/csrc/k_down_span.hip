@@ -38,6 +38,9 @@ constexpr int DS_WAVES = 8;
 constexpr int DS_R = 3;            // weight register sets per wavefront (2 steps in flight)
 constexpr int DS_SLOTS = 3;        // units whose activations a workgroup holds
 constexpr int DS_MAX_SB = 4;       // super-blocks of the reduction (moe_ff <= 1024)
+constexpr int DS_TAB_E = 1024;   // routed experts whose offsets and counts are staged in LDS
+constexpr int DS_TAB_EC = 2048;  // work-list entries staged in LDS
+constexpr int DS_TAB_P = 2048;   // (token, slot) pairs whose permutation entries are staged
 
 typedef unsigned int ds_u4v __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) ds_u4v *ds_gu4v_ptr;
@@ -60,6 +63,10 @@ __device__ __forceinline__ uint4 ds_ld_nt16(const void *p)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// TABS: the work list and the routing's offsets, counts and permutation fit
+// the LDS tables (ds_tabs); they are loaded there at the start, all at once,
+// and every lookup of the prologue after that is an LDS read.
+template <bool TABS>
 __global__ __launch_bounds__(DS_WAVES * 64) void k_down_span(DownRowsJob job)
 {
 #pragma clang fp contract(off)
@@ -68,6 +75,8 @@ __global__ __launch_bounds__(DS_WAVES * 64) void k_down_span(DownRowsJob job)
     __shared__ int32_t s_up0[DS_SLOTS];           // first pair (routed) / first token (shared)
     __shared__ int32_t s_unp[DS_SLOTS];           // pairs (> 0) / -tokens (shared)
     __shared__ int32_t s_pid[DS_SLOTS][16];       // routed: the unit's pair ids
+    __shared__ int32_t s_ecx[TABS ? DS_TAB_EC : 1], s_ecc[TABS ? DS_TAB_EC : 1];
+    __shared__ int32_t s_off[TABS ? DS_TAB_E : 1], s_cnt[TABS ? DS_TAB_E : 1], s_perm[TABS ? DS_TAB_P : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -75,6 +84,21 @@ __global__ __launch_bounds__(DS_WAVES * 64) void k_down_span(DownRowsJob job)
     const int N = job.N, H = job.H, FF = job.FF;
     const int nsb = FF / 256, NT = H / 16;
     const int n_ec = job.wl.n_ec[0];
+    // the work list and the routing tables, independent loads issued
+    // together: one round trip, where the count, the entries, the offsets
+    // and the pair ids in turn take four
+    if constexpr (TABS) {
+        for (int i = tid; i < job.ec_cap; i += DS_WAVES * 64) {
+            s_ecx[i] = job.wl.ec_expert[i];
+            s_ecc[i] = job.wl.ec_chunk[i];
+        }
+        for (int i = tid; i < job.E; i += DS_WAVES * 64) {
+            s_off[i] = job.offsets[i];
+            s_cnt[i] = job.counts[i];
+        }
+        for (int i = tid; i < N * job.K; i += DS_WAVES * 64) s_perm[i] = job.perm[i];
+        __syncthreads();
+    }
     const int nsh = job.has_shared ? (N + 7) / 8 : 0;
     const int nu = n_ec + nsh;
     const long W = (long)nu * NT;
@@ -87,10 +111,21 @@ __global__ __launch_bounds__(DS_WAVES * 64) void k_down_span(DownRowsJob job)
     if (tid < nslot) {
         const int u = u_first + tid;
         if (u < n_ec) {
-            const int e = job.wl.ec_expert[u], c = job.wl.ec_chunk[u];
+            int e, c, off, cnt;
+            if constexpr (TABS) {
+                e = s_ecx[u];
+                c = s_ecc[u];
+                off = s_off[e];
+                cnt = s_cnt[e];
+            } else {
+                e = job.wl.ec_expert[u];
+                c = job.wl.ec_chunk[u];
+                off = job.offsets[e];
+                cnt = job.counts[e];
+            }
             s_uw[tid] = job.ed.data + (size_t)e * job.ed.nb2;
-            s_up0[tid] = job.offsets[e] + EXPERT_CHUNK * c;
-            s_unp[tid] = min(EXPERT_CHUNK, job.counts[e] - EXPERT_CHUNK * c);
+            s_up0[tid] = off + EXPERT_CHUNK * c;
+            s_unp[tid] = min(EXPERT_CHUNK, cnt - EXPERT_CHUNK * c);
         } else {
             const int c = u - n_ec;
             s_uw[tid] = job.sd.data;
@@ -173,7 +208,13 @@ __global__ __launch_bounds__(DS_WAVES * 64) void k_down_span(DownRowsJob job)
     if (Q > 0) ds_unroll<0, DS_R - 1>([&](auto jc) { load(o[decltype(jc)::value]); });
     if (tid < 16 * nslot) {
         const int sl = tid >> 4, i = tid & 15, np = s_unp[sl];
-        if (np > 0) s_pid[sl][i] = job.perm[s_up0[sl] + min(i, np - 1)];
+        if (np > 0) {
+            const int pi = s_up0[sl] + min(i, np - 1);
+            if constexpr (TABS)
+                s_pid[sl][i] = s_perm[pi];
+            else
+                s_pid[sl][i] = job.perm[pi];
+        }
     }
     __syncthreads();
 
@@ -255,7 +296,10 @@ hipError_t launch_down_span(const DownRowsJob &job, hipStream_t s)
         job.wl.chunk != EXPERT_CHUNK || job.ah.K != job.FF || (job.has_shared && job.ahs.K != job.FF) ||
         !job.ye || (job.has_shared && !job.ys))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_down_span, dim3(n_cu), dim3(DS_WAVES * 64), 0, s, job);
+    if (job.E <= DS_TAB_E && job.ec_cap <= DS_TAB_EC && job.N * job.K <= DS_TAB_P)
+        hipLaunchKernelGGL(k_down_span<true>, dim3(n_cu), dim3(DS_WAVES * 64), 0, s, job);
+    else
+        hipLaunchKernelGGL(k_down_span<false>, dim3(n_cu), dim3(DS_WAVES * 64), 0, s, job);
     return hipGetLastError();
 }
 
