@@ -189,7 +189,7 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
                     return n + (n // 16) * 2 + (n // 256) * 4
                 # items of one column block (fewer than 32 pairs per expert on
                 # average) run on the register-ring kernel
-                dom_kernel = "dmoe::k_gateup_rr" if N * K // E < 32 else "dmoe::k_expert_q4k<0>"
+                dom_kernel = "dmoe::k_gateup_rr<true>" if N * K // E < 32 else "dmoe::k_expert_q4k<0>"
             else:
                 def act_row(n):
                     return n + (n // 32) * 4
