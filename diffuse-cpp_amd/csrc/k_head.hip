@@ -2,17 +2,20 @@
 // (the temperature-0 branch of sample_token, src/diffuse-sampler.cpp:29-49).
 //
 // Two launches so that a row of a large vocabulary spreads over many
-// workgroups (32 positions of 157184 logits are 2464 chunks, not 32 rows).
+// workgroups (32 positions of 157184 logits are 1248 chunks, not 32 rows).
 //
 // k_argmax_part: one workgroup per chunk of AP_CHUNK logits of a row, held in
 // registers.  Its argmax: each thread's values in ascending index order keep
 // the first of equal maxima (a NaN never compares greater), then the
-// threads' (value, index) pairs combine in a fixed tree, larger value first,
-// lower index on ties.  Its exp-sum s_c = sum exp(l - m_c) over the chunk,
-// about the chunk's own maximum m_c (0 when the chunk holds no value above
-// -inf, so that its -inf logits add 0 and a NaN still adds NaN), with exp the
-// correctly rounded binary32 exp of the difference, each thread adding its
-// terms in binary64 and the partials in a fixed tree.
+// threads' (value, index) pairs combine by xor butterflies in each
+// wavefront and the wavefronts' results in wavefront order, larger value
+// first, lower index on ties.  Its exp-sum s_c = sum exp(l - m_c) over the
+// chunk, about the chunk's own maximum m_c (0 when the chunk holds no value
+// above -inf, so that its -inf logits add 0 and a NaN still adds NaN), each
+// term 2^((l - m_c) log2 e) by the hardware exp2 in binary32 (a few ulp of
+// the exact value; the correctly rounded binary32 exp through binary64 made
+// the launch VALU bound at twice the time), each thread adding its terms in
+// binary64 and the partials in the same fixed order.
 //
 // k_argmax_final: one wave per row combines the chunks in the same rule (the
 // first index of the largest; every logit -inf, or a NaN logits[0], gives
@@ -28,7 +31,8 @@
 namespace dmoe {
 
 constexpr int AP_THREADS = 256;
-constexpr int AP_PER = 8;                                  // logits per thread
+constexpr int AP_WAVES = AP_THREADS / 64;
+constexpr int AP_PER = 16;                                 // logits per thread
 constexpr int AP_CHUNK = AP_THREADS * AP_PER;              // logits per workgroup
 
 size_t argmax_partials_bytes(int N, int V)
@@ -42,14 +46,19 @@ __device__ __forceinline__ bool ap_better(float b, int ib, float a, int ia)
     return b > a || (b == a && ib < ia);
 }
 
+// The chunk's reductions run in registers: xor butterflies inside each
+// wavefront (rounds 32 .. 1), then the four wavefronts' results combined by
+// one thread in wavefront order, so a chunk costs two barriers.
 __global__ __launch_bounds__(AP_THREADS) void k_argmax_part(const float *__restrict__ logits, int V, int C,
                                                             ArgmaxPart *__restrict__ part)
 {
 #pragma clang fp contract(off)
-    __shared__ float s_v[AP_THREADS];
-    __shared__ int s_i[AP_THREADS];
-    __shared__ double s_d[AP_THREADS];
+    __shared__ float s_v[AP_WAVES];
+    __shared__ int s_i[AP_WAVES];
+    __shared__ double s_d[AP_WAVES];
+    __shared__ float s_mc;
     const int c = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const float *row = logits + (size_t)t * V;
     const int v0 = c * AP_CHUNK;
     float l[AP_PER];
@@ -66,33 +75,50 @@ __global__ __launch_bounds__(AP_THREADS) void k_argmax_part(const float *__restr
             m = l[k];
             mi = v0 + k * AP_THREADS + tid;
         }
-    s_v[tid] = m;
-    s_i[tid] = mi;
-    __syncthreads();
-    for (int w = AP_THREADS / 2; w > 0; w >>= 1) {
-        if (tid < w && ap_better(s_v[tid + w], s_i[tid + w], s_v[tid], s_i[tid])) {
-            s_v[tid] = s_v[tid + w];
-            s_i[tid] = s_i[tid + w];
+#pragma unroll
+    for (int r = 32; r >= 1; r >>= 1) {
+        const float om = __shfl_xor(m, r, 64);
+        const int oi = __shfl_xor(mi, r, 64);
+        if (ap_better(om, oi, m, mi)) {
+            m = om;
+            mi = oi;
         }
-        __syncthreads();
     }
-    const float mc = s_v[0];
+    if (lane == 0) {
+        s_v[wave] = m;
+        s_i[wave] = mi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float bm = s_v[0];
+        int bi = s_i[0];
+        for (int w = 1; w < AP_WAVES; w++)
+            if (ap_better(s_v[w], s_i[w], bm, bi)) {
+                bm = s_v[w];
+                bi = s_i[w];
+            }
+        s_mc = bm;
+        s_i[0] = bi;
+    }
+    __syncthreads();
+    const float mc = s_mc;
     const float base = mc == -__builtin_inff() ? 0.0f : mc;
     double acc = 0.0;
 #pragma unroll
     for (int k = 0; k < AP_PER; k++)
-        if (v0 + k * AP_THREADS + tid < V) acc += (double)exp_f32(l[k] - base);
-    s_d[tid] = acc;
+        if (v0 + k * AP_THREADS + tid < V)
+            acc += (double)__builtin_amdgcn_exp2f((l[k] - base) * 1.44269504088896341f);
+#pragma unroll
+    for (int r = 32; r >= 1; r >>= 1) acc = acc + __shfl_xor(acc, r, 64);
+    if (lane == 0) s_d[wave] = acc;
     __syncthreads();
-    for (int w = AP_THREADS / 2; w > 0; w >>= 1) {
-        if (tid < w) s_d[tid] = s_d[tid] + s_d[tid + w];
-        __syncthreads();
-    }
     if (tid == 0) {
+        double sum = s_d[0];
+        for (int w = 1; w < AP_WAVES; w++) sum = sum + s_d[w];
         ArgmaxPart p;
         p.m = mc;
         p.idx = s_i[0];
-        p.sum = s_d[0];
+        p.sum = sum;
         part[(size_t)t * C + c] = p;
     }
 }

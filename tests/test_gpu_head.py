@@ -6,7 +6,8 @@ Bars: logits max|l - l_oracle| / max|l_oracle| <= 5e-4 for the int8-digit and
 f16-pair paths (F32 weight semantics with about 16-bit activations; the
 dense MLP's measured error is 1.2e-4) and 1e-5 for plain F32; confidence
 within 1e-3 relative (the oracle adds the exponentials in float,
-sequentially, as the reference does, the GPU in binary64 in a tree); the
+sequentially, as the reference does, the GPU hardware-exp2 terms in
+binary64 in a fixed tree); the
 token equals the oracle's wherever the oracle's top two logits are further
 apart than twice the logit tolerance (closer ones may swap within it, and
 then the GPU's token must be one of the two)."""
