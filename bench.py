@@ -176,10 +176,20 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
         dom_kernel = "dmoe::k_gemm_f16<0>"
         dom_flops = 2.0 * (P * 2 * H * FF + N * 2 * H * SF)
         achieved = dom_flops / (dom_us * 1e-6) / 1e12 if dom_us else None
+        # the launch must also stream the touched experts' gate and up
+        # weights: the MFMA fraction it can reach is its MFMA time over the
+        # longer of that and the weights' HBM time
+        w_bytes = touched * 2 * FF * rs_h + 2 * SF * rs_h
+        t_mfma = dom_flops / (MFMA_F16_PEAK_TFLOPS * 1e12)
+        t_hbm = w_bytes / (HBM_PEAK_GBS * 1e9)
         roofline = {"bound": "mfma", "kernel": dom_stage,
                     "achieved": round(achieved, 1) if achieved else None,
                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4) if achieved else None,
+                    "attainable_frac": round(t_mfma / max(t_mfma, t_hbm), 4),
+                    "weight_bytes": w_bytes,
+                    "weight_hbm_frac": (round(w_bytes / (dom_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                                        if dom_us else None),
                     "traffic": traffic_from_profile(dom_stage, cfg.name),
                     "algorithmic_flops": dom_flops, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
     else:
