@@ -24,7 +24,7 @@ def _say(msg):
 
 
 @pytest.mark.parametrize("wtype", [12, 8, 1, 0], ids=["Q4_K", "Q8_0", "F16", "F32"])
-@pytest.mark.parametrize("N", [32, 40, 96])
+@pytest.mark.parametrize("N", [9, 17, 32, 40, 96])
 def test_dense_small(ctx, O, wtype, N):
     from dmoe import synth
     H, FF = 512, 768

@@ -59,6 +59,24 @@ def test_head_small(ctx, O, wtype, N):
     head.free()
 
 
+@pytest.mark.parametrize("N", [1, 9, 17, 25])
+def test_head_q4k_column_blocks(ctx, O, N):
+    """The few-token projection at each column-block count (1 to 4 blocks of
+    8 tokens, the last one partly filled), Q4_K, against the oracle."""
+    from dmoe import synth
+    H, V = 512, 4096
+    _say(f"case: step tail Q4_K H={H} V={V} N={N}")
+    w = synth.host_head(H, V, 12, 90 + N, O.quantize_rows)
+    h = (synth.normal(91 + N, synth.S_X, N * H).reshape(N, H) * 2).astype(np.float32)
+    head = ctx.head_upload(w)
+    assert head.kernel_path() == PATH[12]
+    tok, prob, lg = ctx.head_forward(head, h, 1e-6, logits=True)
+    tr, pr, lr = O.head_forward(w, h, 1e-6)
+    err = _check(tok, prob, lg, tr, pr, lr, TOL[12])
+    _say(f"  logits max rel err {err:.3e}")
+    head.free()
+
+
 def test_head_gemv_vocab(ctx, O):
     """A vocabulary that is not a whole number of row groups: GEMV kernels."""
     from dmoe import synth
