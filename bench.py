@@ -55,14 +55,19 @@ def parse():
 
 
 def traffic_from_profile(kernel, workload):
-    """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
+    """{"traffic": HBM bytes per launch, "traffic_source": where it comes from}
+    for `kernel`: the counters are not read in this run (rocprofv3 --pmc runs
+    apart from the timed ones), so the value is the one the committed summary
+    under profiles/ holds (FETCH_SIZE + WRITE_SIZE of that launch, scaled by
+    the counters' reading of a device copy of known size); None without one."""
     f = ROOT / "profiles" / f"{kernel}_{workload}_traffic.md"
-    if not f.exists():
-        return None
-    for line in f.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1].strip())
-    return None
+    if f.exists():
+        for line in f.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return {"traffic": int(line.split(":", 1)[1].strip()),
+                        "traffic_source": f"profiles/{f.name} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                                          "copied from the committed summary, not measured in this run)"}
+    return {"traffic": None, "traffic_source": None}
 
 
 def cpu_info():
@@ -190,7 +195,7 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
                     "weight_bytes": w_bytes,
                     "weight_hbm_frac": (round(w_bytes / (dom_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
                                         if dom_us else None),
-                    "traffic": traffic_from_profile(dom_stage, cfg.name),
+                    **traffic_from_profile(dom_stage, cfg.name),
                     "algorithmic_flops": dom_flops, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
     else:
         if cfg.wtype in (dmoe.TYPE_Q4_K, dmoe.TYPE_Q8_0):
@@ -216,7 +221,7 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
                     "achieved": round(achieved, 1) if achieved else None,
                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-                    "traffic": traffic_from_profile(dom_stage, cfg.name),
+                    **traffic_from_profile(dom_stage, cfg.name),
                     "algorithmic_bytes": dom_bytes, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
 
     # layer-level: every weight byte the layer must read

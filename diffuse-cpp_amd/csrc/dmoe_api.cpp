@@ -25,6 +25,7 @@ using namespace dmoe;
 
 struct dmoe_ctx {
     int device = 0;
+    KernelSwitches sw;              // kernel choices, read from the environment at creation
     hipStream_t stream = nullptr;
     // device address of this GPU's `scratch` array (the allocation-free forward)
     uint8_t *scratch = nullptr;
@@ -330,12 +331,9 @@ bool use_mfma_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
 // prefill-sized windows); few tokens per expert keep the 16-pair items, whose
 // finer work division fills the chip.  DMOE_Q4K_COLUMN_BLOCKS (1, 2, 4)
 // overrides the choice.
-int q4k_column_blocks(const dmoe_hparams &hp, int N)
+int q4k_column_blocks(const KernelSwitches &sw, const dmoe_hparams &hp, int N)
 {
-    if (const char *ov = getenv("DMOE_Q4K_COLUMN_BLOCKS")) {
-        const int v = atoi(ov);
-        if (v == 1 || v == 2 || v == 4) return v;
-    }
+    if (sw.q4k_column_blocks) return sw.q4k_column_blocks;
     const long avg = (long)N * hp.top_k / (hp.n_experts > 0 ? hp.n_experts : 1);
     return avg >= 64 ? 4 : avg >= 32 ? 2 : 1;
 }
@@ -343,10 +341,11 @@ int q4k_column_blocks(const dmoe_hparams &hp, int N)
 // Few tokens of Q4_K experts: the down products and the combine run as one
 // launch over 16-row tiles of every expert (k_down_rows.hip); it takes the
 // 16-pair work list.
-bool use_down_rows(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N)
+bool use_down_rows(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
+                   int N)
 {
     return use_mfma_path(hp, wtype, stype, shared) &&
-           down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff) && q4k_column_blocks(hp, N) == 1;
+           down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff) && q4k_column_blocks(sw, hp, N) == 1;
 }
 
 // Of those, the shapes whose down products run by spans of (unit, tile) work
@@ -355,11 +354,11 @@ bool use_down_rows(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
 // against 36.0 us at the flash shape, 32 tokens; at 256 tokens the item
 // kernel is faster, 98.6 against 107.2 us).  DMOE_DOWN_FUSED=1 selects the
 // single fused launch (k_down_rows.hip) instead: the same bits.
-bool use_down_span(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N)
+bool use_down_span(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
+                   int N)
 {
-    const char *ov = getenv("DMOE_DOWN_FUSED");
-    if (ov && atoi(ov) == 1) return false;
-    return use_down_rows(hp, wtype, stype, shared, N) &&
+    if (sw.down_fused) return false;
+    return use_down_rows(sw, hp, wtype, stype, shared, N) &&
            down_span_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff, shared);
 }
 
@@ -397,7 +396,7 @@ ActI8 take_act(const std::function<uint8_t *(size_t)> &take, int rows, int K, bo
 
 // host_io: room for x and y (the host-buffer forward copies them through HBM).
 // Buffers only one kernel family reads are planned only for that family.
-size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N,
+size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared, int N,
                       bool host_io, uint8_t *base, Workspace *w)
 {
     const int H = hp.n_embd, E = hp.n_experts, K = hp.top_k, FF = hp.moe_ff;
@@ -437,7 +436,7 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
     const bool gemv = !gemm && !use_mfma_path(hp, wtype, stype, shared) &&
                       !use_q80_path(hp, wtype, stype, shared);
     t.wl.chunk = gemm ? GM
-                      : EXPERT_CHUNK * (use_mfma_path(hp, wtype, stype, shared) ? q4k_column_blocks(hp, N) : 1);
+                      : EXPERT_CHUNK * (use_mfma_path(hp, wtype, stype, shared) ? q4k_column_blocks(sw, hp, N) : 1);
     t.wl.n_ec = (int32_t *)take(4);
     t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
     t.wl.ec_chunk = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
@@ -485,7 +484,7 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
         t.hq.bsums = (int16_t *)take((size_t)P * (FF / 16 + 1) * 2);
         t.hs = (float *)take((size_t)N * (SF > 0 ? SF : 1) * 4);
     }
-    if (!use_down_rows(hp, wtype, stype, shared, N) || use_down_span(hp, wtype, stype, shared, N)) {
+    if (!use_down_rows(sw, hp, wtype, stype, shared, N) || use_down_span(sw, hp, wtype, stype, shared, N)) {
         // per-pair and shared down results, folded by the combine launch
         t.ye = (float *)take((size_t)P * H * 4);
         t.ys = (float *)take((size_t)N * H * 4);
@@ -497,7 +496,7 @@ size_t plan_workspace(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool
 int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, Workspace *w)
 {
     const size_t need =
-        plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, host_io, nullptr, nullptr);
+        plan_workspace(ctx->sw, L->hp, L->eg.type, L->sg.type, L->has_shared, N, host_io, nullptr, nullptr);
     if (need > ctx->ws_bytes) {
         if (ctx->ws) {
             // work queued on any stream may still read the old workspace
@@ -511,7 +510,7 @@ int ensure_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, Wo
         HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
         ctx->ws_bytes = need;
     }
-    plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, N, host_io, (uint8_t *)ctx->ws, w);
+    plan_workspace(ctx->sw, L->hp, L->eg.type, L->sg.type, L->has_shared, N, host_io, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
 }
 
@@ -587,9 +586,9 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
     const bool gemm = use_gemm_path(hp, L->eg.type, L->sg.type, L->has_shared);
     // activation layouts of the int8 MFMA kernels (routed, shared expert)
     const int mode_r = q8 ? ACT_Q80 : ACT_Q8K, mode_s = q8 ? ACT_SPLIT32 : ACT_SPLIT;
-    const int nc = q4 ? q4k_column_blocks(hp, N) : 1;
+    const int nc = q4 ? q4k_column_blocks(ctx->sw, hp, N) : 1;
     auto expert = [&](int phase, const MoeJob &j) {
-        return q8 ? launch_expert_q80(phase, j, s) : launch_expert_q4k(phase, j, s, nc);
+        return q8 ? launch_expert_q80(phase, j, s) : launch_expert_q4k(phase, j, s, nc, ctx->sw.gateup_lds);
     };
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
     // router logits, sigmoid, selection scores (+ x in the MFMA operand layout)
@@ -638,8 +637,8 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.ys = w.ys;
         // the gate/up launch converts h to the down products' layout itself
         STAGE(ST_GATEUP, expert(0, job));
-        const bool span = use_down_span(hp, L->eg.type, L->sg.type, L->has_shared, N);
-        if (span || use_down_rows(hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+        const bool span = use_down_span(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N);
+        if (span || use_down_rows(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N)) {
             // down products and the combine in one launch
             DownRowsJob dj{};
             dj.ed = L->ed;
@@ -1099,7 +1098,7 @@ int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const fl
     job.ys = y;                          // the shared expert's down output is the MLP's
     PrepJob pj{x, N, H, q8 ? ACT_SPLIT32 : ACT_SPLIT, w.axs};
     STAGE(ST_ACTQ_X, launch_prep(&pj, 1, s));
-    STAGE(ST_SH_GATEUP, q8 ? launch_expert_q80(0, job, s) : launch_expert_q4k(0, job, s));
+    STAGE(ST_SH_GATEUP, q8 ? launch_expert_q80(0, job, s) : launch_expert_q4k(0, job, s, 1, ctx->sw.gateup_lds));
     STAGE(ST_SH_DOWN, q8 ? launch_expert_q80(1, job, s) : launch_expert_q4k(1, job, s));
 #undef STAGE
     return DMOE_OK;
@@ -1490,6 +1489,22 @@ int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const floa
 
 } // namespace
 
+KernelSwitches read_kernel_switches()
+{
+    KernelSwitches sw;
+    auto flag = [](const char *name) {
+        const char *v = getenv(name);
+        return v && atoi(v) == 1;
+    };
+    if (const char *v = getenv("DMOE_Q4K_COLUMN_BLOCKS")) {
+        const int n = atoi(v);
+        if (n == 1 || n == 2 || n == 4) sw.q4k_column_blocks = n;
+    }
+    sw.down_fused = flag("DMOE_DOWN_FUSED");
+    sw.gateup_lds = flag("DMOE_GATEUP_LDS");
+    return sw;
+}
+
 // ===========================================================================
 extern "C" {
 
@@ -1503,6 +1518,7 @@ int dmoe_create(int hip_device, dmoe_ctx **out)
     dmoe_ctx *ctx = new (std::nothrow) dmoe_ctx();
     if (!ctx) return DMOE_ERR_OOM;
     ctx->device = hip_device;
+    ctx->sw = read_kernel_switches();
     if (hip_device >= kMaxDevices || hipSetDevice(hip_device) != hipSuccess ||
         scratch_address(hip_device, &ctx->scratch) != hipSuccess ||
         hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
@@ -1995,7 +2011,7 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
     if (!ctx->scratch)
         return set_err(ctx, DMOE_ERR_HIP, "scratch address of device %d not resolved", ctx->device);
     const size_t need = L->dense ? plan_dense(L, n_tokens, false, nullptr, nullptr)
-                                 : plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens,
+                                 : plan_workspace(ctx->sw, L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens,
                                                   false, nullptr, nullptr);
     if (need > DMOE_NOALLOC_SCRATCH_BYTES)
         return set_err(ctx, DMOE_ERR_INVALID_ARG,
@@ -2011,7 +2027,7 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
         return enqueue_dense(ctx, L, dw, x_dev, n_tokens, y_dev, (hipStream_t)stream, false);
     }
     Workspace w;
-    plan_workspace(L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens, false, ctx->scratch, &w);
+    plan_workspace(ctx->sw, L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens, false, ctx->scratch, &w);
     return enqueue_forward(ctx, L, w, x_dev, n_tokens, y_dev, (hipStream_t)stream, false);
 }
 

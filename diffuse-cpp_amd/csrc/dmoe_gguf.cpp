@@ -212,10 +212,18 @@ int find_f32(const dmoe_gguf *g, const char *suffix, float *v)
     return DMOE_ERR_NOT_FOUND;
 }
 
-uint32_t u32_or(const dmoe_gguf *g, const char *suffix, uint32_t def)
+// An optional key: *v = its value, or def when the key is absent.  A key
+// that is present but not a non-negative integer below 2^32 is an error
+// (DMOE_ERR_FORMAT), as a type mismatch is for the reference's
+// gguf_get_val_u32, never a silent default.
+int u32_or(const dmoe_gguf *g, const char *suffix, uint32_t def, uint32_t *v)
 {
-    uint32_t v;
-    return find_u32(g, suffix, &v) == DMOE_OK ? v : def;
+    const int rc = find_u32(g, suffix, v);
+    if (rc == DMOE_ERR_NOT_FOUND) {
+        *v = def;
+        return DMOE_OK;
+    }
+    return rc;
 }
 
 int tensor_view(const dmoe_gguf *g, const std::string &name, dmoe_tensor *out)
@@ -397,20 +405,30 @@ int dmoe_gguf_moe_hparams(const dmoe_gguf *g, dmoe_hparams *hp, int32_t *n_layer
     uint32_t nl = 0;
     if ((rc = find_u32(g, "block_count", &nl))) return rc;
     // the MoE keys with the reference's defaults (:143-158)
-    h.n_experts = (int32_t)u32_or(g, "expert_count", 0);
-    h.top_k = (int32_t)u32_or(g, "expert_used_count", 0);
-    h.n_shared = (int32_t)u32_or(g, "expert_shared_count", 0);
-    h.moe_ff = (int32_t)u32_or(g, "expert_feed_forward_length", 0);
-    h.norm_topk_prob = u32_or(g, "norm_topk_prob", 1) != 0;
-    h.capacity = (int32_t)u32_or(g, "expert_capacity", 48);
-    const uint32_t block_length = u32_or(g, "block_length", 0);
-    h.block_size = (int32_t)u32_or(g, "moe_block_size", block_length ? block_length : 32);
+    uint32_t ne = 0, nk = 0, ns = 0, nff = 0, norm = 0, cap = 0, block_length = 0, bs = 0;
+    if ((rc = u32_or(g, "expert_count", 0, &ne)) || (rc = u32_or(g, "expert_used_count", 0, &nk)) ||
+        (rc = u32_or(g, "expert_shared_count", 0, &ns)) ||
+        (rc = u32_or(g, "expert_feed_forward_length", 0, &nff)) || (rc = u32_or(g, "norm_topk_prob", 1, &norm)) ||
+        (rc = u32_or(g, "expert_capacity", 48, &cap)) || (rc = u32_or(g, "block_length", 0, &block_length)) ||
+        (rc = u32_or(g, "moe_block_size", block_length ? block_length : 32, &bs)))
+        return rc;
+    // the counts and sizes feed int32 fields
+    if (ne > INT32_MAX || nk > INT32_MAX || ns > INT32_MAX || nff > INT32_MAX || cap > INT32_MAX || bs > INT32_MAX)
+        return DMOE_ERR_FORMAT;
+    h.n_experts = (int32_t)ne;
+    h.top_k = (int32_t)nk;
+    h.n_shared = (int32_t)ns;
+    h.moe_ff = (int32_t)nff;
+    h.norm_topk_prob = norm != 0;
+    h.capacity = (int32_t)cap;
+    h.block_size = (int32_t)bs;
     float rs = 1.0f;
     if ((rc = find_f32(g, "routed_scaling_factor", &rs)) && rc != DMOE_ERR_NOT_FOUND) return rc;
     h.routed_scaling = rs;
     // shared_ff from the tensor, as the segment reads it (ne[1] of moe_shared_gate)
     h.shared_ff = 0;
-    const uint32_t fk = u32_or(g, "first_k_dense_replace", 0);
+    uint32_t fk = 0;
+    if ((rc = u32_or(g, "first_k_dense_replace", 0, &fk))) return rc;
     if (h.n_shared > 0) {
         for (uint32_t il = fk; il < nl; il++) {
             dmoe_tensor t;
@@ -439,7 +457,9 @@ int dmoe_gguf_layer_desc(const dmoe_gguf *g, int32_t il, dmoe_layer_desc *desc)
     if ((rc = tensor_view(g, layer_name("blk.%d.moe_experts_up.weight", il), &d.exp_up))) return rc;
     if ((rc = tensor_view(g, layer_name("blk.%d.moe_experts_down.weight", il), &d.exp_down))) return rc;
     // :192-196, present when the model has a shared expert
-    if (u32_or(g, "expert_shared_count", 0) > 0) {
+    uint32_t ns = 0;
+    if ((rc = u32_or(g, "expert_shared_count", 0, &ns))) return rc;
+    if (ns > 0) {
         if ((rc = tensor_view(g, layer_name("blk.%d.moe_shared_gate.weight", il), &d.sh_gate))) return rc;
         if ((rc = tensor_view(g, layer_name("blk.%d.moe_shared_up.weight", il), &d.sh_up))) return rc;
         if ((rc = tensor_view(g, layer_name("blk.%d.moe_shared_down.weight", il), &d.sh_down))) return rc;
@@ -476,10 +496,16 @@ int dmoe_gguf_attn_hparams(const dmoe_gguf *g, dmoe_attn_hparams *ap)
     a.n_head_kv = (int32_t)v;
     if (a.n_head <= 0) return DMOE_ERR_FORMAT;
     // defaults as the reference's loader (:90-93, :148-150)
-    a.head_dim = (int32_t)u32_or(g, "head_dim", (uint32_t)(a.n_embd / a.n_head));
-    a.rotary_dim = (int32_t)u32_or(g, "rotary_dim", (uint32_t)a.head_dim);
-    a.use_qk_norm = u32_or(g, "use_qk_norm", 0) != 0;
-    a.block_length = (int32_t)u32_or(g, "block_length", 0);
+    uint32_t hd = 0, rd = 0, qkn = 0, bl = 0;
+    if ((rc = u32_or(g, "head_dim", (uint32_t)(a.n_embd / a.n_head), &hd)) ||
+        (rc = u32_or(g, "rotary_dim", hd, &rd)) || (rc = u32_or(g, "use_qk_norm", 0, &qkn)) ||
+        (rc = u32_or(g, "block_length", 0, &bl)))
+        return rc;
+    if (hd > INT32_MAX || rd > INT32_MAX || bl > INT32_MAX) return DMOE_ERR_FORMAT;
+    a.head_dim = (int32_t)hd;
+    a.rotary_dim = (int32_t)rd;
+    a.use_qk_norm = qkn != 0;
+    a.block_length = (int32_t)bl;
     a.rope_base = 1000000.0f;
     if ((rc = find_f32(g, "rope.freq_base", &a.rope_base)) && rc != DMOE_ERR_NOT_FOUND) return rc;
     a.rms_eps = 1e-6f;

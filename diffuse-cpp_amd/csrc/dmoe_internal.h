@@ -112,6 +112,17 @@ struct MoeJob {
     float *ye, *ys;          // down results [N*K][H], [N][H]
 };
 
+// Alternative kernels kept selectable for measurement, read from the
+// environment by dmoe_create into its context (never in a forward):
+//   DMOE_Q4K_COLUMN_BLOCKS = 1, 2, 4  column blocks of the Q4_K items (0: by tokens per expert)
+//   DMOE_DOWN_FUSED = 1               few-token Q4_K down products as the single fused launch
+//   DMOE_GATEUP_LDS = 1               the LDS-ring gate/up kernel instead of the register ring
+struct KernelSwitches {
+    int q4k_column_blocks = 0;
+    bool down_fused = false;
+    bool gateup_lds = false;
+};
+
 struct RouteParams {
     int32_t n_tokens, n_experts, top_k, capacity, block_size;
     int32_t use_block;      // block routing on (diffuse-moe-graph.cpp:215-216)
@@ -258,7 +269,7 @@ constexpr int EXPERT_CHUNK = 16;    // pairs of one expert per work item
 constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
 // nc: activation column blocks of 16 pairs per routed item (1, 2 or 4; the
 // work list's chunk is 16 nc): each weight tile read serves 16 nc pairs.
-hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc = 1);
+hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc = 1, bool gateup_lds = false);
 // Down products of the Q4_K experts and the weighted combine in one launch
 // for few tokens (k_down_rows.hip): one workgroup per 16 output rows, every
 // touched expert's 16-row tile, results folded in slot order in LDS.

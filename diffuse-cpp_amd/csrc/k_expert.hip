@@ -731,7 +731,7 @@ static hipError_t launch_phase(int nc, const MoeJob &job, dim3 grid, hipStream_t
     return hipGetLastError();
 }
 
-hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc)
+hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc, bool gateup_lds)
 {
     if (job.FF % GROWS_GU || job.FF % 256 || job.H % GROWS_DN || job.H % 256 ||
         job.ax.K != job.H || job.ah.K != job.FF ||
@@ -741,10 +741,9 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc
     if ((nc != 1 && nc != 2 && nc != 4) || (job.wl.n_ec && job.wl.chunk != EXPERT_CHUNK * nc))
         return hipErrorInvalidValue;
     if (phase == 0) {
-        // one column block: the register-ring kernel unless DMOE_GATEUP_LDS=1
-        // selects the LDS-ring one (the same bits)
-        const char *ov = getenv("DMOE_GATEUP_LDS");
-        if (nc == 1 && job.H / 256 <= GR_MAX_SB && !(ov && atoi(ov) == 1)) {
+        // one column block: the register-ring kernel unless the LDS-ring one
+        // is selected (gateup_lds; the same bits)
+        if (nc == 1 && job.H / 256 <= GR_MAX_SB && !gateup_lds) {
             if (job.E > 0 && job.E <= GR_TAB_E && job.n_tokens * job.top_k <= GR_TAB_P)
                 hipLaunchKernelGGL(k_gateup_rr<true>, dim3(DMOE_X_BLOCKS), dim3(WAVES * 64), 0, s, job);
             else

@@ -422,7 +422,10 @@ class Context:
         lw = LayerWeights(n_embd=w.n_embd, n_experts=0, top_k=0, capacity=0, block_size=0,
                           moe_ff=w.n_ff, wtype=w.wtype, gate_w=None, exp_gate=None, exp_up=None,
                           exp_down=None)
-        return Layer(self, out.value, lw)
+        layer = Layer(self, out.value, lw)
+        # in device mode the library keeps pointers into w's tensors
+        layer.src = w
+        return layer
 
     def dense_upload(self, w: DenseWeights) -> Layer:
         """Copy a dense MLP (host arrays) into HBM (dmoe_dense_upload)."""
@@ -441,6 +444,9 @@ class Context:
                           exp_down=None)
         layer = Layer(self, out.value, lw)
         layer.n_vocab = w.n_vocab
+        # in device mode the library keeps pointers into w's tensors (the
+        # output norm, untiled weight types)
+        layer.src = w
         return layer
 
     def head_upload(self, w: "HeadWeights") -> Layer:

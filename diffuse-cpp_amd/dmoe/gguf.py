@@ -5,8 +5,12 @@
     w = g.layer_weights(il)           # LayerWeights of numpy views onto the file
     layer = ctx.upload(w)             # dmoe_layer_upload straight from the mapping
 
-The tensors stay memory-mapped (read-only) until close(); the arrays
-layer_weights / dense_weights return are views of that mapping.
+The tensors are memory-mapped read-only.  The arrays layer_weights,
+dense_weights and attn_weights return are views of that mapping, and each
+view keeps the mapping alive: close() (or dropping the GGUF object) releases
+the file once no view of it remains.  Every view is sized from its tensor's
+own ne (bounds-checked against the file by the C reader) and must agree with
+the hyper-parameters, or DmoeError(DMOE_ERR_SHAPE) is raised.
 """
 from __future__ import annotations
 
@@ -42,12 +46,51 @@ def _bind(lib):
     return lib
 
 
-def _bytes_view(t: Tensor, rows: int) -> np.ndarray:
-    """u8 [rows, row bytes] view of a tensor in the mapping."""
+class _Mapping:
+    """Owner of one dmoe_gguf handle: the file stays mapped while this object
+    lives, and the views hold a reference to it."""
+
+    def __init__(self, lib, handle):
+        self.lib, self.handle = lib, handle
+
+    def __del__(self):
+        h, self.handle = self.handle, None
+        if h:
+            self.lib.dmoe_gguf_close(h)
+
+
+def _ne(t: Tensor, nd: int):
+    return tuple(int(t.ne[i]) for i in range(nd))
+
+
+def _expect(name: str, t: Tensor, ne: tuple):
+    """Refuse a tensor whose own ne disagrees with what the hyper-parameters
+    say it holds (the view would otherwise reach past the tensor)."""
+    got = _ne(t, 4)
+    want = tuple(ne) + (1,) * (4 - len(ne))
+    if got != want:
+        raise DmoeError(3, "%s: ne %s in the file, %s expected from the hyper-parameters" % (name, list(got), list(want)))
+
+
+def _view(owner: _Mapping, t: Tensor, nbytes: int) -> np.ndarray:
+    """u8 view of nbytes at the tensor's data, keeping the mapping alive."""
+    buf = (C.c_uint8 * nbytes).from_address(t.data)
+    buf._owner = owner          # np.frombuffer keeps buf, buf keeps the mapping
+    return np.frombuffer(buf, dtype=np.uint8)
+
+
+def _bytes_view(owner: _Mapping, t: Tensor) -> np.ndarray:
+    """u8 [rows, row bytes] view of a tensor, rows = ne1 ne2 ne3 of its own ne."""
     rb = row_size(t.type, t.ne[0])
-    n = rb * rows
-    buf = (C.c_uint8 * n).from_address(t.data)
-    return np.frombuffer(buf, dtype=np.uint8).reshape(rows, rb)
+    rows = int(t.ne[1]) * int(t.ne[2]) * int(t.ne[3])
+    return _view(owner, t, rb * rows).reshape(rows, rb)
+
+
+def _f32_view(owner: _Mapping, t: Tensor, what: str) -> np.ndarray:
+    if t.type != 0:
+        raise DmoeError(2, "%s of type %d (F32 expected here)" % (what, t.type))
+    n = int(t.ne[0]) * int(t.ne[1]) * int(t.ne[2]) * int(t.ne[3])
+    return _view(owner, t, 4 * n).view(np.float32)
 
 
 class GGUF:
@@ -58,24 +101,25 @@ class GGUF:
         rc = self.lib.dmoe_gguf_open(str(path).encode(), C.byref(h), err, len(err))
         if rc:
             raise DmoeError(rc, err.value.decode())
-        self.handle = h.value
+        self._map = _Mapping(self.lib, h.value)
+
+    @property
+    def handle(self):
+        m = getattr(self, "_map", None)
+        if m is None:
+            raise DmoeError(1, "GGUF file already closed")
+        return m.handle
 
     def close(self):
-        if getattr(self, "handle", None):
-            self.lib.dmoe_gguf_close(self.handle)
-            self.handle = None
+        """Drop this object's hold on the mapping; views made earlier keep it
+        mapped until they are gone."""
+        self._map = None
 
     def __enter__(self):
         return self
 
     def __exit__(self, *exc):
         self.close()
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
 
     def _check(self, rc, what):
         if rc:
@@ -117,25 +161,31 @@ class GGUF:
         hp, _, _ = self.moe_hparams()
         d = self.layer_desc(il)
         H, E, FF = hp.n_embd, hp.n_experts, hp.moe_ff
-        gw = d.gate_w
-        if gw.type != 0:
-            raise DmoeError(2, "router weight of type %d (F32 expected here)" % gw.type)
-        gate_w = np.frombuffer((C.c_uint8 * (4 * H * E)).from_address(gw.data), np.float32).reshape(E, H)
+        m = self._map
+        _expect("moe_gate", d.gate_w, (H, E))
+        gate_w = _f32_view(m, d.gate_w, "router weight").reshape(E, H)
         bias = None
         if d.gate_bias.data:
-            bias = np.frombuffer((C.c_uint8 * (4 * E)).from_address(d.gate_bias.data), np.float32)
+            _expect("moe_gate_bias", d.gate_bias, (E,))
+            bias = _f32_view(m, d.gate_bias, "router bias")
+        _expect("moe_experts_gate", d.exp_gate, (H, FF, E))
+        _expect("moe_experts_up", d.exp_up, (H, FF, E))
+        _expect("moe_experts_down", d.exp_down, (FF, H, E))
         w = LayerWeights(n_embd=H, n_experts=E, top_k=hp.top_k, capacity=hp.capacity,
                          block_size=hp.block_size, moe_ff=FF, wtype=d.exp_gate.type, gate_w=gate_w,
-                         exp_gate=_bytes_view(d.exp_gate, E * FF).reshape(E, FF, -1),
-                         exp_up=_bytes_view(d.exp_up, E * FF).reshape(E, FF, -1),
-                         exp_down=_bytes_view(d.exp_down, E * H).reshape(E, H, -1), gate_bias=bias,
+                         exp_gate=_bytes_view(m, d.exp_gate).reshape(E, FF, -1),
+                         exp_up=_bytes_view(m, d.exp_up).reshape(E, FF, -1),
+                         exp_down=_bytes_view(m, d.exp_down).reshape(E, H, -1), gate_bias=bias,
                          norm_topk_prob=hp.norm_topk_prob, routed_scaling=hp.routed_scaling)
         if d.sh_gate.data and hp.n_shared > 0:
             SF = hp.shared_ff
+            _expect("moe_shared_gate", d.sh_gate, (H, SF))
+            _expect("moe_shared_up", d.sh_up, (H, SF))
+            _expect("moe_shared_down", d.sh_down, (SF, H))
             w.n_shared, w.shared_ff, w.stype = 1, SF, d.sh_gate.type
-            w.sh_gate = _bytes_view(d.sh_gate, SF)
-            w.sh_up = _bytes_view(d.sh_up, SF)
-            w.sh_down = _bytes_view(d.sh_down, H)
+            w.sh_gate = _bytes_view(m, d.sh_gate)
+            w.sh_up = _bytes_view(m, d.sh_up)
+            w.sh_down = _bytes_view(m, d.sh_down)
         return w
 
     def dense_weights(self, il: int) -> DenseWeights:
@@ -144,8 +194,12 @@ class GGUF:
         self._check(self.lib.dmoe_gguf_dense_desc(self.handle, il, C.byref(g), C.byref(u), C.byref(dn),
                                                   C.byref(nff)), f"dense layer {il}")
         H, FF = int(g.ne[0]), nff.value
-        return DenseWeights(n_embd=H, n_ff=FF, wtype=g.type, gate=_bytes_view(g, FF),
-                            up=_bytes_view(u, FF), down=_bytes_view(dn, H))
+        _expect("ffn_gate", g, (H, FF))
+        _expect("ffn_up", u, (H, FF))
+        _expect("ffn_down", dn, (FF, H))
+        m = self._map
+        return DenseWeights(n_embd=H, n_ff=FF, wtype=g.type, gate=_bytes_view(m, g),
+                            up=_bytes_view(m, u), down=_bytes_view(m, dn))
 
     def attn_hparams(self) -> AttnHParams:
         a = AttnHParams()
@@ -162,16 +216,20 @@ class GGUF:
         """The attention tensors of layer il as an AttnWeights of views onto the file."""
         a = self.attn_hparams()
         d = self.attn_desc(il, bool(a.use_qk_norm))
-        QD, QKV = a.n_head * a.head_dim, (a.n_head + 2 * a.n_head_kv) * a.head_dim
-
-        def f32(t, n):
-            if t.type != 0:
-                raise DmoeError(2, "norm weight of type %d (F32 expected here)" % t.type)
-            return np.frombuffer((C.c_uint8 * (4 * n)).from_address(t.data), np.float32)
-        return AttnWeights(n_embd=a.n_embd, n_head=a.n_head, n_head_kv=a.n_head_kv, head_dim=a.head_dim,
+        H, HD = a.n_embd, a.head_dim
+        QD, QKV = a.n_head * HD, (a.n_head + 2 * a.n_head_kv) * HD
+        _expect("attn_norm", d.attn_norm, (H,))
+        _expect("attn_qkv", d.qkv, (H, QKV))
+        _expect("attn_output", d.wo, (QD, H))
+        _expect("post_attn_norm", d.post_attn_norm, (H,))
+        if a.use_qk_norm:
+            _expect("attn_q_norm", d.q_norm, (HD,))
+            _expect("attn_k_norm", d.k_norm, (HD,))
+        m = self._map
+        return AttnWeights(n_embd=H, n_head=a.n_head, n_head_kv=a.n_head_kv, head_dim=HD,
                            rotary_dim=a.rotary_dim, block_length=a.block_length, rope_base=a.rope_base,
-                           rms_eps=a.rms_eps, wtype=d.qkv.type, attn_norm=f32(d.attn_norm, a.n_embd),
-                           qkv=_bytes_view(d.qkv, QKV), wo=_bytes_view(d.wo, a.n_embd),
-                           post_norm=f32(d.post_attn_norm, a.n_embd),
-                           q_norm=f32(d.q_norm, a.head_dim) if a.use_qk_norm else None,
-                           k_norm=f32(d.k_norm, a.head_dim) if a.use_qk_norm else None)
+                           rms_eps=a.rms_eps, wtype=d.qkv.type, attn_norm=_f32_view(m, d.attn_norm, "norm weight"),
+                           qkv=_bytes_view(m, d.qkv), wo=_bytes_view(m, d.wo),
+                           post_norm=_f32_view(m, d.post_attn_norm, "norm weight"),
+                           q_norm=_f32_view(m, d.q_norm, "norm weight") if a.use_qk_norm else None,
+                           k_norm=_f32_view(m, d.k_norm, "norm weight") if a.use_qk_norm else None)

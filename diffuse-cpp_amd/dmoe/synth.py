@@ -93,9 +93,11 @@ CONFIGS = {
     # 8 independent 32-token blocks
     "flash_q4k_n256": LayerConfig("flash_q4k_n256", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
                                   TYPE_Q4_K, 256, -0.1, 0.1),
-    # the sampler's growing window (N = 32 (blk + 1)): 16, 32 and 64 blocks
+    # the sampler's growing window (N = 32 (blk + 1)): 16, 24, 32 and 64 blocks
     "flash_q4k_n512": LayerConfig("flash_q4k_n512", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
                                   TYPE_Q4_K, 512, -0.1, 0.1),
+    "flash_q4k_n768": LayerConfig("flash_q4k_n768", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
+                                  TYPE_Q4_K, 768, -0.1, 0.1),
     "flash_q4k_n1024": LayerConfig("flash_q4k_n1024", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,
                                    TYPE_Q4_K, 1024, -0.1, 0.1),
     "flash_q4k_n2048": LayerConfig("flash_q4k_n2048", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K,

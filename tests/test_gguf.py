@@ -12,7 +12,7 @@ import struct
 import numpy as np
 import pytest
 
-from gguf_writer import (ARR, F32, GGUFWriter, STR, U32, U8, add_attn_layer, add_dense_layer, add_moe_layer,
+from gguf_writer import (ARR, F32, GGUFWriter, I32, STR, U32, U8, add_attn_layer, add_dense_layer, add_moe_layer,
                          attn_keys, moe_keys)
 
 
@@ -244,3 +244,70 @@ def test_alignment_key_and_u8_values(tmp_path):
         t, u = g.tensor("t.weight"), g.tensor("u.weight")
         assert t.data % 64 == 0 and u.data - t.data == 64
         assert np.frombuffer(C.string_at(u.data, 8), np.float32).tolist() == [4.0, 5.0]
+
+
+def test_views_keep_the_mapping(tmp_path, O):
+    """The arrays layer_weights / dense_weights return stay readable after the
+    GGUF object is closed or dropped: each view holds the mapping."""
+    import gc
+    from dmoe.gguf import GGUF
+    p, w, d = _tiny_file(tmp_path, O)
+    lw = GGUF(p).layer_weights(1)            # the handle object is dropped at once
+    gc.collect()
+    assert np.array_equal(lw.exp_down.reshape(-1), np.asarray(w.exp_down).view(np.uint8).reshape(-1))
+    g = GGUF(p)
+    dw = g.dense_weights(0)
+    g.close()
+    del g
+    gc.collect()
+    assert np.array_equal(dw.down, d.down)
+    with GGUF(p) as g2:
+        gw = g2.layer_weights(1).gate_w
+    assert np.array_equal(gw, w.gate_w)
+    import dmoe
+    with pytest.raises(dmoe.DmoeError):
+        g2.layer_desc(1)                     # the object itself is closed
+
+
+def _mismatch_file(tmp_path, O, key, value, vtype=U32):
+    from dmoe import synth
+    cfg = synth.CONFIGS["tiny"]
+    w = synth.host_layer(cfg, 3, O.quantize_rows)
+    wr = GGUFWriter()
+    for k, t, v in moe_keys(w, n_layer=1):
+        if k == f"diffuse.{key}":
+            t, v = vtype, value
+        wr.add(k, t, v)
+    add_moe_layer(wr, 0, w)
+    p = tmp_path / f"mm_{key}.gguf"
+    wr.write(p)
+    return p
+
+
+@pytest.mark.parametrize("key,value", [("expert_count", 64), ("expert_feed_forward_length", 256),
+                                       ("embedding_length", 512)])
+def test_tensor_shape_against_hparams(tmp_path, O, key, value):
+    """Hyper-parameters that disagree with a tensor's own ne (64 experts in
+    the metadata, 16 in the tensors) are refused with DMOE_ERR_SHAPE instead
+    of a view sized from the metadata, which would reach past the tensor."""
+    import dmoe
+    from dmoe.gguf import GGUF
+    p = _mismatch_file(tmp_path, O, key, value)
+    with GGUF(p) as g:
+        with pytest.raises(dmoe.DmoeError) as ei:
+            g.layer_weights(0)
+        assert ei.value.code == dmoe._abi.ERR_SHAPE
+
+
+@pytest.mark.parametrize("vtype,value", [(F32, 16.0), (I32, -4), (STR, "16")])
+def test_optional_key_of_wrong_type(tmp_path, O, vtype, value):
+    """An optional key that is present but not a non-negative integer (an f32
+    expert_count, a negative one, a string) is DMOE_ERR_FORMAT, as a type
+    mismatch is for gguf_get_val_u32, not the default."""
+    import dmoe
+    from dmoe.gguf import GGUF
+    p = _mismatch_file(tmp_path, O, "expert_count", value, vtype)
+    with GGUF(p) as g:
+        with pytest.raises(dmoe.DmoeError) as ei:
+            g.moe_hparams()
+        assert ei.value.code == dmoe._abi.ERR_FORMAT

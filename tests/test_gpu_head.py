@@ -136,3 +136,80 @@ def test_head_errors(ctx, O):
     out = C.c_void_p()
     rc = dmoe.load().dmoe_head_upload(ctx.handle, 512, 1024, C.byref(nv), C.byref(ov), C.byref(out))
     assert rc == dmoe._abi.ERR_SHAPE and not out.value
+
+
+def _tie_head(H, V, wtype, quantize_rows, h, g, plan, nan_rows=()):
+    """An output matrix whose rows listed in plan[t] are all equal and point
+    along position t's normalised hidden state (so they hold that position's
+    largest logit, bit-equal across the copies: equal weight rows give equal
+    logits on every kernel path); the other rows N(0, 0.02).  nan_rows are
+    set to NaN (F32 only)."""
+    from dmoe import HeadWeights, row_size, synth
+    f = synth.normal(404, synth.S_OUT, V * H, 0.02).reshape(V, H).astype(np.float32)
+    hn = h / np.sqrt((h.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    u = hn * g
+    for t, rows in enumerate(plan):
+        d = (0.5 * u[t] / np.linalg.norm(u[t])).astype(np.float32)
+        for r in rows:
+            f[r] = d
+    for r in nan_rows:
+        f[r] = np.nan
+    out = np.ascontiguousarray(quantize_rows(wtype, f)).view(np.uint8).reshape(V, row_size(wtype, H))
+    return HeadWeights(n_embd=H, n_vocab=V, wtype=wtype, norm=g, output=out)
+
+
+@pytest.mark.parametrize("wtype", [12, 0], ids=["Q4_K", "F32"])
+def test_head_argmax_ties(ctx, O, wtype):
+    """The sampler's argmax rule on the GPU (src/diffuse-sampler.cpp:33-40:
+    the first index of the largest logit): equal largest logits inside one
+    4096-logit chunk (one thread's two values, two threads), in chunks far
+    apart, across a chunk boundary, three copies over three chunks, and a
+    largest logit at the very last index; the token is the lower index every
+    time, as the oracle's."""
+    from dmoe import synth
+    H, V = 512, 16384
+    plan = [(100, 200), (4000, 9000), (V - 1,), (4095, 4096), (5, V - 2), (8191, 8192, 12000),
+            (12295, 12588), (259, 3)]
+    expect = np.array([min(r) for r in plan], np.int32)
+    N = len(plan)
+    _say(f"case: argmax ties, type={wtype}, V={V}, N={N}")
+    h = (synth.normal(405, synth.S_X, N * H).reshape(N, H) * 2).astype(np.float32)
+    g = synth.uniform(405, synth.S_ONORM, H, 0.5, 1.5)
+    w = _tie_head(H, V, wtype, O.quantize_rows, h, g, plan)
+    head = ctx.head_upload(w)
+    tok, prob, lg = ctx.head_forward(head, h, 1e-6, logits=True)
+    tr, pr, lr = O.head_forward(w, h, 1e-6)
+    for t, rows in enumerate(plan):
+        vals = lg[t, list(rows)].view(np.uint32)
+        assert np.all(vals == vals[0]), (t, rows)            # the copies' logits are bit-equal
+        assert lg[t, rows[0]] == lg[t].max()
+    assert np.array_equal(tr, expect)
+    assert np.array_equal(tok, expect), (tok, expect)
+    assert np.all(np.abs(prob - pr) <= 1e-3 * np.abs(pr))
+    head.free()
+
+
+def test_head_argmax_nan(ctx, O):
+    """NaN logits on the GPU as the sampler's loop treats them
+    (src/diffuse-sampler.cpp:34-40): a NaN never becomes the maximum, so a
+    NaN at index 0 keeps index 0 for the row, and one later in the row leaves
+    the argmax where it was; the confidence is NaN either way (its sum has a
+    NaN term).  F32 weights with a NaN row give a NaN logit at that index in
+    every row."""
+    from dmoe import synth
+    H, V = 512, 16384
+    plan = [(100, 200), (4000, 9000), (V - 1,), (4095, 4096)]
+    N = len(plan)
+    h = (synth.normal(406, synth.S_X, N * H).reshape(N, H) * 2).astype(np.float32)
+    g = synth.uniform(406, synth.S_ONORM, H, 0.5, 1.5)
+    for nan_row, expect in ((0, np.zeros(N, np.int32)), (4097, np.array([100, 4000, V - 1, 4095], np.int32))):
+        _say(f"case: argmax with NaN logits at index {nan_row}")
+        w = _tie_head(H, V, 0, O.quantize_rows, h, g, plan, nan_rows=(nan_row,))
+        head = ctx.head_upload(w)
+        tok, prob, lg = ctx.head_forward(head, h, 1e-6, logits=True)
+        tr, pr, _ = O.head_forward(w, h, 1e-6)
+        assert np.isnan(lg[:, nan_row]).all()
+        assert np.array_equal(tr, expect)
+        assert np.array_equal(tok, expect), (tok, expect)
+        assert np.isnan(pr).all() and np.isnan(prob).all()
+        head.free()

@@ -37,6 +37,18 @@ def _check_routing(dg, dr, keys=ROUTE_KEYS):
             assert a == b, k
 
 
+def _ctx_with(monkeypatch, env):
+    """A context created with the kernel-selection variables in env set (a
+    context reads them once, at creation); they are cleared again after."""
+    import dmoe
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    c = dmoe.Context(0)
+    for k in env:
+        monkeypatch.delenv(k)
+    return c
+
+
 def _small(dmoe, synth, wtype, n_tokens=64, seed=3):
     return synth.LayerConfig(f"small_{wtype}", 512, 32, 256, 8, 4, 32, 256, wtype, wtype,
                              n_tokens, -0.05, 0.05)
@@ -98,13 +110,15 @@ def test_small_layer_many_items(ctx, O, wtype):
     assert err <= TOL[wtype]
 
 
-@pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "flash_q4k_n1024",
-                                  "flash_q4k_n2048", "prefill_f16"])
+@pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "flash_q4k_n512",
+                                  "flash_q4k_n768", "flash_q4k_n1024", "flash_q4k_n2048", "prefill_f16"])
 def test_flash_layer(ctx, O, name):
     """Flash-shaped layers: one 32-token block (Q4_K, Q8_0), eight blocks
-    (Q4_K, 256 tokens, each block its own allowed set), the sampler's 1024-
-    and 2048-token windows (Q4_K items of 2 and 4 column blocks) and the
-    2048-token F16 prefill."""
+    (Q4_K, 256 tokens, each block its own allowed set), the sampler's 512-
+    and 768-token windows (one column block with more pairs than the
+    register-ring kernel's LDS routing tables hold), its 1024- and 2048-token
+    windows (Q4_K items of 2 and 4 column blocks) and the 2048-token F16
+    prefill."""
     import torch
     import dmoe
     from dmoe import synth
@@ -144,9 +158,9 @@ def test_q4k_column_blocks_bit_exact(ctx, name, monkeypatch):
     x = synth.make_x(cfg, 23, cfg.n_tokens)
     ys = []
     for nc in ("1", "2", "4"):
-        monkeypatch.setenv("DMOE_Q4K_COLUMN_BLOCKS", nc)
-        ys.append(ctx.forward(layer, x))
-    monkeypatch.delenv("DMOE_Q4K_COLUMN_BLOCKS")
+        c = _ctx_with(monkeypatch, {"DMOE_Q4K_COLUMN_BLOCKS": nc})
+        ys.append(c.forward(layer, x))
+        c.close()
     ys.append(ctx.forward(layer, x))                      # the automatic choice
     for y in ys[1:]:
         assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32))
@@ -171,20 +185,23 @@ def test_down_span_bit_exact(ctx, name, monkeypatch):
     x = synth.make_x(cfg, 27, cfg.n_tokens)
     xo = synth.make_x(cfg, 28, cfg.n_tokens)
     n2 = cfg.n_tokens // 2 + 3
-    monkeypatch.setenv("DMOE_DOWN_FUSED", "1")
-    ref = [ctx.forward(layer, a) for a in (x, xo, x[:n2], xo[:n2])]
-    monkeypatch.delenv("DMOE_DOWN_FUSED")
+    c = _ctx_with(monkeypatch, {"DMOE_DOWN_FUSED": "1"})
+    ref = [c.forward(layer, a) for a in (x, xo, x[:n2], xo[:n2])]
+    c.close()
     got = [ctx.forward(layer, a) for a in (xo, x, xo[:n2], x[:n2])]
     for r, g in zip(ref, (got[1], got[0], got[3], got[2])):
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32))
 
 
-@pytest.mark.parametrize("name", ["flash_q4k", "flash_q4k_n256", "small_q4k_n40", "small_q4k_n128"])
+@pytest.mark.parametrize("name", ["flash_q4k", "flash_q4k_n256", "flash_q4k_n512", "flash_q4k_n768",
+                                  "small_q4k_n40", "small_q4k_n128"])
 def test_gateup_register_ring_bit_exact(ctx, name, monkeypatch):
     """Q4_K gate/up items of one column block with the weights streamed to
     registers and the item's activations in LDS, against the kernel with LDS
     rings for both: the same products in the same order, so the layer
-    outputs are identical bit for bit."""
+    outputs are identical bit for bit.  At 512 and 768 tokens the
+    register-ring kernel looks its routing up in HBM (more pairs than its
+    LDS tables hold)."""
     import dmoe
     from dmoe import synth
     if name.startswith("small"):
@@ -196,9 +213,9 @@ def test_gateup_register_ring_bit_exact(ctx, name, monkeypatch):
     layer = ctx.wrap_device(wd)
     x = synth.make_x(cfg, 29, cfg.n_tokens)
     xo = synth.make_x(cfg, 30, cfg.n_tokens)
-    monkeypatch.setenv("DMOE_GATEUP_LDS", "1")
-    ref = [ctx.forward(layer, a) for a in (x, xo)]
-    monkeypatch.delenv("DMOE_GATEUP_LDS")
+    c = _ctx_with(monkeypatch, {"DMOE_GATEUP_LDS": "1"})
+    ref = [c.forward(layer, a) for a in (x, xo)]
+    c.close()
     got = [ctx.forward(layer, a) for a in (xo, x)]
     assert np.array_equal(got[1].view(np.uint32), ref[0].view(np.uint32))
     assert np.array_equal(got[0].view(np.uint32), ref[1].view(np.uint32))
