@@ -117,7 +117,8 @@ int set_err(dmoe_ctx *ctx, int code, const char *fmt, ...)
 
 bool type_supported(int32_t t)
 {
-    return t == DMOE_TYPE_F32 || t == DMOE_TYPE_F16 || t == DMOE_TYPE_Q8_0 || t == DMOE_TYPE_Q4_K;
+    return t == DMOE_TYPE_F32 || t == DMOE_TYPE_F16 || t == DMOE_TYPE_Q8_0 || t == DMOE_TYPE_Q4_K ||
+           t == DMOE_TYPE_Q6_K;
 }
 
 // elements per block of the weight type (ggml_blck_size)
@@ -125,6 +126,7 @@ int64_t block_elems(int32_t t)
 {
     switch (t) {
     case DMOE_TYPE_Q4_K: return 256;
+    case DMOE_TYPE_Q6_K: return 256;
     case DMOE_TYPE_Q8_0: return 32;
     case DMOE_TYPE_F16: return 8;      // the kernels read 16-byte units
     case DMOE_TYPE_F32: return 4;
@@ -139,6 +141,7 @@ size_t row_bytes(int32_t t, int64_t n)
     case DMOE_TYPE_F16: return (size_t)n * 2;
     case DMOE_TYPE_Q8_0: return (n % 32) ? 0 : (size_t)(n / 32) * Q8_0_BYTES;
     case DMOE_TYPE_Q4_K: return (n % 256) ? 0 : (size_t)(n / 256) * Q4K_BYTES;
+    case DMOE_TYPE_Q6_K: return (n % 256) ? 0 : (size_t)(n / 256) * Q6K_BYTES;
     default: return 0;
     }
 }
@@ -146,7 +149,7 @@ size_t row_bytes(int32_t t, int64_t n)
 // activation type of the routed products (ggml vec_dot_type)
 int32_t act_type_of(int32_t wt)
 {
-    return wt == DMOE_TYPE_Q4_K ? DMOE_ACT_Q8_K : wt;
+    return wt == DMOE_TYPE_Q4_K || wt == DMOE_TYPE_Q6_K ? DMOE_ACT_Q8_K : wt;
 }
 
 size_t act_row_vals_bytes(int32_t at, int64_t n)
@@ -179,8 +182,9 @@ int check_tensor(dmoe_ctx *ctx, const char *name, const dmoe_tensor &t, int64_t 
     if (ne2 > 0 && t.nb[2] < t.nb[1] * (size_t)ne1)
         return set_err(ctx, DMOE_ERR_SHAPE, "%s: nb[2] below nb[1]*ne[1]", name);
     if (device_mode) {
-        // the kernels load 16-byte units (2-byte for Q8_0 blocks)
-        const size_t al = t.type == DMOE_TYPE_Q8_0 ? 2 : 16;
+        // the kernels load 16-byte units (2-byte for Q8_0 and Q6_K blocks,
+        // 34 and 210 bytes long)
+        const size_t al = t.type == DMOE_TYPE_Q8_0 || t.type == DMOE_TYPE_Q6_K ? 2 : 16;
         if ((uintptr_t)t.data % al || t.nb[1] % al || (ne2 > 0 && t.nb[2] % al))
             return set_err(ctx, DMOE_ERR_SHAPE, "%s: device data/strides not %zu-byte aligned",
                            name, al);
@@ -772,6 +776,27 @@ int tile_tensor(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int m
     return DMOE_OK;
 }
 
+// Q6_K [mats][rows][K] -> the tiled layout of the Q6_K projections
+// (k_tile_q6k), in a library-owned copy (a library-owned original is freed).
+int tile_tensor_q6k(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int mats)
+{
+    const size_t bytes = (size_t)rows * (K / 256) * Q6K_BYTES * mats;
+    void *dev = nullptr;
+    HIP_TRY(ctx, hipMalloc(&dev, bytes));
+    L->owned.push_back(dev);
+    HIP_TRY(ctx, launch_tile_q6k(t.data, t.nb1, t.nb2, rows, K, mats, (uint8_t *)dev, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    auto it = std::find(L->owned.begin(), L->owned.end(), (void *)t.data);
+    if (it != L->owned.end()) {
+        HIP_TRY(ctx, hipFree(*it));
+        L->owned.erase(it);
+    }
+    t.data = (const uint8_t *)dev;
+    t.nb1 = (size_t)(K / 256) * Q6K_BYTES;
+    t.nb2 = (size_t)rows * (K / 256) * Q6K_BYTES;
+    return DMOE_OK;
+}
+
 // Q8_0 [mats][rows][K] -> the tiled layout of k_expert_q80.hip, in a
 // library-owned copy (a library-owned original is freed).
 int tile_tensor_q80(dmoe_ctx *ctx, dmoe_layer *L, WTensor &t, int rows, int K, int mats)
@@ -871,7 +896,7 @@ int finish_layer(dmoe_ctx *ctx, dmoe_layer *L, const dmoe_hparams *hp, const dmo
 // ---------------------------------------------------------------------------
 // Dense MLP (src/diffuse-moe-graph.cpp:181-187): the shared expert's kernels
 // with an empty routed work list; the down launch writes y directly.
-enum DensePath { DP_GEMV = 0, DP_Q4K, DP_Q80, DP_F16 };
+enum DensePath { DP_GEMV = 0, DP_Q4K, DP_Q80, DP_F16, DP_Q6K };
 
 int dense_path(int32_t type, int H, int FF)
 {
@@ -881,6 +906,7 @@ int dense_path(int32_t type, int H, int FF)
         if (type == DMOE_TYPE_Q8_0 && FF % expert_q80_rows_per_item(0) == 0 &&
             H % expert_q80_rows_per_item(1) == 0)
             return DP_Q80;
+        if (type == DMOE_TYPE_Q6_K) return DP_Q6K;
     }
     if (type == DMOE_TYPE_F16 && gemm_shapes_ok(H, FF, FF, true)) return DP_F16;
     return DP_GEMV;
@@ -929,6 +955,10 @@ int dense_finish(dmoe_ctx *ctx, dmoe_layer *L)
         if ((rc = tile_tensor_f16(ctx, L, L->sg, FF, H, 1))) return rc;
         if ((rc = tile_tensor_f16(ctx, L, L->su, FF, H, 1))) return rc;
         return tile_tensor_f16(ctx, L, L->sd, H, FF, 1);
+    case DP_Q6K:
+        if ((rc = tile_tensor_q6k(ctx, L, L->sg, FF, H, 1))) return rc;
+        if ((rc = tile_tensor_q6k(ctx, L, L->su, FF, H, 1))) return rc;
+        return tile_tensor_q6k(ctx, L, L->sd, H, FF, 1);
     default:
         return DMOE_OK;
     }
@@ -943,11 +973,29 @@ struct DenseWs {
     float *part_gu, *part_d;             // slice sums of the few-token Q4_K projections
 };
 
-// Few tokens of a Q4_K dense MLP: gate and up as one two-matrix projection,
-// h formed and converted from their slice sums, down as a projection.
+// Few tokens of a Q4_K or Q6_K dense MLP: gate and up as one two-matrix
+// projection, h formed and converted from their slice sums, down as a
+// projection.  Q6_K weights take every token count this way, in chunks of up
+// to PROJ_MAX_TOKENS tokens (dense_chunk).
 bool dense_few(int path, int H, int FF, int N)
 {
-    return path == DP_Q4K && proj_ok(FF, H, N) && proj_ok(H, FF, N) && FF % 256 == 0;
+    return (path == DP_Q4K || path == DP_Q6K) && proj_ok(FF, H, N) && proj_ok(H, FF, N) && FF % 256 == 0;
+}
+
+int dense_chunk(int path, int N) { return path == DP_Q6K ? std::min(N, PROJ_MAX_TOKENS) : N; }
+
+// Slice-sum floats the few-token projection of R x K (M matrices) needs at
+// any token count 1 .. nmax (a smaller last chunk may split its reduction
+// into more slices than a full one); with split_only, counting only launches
+// whose reduction is split (KS > 1), 0 when none is.
+size_t proj_partial_max(int R, int K, int M, int nmax, bool split_only)
+{
+    size_t best = 0;
+    for (int n = 1; n <= nmax; n++) {
+        if (split_only && proj_plan(R, K, M, n).KS <= 1) continue;
+        best = std::max(best, proj_partial_floats(R, K, M, n));
+    }
+    return best;
 }
 
 size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, DenseWs *w)
@@ -965,15 +1013,20 @@ size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, Dense
         t.y = (float *)take((size_t)N * H * 4);
     }
     t.n_ec = (int32_t *)take(4);
-    switch (dense_path(L->sg.type, H, FF)) {
+    const int path = dense_path(L->sg.type, H, FF);
+    switch (path) {
     case DP_Q4K:
-        t.axs = take_act(take, N, H, true);
-        t.ahs = take_act(take, N, FF, true);
-        if (dense_few(DP_Q4K, H, FF, N)) {
-            t.part_gu = (float *)take(proj_partial_floats(FF, H, 2, N) * 4);
-            if (proj_plan(H, FF, 1, N).KS > 1) t.part_d = (float *)take(proj_partial_floats(H, FF, 1, N) * 4);
+    case DP_Q6K: {
+        // Q6_K: workspace for one chunk of tokens, reused chunk after chunk
+        const int n = dense_chunk(path, N);
+        t.axs = take_act(take, n, H, true);
+        t.ahs = take_act(take, n, FF, true);
+        if (dense_few(path, H, FF, n)) {
+            t.part_gu = (float *)take(proj_partial_max(FF, H, 2, n, false) * 4);
+            if (const size_t pd = proj_partial_max(H, FF, 1, n, true)) t.part_d = (float *)take(pd * 4);
         }
         break;
+    }
     case DP_Q80:
         t.axs = take_act(take, N, H, true, true);
         t.ahs = take_act(take, N, FF, true, true);
@@ -1020,36 +1073,42 @@ int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const fl
         STAGE(ST_SH_DOWN, launch_down_shared(L->sd, w.hs, N, FF, H, y, s));
         return DMOE_OK;
     }
-    if (dense_few(path, H, FF, N)) {
-        // gate and up: one launch over both matrices, h from their slices
-        ProjJob gu{};
-        gu.w[0] = L->sg.data;
-        gu.w[1] = L->su.data;
-        gu.M = 2;
-        gu.R = FF;
-        gu.K = H;
-        gu.N = N;
-        gu.KS = proj_plan(FF, H, 2, N).KS;
-        gu.x = w.axs;
-        gu.partial = 1;
-        gu.out = w.part_gu;
-        ProjJob dn{};
-        dn.w[0] = L->sd.data;
-        dn.M = 1;
-        dn.R = H;
-        dn.K = FF;
-        dn.N = N;
-        dn.KS = proj_plan(H, FF, 1, N).KS;
-        dn.x = w.ahs;
-        dn.partial = dn.KS > 1;
-        dn.out = dn.partial ? w.part_d : y;
-        dn.ldo = H;
-        PrepJob pj{x, N, H, ACT_SPLIT, w.axs};
-        STAGE(ST_ACTQ_X, launch_prep(&pj, 1, s));
-        STAGE(ST_SH_GATEUP, launch_proj_q4k(gu, s));
-        STAGE(ST_ACTQ_H, launch_proj_swiglu(w.part_gu, gu.KS, N, FF, w.ahs, s));
-        STAGE(ST_SH_DOWN, launch_proj_q4k(dn, s));
-        if (dn.partial) STAGE(ST_COMBINE, launch_proj_reduce(w.part_d, dn.KS, N, H, y, H, s));
+    if (dense_few(path, H, FF, dense_chunk(path, N))) {
+        // gate and up: one launch over both matrices, h from their slices;
+        // tokens t0 .. t0 + n - 1 at a time (every token at once for Q4_K)
+        const bool q6 = path == DP_Q6K;
+        const int nc = dense_chunk(path, N);
+        for (int t0 = 0; t0 < N; t0 += nc) {
+            const int n = std::min(nc, N - t0);
+            ProjJob gu{};
+            gu.w[0] = L->sg.data;
+            gu.w[1] = L->su.data;
+            gu.M = 2;
+            gu.R = FF;
+            gu.K = H;
+            gu.N = n;
+            gu.KS = proj_plan(FF, H, 2, n).KS;
+            gu.x = w.axs;
+            gu.partial = 1;
+            gu.out = w.part_gu;
+            ProjJob dn{};
+            dn.w[0] = L->sd.data;
+            dn.M = 1;
+            dn.R = H;
+            dn.K = FF;
+            dn.N = n;
+            dn.KS = proj_plan(H, FF, 1, n).KS;
+            dn.x = w.ahs;
+            dn.partial = dn.KS > 1;
+            dn.out = dn.partial ? w.part_d : y + (size_t)t0 * H;
+            dn.ldo = H;
+            PrepJob pj{x + (size_t)t0 * H, n, H, ACT_SPLIT, w.axs};
+            STAGE(ST_ACTQ_X, launch_prep(&pj, 1, s));
+            STAGE(ST_SH_GATEUP, q6 ? launch_proj_q6k(gu, s) : launch_proj_q4k(gu, s));
+            STAGE(ST_ACTQ_H, launch_proj_swiglu(w.part_gu, gu.KS, n, FF, w.ahs, s));
+            STAGE(ST_SH_DOWN, q6 ? launch_proj_q6k(dn, s) : launch_proj_q4k(dn, s));
+            if (dn.partial) STAGE(ST_COMBINE, launch_proj_reduce(w.part_d, dn.KS, n, H, y + (size_t)t0 * H, H, s));
+        }
         return DMOE_OK;
     }
     // the expert kernels read an empty routed work list
@@ -1114,6 +1173,7 @@ int head_path(int32_t type, int V, int H)
     if (H % 256 == 0) {
         if (type == DMOE_TYPE_Q4_K && V % expert_rows_per_item(1) == 0 && V % 256 == 0) return DP_Q4K;
         if (type == DMOE_TYPE_Q8_0 && V % expert_q80_rows_per_item(1) == 0 && V % 256 == 0) return DP_Q80;
+        if (type == DMOE_TYPE_Q6_K && V % 16 == 0) return DP_Q6K;
     }
     if (type == DMOE_TYPE_F16 && gemm_shapes_ok(V, H, H, true)) return DP_F16;
     return DP_GEMV;
@@ -1133,6 +1193,10 @@ struct ProjWs {
     float *part;                         // slice sums of the few-token Q4_K projection
 };
 
+// Tokens per launch of a projection: Q6_K runs only the few-token kernel,
+// in chunks of up to PROJ_MAX_TOKENS tokens.
+int proj_chunk(int path, int N) { return path == DP_Q6K ? std::min(N, PROJ_MAX_TOKENS) : N; }
+
 template <class Take>
 ProjWs plan_proj(int path, int N, int K, int rows, Take &&take)
 {
@@ -1140,10 +1204,13 @@ ProjWs plan_proj(int path, int N, int K, int rows, Take &&take)
     p.n_ec = (int32_t *)take(4);
     switch (path) {
     case DP_Q4K:
-        p.act = take_act(take, N, K, true);
-        if (proj_ok(rows, K, N) && proj_plan(rows, K, 1, N).KS > 1)
-            p.part = (float *)take(proj_partial_floats(rows, K, 1, N) * 4);
+    case DP_Q6K: {
+        const int n = proj_chunk(path, N);
+        p.act = take_act(take, n, K, true);
+        if (proj_ok(rows, K, n))
+            if (const size_t pf = proj_partial_max(rows, K, 1, n, true)) p.part = (float *)take(pf * 4);
         break;
+    }
     case DP_Q80: p.act = take_act(take, N, K, true, true); break;
     case DP_F16: p.x16 = (uint16_t *)take((size_t)2 * N * K * 2); break;
     default: break;
@@ -1151,8 +1218,12 @@ ProjWs plan_proj(int path, int N, int K, int rows, Take &&take)
     return p;
 }
 
-// Few tokens of Q4_K weights: k_proj.hip on x already converted to p.act.
-bool proj_few(int path, int rows, int K, int N) { return path == DP_Q4K && proj_ok(rows, K, N); }
+// Few tokens of Q4_K or Q6_K weights: k_proj.hip on x already converted to
+// p.act.
+bool proj_few(int path, int rows, int K, int N)
+{
+    return (path == DP_Q4K || path == DP_Q6K) && proj_ok(rows, K, N);
+}
 
 // y [N][rows] = W x from p.act: 128 T-row tiles x reduction slices over every
 // CU.  With ks_out the slices are left for the consumer to add in order
@@ -1173,7 +1244,7 @@ int enqueue_proj_few(dmoe_ctx *ctx, bool prof, int st_prod, const WTensor &W, in
     j.partial = j.KS > 1;
     j.out = j.partial ? p.part : y;
     j.ldo = rows;
-    STAGE(st_prod, launch_proj_q4k(j, s));
+    STAGE(st_prod, W.type == DMOE_TYPE_Q6_K ? launch_proj_q6k(j, s) : launch_proj_q4k(j, s));
     if (ks_out) {
         *ks_out = j.KS;
         *src_out = j.out;
@@ -1193,10 +1264,17 @@ int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTens
         STAGE(st_prod, launch_down_shared(W, x, N, K, rows, y, s));
         return DMOE_OK;
     }
-    if (proj_few(path, rows, K, N)) {
-        PrepJob pj{x, N, K, ACT_SPLIT, p.act};
-        STAGE(st_conv, launch_prep(&pj, 1, s));
-        return enqueue_proj_few(ctx, prof, st_prod, W, rows, K, N, p, y, nullptr, nullptr, s);
+    if (proj_few(path, rows, K, proj_chunk(path, N))) {
+        // every token at once, or (Q6_K) chunks of up to PROJ_MAX_TOKENS
+        const int nc = proj_chunk(path, N);
+        for (int t0 = 0; t0 < N; t0 += nc) {
+            const int n = std::min(nc, N - t0);
+            PrepJob pj{x + (size_t)t0 * K, n, K, ACT_SPLIT, p.act};
+            STAGE(st_conv, launch_prep(&pj, 1, s));
+            int rc = enqueue_proj_few(ctx, prof, st_prod, W, rows, K, n, p, y + (size_t)t0 * rows, nullptr, nullptr, s);
+            if (rc) return rc;
+        }
+        return DMOE_OK;
     }
     LAUNCH_TRY(ctx, launch_fill_i32(p.n_ec, 0, 1, s));
     WorkList wl{};
@@ -1271,6 +1349,7 @@ int tile_proj(dmoe_ctx *ctx, dmoe_layer *L, WTensor &W, int rows, int K)
 {
     switch (head_path(W.type, rows, K)) {
     case DP_Q4K: return tile_tensor(ctx, L, W, rows, K, 1);
+    case DP_Q6K: return tile_tensor_q6k(ctx, L, W, rows, K, 1);
     case DP_Q80: return tile_tensor_q80(ctx, L, W, rows, K, 1);
     case DP_F16: return tile_tensor_f16(ctx, L, W, rows, K, 1);
     default: return DMOE_OK;
@@ -1922,7 +2001,8 @@ void dmoe_layer_free(dmoe_layer *L)
 int dmoe_layer_kernel_path(const dmoe_layer *L)
 {
     if (!L) return -1;
-    static const int kmap[] = {DMOE_PATH_GEMV, DMOE_PATH_Q4K_MFMA, DMOE_PATH_Q80_MFMA, DMOE_PATH_F16_GEMM};
+    static const int kmap[] = {DMOE_PATH_GEMV, DMOE_PATH_Q4K_MFMA, DMOE_PATH_Q80_MFMA, DMOE_PATH_F16_GEMM,
+                               DMOE_PATH_Q6K_MFMA};
     if (L->dense) return kmap[dense_path(L->sg.type, L->hp.n_embd, L->hp.shared_ff)];
     if (L->head) return kmap[head_path(L->sd.type, L->n_vocab, L->hp.n_embd)];
     if (L->attn) {

@@ -19,6 +19,7 @@ constexpr int QK_K = 256;          // super-block of Q4_K / Q8_K
 constexpr int QK8_0 = 32;          // block of Q8_0
 constexpr int Q4K_BYTES = 144;     // f16 d, f16 dmin, u8 scales[12], u8 qs[128]
 constexpr int Q8_0_BYTES = 34;     // f16 d, i8 qs[32]
+constexpr int Q6K_BYTES = 210;     // u8 ql[128], u8 qh[64], i8 scales[16], f16 d
 
 // Activation operand of one expert product, in the layout the kernels read.
 //   F32 : f32  [rows][n]
@@ -258,6 +259,8 @@ struct ProjPlan {
 ProjPlan proj_plan(int R, int K, int M, int N);          // the launch shape for a projection
 size_t proj_partial_floats(int R, int K, int M, int N);  // partial buffer of that KS
 hipError_t launch_proj_q4k(const ProjJob &j, hipStream_t s);
+// the same for Q6_K matrices (tiled by launch_tile_q6k)
+hipError_t launch_proj_q6k(const ProjJob &j, hipStream_t s);
 // y [N][ldy] = the KS slices of part [KS][N][R] added in slice order
 hipError_t launch_proj_reduce(const float *part, int KS, int N, int R, float *y, int ldy, hipStream_t s);
 // h = silu(gate) up from part [2][KS][N][R], to ah (two int8 digit rows per token)
@@ -319,6 +322,10 @@ bool expert_k_ok(int K);                 // reduction length the expert kernels 
 // first) and the 128 quant bytes are reordered so that byte 16 + 32g + 8c + b
 // holds quant byte 32c + 8g + b.
 hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
+                           uint8_t *dst, hipStream_t s);
+// Q6_K rows -> the tiled layout of the Q6_K projections (k_quant.hip
+// describes the 3360-byte tile-step runs); same byte count.
+hipError_t launch_tile_q6k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
                            uint8_t *dst, hipStream_t s);
 
 hipError_t launch_act_quant(const float *src, int rows, int n, const ActBuf &dst,

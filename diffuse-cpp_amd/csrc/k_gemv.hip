@@ -159,6 +159,88 @@ template <> struct WUnit<DMOE_TYPE_Q8_0> {
     }
 };
 
+// Q6_K (ggml's block_q6_K: ql[128], qh[64], int8 scales[16], f16 d; 210
+// bytes per 256 weights).  Unit u: weights 64 c .. 64 c + 63 of super-block
+// u / 4 (c = u % 4), i.e. half h = c / 2, quarters k0 = 2 (c % 2) and k0 + 1:
+// weight 64 c + l (l < 32) has the low (k0 = 0) or high (k0 = 2) nibble of
+// ql[64 h + l] and bits 2 k0 of qh[32 h + l]; weight 64 c + 32 + l the same
+// nibble of ql[64 h + 32 + l] and bits 2 k0 + 2.  Sub-block 4 c + j (16
+// weights) has scale scales[4 c + j].
+template <> struct WUnit<DMOE_TYPE_Q6_K> {
+    static constexpr int N = 64;
+    float d;
+    int sc[4];
+    uint32_t q[16];     // 6-bit quants (0..63) as bytes: q[0..7] weights 0..31, q[8..15] 32..63
+    // 210-byte blocks are only 2-byte aligned inside a row: dwords are read
+    // as two halves
+    __device__ __forceinline__ static uint32_t ld32(const uint16_t *p, int i)
+    {
+        return (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
+    }
+    __device__ __forceinline__ void load(const uint8_t *row, int u)
+    {
+        const uint8_t *blk = row + (size_t)(u >> 2) * Q6K_BYTES;
+        const int c = u & 3, h = c >> 1, k0 = 2 * (c & 1);
+        const uint16_t *ql = reinterpret_cast<const uint16_t *>(blk + 64 * h);
+        const uint16_t *qh = reinterpret_cast<const uint16_t *>(blk + 128 + 32 * h);
+        const int ns = 2 * k0;          // nibble shift 0 or 4
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t H = ld32(qh, i);
+            q[i] = ((ld32(ql, i) >> ns) & 0x0f0f0f0fu) | (((H >> (2 * k0)) & 0x03030303u) << 4);
+            q[8 + i] = ((ld32(ql, 8 + i) >> ns) & 0x0f0f0f0fu) | (((H >> (2 * k0 + 2)) & 0x03030303u) << 4);
+        }
+        const uint32_t s4 = ld32(reinterpret_cast<const uint16_t *>(blk + 192 + 4 * c), 0);
+#pragma unroll
+        for (int j = 0; j < 4; j++) sc[j] = (int)(int8_t)(s4 >> (8 * j));
+        d = h2f(*reinterpret_cast<const uint16_t *>(blk + 208));
+    }
+    // Q8_K activation row `row` of xq: per sub-block sum (q - 32) a =
+    // sum q a - 32 (the row's sum of those 16 activations)
+    __device__ __forceinline__ float dot(const ActBuf &xq, int row, int u) const
+    {
+        const int n = xq.n;
+        const int b = u >> 2, c = u & 3;
+        const uint4 *xp = reinterpret_cast<const uint4 *>((const int8_t *)xq.vals + (size_t)row * n +
+                                                          b * 256 + 64 * c);
+        const int16_t *bs = xq.bsums + (size_t)row * (n / 16) + b * 16 + 4 * c;
+        int sumi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 xv = xp[j];
+            int sj = 0;
+            sj = __builtin_amdgcn_sdot4((int)q[4 * j + 0], (int)xv.x, sj, false);
+            sj = __builtin_amdgcn_sdot4((int)q[4 * j + 1], (int)xv.y, sj, false);
+            sj = __builtin_amdgcn_sdot4((int)q[4 * j + 2], (int)xv.z, sj, false);
+            sj = __builtin_amdgcn_sdot4((int)q[4 * j + 3], (int)xv.w, sj, false);
+            sumi += sc[j] * (sj - 32 * (int)bs[j]);
+        }
+        const float xd = xq.d[(size_t)row * (n / 256) + b];
+        return (xd * d) * (float)sumi;
+    }
+    // f32 activations against the dequantised unit (w = (d sc) (q - 32), exact)
+    __device__ __forceinline__ float dotf(const float *x, int u) const
+    {
+        const int b = u >> 2, c = u & 3;
+        const float4 *xp = reinterpret_cast<const float4 *>(x + b * 256 + 64 * c);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float ds = d * (float)sc[j];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 xv = xp[4 * j + i];
+                const uint32_t w = q[4 * j + i];
+                acc = __builtin_fmaf(ds * (float)((int)(w & 0xffu) - 32), xv.x, acc);
+                acc = __builtin_fmaf(ds * (float)((int)((w >> 8) & 0xffu) - 32), xv.y, acc);
+                acc = __builtin_fmaf(ds * (float)((int)((w >> 16) & 0xffu) - 32), xv.z, acc);
+                acc = __builtin_fmaf(ds * (float)((int)(w >> 24) - 32), xv.w, acc);
+            }
+        }
+        return acc;
+    }
+};
+
 template <> struct WUnit<DMOE_TYPE_F16> {
     static constexpr int N = 8;
     uint4 w;
@@ -382,6 +464,7 @@ __global__ __launch_bounds__(256) void k_down_shared(WTensor wd, const float *__
 #define DMOE_TYPE_SWITCH(T, ...)                                                                   \
     switch (T) {                                                                                   \
     case DMOE_TYPE_Q4_K: { constexpr int WT = DMOE_TYPE_Q4_K; __VA_ARGS__; } break;                \
+    case DMOE_TYPE_Q6_K: { constexpr int WT = DMOE_TYPE_Q6_K; __VA_ARGS__; } break;                \
     case DMOE_TYPE_Q8_0: { constexpr int WT = DMOE_TYPE_Q8_0; __VA_ARGS__; } break;                \
     case DMOE_TYPE_F16:  { constexpr int WT = DMOE_TYPE_F16;  __VA_ARGS__; } break;                \
     case DMOE_TYPE_F32:  { constexpr int WT = DMOE_TYPE_F32;  __VA_ARGS__; } break;                \

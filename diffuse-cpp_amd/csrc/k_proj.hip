@@ -282,6 +282,259 @@ __global__ __launch_bounds__(PJ_WAVES * 64) void k_proj_q4k(ProjJob j)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K projections of few tokens (F32 weight semantics: the weights
+// d sc_j (q - 32) are exact in binary32; ggml's block_q6_K, tiled by
+// k_tile_q6k: a tile step is 16 rows x one super-block, 3360 bytes).
+// Per 16-weight sub-block j of weight row r and activation digit row t the
+// integer sum M_j = sum q a (q = 0..63, int8 a) comes from one
+// v_mfma_i32_16x16x32_i8: the A operand holds a 32-weight pair of sub-blocks
+// (k = 8 g + b: lane groups 0, 1 sub-block 2p, groups 2, 3 sub-block 2p + 1),
+// the B operand the quants of the lanes of one sub-block and zeros in the
+// others, so each MFMA sums exactly one sub-block.  Then
+//   S = sum_j sc_j M_j - 32 sum_j sc_j bs_j
+// with bs_j the activation row's sum of those 16 digits (the f16 sums of 16 of
+// the operand layout): the second sum is one v_mfma_f32_16x16x16f16 of the
+// sums against the scales, exact (|terms| < 2^24), so S is the exact integer
+// sum_j sc_j sum (q - 32) a.  A token's two digit rows then give
+//   d dx1 (S1 + S0 / 256)
+// as for Q4_K.  The weight ring holds PJ6_WST stages (3360-byte steps leave
+// room for four next to the activation stages).
+constexpr int TILE6_BYTES = 16 * Q6K_BYTES;       // 3360
+constexpr int PJ6_WST = 4;
+constexpr int PJ6_AHEAD = PJ6_WST - 1;
+constexpr int PJ6_LOADS = 4;                      // 16-byte LDS-direct loads per weight step
+
+struct Q6Tile {                                   // a lane's share of one tile step
+    uint32_t L[8], H[4];                          // its 64 quants (k_tile_q6k's packing)
+    uint4 sc;                                     // the row's 16 int8 scales
+    float d;
+};
+
+__device__ __forceinline__ void read_tile6(Q6Tile &t, const uint8_t *tile, int lane, int r16)
+{
+    const uint4 *p = reinterpret_cast<const uint4 *>(tile);
+    const uint4 a = p[lane], b = p[64 + lane], c = p[128 + lane];
+    t.L[0] = a.x; t.L[1] = a.y; t.L[2] = a.z; t.L[3] = a.w;
+    t.L[4] = b.x; t.L[5] = b.y; t.L[6] = b.z; t.L[7] = b.w;
+    t.H[0] = c.x; t.H[1] = c.y; t.H[2] = c.z; t.H[3] = c.w;
+    t.sc = p[192 + r16];
+    t.d = h16f(reinterpret_cast<const uint16_t *>(tile + 208 * 16)[r16]);
+}
+
+// The tile's B operands (quants of pair p as 8 bytes, k = 8 g + b), masked to
+// the lane groups of sub-block 2p (be) and 2p + 1 (bo); the 16 scales as
+// integers; the f16 scales of sub-blocks 4 g .. 4 g + 3 (the offset MFMA's B).
+struct Q6Folded {
+    long be[8], bo[8];
+    int sc[16];
+    h4 bsc;
+    float d;
+};
+
+// int -> float with v_cvt_f32_i32 as written: left to the compiler, the
+// conversion of a sign-extended byte (sbfe x, 8 k, 8) was folded into
+// v_cvt_f32_u32 of an SDWA sign-extended byte, which reads a negative scale
+// as 2^32 + sc.
+__device__ __forceinline__ float cvt_f32_i32(int v)
+{
+    float f;
+    asm volatile("v_cvt_f32_i32 %0, %1" : "=v"(f) : "v"(v));
+    return f;
+}
+
+__device__ __forceinline__ void fold_tile6(const Q6Tile &t, int g, Q6Folded &f)
+{
+    const uint32_t keep = g < 2 ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        const uint32_t L = t.L[p], H = t.H[p >> 1];
+        uint32_t qa, qb;
+        if (p & 1) {
+            qa = (L & 0x0f0f0f0fu) | (H & 0x30303030u);
+            qb = ((L >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+        } else {
+            qa = (L & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+            qb = ((L >> 4) & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+        }
+        f.be[p] = (long)(((uint64_t)(qb & keep) << 32) | (qa & keep));
+        f.bo[p] = (long)(((uint64_t)(qb & ~keep) << 32) | (qa & ~keep));
+    }
+    const uint32_t sw[4] = {t.sc.x, t.sc.y, t.sc.z, t.sc.w};
+#pragma unroll
+    for (int j = 0; j < 16; j++) f.sc[j] = __builtin_amdgcn_sbfe(sw[j >> 2], 8 * (j & 3), 8);
+    const uint32_t sg = sw[g];
+    f.bsc = (h4){(_Float16)cvt_f32_i32(__builtin_amdgcn_sbfe(sg, 0, 8)),
+                 (_Float16)cvt_f32_i32(__builtin_amdgcn_sbfe(sg, 8, 8)),
+                 (_Float16)cvt_f32_i32(__builtin_amdgcn_sbfe(sg, 16, 8)),
+                 (_Float16)cvt_f32_i32(__builtin_amdgcn_sbfe(sg, 24, 8))};
+    f.d = t.d;
+}
+
+// One column block: S for the lane's four digit rows, then the two tokens'
+// epilogue (as pj_epilogue: the a0 row's scale is the a1 row's / 256).
+__device__ __forceinline__ void pj6_block(const Q6Folded &f, const PjOps &o, float (&acc)[2])
+{
+    const long a[8] = {(long)((uint64_t)(uint32_t)o.a[0][1] << 32 | (uint32_t)o.a[0][0]),
+                       (long)((uint64_t)(uint32_t)o.a[0][3] << 32 | (uint32_t)o.a[0][2]),
+                       (long)((uint64_t)(uint32_t)o.a[1][1] << 32 | (uint32_t)o.a[1][0]),
+                       (long)((uint64_t)(uint32_t)o.a[1][3] << 32 | (uint32_t)o.a[1][2]),
+                       (long)((uint64_t)(uint32_t)o.a[2][1] << 32 | (uint32_t)o.a[2][0]),
+                       (long)((uint64_t)(uint32_t)o.a[2][3] << 32 | (uint32_t)o.a[2][2]),
+                       (long)((uint64_t)(uint32_t)o.a[3][1] << 32 | (uint32_t)o.a[3][0]),
+                       (long)((uint64_t)(uint32_t)o.a[3][3] << 32 | (uint32_t)o.a[3][2])};
+    f4 c2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    c2 = __builtin_amdgcn_mfma_f32_16x16x16f16(o.ab, f.bsc, c2, 0, 0, 0);
+    // sum_j sc_j bs_j is an integer below 2^23 in magnitude: exact in the f32
+    // accumulator and as a 24-bit multiplicand
+    int S[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) S[i] = __mul24((int)c2[i], -32);
+    const v4i z = {0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        const v4i m0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[p], f.be[p], z, 0, 0, 0);
+        const v4i m1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[p], f.bo[p], z, 0, 0, 0);
+        // |M_j| <= 16 * 63 * 128 and |sc_j| <= 128: 24-bit multiplicands
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            S[i] = __mul24(f.sc[2 * p], m0[i]) + S[i];
+            asm volatile("" : "+v"(S[i]));
+            S[i] = __mul24(f.sc[2 * p + 1], m1[i]) + S[i];
+            asm volatile("" : "+v"(S[i]));
+        }
+    }
+    const float dx1[2] = {o.dx.x, o.dx.z};
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const float sv = __builtin_fmaf((float)S[2 * u + 1], 0.00390625f, (float)S[2 * u]);
+        acc[u] = __builtin_fmaf(dx1[u], f.d * sv, acc[u]);
+    }
+}
+
+// The launch structure of k_proj_q4k (work division, activation staging,
+// compile-time waits; see there) with Q6_K tile steps: PJ6_LOADS loads per
+// weight step (the fourth of lanes 0..17: 3360 = 3 x 1024 + 288 bytes).
+template <int T, int NB>
+__global__ __launch_bounds__(PJ_WAVES * 64) void k_proj_q6k(ProjJob j)
+{
+    __shared__ __align__(16) uint8_t s_act[2][NB][ASTEP_BYTES];
+    __shared__ __align__(16) uint8_t s_w[PJ_WAVES][PJ6_WST][TILE6_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, r16 = lane & 15;
+    const int N = j.N, K = j.K, R = j.R, KS = j.KS;
+    const int nsb = K / 256, S = nsb / KS;
+    const int m = blockIdx.z, sl = blockIdx.y;
+    const int ntile = R / 16;
+    const int tile0 = blockIdx.x * PJ_WAVES * T + wave;
+    const int Q = S * T;
+    const int nbr = (N + 7) / 8;
+    const int sb0 = sl * S;
+    const uint8_t *wm = j.w[m];
+    const int ar = wave < 4 ? 4 * wave + (lane >> 4) : (wave == 4 ? (lane >> 1) & 15 : lane & 15);
+    const int aunit = (lane & 15) ^ (ar & 11);
+    const bool aload = wave < 4 || (wave == 4 && lane < 32) || (wave == 5 && lane < 16);
+    const bool loader = wave < ADMA_WAVES;
+    const uint32_t loff = lane * 16;
+    const int astride = wave < 4 ? 256 : (wave == 4 ? 32 : 4);
+    const int adst = wave < 4 ? 1024 * wave : (wave == 4 ? ABS_OFF : AD_OFF);
+    const uint8_t *asrc[NB];
+#pragma unroll
+    for (int c = 0; c < NB; c++) {
+        const int row = min(8 * c + (ar >> 1), N - 1) + (ar & 1) * N;
+        asrc[c] = wave < 4 ? reinterpret_cast<const uint8_t *>(j.x.q + (size_t)row * K + sb0 * 256 + aunit * 16)
+                : wave == 4 ? reinterpret_cast<const uint8_t *>(j.x.bs + (size_t)row * (K / 16) + sb0 * 16) +
+                                  (lane & 1) * 16
+                            : reinterpret_cast<const uint8_t *>(j.x.d + (size_t)row * nsb + sb0);
+    }
+    auto issue_a = [&](int s, int st) __attribute__((always_inline)) {
+        const int off = min(s, S - 1) * astride;
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            const uint8_t *st8 = &s_act[st][c][0] + adst;
+            if (wave < 5) {
+                if (aload) lds_load16(asrc[c] + off, st8);
+            } else if (wave == 5 && aload) {
+                lds_load4(asrc[c] + off, st8);
+            }
+        }
+    };
+    auto issue_w = [&](int q) __attribute__((always_inline)) {
+        const int qc = min(q, Q - 1);
+        const int s = qc / T, k = qc - s * T;
+        const int tile = min(tile0 + PJ_WAVES * k, ntile - 1);
+        const uint8_t *t = wm + ((size_t)tile * nsb + sb0 + s) * TILE6_BYTES;
+        const uint8_t *d = &s_w[wave][q % PJ6_WST][0];
+        lds_load16_sa(t, loff, d);
+        lds_load16_sa(t, loff + 1024, d + 1024);
+        lds_load16_sa(t, loff + 2048, d + 2048);
+        if (lane < (TILE6_BYTES - 3072) / 16) lds_load16_sa(t, loff + 3072, d + 3072);
+    };
+
+    float acc[T][NB][2];
+#pragma unroll
+    for (int k = 0; k < T; k++)
+#pragma unroll
+        for (int c = 0; c < NB; c++) acc[k][c][0] = acc[k][c][1] = 0.0f;
+
+    issue_a(0, 0);
+    for (int q = 0; q < PJ6_AHEAD; q++) issue_w(q);
+    for (int s = 0; s < S; s++) {
+        if (loader) {
+            if (s == 0)
+                pj_wait<PJ6_LOADS * PJ6_AHEAD>();
+            else
+                pj_wait<PJ6_LOADS * T>();
+        }
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue_a(s + 1, (s + 1) & 1);
+        const uint8_t *ast = &s_act[s & 1][0][0];
+        PjOps o[NB];
+#pragma unroll
+        for (int c = 0; c < NB; c++) pj_read_ops(o[c], ast + c * ASTEP_BYTES, r16, g);
+#pragma unroll
+        for (int k = 0; k < T; k++) {
+            const int q = s * T + k;
+            issue_w(q + PJ6_AHEAD);
+            constexpr int nw = PJ6_LOADS * PJ6_AHEAD;
+            if (k < PJ6_AHEAD && loader)
+                pj_wait<nw + NB>();
+            else
+                pj_wait<nw>();
+            asm volatile("" ::: "memory");
+            Q6Tile t;
+            read_tile6(t, &s_w[wave][q % PJ6_WST][0], lane, r16);
+            Q6Folded f;
+            fold_tile6(t, g, f);
+#pragma unroll
+            for (int c = 0; c < NB; c++)
+                if (c < nbr) pj6_block(f, o[c], acc[k][c]);
+        }
+    }
+    pj_wait<0>();
+#pragma unroll
+    for (int k = 0; k < T; k++) {
+        const int tile = tile0 + PJ_WAVES * k;
+        if (tile >= ntile) break;
+        const int row = tile * 16 + r16;
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int t = 8 * c + 2 * g + u;
+                if (t >= N) continue;
+                const float v = acc[k][c][u];
+                if (j.partial)
+                    j.out[((size_t)(m * KS + sl) * N + t) * R + row] = v;
+                else
+                    j.out[(size_t)t * j.ldo + row] = v;
+            }
+        }
+    }
+}
+
 // y [N][ldy] = the slices' sums, added in slice order (four rows' values per
 // thread)
 __global__ __launch_bounds__(256) void k_proj_reduce(const float4 *__restrict__ part, int KS, int N, int R4,
@@ -371,30 +624,34 @@ size_t proj_partial_floats(int R, int K, int M, int N)
     return (size_t)M * proj_plan(R, K, M, N).KS * N * R;
 }
 
-template <int T, int NB>
+template <bool Q6, int T, int NB>
 static hipError_t proj_launch_nb(int nb, dim3 grid, const ProjJob &j, hipStream_t s)
 {
     if constexpr (NB > PJ_BLOCKS) {
         return hipErrorInvalidValue;
     } else {
-        if (nb != NB) return proj_launch_nb<T, NB + 1>(nb, grid, j, s);
-        hipLaunchKernelGGL((k_proj_q4k<T, NB>), grid, dim3(PJ_WAVES * 64), 0, s, j);
+        if (nb != NB) return proj_launch_nb<Q6, T, NB + 1>(nb, grid, j, s);
+        if constexpr (Q6)
+            hipLaunchKernelGGL((k_proj_q6k<T, NB>), grid, dim3(PJ_WAVES * 64), 0, s, j);
+        else
+            hipLaunchKernelGGL((k_proj_q4k<T, NB>), grid, dim3(PJ_WAVES * 64), 0, s, j);
         return hipGetLastError();
     }
 }
 
-template <int T>
+template <bool Q6, int T>
 static hipError_t proj_launch_t(int t, int nb, dim3 grid, const ProjJob &j, hipStream_t s)
 {
     if constexpr (T < 1) {
         return hipErrorInvalidValue;
     } else {
-        if (t != T) return proj_launch_t<T - 1>(t, nb, grid, j, s);
-        return proj_launch_nb<T, 1>(nb, grid, j, s);
+        if (t != T) return proj_launch_t<Q6, T - 1>(t, nb, grid, j, s);
+        return proj_launch_nb<Q6, T, 1>(nb, grid, j, s);
     }
 }
 
-hipError_t launch_proj_q4k(const ProjJob &j, hipStream_t s)
+template <bool Q6>
+static hipError_t launch_proj(const ProjJob &j, hipStream_t s)
 {
     const ProjPlan pl = proj_plan(j.R, j.K, j.M, j.N);
     if (!proj_ok(j.R, j.K, j.N) || j.M < 1 || j.M > 2 || j.KS != pl.KS || j.x.K != j.K ||
@@ -402,8 +659,12 @@ hipError_t launch_proj_q4k(const ProjJob &j, hipStream_t s)
         return hipErrorInvalidValue;
     const dim3 grid((j.R / 16 + PJ_WAVES * pl.T - 1) / (PJ_WAVES * pl.T), j.KS, j.M);
     const int nb = (j.N + 7) / 8;
-    return proj_launch_t<PJ_TMAX>(pl.T, nb, grid, j, s);
+    return proj_launch_t<Q6, PJ_TMAX>(pl.T, nb, grid, j, s);
 }
+
+hipError_t launch_proj_q4k(const ProjJob &j, hipStream_t s) { return launch_proj<false>(j, s); }
+
+hipError_t launch_proj_q6k(const ProjJob &j, hipStream_t s) { return launch_proj<true>(j, s); }
 
 hipError_t launch_proj_reduce(const float *part, int KS, int N, int R, float *y, int ldy, hipStream_t s)
 {

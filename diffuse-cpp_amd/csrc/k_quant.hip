@@ -238,6 +238,73 @@ __global__ __launch_bounds__(256) void k_wq_q4K(const float *__restrict__ src, i
     }
 }
 
+// Q6_K (a plain quantiser, not ggml's make_qx_quants search): per 16-value
+// sub-block the value of largest magnitude v_j (first on ties) gives the
+// signed scale s_j = -v_j / 32; the s of largest magnitude gives d = -s / 128
+// (fp16); sc_j = nearest(s_j / d) clamped to -128..127, q = nearest(x / (d
+// sc_j)) clamped to -32..31, stored as q + 32 in ggml's block_q6_K layout
+// (ql: low nibbles of weights 128 h + 32 k + l at ql[64 h + 32 (k % 2) + l],
+// low half for k < 2, high half for k >= 2; qh[32 h + l]: bits 2k, 2k + 1).
+__device__ __forceinline__ int q6_of(const float *x, const float *ds, int v)
+{
+    const float s = ds[v >> 4];
+    int q = 0;
+    if (s != 0.0f) q = nearest_int(x[v] / s);
+    q = q < -32 ? -32 : q > 31 ? 31 : q;
+    return q + 32;
+}
+
+__global__ __launch_bounds__(256) void k_wq_q6K(const float *__restrict__ src, int64_t nblk,
+                                                uint8_t *__restrict__ dst)
+{
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblk) return;
+    const float *x = src + b * 256;
+    uint8_t *y = dst + b * Q6K_BYTES;
+    float sj[16];
+    float smax = 0.0f, samax = 0.0f;
+    for (int j = 0; j < 16; j++) {
+        float amax = 0.0f, vmax = 0.0f;
+        for (int l = 0; l < 16; l++) {
+            const float a = fabsf(x[16 * j + l]);
+            if (a > amax) {
+                amax = a;
+                vmax = x[16 * j + l];
+            }
+        }
+        sj[j] = -vmax / 32.0f;
+        if (amax / 32.0f > samax) {
+            samax = amax / 32.0f;
+            smax = sj[j];
+        }
+    }
+    if (samax == 0.0f) {
+        for (int i = 0; i < Q6K_BYTES; i++) y[i] = 0;
+        return;
+    }
+    const uint16_t dh = f32_to_f16_bits(-smax / 128.0f);
+    const float d = f16_bits_to_f32(dh);
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    float ds[16];
+    for (int j = 0; j < 16; j++) {
+        int sc = nearest_int(sj[j] * id);
+        sc = sc < -128 ? -128 : sc > 127 ? 127 : sc;
+        y[192 + j] = (uint8_t)(int8_t)sc;
+        ds[j] = d * (float)sc;
+    }
+    for (int h = 0; h < 2; h++)
+        for (int l = 0; l < 32; l++) {
+            const int v = 128 * h + l;
+            const int q0 = q6_of(x, ds, v), q1 = q6_of(x, ds, v + 32);
+            const int q2 = q6_of(x, ds, v + 64), q3 = q6_of(x, ds, v + 96);
+            y[64 * h + l] = (uint8_t)((q0 & 15) | ((q2 & 15) << 4));
+            y[64 * h + 32 + l] = (uint8_t)((q1 & 15) | ((q3 & 15) << 4));
+            y[128 + 32 * h + l] = (uint8_t)((q0 >> 4) | ((q1 >> 4) << 2) | ((q2 >> 4) << 4) | ((q3 >> 4) << 6));
+        }
+    y[208] = (uint8_t)(dh & 0xff);
+    y[209] = (uint8_t)(dh >> 8);
+}
+
 __global__ __launch_bounds__(256) void k_wq_f16(const float *__restrict__ src, int64_t total,
                                                 uint16_t *__restrict__ dst)
 {
@@ -311,6 +378,90 @@ hipError_t launch_tile_q4k(const uint8_t *src, size_t nb1, size_t nb2, int rows,
     return hipGetLastError();
 }
 
+// Q6_K row layout -> the tiled layout of the few-token projections
+// (k_proj.hip): per matrix, 16-row tiles, super-block-major, the 16 rows of
+// one super-block a contiguous 3360-byte run at ((r / 16) nsb + sb) 3360 of
+// 210 16-byte pieces (the same bytes as the GGUF blocks, rearranged):
+//   pieces k 64 + 16 g + r (k = 0, 1, 2): what lane (r, g) of a wavefront
+//     reads for row r: twelve dwords L[0..7], H[0..3] of its 64 quants
+//     32 p + 8 g + b (p = 0..7 pairs of 32 weights, b = 0..7):
+//       L[p] byte i: low nibbles of quants (p, b = i) and (p, b = 4 + i)
+//       H[p'] byte i: the high 2 bits of quants (2p', i), (2p', 4 + i),
+//                     (2p' + 1, i), (2p' + 1, 4 + i) at bits 0, 2, 4, 6
+//   pieces 192 + r: the 16 int8 scales of row r
+//   pieces 208, 209: the 16 rows' f16 d (row r at byte 2 r)
+__global__ __launch_bounds__(256) void k_tile_q6k(const uint8_t *__restrict__ src, size_t nb1,
+                                                  size_t nb2, int rows, int nsb, int mats,
+                                                  uint8_t *__restrict__ dst)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t per_mat = (size_t)rows * nsb;
+    if (i >= per_mat * mats) return;
+    const int m = (int)(i / per_mat);
+    const size_t j = i - (size_t)m * per_mat;
+    const int sb = (int)(j % nsb);
+    const int r = (int)(j / nsb);
+    // 210-byte blocks are 2-byte aligned
+    const uint16_t *in = reinterpret_cast<const uint16_t *>(src + (size_t)m * nb2 + (size_t)r * nb1 +
+                                                            (size_t)sb * Q6K_BYTES);
+    uint8_t blk[Q6K_BYTES];
+    for (int k = 0; k < Q6K_BYTES / 2; k++) {
+        const uint16_t v = in[k];
+        blk[2 * k] = (uint8_t)(v & 0xff);
+        blk[2 * k + 1] = (uint8_t)(v >> 8);
+    }
+    uint8_t q[256];
+    for (int v = 0; v < 256; v++) {
+        const int h = v >> 7, rr = v & 127, k = rr >> 5, l = rr & 31;
+        const uint8_t lb = blk[64 * h + l + 32 * (k & 1)];
+        const int lo = (k >> 1) ? (lb >> 4) : (lb & 15);
+        const int hi = (blk[128 + 32 * h + l] >> (2 * k)) & 3;
+        q[v] = (uint8_t)(lo | (hi << 4));
+    }
+    uint8_t *run = dst + (size_t)m * rows * nsb * Q6K_BYTES + ((size_t)(r / 16) * nsb + sb) * (16 * Q6K_BYTES);
+    const int r16 = r % 16;
+    for (int g = 0; g < 4; g++) {
+        uint32_t w[12];
+        for (int p = 0; p < 8; p++) {
+            uint32_t v = 0;
+            for (int b = 0; b < 4; b++) {
+                const uint32_t lo = q[32 * p + 8 * g + b] & 15u, hi = q[32 * p + 8 * g + 4 + b] & 15u;
+                v |= (lo | (hi << 4)) << (8 * b);
+            }
+            w[p] = v;
+        }
+        for (int pp = 0; pp < 4; pp++) {
+            uint32_t v = 0;
+            for (int b = 0; b < 4; b++) {
+                const int e0 = 64 * pp + 8 * g + b;
+                const uint32_t byte = (uint32_t)(q[e0] >> 4) | ((uint32_t)(q[e0 + 4] >> 4) << 2) |
+                                      ((uint32_t)(q[e0 + 32] >> 4) << 4) | ((uint32_t)(q[e0 + 36] >> 4) << 6);
+                v |= byte << (8 * b);
+            }
+            w[8 + pp] = v;
+        }
+        for (int k = 0; k < 3; k++)
+            *reinterpret_cast<uint4 *>(run + (size_t)(64 * k + 16 * g + r16) * 16) =
+                make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+    }
+    uint32_t sc[4];
+    for (int k = 0; k < 4; k++)
+        sc[k] = (uint32_t)blk[192 + 4 * k] | ((uint32_t)blk[193 + 4 * k] << 8) | ((uint32_t)blk[194 + 4 * k] << 16) |
+                ((uint32_t)blk[195 + 4 * k] << 24);
+    *reinterpret_cast<uint4 *>(run + (size_t)(192 + r16) * 16) = make_uint4(sc[0], sc[1], sc[2], sc[3]);
+    *reinterpret_cast<uint16_t *>(run + 208 * 16 + 2 * r16) = (uint16_t)(blk[208] | (blk[209] << 8));
+}
+
+hipError_t launch_tile_q6k(const uint8_t *src, size_t nb1, size_t nb2, int rows, int K, int mats,
+                           uint8_t *dst, hipStream_t s)
+{
+    if (rows % 16 || K % 256 || nb1 % 2 || (mats > 1 && nb2 % 2)) return hipErrorInvalidValue;
+    const size_t total = (size_t)rows * (K / 256) * mats;
+    hipLaunchKernelGGL(k_tile_q6k, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
+                       nb1, nb2, rows, K / 256, mats, dst);
+    return hipGetLastError();
+}
+
 hipError_t launch_quantize_weights(int32_t type, const float *src, void *dst, int64_t nrows,
                                    int64_t n_per_row, hipStream_t s)
 {
@@ -319,6 +470,12 @@ hipError_t launch_quantize_weights(int32_t type, const float *src, void *dst, in
     case DMOE_TYPE_Q4_K: {
         const int64_t nblk = total / 256;
         hipLaunchKernelGGL(k_wq_q4K, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, src,
+                           nblk, (uint8_t *)dst);
+        break;
+    }
+    case DMOE_TYPE_Q6_K: {
+        const int64_t nblk = total / 256;
+        hipLaunchKernelGGL(k_wq_q6K, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, src,
                            nblk, (uint8_t *)dst);
         break;
     }

@@ -40,7 +40,7 @@ EXPORTS = ("dmoe_create", "dmoe_destroy", "dmoe_last_error", "dmoe_layer_upload"
            "dmoe_gguf_attn_hparams", "dmoe_gguf_attn_desc")
 NOALLOC_SCRATCH_BYTES = 64 << 20
 N_STAGES = 10
-PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", -1: "none"}
+PATH_NAMES = {0: "gemv", 1: "q4k_mfma", 2: "q80_mfma", 3: "f16_gemm", 4: "q6k_mfma", -1: "none"}
 
 
 class DmoeError(RuntimeError):

@@ -6,9 +6,10 @@ TYPE_F32 = 0
 TYPE_F16 = 1
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
-TYPE_Q8_K = 15          # activation-only type (vec_dot_type of Q4_K)
+TYPE_Q6_K = 14
+TYPE_Q8_K = 15          # activation-only type (vec_dot_type of Q4_K and Q6_K)
 
-TYPE_NAMES = {TYPE_F32: "F32", TYPE_F16: "F16", TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K"}
+TYPE_NAMES = {TYPE_F32: "F32", TYPE_F16: "F16", TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K", TYPE_Q6_K: "Q6_K"}
 TYPE_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
 
 OK = 0
@@ -57,11 +58,11 @@ class Debug(C.Structure):
 
 
 def block_elems(t: int) -> int:
-    return {TYPE_F32: 1, TYPE_F16: 1, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q8_K: 256}[t]
+    return {TYPE_F32: 1, TYPE_F16: 1, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q6_K: 256, TYPE_Q8_K: 256}[t]
 
 
 def block_bytes(t: int) -> int:
-    return {TYPE_F32: 4, TYPE_F16: 2, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q8_K: 292}[t]
+    return {TYPE_F32: 4, TYPE_F16: 2, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q8_K: 292}[t]
 
 
 def row_size(t: int, n: int) -> int:

@@ -18,7 +18,7 @@ import ctypes as C
 
 import numpy as np
 
-from . import AttnWeights, DenseWeights, DmoeError, LayerWeights, load
+from . import AttnWeights, DenseWeights, DmoeError, HeadWeights, LayerWeights, load
 from ._abi import AttnDesc, AttnHParams, HParams, LayerDesc, Tensor, row_size
 
 
@@ -200,6 +200,24 @@ class GGUF:
         m = self._map
         return DenseWeights(n_embd=H, n_ff=FF, wtype=g.type, gate=_bytes_view(m, g),
                             up=_bytes_view(m, u), down=_bytes_view(m, dn))
+
+    def head_weights(self) -> HeadWeights:
+        """The step tail's tensors as a HeadWeights of views onto the file:
+        output_norm.weight, and output.weight or, when the file has none (tied
+        embeddings), token_embd.weight (src/diffuse-model.cpp:129-138)."""
+        m = self._map
+        norm = self.tensor("output_norm.weight")
+        try:
+            out = self.tensor("output.weight")
+        except DmoeError as e:
+            if e.code != 8:
+                raise
+            out = self.tensor("token_embd.weight")
+        H, V = int(out.ne[0]), int(out.ne[1])
+        _expect("output_norm", norm, (H,))
+        _expect("output", out, (H, V))
+        return HeadWeights(n_embd=H, n_vocab=V, wtype=out.type, norm=_f32_view(m, norm, "output norm"),
+                           output=_bytes_view(m, out))
 
     def attn_hparams(self) -> AttnHParams:
         a = AttnHParams()

@@ -32,11 +32,15 @@
 extern "C" {
 #endif
 
-/* ggml type ids, as enumerated in tools/quantize_streaming.py:109-110. */
+/* ggml type ids, as enumerated in tools/quantize_streaming.py:109-110.
+ * Q6_K is the type the reference's quantisers give output.weight (both Q4_K
+ * schemes), the layer-0 ffn tensors (Q4_K_M) and every tensor of the q6_k
+ * scheme (tools/quantize_streaming.py:113-124, tools/quantize.cpp:40-45). */
 #define DMOE_TYPE_F32   0
 #define DMOE_TYPE_F16   1
 #define DMOE_TYPE_Q8_0  8
 #define DMOE_TYPE_Q4_K 12
+#define DMOE_TYPE_Q6_K 14
 
 typedef enum dmoe_status {
     DMOE_OK                   = 0,
@@ -250,7 +254,11 @@ void dmoe_layer_free(dmoe_layer *layer);
  *   DMOE_PATH_Q4K_MFMA  Q4_K routed + shared experts on int8 MFMA tiles
  *   DMOE_PATH_Q80_MFMA  Q8_0 routed + shared experts on int8 MFMA tiles
  *   DMOE_PATH_F16_GEMM  F16 experts on the f16 MFMA grouped GEMM
- *   DMOE_PATH_GEMV      every other type / shape mix (F32 experts; widths
+ *   DMOE_PATH_Q6K_MFMA  Q6_K dense MLP, step-tail LM head or attention
+ *                       projections on int8 MFMA tiles (few-token kernel, in
+ *                       chunks of 32 tokens)
+ *   DMOE_PATH_GEMV      every other type / shape mix (F32 experts; Q6_K
+ *                       routed or shared experts; widths
  *                       that are not whole MFMA work items; a shared expert
  *                       whose type or width differs from the routed ones)
  * Returns -1 for a NULL layer. */
@@ -258,6 +266,7 @@ void dmoe_layer_free(dmoe_layer *layer);
 #define DMOE_PATH_Q4K_MFMA  1
 #define DMOE_PATH_Q80_MFMA  2
 #define DMOE_PATH_F16_GEMM  3
+#define DMOE_PATH_Q6K_MFMA  4
 int  dmoe_layer_kernel_path(const dmoe_layer *layer);
 
 /* moe_out = MoE(x) for host buffers x, y of n_tokens*n_embd floats.

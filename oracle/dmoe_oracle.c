@@ -150,6 +150,7 @@ size_t dmo_row_size(int32_t type, int64_t n)
     case DMOE_TYPE_Q8_0: return (n % 32) ? 0 : (size_t)(n / 32) * sizeof(dmo_block_q8_0);
     case DMOE_TYPE_Q4_K: return (n % 256) ? 0 : (size_t)(n / 256) * sizeof(dmo_block_q4_K);
     case DMO_TYPE_Q8_K:  return (n % 256) ? 0 : (size_t)(n / 256) * sizeof(dmo_block_q8_K);
+    case DMOE_TYPE_Q6_K: return (n % 256) ? 0 : (size_t)(n / 256) * sizeof(dmo_block_q6_K);
     default: return 0;
     }
 }
@@ -163,6 +164,7 @@ int32_t dmo_vec_dot_type(int32_t type)
     case DMOE_TYPE_F16:  return DMOE_TYPE_F16;
     case DMOE_TYPE_Q8_0: return DMOE_TYPE_Q8_0;
     case DMOE_TYPE_Q4_K: return DMO_TYPE_Q8_K;
+    case DMOE_TYPE_Q6_K: return DMO_TYPE_Q8_K;
     default: return -1;
     }
 }
@@ -178,6 +180,21 @@ void dmo_q4K_scale_min(int j, const uint8_t *q, uint8_t *sc, uint8_t *m)
         *sc = (uint8_t)((q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4));
         *m  = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
     }
+}
+
+/* The 6-bit quant of weight i (0..255) of a Q6_K super-block, in 0..63
+ * (ggml-internal block_q6_K layout): in half h = i / 128, at r = i % 128,
+ * quarter k = r / 32 and l = r % 32, the low 4 bits are the low (k < 2) or
+ * high (k >= 2) nibble of ql[64 h + l + 32 (k & 1)] and the high 2 bits are
+ * bits 2k, 2k + 1 of qh[32 h + l].  Weight i belongs to sub-block i / 16,
+ * whose scale is scales[i / 16]. */
+int dmo_q6K_quant(const dmo_block_q6_K *b, int i)
+{
+    const int h = i >> 7, r = i & 127, k = r >> 5, l = r & 31;
+    const uint8_t lb = b->ql[64 * h + l + 32 * (k & 1)];
+    const int lo = (k >> 1) ? (lb >> 4) : (lb & 0x0f);
+    const int hi = (b->qh[32 * h + l] >> (2 * k)) & 3;
+    return lo | (hi << 4);
 }
 
 int dmo_dequant_row(int32_t type, const void *src, float *dst, int64_t n)
@@ -213,6 +230,20 @@ int dmo_dequant_row(int32_t type, const void *src, float *dst, int64_t n)
                 const uint8_t *q = b[i].qs + 32 * c;
                 for (int l = 0; l < 32; l++) y[64 * c + l]      = d0 * (float)(q[l] & 0x0f) - mm0;
                 for (int l = 0; l < 32; l++) y[64 * c + 32 + l] = d1 * (float)(q[l] >> 4) - mm1;
+            }
+        }
+        return 0;
+    }
+    case DMOE_TYPE_Q6_K: {
+        /* w = d * sc * (q - 32), as ggml's dequantize_row_q6_K evaluates it:
+         * (d * sc) first, then times the signed quant (ggml-internal) */
+        if (n % 256) return -1;
+        const dmo_block_q6_K *b = (const dmo_block_q6_K *)src;
+        for (int64_t i = 0; i < n / 256; i++) {
+            const float d = dmo_f16_to_f32(b[i].d);
+            for (int v = 0; v < 256; v++) {
+                const float ds = d * (float)b[i].scales[v >> 4];
+                dst[i * 256 + v] = ds * (float)(dmo_q6K_quant(&b[i], v) - 32);
             }
         }
         return 0;
@@ -336,6 +367,61 @@ static void quant_q4_K_block(const float *x, dmo_block_q4_K *y)
             y->qs[32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
 }
 
+/* Writes the 6-bit quant q (0..63) of weight i into a Q6_K block (the
+ * inverse of dmo_q6K_quant). */
+static void q6K_put(dmo_block_q6_K *b, int i, int q)
+{
+    const int h = i >> 7, r = i & 127, k = r >> 5, l = r & 31;
+    uint8_t *lb = &b->ql[64 * h + l + 32 * (k & 1)];
+    if (k >> 1)
+        *lb = (uint8_t)((*lb & 0x0f) | ((q & 15) << 4));
+    else
+        *lb = (uint8_t)((*lb & 0xf0) | (q & 15));
+    uint8_t *hb = &b->qh[32 * h + l];
+    *hb = (uint8_t)((*hb & ~(3 << (2 * k))) | (((q >> 4) & 3) << (2 * k)));
+}
+
+/* Synthetic Q6_K quantiser.  Not ggml's make_qx_quants search: per 16-weight
+ * sub-block the value of largest magnitude (first on ties) v_j sets the
+ * signed scale s_j = -v_j / 32 (so v_j maps to quant -32, as ggml's
+ * quantiser maps its extreme value); the super-block's s of largest
+ * magnitude sets d = -s_max / 128 (f16), sc_j = min(127, nearest(s_j / d))
+ * in -128..127, q = clamp(nearest(x / (d sc_j)), -32, 31) + 32.  Scales and
+ * d take both signs, as ggml's do.  The same steps run on the GPU in
+ * dmoe_quantize_device. */
+static void quant_q6_K_block(const float *x, dmo_block_q6_K *y)
+{
+    float sj[16];
+    float smax = 0.0f, samax = 0.0f;
+    for (int j = 0; j < 16; j++) {
+        float amax = 0.0f, vmax = 0.0f;
+        for (int l = 0; l < 16; l++) {
+            const float a = fabsf(x[16 * j + l]);
+            if (a > amax) { amax = a; vmax = x[16 * j + l]; }
+        }
+        sj[j] = -vmax / 32.0f;
+        if (amax / 32.0f > samax) { samax = amax / 32.0f; smax = sj[j]; }
+    }
+    memset(y, 0, sizeof(*y));
+    if (samax == 0.0f) return;
+    const uint16_t dh = dmo_f32_to_f16(-smax / 128.0f);
+    const float d = dmo_f16_to_f32(dh);
+    y->d = dh;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int j = 0; j < 16; j++) {
+        int sc = dmo_nearest_int(sj[j] * id);
+        sc = sc < -128 ? -128 : sc > 127 ? 127 : sc;
+        y->scales[j] = (int8_t)sc;
+        const float ds = d * (float)sc;
+        for (int l = 0; l < 16; l++) {
+            int q = 0;
+            if (ds != 0.0f) q = dmo_nearest_int(x[16 * j + l] / ds);
+            q = q < -32 ? -32 : q > 31 ? 31 : q;
+            q6K_put(y, 16 * j + l, q + 32);
+        }
+    }
+}
+
 int dmo_quantize_rows(int32_t type, const float *src, void *dst,
                       int64_t nrows, int64_t n_per_row, int n_threads)
 {
@@ -358,6 +444,10 @@ int dmo_quantize_rows(int32_t type, const float *src, void *dst,
         case DMOE_TYPE_Q4_K:
             for (int64_t b = 0; b < n_per_row / 256; b++)
                 quant_q4_K_block(x + 256 * b, (dmo_block_q4_K *)y + b);
+            break;
+        case DMOE_TYPE_Q6_K:
+            for (int64_t b = 0; b < n_per_row / 256; b++)
+                quant_q6_K_block(x + 256 * b, (dmo_block_q6_K *)y + b);
             break;
         default: break;
         }
@@ -446,6 +536,29 @@ static float dot_q4K(int64_t n, const dmo_block_q4_K *w, const dmo_block_q8_K *x
     return s;
 }
 
+/* Q6_K x Q8_K: per super-block
+ *   sumi = sum_j sc_j * sum_{i in j} (q_i - 32) * xq_i     (exact int; 16
+ *          sub-blocks of 16, |sumi| < 2^31)
+ *   s   += (fp16(d) * xd) * sumi                          (binary32)
+ * ggml's vec_dot_q6_K_q8_K forms the same integers; the float accumulation
+ * order of its SIMD versions is not pinned (ggml-internal). */
+static float dot_q6K(int64_t n, const dmo_block_q6_K *w, const dmo_block_q8_K *x)
+{
+    float s = 0.0f;
+    for (int64_t b = 0; b < n / 256; b++) {
+        int32_t sumi = 0;
+        for (int j = 0; j < 16; j++) {
+            int32_t sj = 0;
+            for (int l = 0; l < 16; l++)
+                sj += (int32_t)(dmo_q6K_quant(&w[b], 16 * j + l) - 32) * x[b].qs[16 * j + l];
+            sumi += (int32_t)w[b].scales[j] * sj;
+        }
+        const float d = dmo_f16_to_f32(w[b].d) * x[b].d;
+        s += d * (float)sumi;
+    }
+    return s;
+}
+
 /* The AVX-512 VNNI dots of dmoe_cpu_simd.c (bit-identical results), used
  * for the quantised types once dmo_set_simd(1) has found them supported. */
 static int g_simd = 0;
@@ -469,6 +582,7 @@ float dmo_vec_dot(int32_t wtype, int64_t n, const void *wrow, const void *xrow)
     case DMOE_TYPE_F16:  return dot_f16(n, (const uint16_t *)wrow, (const uint16_t *)xrow);
     case DMOE_TYPE_Q8_0: return dot_q8_0(n, (const dmo_block_q8_0 *)wrow, (const dmo_block_q8_0 *)xrow);
     case DMOE_TYPE_Q4_K: return dot_q4K(n, (const dmo_block_q4_K *)wrow, (const dmo_block_q8_K *)xrow);
+    case DMOE_TYPE_Q6_K: return dot_q6K(n, (const dmo_block_q6_K *)wrow, (const dmo_block_q8_K *)xrow);
     default: return NAN;
     }
 }

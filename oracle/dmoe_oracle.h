@@ -19,6 +19,10 @@
  *                                    (correctly rounded) on 10^7 inputs + edges
  *   dmo_dequant_row (F16/Q8_0/Q4_K)  pinned: hand-built blocks with known values,
  *                                    all 8 get_scale_min_k4 indices
+ *   dmo_dequant_row (Q6_K)           pinned: hand-built blocks (every quant
+ *                                    value 0..63 at every position class,
+ *                                    negative scales, the published bit
+ *                                    layout written out independently)
  *   dmo_quantize_row_act (Q8_K/Q8_0) pinned: hand-computed blocks, half-even /
  *                                    half-away rounding cases, numpy restatement
  *   dmo_vec_dot                      pinned: float64 dot of the dequantised rows
@@ -66,6 +70,9 @@ extern "C" {
 typedef struct { uint16_t d; int8_t qs[32]; } dmo_block_q8_0;            /* 34 B  */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } dmo_block_q4_K; /* 144 B */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } dmo_block_q8_K;  /* 292 B */
+/* Q6_K: low 4 bits of the 256 quants, their high 2 bits, 16 signed 8-bit
+ * sub-block scales (one per 16 weights), the f16 super-block scale */
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } dmo_block_q6_K; /* 210 B */
 
 float    dmo_f16_to_f32(uint16_t h);
 uint16_t dmo_f32_to_f16(float f);
@@ -92,6 +99,7 @@ int32_t  dmo_vec_dot_type(int32_t type);   /* activation type ggml converts to *
 
 /* get_scale_min_k4 of ggml's Q4_K */
 void     dmo_q4K_scale_min(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
+int      dmo_q6K_quant(const dmo_block_q6_K *b, int i);
 
 int      dmo_dequant_row(int32_t type, const void *src, float *dst, int64_t n);
 /* weight quantisers used to build synthetic GGUF tensors */

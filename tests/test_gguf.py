@@ -311,3 +311,33 @@ def test_optional_key_of_wrong_type(tmp_path, O, vtype, value):
         with pytest.raises(dmoe.DmoeError) as ei:
             g.moe_hparams()
         assert ei.value.code == dmoe._abi.ERR_FORMAT
+
+
+@pytest.mark.parametrize("tied", [False, True])
+def test_head_weights(tmp_path, O, tied):
+    """output_norm.weight and output.weight (Q6_K, as the reference's Q4_K
+    schemes write it) read back as a HeadWeights of views; without
+    output.weight the tied token_embd.weight (F16) is the LM head, as the
+    reference's loader falls back (src/diffuse-model.cpp:137-138)."""
+    from dmoe.gguf import GGUF
+    rng = np.random.default_rng(5)
+    H, V = 512, 96
+    norm = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    f = (rng.standard_normal((V, H)) * 0.02).astype(np.float32)
+    wr = GGUFWriter()
+    wr.add("diffuse.embedding_length", U32, H)
+    wr.add_tensor("output_norm.weight", 0, [H], norm)
+    if tied:
+        out, t = f.astype(np.float16).view(np.uint8).reshape(V, -1), 1
+        wr.add_tensor("token_embd.weight", 1, [H, V], out)
+    else:
+        out, t = O.quantize_rows(14, f), 14
+        wr.add_tensor("output.weight", 14, [H, V], out)
+    p = tmp_path / "h.gguf"
+    wr.write(p)
+    with GGUF(p) as g:
+        hw = g.head_weights()
+    assert (hw.n_embd, hw.n_vocab, hw.wtype) == (H, V, t)
+    assert np.array_equal(hw.norm, norm)
+    assert np.array_equal(hw.output, out)
+    assert hw.output.shape == (V, 210 * H // 256 if t == 14 else 2 * H)

@@ -18,8 +18,8 @@ from conftest import max_rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = {12: 1e-4, 8: 1e-4, 1: 1e-5, 0: 1e-5}
-PATH = {12: "q4k_mfma", 8: "q80_mfma", 1: "f16_gemm", 0: "gemv"}
+TOL = {12: 1e-4, 14: 1e-4, 8: 1e-4, 1: 1e-5, 0: 1e-5}
+PATH = {12: "q4k_mfma", 14: "q6k_mfma", 8: "q80_mfma", 1: "f16_gemm", 0: "gemv"}
 
 
 def _say(msg):
@@ -38,7 +38,7 @@ def _run(ctx, O, w, N, seed, tol):
     return layer, h, h_out, moe_in
 
 
-@pytest.mark.parametrize("wtype", [12, 8, 1, 0], ids=["Q4_K", "Q8_0", "F16", "F32"])
+@pytest.mark.parametrize("wtype", [12, 14, 8, 1, 0], ids=["Q4_K", "Q6_K", "Q8_0", "F16", "F32"])
 def test_attn_small(ctx, O, wtype):
     from dmoe import synth
     _say(f"case: attn H=256 4/2 heads d64 r32 B8 N40 type={wtype}")
@@ -129,4 +129,17 @@ def test_attn_rejects(ctx, O):
     with pytest.raises(dmoe.DmoeError):
         ctx.attn_forward(dl, np.zeros((8, 256), np.float32))    # not an attention layer
     dl.free()
+    layer.free()
+
+
+@pytest.mark.parametrize("N", [32, 96])
+def test_attn_flash_q6k(ctx, O, N):
+    """The flash-shaped attention half with Q6_K projections (the q6_k
+    scheme's attn tensors): 32 tokens through the fused norm and few-token
+    kernel, 96 in chunks of 32."""
+    from dmoe import synth
+    _say(f"case: attn flash shape Q6_K N={N}")
+    w = synth.host_attn(14, 6, O.quantize_rows, **synth.ATTN_FLASH)
+    layer, *_ = _run(ctx, O, w, N, 110 + N, TOL[14])
+    assert layer.kernel_path() == PATH[14]
     layer.free()

@@ -15,15 +15,15 @@ from conftest import max_rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = {12: 5e-4, 8: 5e-4, 1: 5e-4, 0: 1e-5}
-PATH = {12: "q4k_mfma", 8: "q80_mfma", 1: "f16_gemm", 0: "gemv"}
+TOL = {12: 5e-4, 14: 5e-4, 8: 5e-4, 1: 5e-4, 0: 1e-5}
+PATH = {12: "q4k_mfma", 14: "q6k_mfma", 8: "q80_mfma", 1: "f16_gemm", 0: "gemv"}
 
 
 def _say(msg):
     print(msg, flush=True)
 
 
-@pytest.mark.parametrize("wtype", [12, 8, 1, 0], ids=["Q4_K", "Q8_0", "F16", "F32"])
+@pytest.mark.parametrize("wtype", [12, 14, 8, 1, 0], ids=["Q4_K", "Q6_K", "Q8_0", "F16", "F32"])
 @pytest.mark.parametrize("N", [9, 17, 32, 40, 96])
 def test_dense_small(ctx, O, wtype, N):
     from dmoe import synth
@@ -53,10 +53,11 @@ def test_dense_gemv_shape(ctx, O):
     assert err <= TOL[0]
 
 
-@pytest.mark.parametrize("wtype", [12, 8], ids=["Q4_K", "Q8_0"])
+@pytest.mark.parametrize("wtype", [12, 8, 14], ids=["Q4_K", "Q8_0", "Q6_K"])
 def test_dense_flash_layer0(ctx, O, wtype):
     """Layer 0 of LLaDA2-flash: hidden 4096, n_ff 9216, 32 tokens, device
-    weights; host and device forwards agree bit for bit."""
+    weights (Q6_K: the ffn_edge type of the reference's Q4_K_M scheme); host
+    and device forwards agree bit for bit."""
     import torch
     from dmoe import synth
     H, FF = synth.DENSE_FLASH

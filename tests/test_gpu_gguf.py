@@ -92,3 +92,36 @@ def test_attention_from_gguf(ctx, O, tmp_path):
         _say(f"  h_out err {e1:.3e}  moe_in err {e2:.3e}")
         assert e1 <= 1e-4 and e2 <= 1e-4
         layer.free()
+
+
+def test_head_q6k_from_gguf(ctx, O, tmp_path):
+    """The step tail of a file quantised as the reference's Q4_K schemes do
+    it: output.weight Q6_K (hidden 4096, 32768 tokens of vocabulary) and an
+    F32 output_norm, read by GGUF.head_weights from the mapping, uploaded and
+    run on 32 positions against the oracle on the same mapped bytes (bars of
+    tests/test_gpu_head.py)."""
+    import torch
+    from dmoe import synth
+    from dmoe.gguf import GGUF
+    from test_gpu_head import TOL, _check
+    H, V, N = 4096, 32768, 32
+    _say(f"case: Q6_K output.weight through a GGUF file, V={V}")
+    w = synth.head_to_host(synth.device_head(H, V, 14, 31, ctx))
+    torch.cuda.empty_cache()
+    wr = GGUFWriter()
+    wr.add("diffuse.embedding_length", 4, H)
+    wr.add_tensor("output_norm.weight", 0, [H], np.ascontiguousarray(w.norm, np.float32))
+    wr.add_tensor("output.weight", 14, [H, V], w.output)
+    path = tmp_path / "head.gguf"
+    wr.write(path)
+    with GGUF(path) as g:
+        hw = g.head_weights()
+        assert (hw.n_embd, hw.n_vocab, hw.wtype) == (H, V, 14)
+        head = ctx.head_upload(hw)
+        assert head.kernel_path() == "q6k_mfma"
+        h = (synth.normal(32, synth.S_X, N * H).reshape(N, H) * 2).astype(np.float32)
+        tok, prob, lg = ctx.head_forward(head, h, 1e-6, logits=True)
+        tr, pr, lr = O.head_forward(hw, h, 1e-6)
+        err = _check(tok, prob, lg, tr, pr, lr, TOL[14])
+        _say(f"  logits max rel err {err:.3e}")
+        head.free()

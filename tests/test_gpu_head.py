@@ -18,8 +18,8 @@ from conftest import max_rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = {12: 5e-4, 8: 5e-4, 1: 5e-4, 0: 1e-5}
-PATH = {12: "q4k_mfma", 8: "q80_mfma", 1: "f16_gemm", 0: "gemv"}
+TOL = {12: 5e-4, 14: 5e-4, 8: 5e-4, 1: 5e-4, 0: 1e-5}
+PATH = {12: "q4k_mfma", 14: "q6k_mfma", 8: "q80_mfma", 1: "f16_gemm", 0: "gemv"}
 
 
 def _say(msg):
@@ -40,7 +40,7 @@ def _check(tok, prob, lg, tr, pr, lr, tol):
     return err
 
 
-@pytest.mark.parametrize("wtype", [12, 8, 1, 0], ids=["Q4_K", "Q8_0", "F16", "F32"])
+@pytest.mark.parametrize("wtype", [12, 14, 8, 1, 0], ids=["Q4_K", "Q6_K", "Q8_0", "F16", "F32"])
 @pytest.mark.parametrize("N", [32, 40])
 def test_head_small(ctx, O, wtype, N):
     from dmoe import synth
@@ -59,20 +59,22 @@ def test_head_small(ctx, O, wtype, N):
     head.free()
 
 
-@pytest.mark.parametrize("N", [1, 9, 17, 25])
-def test_head_q4k_column_blocks(ctx, O, N):
+@pytest.mark.parametrize("wtype", [12, 14], ids=["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("N", [1, 9, 17, 25, 72])
+def test_head_q4k_column_blocks(ctx, O, N, wtype):
     """The few-token projection at each column-block count (1 to 4 blocks of
-    8 tokens, the last one partly filled), Q4_K, against the oracle."""
+    8 tokens, the last one partly filled), Q4_K and Q6_K, against the
+    oracle; 72 tokens: Q6_K in chunks of 32, 32 and 8 tokens."""
     from dmoe import synth
     H, V = 512, 4096
-    _say(f"case: step tail Q4_K H={H} V={V} N={N}")
-    w = synth.host_head(H, V, 12, 90 + N, O.quantize_rows)
+    _say(f"case: step tail type={wtype} H={H} V={V} N={N}")
+    w = synth.host_head(H, V, wtype, 90 + N, O.quantize_rows)
     h = (synth.normal(91 + N, synth.S_X, N * H).reshape(N, H) * 2).astype(np.float32)
     head = ctx.head_upload(w)
-    assert head.kernel_path() == PATH[12]
+    assert head.kernel_path() == PATH[wtype]
     tok, prob, lg = ctx.head_forward(head, h, 1e-6, logits=True)
     tr, pr, lr = O.head_forward(w, h, 1e-6)
-    err = _check(tok, prob, lg, tr, pr, lr, TOL[12])
+    err = _check(tok, prob, lg, tr, pr, lr, TOL[wtype])
     _say(f"  logits max rel err {err:.3e}")
     head.free()
 
@@ -89,11 +91,12 @@ def test_head_gemv_vocab(ctx, O):
     _check(tok, prob, lg, tr, pr, lr, 1e-5)
 
 
-@pytest.mark.parametrize("wtype", [8, 12], ids=["Q8_0", "Q4_K"])
+@pytest.mark.parametrize("wtype", [8, 12, 14], ids=["Q8_0", "Q4_K", "Q6_K"])
 def test_head_flash(ctx, O, wtype):
     """LLaDA2-flash's step tail: hidden 4096, 157184 tokens of vocabulary,
-    32 positions, device weights; the device forward writes tokens and
-    probs only, equal to the host forward's."""
+    32 positions, device weights (Q6_K: the output.weight type of the
+    reference's Q4_K schemes); the device forward writes tokens and probs
+    only, equal to the host forward's."""
     import torch
     from dmoe import synth
     H, V = synth.HEAD_FLASH

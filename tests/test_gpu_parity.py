@@ -17,7 +17,7 @@ from conftest import max_rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = {0: 1e-4, 1: 1e-3, 8: 3e-3, 12: 3e-3}
+TOL = {0: 1e-4, 1: 1e-3, 8: 3e-3, 12: 3e-3, 14: 3e-3}
 TOL_CHAIN = 2e-2
 ROUTE_KEYS = ("logits", "probs", "bmax", "thr", "allowed", "idx", "weights", "counts",
               "offsets", "perm", "use_block_routing")
@@ -359,6 +359,10 @@ _GEMV_CASES = {
     "q80_ff96": (512, 96, 96, 8, 8),
     # F16 routed experts with an F32 shared expert
     "f16_f32_shared": (512, 256, 256, 1, 0),
+    # Q6_K routed and shared experts (the reference's q6_k scheme)
+    "q6k_experts": (512, 256, 256, 14, 14),
+    # Q4_K routed experts with a Q6_K shared expert
+    "q4k_q6k_shared": (512, 256, 256, 12, 14),
 }
 
 
@@ -418,7 +422,7 @@ def test_sigmoid_sweep(ctx, O):
     assert np.array_equal(probs.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("wtype", [12, 8, 1])
+@pytest.mark.parametrize("wtype", [12, 14, 8, 1])
 def test_device_quantizer_matches_oracle(ctx, O, wtype):
     import torch
     _say(f"case: device quantizer type {wtype}")

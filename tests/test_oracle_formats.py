@@ -8,7 +8,7 @@ closed-form error bounds.  No check restates the oracle's own code.
 import numpy as np
 import pytest
 
-F32, F16, Q8_0, Q4_K, Q8_K = 0, 1, 8, 12, 15
+F32, F16, Q8_0, Q4_K, Q6_K, Q8_K = 0, 1, 8, 12, 14, 15
 
 
 def test_f16_to_f32_all_halves(O):
@@ -117,6 +117,121 @@ def test_weight_quantiser_error_bound(O, t):
         assert np.sqrt((err.astype(np.float64) ** 2).mean()) < 0.15 * 0.02
 
 
+# --- Q6_K ------------------------------------------------------------------
+# block_q6_K: ql[128] (low 4 bits), qh[64] (high 2 bits), scales[16] (int8,
+# one per 16 weights), d (f16): 210 bytes.
+def _q6k_ggml_loop(ql, qh, sc, d):
+    """ggml's dequantize_row_q6_K loop structure for one super-block, written
+    out here as the published format describes it: two halves of 128 weights,
+    each of 32 columns l holding four weights l, l+32, l+64, l+96 from the
+    low nibbles of ql[l], ql[l+32], their high nibbles, and the 2-bit fields
+    0, 2, 4, 6 of qh[l]; the scale of weight l + 32 k is sc[l // 16 + 2 k]."""
+    y = np.zeros(256, np.float64)
+    for half in range(2):
+        L, H, S = ql[64 * half:], qh[32 * half:], sc[8 * half:]
+        for l in range(32):
+            is_ = l // 16
+            q1 = ((int(L[l]) & 15) | (((int(H[l]) >> 0) & 3) << 4)) - 32
+            q2 = ((int(L[l + 32]) & 15) | (((int(H[l]) >> 2) & 3) << 4)) - 32
+            q3 = ((int(L[l]) >> 4) | (((int(H[l]) >> 4) & 3) << 4)) - 32
+            q4 = ((int(L[l + 32]) >> 4) | (((int(H[l]) >> 6) & 3) << 4)) - 32
+            y[128 * half + l] = d * S[is_] * q1
+            y[128 * half + l + 32] = d * S[is_ + 2] * q2
+            y[128 * half + l + 64] = d * S[is_ + 4] * q3
+            y[128 * half + l + 96] = d * S[is_ + 6] * q4
+    return y
+
+
+def _q6k_block(ql, qh, sc, d_bits):
+    return np.frombuffer(bytes(ql) + bytes(qh) + np.asarray(sc, np.int8).tobytes() +
+                         np.array([d_bits], np.uint16).tobytes(), np.uint8)
+
+
+def test_q6k_dequant_known_block(O):
+    # d = 0.5; ql[i] = i (so nibbles vary), qh[i] = 0b11100100 (fields 0, 1, 2, 3),
+    # scales 1..8 then -1..-8
+    ql = list(range(128))
+    qh = [0xE4] * 64
+    sc = list(range(1, 9)) + [-k for k in range(1, 9)]
+    blk = _q6k_block(ql, qh, sc, 0x3800)
+    assert blk.size == 210
+    y = O.dequant_rows(Q6_K, blk, 1, 256)[0]
+    # worked by hand:
+    #  w0:   low nibble of ql[0]=0, qh field 0 = 0  -> q=0  -> 0.5*1*(0-32)  = -16
+    #  w33:  low nibble of ql[33]=1, field 1 = 1    -> q=17 -> 0.5*sc[2]=3 * -15 = -22.5
+    #  w70:  high nibble of ql[6]=0, field 2 = 2    -> q=32 -> 0
+    #  w127: high nibble of ql[63]=3, field 3 = 3   -> q=51 -> 0.5*sc[7]=8 * 19 = 76
+    #  w200: half 1, r=72: k=2, l=8: high nibble of ql[72]=4, field 2 -> q=36 -> 0.5*sc[12]=-5 * 4 = -10
+    assert y[0] == np.float32(-16.0)
+    assert y[33] == np.float32(-22.5)
+    assert y[70] == np.float32(0.0)
+    assert y[127] == np.float32(76.0)
+    assert y[200] == np.float32(-10.0)
+    assert np.array_equal(y.astype(np.float64), _q6k_ggml_loop(ql, qh, sc, 0.5))
+
+
+def test_q6k_dequant_random_blocks(O):
+    """Every quant value at every position class, negative and zero scales,
+    negative d: the oracle's decoder against the published loop."""
+    rng = np.random.default_rng(11)
+    for trial in range(40):
+        ql = rng.integers(0, 256, 128, dtype=np.uint8)
+        qh = rng.integers(0, 256, 64, dtype=np.uint8)
+        sc = rng.integers(-128, 128, 16).astype(np.int8)
+        dh = np.float16(rng.choice([-1, 1]) * rng.uniform(1e-4, 2.0))
+        blk = _q6k_block(ql, qh, sc, dh.view(np.uint16))
+        y = O.dequant_rows(Q6_K, blk, 1, 256)[0]
+        ref = _q6k_ggml_loop(ql, qh, sc.astype(np.float64), float(dh))
+        assert np.array_equal(y.astype(np.float64), ref), trial   # exact in binary32
+
+
+def test_q6k_quantiser_nearest_step(O):
+    """The synthetic Q6_K quantiser: each weight's quant is the nearest step
+    of its sub-block's d*sc grid within -32..31, and the sub-block's value of
+    largest magnitude lands on quant -32 unless its scale had to be clamped
+    or rounded away from -v/32."""
+    rng = np.random.default_rng(12)
+    f = (rng.standard_normal((8, 1024)) * 0.02).astype(np.float32)
+    f[0, :16] = 0.0                                        # an all-zero sub-block
+    q = O.quantize_rows(Q6_K, f)
+    assert q.shape == (8, 4 * 210)
+    y = O.dequant_rows(Q6_K, q, 8, 1024).astype(np.float64)
+    blk = q.reshape(8, 4, 210)
+    d = blk[:, :, 208:210].copy().view(np.float16).astype(np.float64)[..., 0]
+    sc = blk[:, :, 192:208].view(np.int8).astype(np.float64)
+    step = (d[..., None] * sc)                               # [8, 4, 16]
+    x = f.reshape(8, 4, 16, 16).astype(np.float64)
+    qv = np.rint(y.reshape(8, 4, 16, 16) / np.where(step == 0, 1, step)[..., None])
+    assert np.all((qv >= -32) & (qv <= 31))
+    t = x / np.where(step == 0, 1, step)[..., None]
+    inside = (t > -32.5) & (t < 31.5) & (step[..., None] != 0)
+    assert np.all(np.abs(t - qv)[inside] <= 0.5 + 1e-5)
+    assert np.all(y.reshape(8, 4, 16, 16)[0, 0, 0] == 0.0)
+    err = np.abs(y - f)
+    assert np.sqrt((err ** 2).mean()) < 0.03 * 0.02
+
+
+def test_q6k_dot_known_answer(O):
+    """All quants 33 (value +1), scales 1..16, d = 1; activations all 1 with
+    d = 1: the dot is sum_j 16 (j + 1) = 2176; with the quants 31 (value -1)
+    and the activations' sign alternating per sub-block it is
+    -sum_j (-1)^j 16 (j + 1) = 128."""
+    ql = [0x11] * 128                                      # low nibbles 1
+    qh = [0xAA] * 64                                       # every field 2: q = 1 | 32 = 33
+    sc = list(range(1, 17))
+    w = _q6k_block(ql, qh, sc, 0x3C00)
+    x = np.ones((1, 256), np.float32) * 127.0
+    xq = O.quantize_act(Q8_K, x)                           # q = 127 * (-127 / 127) ... d = -1
+    xd, xqs, _ = _q8K_unpack(xq[0])
+    assert abs(O.vec_dot(Q6_K, 256, w, xq[0]) - 2176 * 127.0) <= 1e-3
+    ql2 = [0xFF] * 128                                     # low nibbles 15
+    qh2 = [0x55] * 64                                      # every field 1: q = 15 | 16 = 31
+    w2 = _q6k_block(ql2, qh2, sc, 0x3C00)
+    xs = np.repeat(np.where(np.arange(16) % 2 == 0, 1.0, -1.0), 16).astype(np.float32)[None] * 127.0
+    got = O.vec_dot(Q6_K, 256, w2, O.quantize_act(Q8_K, xs)[0])
+    assert abs(got - 127.0 * -sum((-1) ** j * 16 * (j + 1) for j in range(16))) <= 1e-3
+
+
 # --- activation quantisers (vec_dot_type) ------------------------------------
 def _q8K_unpack(b):
     d = b[:4].view(np.float32)[0]
@@ -185,9 +300,9 @@ def _act_values(at, b, n):
     return (blk[:, 4:260].view(np.int8).astype(np.float64) * d).reshape(-1)
 
 
-@pytest.mark.parametrize("t", [F32, F16, Q8_0, Q4_K])
+@pytest.mark.parametrize("t", [F32, F16, Q8_0, Q4_K, Q6_K])
 def test_vec_dot_matches_float64(O, t):
-    at = {F32: F32, F16: F16, Q8_0: Q8_0, Q4_K: Q8_K}[t]
+    at = {F32: F32, F16: F16, Q8_0: Q8_0, Q4_K: Q8_K, Q6_K: Q8_K}[t]
     rng = np.random.default_rng(2)
     n = 1024
     for trial in range(20):
