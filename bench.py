@@ -47,6 +47,10 @@ def parse():
     ap.add_argument("--prefill-steps", type=int, default=10,
                     help="steps of the 2048-token F16 prefill layer measured after the headline "
                          "(0: skip)")
+    ap.add_argument("--config-steps", type=int, default=20,
+                    help="steps of each further workload recorded under \"configs\" by the default "
+                         "run (Q8_0 at 32 tokens, Q4_K at 256 and 2048 tokens; the 32-layer chain "
+                         "takes a quarter as many); 0: skip")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the bench, run 5 plain device copies of this many MiB "
@@ -419,7 +423,8 @@ def main():
 
     cfg = synth.CONFIGS[a.config]
     if cfg.n_layers != 1:
-        return bench_stack(a, cfg)
+        print(json.dumps(stack_record(a, cfg, a.steps, a.warmup, line=True)))
+        return
     rec = bench_layer(a, cfg, a.steps, a.warmup, a.copies, 0 if a.no_cpu else a.cpu_seconds)
     out = {
         "metric": METRIC,
@@ -450,6 +455,21 @@ def main():
     if a.rows_steps > 0 and cfg.n_tokens <= 256:
         out["rows"] = bench_rows(a)
 
+    # the other single-GPU workloads of the layer, each its own record in the
+    # same run: Q8_0 experts over one 32-token block, 8 independent blocks
+    # (256 tokens) and the sampler's 2048-token window of Q4_K experts, and a
+    # denoising step through 32 stacked Q4_K layers
+    if a.config_steps > 0 and a.config == "flash_q4k":
+        recs = {}
+        for name in ("flash_q8_0", "flash_q4k_n256", "flash_q4k_n2048"):
+            r = bench_layer(a, synth.CONFIGS[name], a.config_steps, max(2, a.config_steps // 4),
+                            a.copies, 0)
+            r["unit"] = "tokens/s"
+            recs[name] = r
+        recs["stack32_q4k"] = stack_record(a, synth.CONFIGS["stack32_q4k"], max(2, a.config_steps // 4),
+                                           max(1, a.config_steps // 10))
+        out["configs"] = recs
+
     if a.copy_probe_mib:
         dev = torch.device("cuda:0")
         n = a.copy_probe_mib * (1 << 20) // 4
@@ -463,11 +483,16 @@ def main():
     print(json.dumps(out))
 
 
-def bench_stack(a, cfg):
+def stack_record(a, cfg, steps, warmup, line=False):
     """A denoising step through cfg.n_layers stacked MoE layers (all resident in
     HBM), chained h <- h + MoE_l(RMSNorm(h)) over one token block; the
     residual add and the next layer's RMSNorm run as one library kernel
-    (dmoe_residual_rmsnorm) between the layers."""
+    (dmoe_residual_rmsnorm) between the layers.  Returns the step's record:
+    tokens/s, per-layer time, the touched experts of every layer on the
+    chain's own inputs and the step's HBM roofline (the touched experts'
+    bytes of all layers over the step time).  line: the fields of a
+    stand-alone bench line as well."""
+    import numpy as np
     import torch
     import dmoe
     from dmoe import synth
@@ -477,14 +502,18 @@ def bench_stack(a, cfg):
     dev = torch.device("cuda:0")
     t0 = time.time()
     layers, keep = [], []
+    eb = sb = None
     for li in range(cfg.n_layers):
         wd = synth.device_layer(cfg, a.seed, ctx, layer=li)
+        if eb is None:
+            eb, sb = wd.expert_bytes(), wd.shared_bytes()
         layers.append(ctx.wrap_device(wd))
         keep.append((wd.gate_w, wd.gate_bias))
         # the library keeps its own tiled copy of the Q4_K experts
         wd.exp_gate = wd.exp_up = wd.exp_down = wd.sh_gate = wd.sh_up = wd.sh_down = None
         torch.cuda.empty_cache()
-    print(f"# built {cfg.n_layers} layers in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    print(f"# {cfg.name}: built {cfg.n_layers} layers in {time.time() - t0:.1f}s", file=sys.stderr,
+          flush=True)
     h0 = torch.from_numpy(synth.make_x(cfg, a.seed)).to(dev)
     y = torch.empty_like(h0)
     x = torch.empty_like(h0)
@@ -500,37 +529,45 @@ def bench_stack(a, cfg):
             ctx.residual_rmsnorm(h, y, x, N, H, eps, stream=sp)         # h += y; x = RMSNorm(h)
         return h
 
-    for _ in range(a.warmup):
+    # touched experts of each layer on the chain's own inputs
+    touched = []
+    h = h0.clone()
+    ctx.residual_rmsnorm(h, None, x, N, H, eps, stream=sp)
+    for L in layers:
+        torch.cuda.synchronize(dev)
+        _, dbg = ctx.forward(L, x.cpu().numpy(), debug=True)
+        touched.append(int((dbg["counts"] > 0).sum()))
+        ctx.forward_device(L, x, N, y, sp)
+        ctx.residual_rmsnorm(h, y, x, N, H, eps, stream=sp)
+    torch.cuda.synchronize(dev)
+
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
-    for _ in range(a.steps):
+    for _ in range(steps):
         step()
     ev1.record(stream)
     torch.cuda.synchronize(dev)
-    ms_step = ev0.elapsed_time(ev1) / a.steps
+    ms_step = ev0.elapsed_time(ev1) / steps
     ctx.profile(True)
     step()
     torch.cuda.synchronize(dev)
     prof = ctx.profile_read()
     ctx.profile(False)
     stages = {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.items()}
-    # touched experts per layer (routing of the chain's inputs)
-    out = {
-        "metric": METRIC,
-        "value": round(N / (ms_step * 1e-3), 1),
+    sec = ms_step * 1e-3
+    t_bytes = sum(touched) * eb
+    all_bytes = t_bytes + cfg.n_layers * (sb + E * H * 4 + E * 4 + 2 * N * H * 4 + 4 * N * H * 4)
+    rec = {
+        "value": round(N / sec, 1),
         "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
         "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "steps": steps,
+        "warmup": warmup,
         "dtype": "i8",
-        "data": "synthetic: random-init weights N(0,0.02) quantised on the GPU, x ~ N(0,1)",
         "config": {
             "workload": (f"{cfg.name}: {cfg.n_layers} stacked LLaDA2 MoE layers (hidden {H}, {E} "
                          f"experts, moe_ff {FF}, top-{K} within capacity {cfg.capacity}, Q4_K, "
@@ -538,11 +575,28 @@ def bench_stack(a, cfg):
             "n_tokens": N,
             "n_layers": cfg.n_layers,
             "expert_type": dmoe.TYPE_NAMES[cfg.wtype],
+            "touched_experts_per_layer": touched,
         },
+        # every layer streams its touched experts once per step: the step is
+        # HBM bound
+        "roofline": {"bound": "hbm", "kernel": "whole step (all layers)",
+                     "achieved": round(t_bytes / sec / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(t_bytes / sec / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "traffic_source": None, "algorithmic_bytes": t_bytes,
+                     "bytes_are": "touched experts' weights of all layers"},
         "layer_us": round(ms_step * 1e3 / cfg.n_layers, 2),
+        "step": {"bytes": all_bytes, "hbm_frac": round(all_bytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+                 "touched_expert_frac": round(t_bytes / sec / 1e9 / HBM_PEAK_GBS, 4)},
         "stage_us": stages,
     }
-    print(json.dumps(out))
+    del layers, keep, x, y, h0, h
+    ctx.close()
+    torch.cuda.empty_cache()
+    if line:
+        rec = {"metric": METRIC, **rec, "n_gpus": 1, "higher_is_better": True, "scaling": "weak",
+               "vs_baseline": None,
+               "data": "synthetic: random-init weights N(0,0.02) quantised on the GPU, x ~ N(0,1)"}
+    return rec
 
 
 if __name__ == "__main__":
