@@ -342,13 +342,31 @@ int q4k_column_blocks(const KernelSwitches &sw, const dmoe_hparams &hp, int N)
     return avg >= 64 ? 4 : avg >= 32 ? 2 : 1;
 }
 
+// Many tokens per expert (pairs per expert averaged over all experts, N k / E,
+// of 8 or more: the flash layer from 256 tokens on): the Q4_K products run on
+// the tile kernels of k_expert_tile.hip, units of up to 128 pairs of an
+// expert (eight column blocks), h through HBM as f32 and one conversion.
+// DMOE_Q4K_TILE = 0 / 1 turns the choice off / on for every N (with the
+// shapes the tile kernels take).
+bool use_tile_path(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
+                   int N)
+{
+    if (!use_mfma_path(hp, wtype, stype, shared) ||
+        !expert_tile_ok(hp.n_embd, hp.moe_ff, hp.shared_ff, shared))
+        return false;
+    if (sw.q4k_tile >= 0) return sw.q4k_tile == 1;
+    if (sw.q4k_column_blocks) return false;
+    const long avg = (long)N * hp.top_k / (hp.n_experts > 0 ? hp.n_experts : 1);
+    return avg >= 8;
+}
+
 // Few tokens of Q4_K experts: the down products and the combine run as one
 // launch over 16-row tiles of every expert (k_down_rows.hip); it takes the
 // 16-pair work list.
 bool use_down_rows(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
                    int N)
 {
-    return use_mfma_path(hp, wtype, stype, shared) &&
+    return use_mfma_path(hp, wtype, stype, shared) && !use_tile_path(sw, hp, wtype, stype, shared, N) &&
            down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff) && q4k_column_blocks(sw, hp, N) == 1;
 }
 
@@ -439,8 +457,10 @@ size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t 
     const bool gemm = use_gemm_path(hp, wtype, stype, shared);
     const bool gemv = !gemm && !use_mfma_path(hp, wtype, stype, shared) &&
                       !use_q80_path(hp, wtype, stype, shared);
+    const bool tile = use_tile_path(sw, hp, wtype, stype, shared, N);
     t.wl.chunk = gemm ? GM
-                      : EXPERT_CHUNK * (use_mfma_path(hp, wtype, stype, shared) ? q4k_column_blocks(sw, hp, N) : 1);
+                 : tile ? expert_tile_chunk()
+                        : EXPERT_CHUNK * (use_mfma_path(hp, wtype, stype, shared) ? q4k_column_blocks(sw, hp, N) : 1);
     t.wl.n_ec = (int32_t *)take(4);
     t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
     t.wl.ec_chunk = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
@@ -451,6 +471,11 @@ size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t 
         if (shared) {
             t.axs = take_act(take, N, H, true);
             t.ahs = take_act(take, N, SF, true);
+        }
+        if (tile) {
+            // the tile kernels' f32 h, converted by one launch
+            t.h = (float *)take((size_t)P * FF * 4);
+            if (shared) t.hs = (float *)take((size_t)N * SF * 4);
         }
     }
     if (use_q80_path(hp, wtype, stype, shared)) {
@@ -639,6 +664,19 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.ahs = w.ahs;
         job.ye = w.ye;
         job.ys = w.ys;
+        if (use_tile_path(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+            // many tokens per expert: the tile kernels, h converted between them
+            STAGE(ST_GATEUP, launch_expert_tile(0, job, s));
+            PrepJob hj[2];
+            int nhj = 0;
+            hj[nhj++] = PrepJob{w.h, N * K, FF, ACT_Q8K, w.ah};
+            if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, ACT_SPLIT, w.ahs};
+            STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
+            STAGE(ST_DOWN, launch_expert_tile(1, job, s));
+            STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
+                                             K, H, y, s));
+            return DMOE_OK;
+        }
         // the gate/up launch converts h to the down products' layout itself
         STAGE(ST_GATEUP, expert(0, job));
         const bool span = use_down_span(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N);
@@ -1581,6 +1619,10 @@ KernelSwitches read_kernel_switches()
     }
     sw.down_fused = flag("DMOE_DOWN_FUSED");
     sw.gateup_lds = flag("DMOE_GATEUP_LDS");
+    if (const char *v = getenv("DMOE_Q4K_TILE")) {
+        const int n = atoi(v);
+        if (n == 0 || n == 1) sw.q4k_tile = n;
+    }
     return sw;
 }
 

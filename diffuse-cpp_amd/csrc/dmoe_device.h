@@ -9,6 +9,16 @@
 
 namespace dmoe {
 
+// The f32 epilogue of one Q4_K super-block product: acc + dx (d S - dmin M),
+// rounded the same way in every kernel whatever its file's contraction
+// setting: d S rounded, then two fused multiply-adds.  (Left to
+// contraction, the compiler fused the expression differently in different
+// inlining contexts, and kernels meant to give the same bits did not.)
+__device__ __forceinline__ float q4k_epi(float acc, float dx, float d, float S, float dmin, float M)
+{
+    return __builtin_fmaf(dx, __builtin_fmaf(-dmin, M, d * S), acc);
+}
+
 // exp(x) in binary64 rounded once to binary32.  Cody-Waite reduction
 // x = k ln2 + r (ln2 split into a 32-significant-bit head and a tail, so k*head
 // is exact), exp(r) by its degree-13 Taylor polynomial in Horner form with

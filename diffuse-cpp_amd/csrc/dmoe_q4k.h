@@ -163,7 +163,7 @@ __device__ __forceinline__ void compute_sb(const Q4KTile (&cur)[NT], const uint8
         s2 = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, bm, s2, 0, 0, 0);
         const float d = h16f(t.h.x & 0xffffu), dmin = h16f(t.h.x >> 16);
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[r][i] += dx[i] * (d * (float)isum[i] - dmin * s2[i]);
+        for (int i = 0; i < 4; i++) acc[r][i] = q4k_epi(acc[r][i], dx[i], d, (float)isum[i], dmin, s2[i]);
     }
 }
 
@@ -244,7 +244,7 @@ __device__ __forceinline__ void compute_folded(const Q4KFolded &f, const uint8_t
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int isum = 8 * sh[i] + sl[i];
-        acc[i] += dx[i] * (f.d * (float)isum - f.dmin * s2[i]);
+        acc[i] = q4k_epi(acc[i], dx[i], f.d, (float)isum, f.dmin, s2[i]);
     }
 }
 

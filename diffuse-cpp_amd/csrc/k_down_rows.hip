@@ -25,7 +25,7 @@
 // Results stay in LDS ([pair][16] and [token][16] f32); after a barrier each
 // output (token, row) is the left fold of its slots' products in slot order
 // plus the shared expert's value, as k_combine computes it.
-#include "dmoe_internal.h"
+#include "dmoe_device.h"
 
 namespace dmoe {
 
@@ -114,7 +114,7 @@ __device__ __forceinline__ void dr_compute(const DrOps &o, int g, float (&acc)[4
         dx[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((4 * g + i) << 2,
                                                                        __builtin_bit_cast(int, o.dself)));
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] += dx[i] * (d * (float)isum[i] - dmin * s2[i]);
+    for (int i = 0; i < 4; i++) acc[i] = q4k_epi(acc[i], dx[i], d, (float)isum[i], dmin, s2[i]);
 }
 
 __global__ __launch_bounds__(DR_WAVES * 64) void k_down_rows(DownRowsJob job)

@@ -117,8 +117,8 @@ def test_flash_layer(ctx, O, name):
     (Q4_K, 256 tokens, each block its own allowed set), the sampler's 512-
     and 768-token windows (one column block with more pairs than the
     register-ring kernel's LDS routing tables hold), its 1024- and 2048-token
-    windows (Q4_K items of 2 and 4 column blocks) and the 2048-token F16
-    prefill."""
+    windows and the 2048-token F16 prefill.  From 256 tokens the Q4_K layers
+    run on the tile kernels (many tokens per expert)."""
     import torch
     import dmoe
     from dmoe import synth
@@ -185,10 +185,14 @@ def test_down_span_bit_exact(ctx, name, monkeypatch):
     x = synth.make_x(cfg, 27, cfg.n_tokens)
     xo = synth.make_x(cfg, 28, cfg.n_tokens)
     n2 = cfg.n_tokens // 2 + 3
-    c = _ctx_with(monkeypatch, {"DMOE_DOWN_FUSED": "1"})
+    # (the few-token kernels at every size: 96 and 128 tokens of the small
+    # layer would otherwise take the tile kernels)
+    c = _ctx_with(monkeypatch, {"DMOE_DOWN_FUSED": "1", "DMOE_Q4K_TILE": "0"})
     ref = [c.forward(layer, a) for a in (x, xo, x[:n2], xo[:n2])]
     c.close()
-    got = [ctx.forward(layer, a) for a in (xo, x, xo[:n2], x[:n2])]
+    c = _ctx_with(monkeypatch, {"DMOE_Q4K_TILE": "0"})
+    got = [c.forward(layer, a) for a in (xo, x, xo[:n2], x[:n2])]
+    c.close()
     for r, g in zip(ref, (got[1], got[0], got[3], got[2])):
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32))
 
@@ -213,10 +217,46 @@ def test_gateup_register_ring_bit_exact(ctx, name, monkeypatch):
     layer = ctx.wrap_device(wd)
     x = synth.make_x(cfg, 29, cfg.n_tokens)
     xo = synth.make_x(cfg, 30, cfg.n_tokens)
-    c = _ctx_with(monkeypatch, {"DMOE_GATEUP_LDS": "1"})
+    # (the one-column-block kernels at every size: from 256 tokens the flash
+    # layer would otherwise take the tile kernels)
+    c = _ctx_with(monkeypatch, {"DMOE_GATEUP_LDS": "1", "DMOE_Q4K_TILE": "0"})
     ref = [c.forward(layer, a) for a in (x, xo)]
     c.close()
-    got = [ctx.forward(layer, a) for a in (xo, x)]
+    c = _ctx_with(monkeypatch, {"DMOE_Q4K_TILE": "0"})
+    got = [c.forward(layer, a) for a in (xo, x)]
+    c.close()
+    assert np.array_equal(got[1].view(np.uint32), ref[0].view(np.uint32))
+    assert np.array_equal(got[0].view(np.uint32), ref[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["flash_q4k_n256", "flash_q4k_n2048", "small_q4k_n40", "small_q4k_n96",
+                                  "small_q4k_n2048", "small_q4k_n1000"])
+def test_tile_path_bit_exact(ctx, name, monkeypatch):
+    """Q4_K products of many tokens per expert on the tile kernels (units of
+    up to 128 pairs of an expert, h through HBM and one conversion) against
+    items of four column blocks: the same products in the same order, so the
+    layer outputs are identical bit for bit.  Each tile call follows one on
+    other inputs of the same size (the work counters and h left by that call
+    must not leak into this one); 40 and 1000 tokens run without block
+    routing, and the small layer's shared expert spans partial units."""
+    import dmoe
+    from dmoe import synth
+    if name.startswith("small"):
+        cfg = _small(dmoe, synth, 12, int(name.rsplit("_n", 1)[1]))
+    else:
+        cfg = synth.CONFIGS[name]
+    _say(f"case: tile kernels vs four column blocks, {name}")
+    wd = synth.device_layer(cfg, 33, ctx)
+    layer = ctx.wrap_device(wd)
+    x = synth.make_x(cfg, 33, cfg.n_tokens)
+    xo = synth.make_x(cfg, 34, cfg.n_tokens)
+    c = _ctx_with(monkeypatch, {"DMOE_Q4K_COLUMN_BLOCKS": "4", "DMOE_Q4K_TILE": "0"})
+    ref = [c.forward(layer, a) for a in (x, xo)]
+    c.close()
+    c = _ctx_with(monkeypatch, {"DMOE_Q4K_TILE": "1"})
+    got = [c.forward(layer, a) for a in (xo, x)]
+    c.close()
+    assert np.isfinite(ref[0]).all()
     assert np.array_equal(got[1].view(np.uint32), ref[0].view(np.uint32))
     assert np.array_equal(got[0].view(np.uint32), ref[1].view(np.uint32))
 
