@@ -342,20 +342,22 @@ int q4k_column_blocks(const KernelSwitches &sw, const dmoe_hparams &hp, int N)
     return avg >= 64 ? 4 : avg >= 32 ? 2 : 1;
 }
 
+bool use_q80_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared);
+
 // Many tokens per expert (pairs per expert averaged over all experts, N k / E,
-// of 8 or more: the flash layer from 256 tokens on): the Q4_K products run on
-// the tile kernels of k_expert_tile.hip, units of up to 128 pairs of an
-// expert (eight column blocks), h through HBM as f32 and one conversion.
-// DMOE_Q4K_TILE = 0 / 1 turns the choice off / on for every N (with the
-// shapes the tile kernels take).
+// of 8 or more: the flash layer from 256 tokens on): the Q4_K and Q8_0
+// products run on the tile kernels of k_expert_tile.hip (units of up to 32
+// pairs of an expert whose activations stay in LDS for the whole reduction,
+// h through HBM as f32 and one conversion).  DMOE_Q4K_TILE = 0 / 1 turns the
+// choice off / on for every N (with the shapes the tile kernels take).
 bool use_tile_path(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
                    int N)
 {
-    if (!use_mfma_path(hp, wtype, stype, shared) ||
+    if (!(use_mfma_path(hp, wtype, stype, shared) || use_q80_path(hp, wtype, stype, shared)) ||
         !expert_tile_ok(hp.n_embd, hp.moe_ff, hp.shared_ff, shared))
         return false;
     if (sw.q4k_tile >= 0) return sw.q4k_tile == 1;
-    if (sw.q4k_column_blocks) return false;
+    if (sw.q4k_column_blocks && wtype == DMOE_TYPE_Q4_K) return false;
     const long avg = (long)N * hp.top_k / (hp.n_experts > 0 ? hp.n_experts : 1);
     return avg >= 8;
 }
@@ -484,6 +486,10 @@ size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t 
         if (shared) {
             t.axs = take_act(take, N, H, true, true);
             t.ahs = take_act(take, N, SF, true, true);
+        }
+        if (tile) {
+            t.h = (float *)take((size_t)P * FF * 4);
+            if (shared) t.hs = (float *)take((size_t)N * SF * 4);
         }
     }
     if (gemm) {
@@ -669,8 +675,8 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
             STAGE(ST_GATEUP, launch_expert_tile(0, job, s));
             PrepJob hj[2];
             int nhj = 0;
-            hj[nhj++] = PrepJob{w.h, N * K, FF, ACT_Q8K, w.ah};
-            if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, ACT_SPLIT, w.ahs};
+            hj[nhj++] = PrepJob{w.h, N * K, FF, q8 ? ACT_Q80 : ACT_Q8K, w.ah};
+            if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, q8 ? ACT_SPLIT32 : ACT_SPLIT, w.ahs};
             STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
             STAGE(ST_DOWN, launch_expert_tile(1, job, s));
             STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,

@@ -33,6 +33,7 @@
 // rows x 256 int8, 16 x 8 scales) into the workgroup's 3-stage ring, with
 // LDS-direct loads; one barrier per step publishes the activations.
 #include "dmoe_prep.h"
+#include "dmoe_q80.h"
 
 namespace dmoe {
 
@@ -287,40 +288,11 @@ __global__ __launch_bounds__(Q8_WAVES * 64, 2) void k_expert_q80(MoeJob job)
             const uint4 wd = wt[r16];
             const uint4 w01 = wt[(1 + 4 * g) * 16 + r16], w23 = wt[(2 + 4 * g) * 16 + r16];
             const uint4 w45 = wt[(3 + 4 * g) * 16 + r16], w67 = wt[(4 + 4 * g) * 16 + r16];
-            // activation operands: row r16, units 4g .. 4g+3 (swizzled)
-            const uint4 *ap = reinterpret_cast<const uint4 *>(ast + r16 * 256);
-            const uint4 a01 = ap[(4 * g + 0) ^ (r16 & 11)], a23 = ap[(4 * g + 1) ^ (r16 & 11)];
-            const uint4 a45 = ap[(4 * g + 2) ^ (r16 & 11)], a67 = ap[(4 * g + 3) ^ (r16 & 11)];
-            const long a[8] = {
-                (long)((uint64_t)a01.y << 32 | a01.x), (long)((uint64_t)a01.w << 32 | a01.z),
-                (long)((uint64_t)a23.y << 32 | a23.x), (long)((uint64_t)a23.w << 32 | a23.z),
-                (long)((uint64_t)a45.y << 32 | a45.x), (long)((uint64_t)a45.w << 32 | a45.z),
-                (long)((uint64_t)a67.y << 32 | a67.x), (long)((uint64_t)a67.w << 32 | a67.z)};
-            const long w[8] = {
-                (long)((uint64_t)w01.y << 32 | w01.x), (long)((uint64_t)w01.w << 32 | w01.z),
-                (long)((uint64_t)w23.y << 32 | w23.x), (long)((uint64_t)w23.w << 32 | w23.z),
-                (long)((uint64_t)w45.y << 32 | w45.x), (long)((uint64_t)w45.w << 32 | w45.z),
-                (long)((uint64_t)w67.y << 32 | w67.x), (long)((uint64_t)w67.w << 32 | w67.z)};
-            const uint32_t wds[4] = {wd.x, wd.y, wd.z, wd.w};
-            // all eight block products first, then their scales (the MFMA
-            // results are read only after the last one is issued)
-            v4i sj[8];
-#pragma unroll
-            for (int jb = 0; jb < 8; jb++) {
-                const v4i z = {0, 0, 0, 0};
-                sj[jb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[jb], w[jb], z, 0, 0, 0);
-            }
+            long a[8], w[8];
+            q80_act_ops(ast, r16, g, a);
+            q80_w_ops(w01, w23, w45, w67, w);
             float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int jb = 0; jb < 8; jb++) {
-                const v4i si = sj[jb];
-                const float dw = q8_h2f(jb & 1 ? wds[jb >> 1] >> 16 : wds[jb >> 1] & 0xffffu);
-                // scales of block jb for activation rows 4g .. 4g+3
-                const float4 dx = *reinterpret_cast<const float4 *>(ast + Q8_AD_OFF + jb * 64 + 16 * g);
-                const float dxa[4] = {dx.x, dx.y, dx.z, dx.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) sum[i] += (float)si[i] * (dw * dxa[i]);
-            }
+            q80_products(a, w, wd, ast, g, sum);
 #pragma unroll
             for (int q = 0; q < IT; q++)
                 if (it == q)

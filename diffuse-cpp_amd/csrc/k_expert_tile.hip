@@ -36,6 +36,7 @@
 // rounded by q4k_epi), so the results equal the column-block kernels' bit
 // for bit.
 #include "dmoe_q4k.h"
+#include "dmoe_q80.h"
 
 #include <type_traits>
 
@@ -110,6 +111,89 @@ __device__ __forceinline__ int xr_arow(const XrItem &I, const int32_t *s_pids, i
 }
 
 // ---------------------------------------------------------------------------
+// Weight formats.  Each gives the bytes of one 16-row tile step (TILE) and of
+// one 16-row block's activation step in LDS (ASTEP), a lane's share of a
+// tile step (Tile, load), the products of two tiles against one activation
+// block (compute2) and the loads of one activation step (load_act: the
+// lane's source rows rq (rows 4j + lane / 16 of the block, for the quants)
+// and ra (its row for the scale and sum loads)).
+
+// Q4_K (ggml's vec_dot_q4_K_q8_K; activations Q8_K, or two int8 digits for
+// the shared expert).
+struct FmtQ4K {
+    static constexpr int TILE = TILE_BYTES;
+    static constexpr int ASTEP = ASTEP_BYTES;
+    typedef Q4KTile Tile;
+    __device__ static void load(Tile &t, const uint8_t *run, int r16, int g)
+    {
+        const uint4 *p = reinterpret_cast<const uint4 *>(run);
+        t.h = xt_ld_nt16(p + r16);
+        t.q0 = xt_ld_nt16(p + (1 + 2 * g) * 16 + r16);
+        t.q1 = xt_ld_nt16(p + (2 + 2 * g) * 16 + r16);
+    }
+    __device__ static void compute2(const Tile (&t)[2], const uint8_t *ast, int r16, int g, float (&acc)[2][4])
+    {
+        compute_sb<2>(t, ast, r16, g, acc);
+    }
+    // the scale / sum loads: bs by lanes 0..31 (row lane / 2, half lane % 2),
+    // d by lanes 0..15 (row lane)
+    __device__ static int arow_lane(int lane, int which) { return which == 0 ? (lane >> 1) & 15 : lane & 15; }
+    __device__ static void load_act(const ActI8 &act, int Kin, int sb, const int (&rq)[4], const int (&ra)[2],
+                                    uint8_t *st, int lane)
+    {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = 4 * j + (lane >> 4);
+            lds_load16(act.q + (size_t)rq[j] * Kin + sb * 256 + (((lane & 15) ^ (row & 11)) * 16), st + 1024 * j);
+        }
+        if (lane < 32) lds_load16(act.bs + (size_t)ra[0] * (Kin / 16) + sb * 16 + (lane & 1) * 8, st + ABS_OFF);
+        if (lane < 16) lds_load4(act.d + (size_t)ra[1] * (Kin / 256) + sb, st + AD_OFF);
+    }
+};
+
+// Q8_0 (ggml's vec_dot_q8_0_q8_0; activations Q8_0, or two int8 digits per
+// 32 values for the shared expert).
+struct FmtQ80 {
+    static constexpr int TILE = Q80_TILE;
+    static constexpr int ASTEP = Q80_ASTEP;
+    struct Tile {
+        uint4 d, q[4];          // piece 0 of row r16; lane group g's quant pieces
+    };
+    __device__ static void load(Tile &t, const uint8_t *run, int r16, int g)
+    {
+        const uint4 *p = reinterpret_cast<const uint4 *>(run);
+        t.d = xt_ld_nt16(p + r16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) t.q[j] = xt_ld_nt16(p + (1 + 4 * g + j) * 16 + r16);
+    }
+    __device__ static void compute2(const Tile (&t)[2], const uint8_t *ast, int r16, int g, float (&acc)[2][4])
+    {
+        long a[8];
+        q80_act_ops(ast, r16, g, a);
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            long w[8];
+            q80_w_ops(t[r].q[0], t[r].q[1], t[r].q[2], t[r].q[3], w);
+            q80_products(a, w, t[r].d, ast, g, acc[r]);
+        }
+    }
+    // the scales: two loads of 64 lanes, lane -> (block 4 h + lane / 16, row lane % 16)
+    __device__ static int arow_lane(int lane, int which) { return lane & 15; }
+    __device__ static void load_act(const ActI8 &act, int Kin, int sb, const int (&rq)[4], const int (&ra)[2],
+                                    uint8_t *st, int lane)
+    {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = 4 * j + (lane >> 4);
+            lds_load16(act.q + (size_t)rq[j] * Kin + sb * 256 + (((lane & 15) ^ (row & 11)) * 16), st + 1024 * j);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            lds_load4(act.d + (size_t)ra[h] * (Kin / 32) + sb * 8 + 4 * h + (lane >> 4), st + Q80_AD_OFF + 256 * h);
+    }
+};
+
+// ---------------------------------------------------------------------------
 // gate/up: h = silu(W_gate x) * (W_up x) for 128 h rows of a unit of up to
 // 32 pairs (two column blocks), as f32.
 //
@@ -122,11 +206,11 @@ __device__ __forceinline__ int xr_arow(const XrItem &I, const int32_t *s_pids, i
 // wavefront streams its gate and up tiles to two register sets, one step
 // ahead, across item boundaries (the last step of an item loads the next
 // item's first weights: the compiler's own loads, its waits exact).
+template <class F>
 __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
 {
-    __shared__ __align__(16) uint8_t s_act[XR_MAX_SB][XR_NC * ASTEP_BYTES];
+    __shared__ __align__(16) uint8_t s_act[XR_MAX_SB][XR_NC * F::ASTEP];
     __shared__ int32_t s_pids[2][XR_CHUNK];          // routed items: their pair ids
-    static_assert(XR_NC * 16 * XR_ROWS * 4 <= XR_MAX_SB * XR_NC * ASTEP_BYTES, "h hand-over fits");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -150,7 +234,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     auto tiles = [&](const XrItem &X, const uint8_t *&tg, const uint8_t *&tu) {
         const WTensor &a = X.shared ? job.sg : job.eg;
         const WTensor &b = X.shared ? job.su : job.eu;
-        const size_t t16 = (size_t)((X.rg * XR_ROWS + 16 * wave) / 16) * nsb * TILE_BYTES;
+        const size_t t16 = (size_t)((X.rg * XR_ROWS + 16 * wave) / 16) * nsb * F::TILE;
         tg = a.data + (size_t)X.e * a.nb2 + t16;
         tu = b.data + (size_t)X.e * b.nb2 + t16;
     };
@@ -162,15 +246,9 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     int l_sb = 0;
     bool l_last = false;                   // the cursor is on the schedule's last step
     XrItem NI{};
-    auto load = [&](Q4KTile (&o)[2]) __attribute__((always_inline)) {
-        const uint4 *pg = reinterpret_cast<const uint4 *>(lg + (size_t)l_sb * TILE_BYTES);
-        const uint4 *pu = reinterpret_cast<const uint4 *>(lu + (size_t)l_sb * TILE_BYTES);
-        o[0].h = xt_ld_nt16(pg + r16);
-        o[0].q0 = xt_ld_nt16(pg + (1 + 2 * g) * 16 + r16);
-        o[0].q1 = xt_ld_nt16(pg + (2 + 2 * g) * 16 + r16);
-        o[1].h = xt_ld_nt16(pu + r16);
-        o[1].q0 = xt_ld_nt16(pu + (1 + 2 * g) * 16 + r16);
-        o[1].q1 = xt_ld_nt16(pu + (2 + 2 * g) * 16 + r16);
+    auto load = [&](typename F::Tile (&o)[2]) __attribute__((always_inline)) {
+        F::load(o[0], lg + (size_t)l_sb * F::TILE, r16, g);
+        F::load(o[1], lu + (size_t)l_sb * F::TILE, r16, g);
         if (l_sb + 1 < steps) {
             l_sb++;
         } else if (!l_last) {
@@ -183,38 +261,26 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
             }
         }
     };
-    Q4KTile o[2][2];
+    typename F::Tile o[2][2];
     NI = xr_decode(job, k + G, rg_n, n_ec, nch);
     load(o[0]);
     __syncthreads();                       // the first item's pair list
 
     for (;;) {
     // the item's activations: wavefront w loads super-blocks w, w + 8, ...
-    // of both blocks (k_gateup_rr's roles per 16-row block: q rows 4j + lane
-    // / 16 at slot lane % 16 (logical unit slot ^ (row & 11)), bs 32 lanes,
-    // d 16 lanes)
+    // of both blocks
     {
         const ActI8 &act = I.shared ? job.axs : job.ax;
         const int32_t *pids = s_pids[buf];
 #pragma unroll
         for (int c = 0; c < XR_NC; c++) {
             if (c >= I.nblk) continue;
-            const int8_t *aq[4];
+            int rq[4], ra[2];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int row = 4 * j + (lane >> 4);
-                aq[j] = act.q + (size_t)xr_arow<false>(I, pids, N, K, c, row) * H + (((lane & 15) ^ (row & 11)) * 16);
-            }
-            const uint16_t *ab = act.bs + (size_t)xr_arow<false>(I, pids, N, K, c, (lane >> 1) & 15) * (H / 16) +
-                                 (lane & 1) * 8;
-            const float *ad = act.d + (size_t)xr_arow<false>(I, pids, N, K, c, lane & 15) * nsb;
-            for (int sb = wave; sb < nsb; sb += XT_WAVES) {
-                uint8_t *st = &s_act[sb][c * ASTEP_BYTES];
+            for (int j = 0; j < 4; j++) rq[j] = xr_arow<false>(I, pids, N, K, c, 4 * j + (lane >> 4));
 #pragma unroll
-                for (int j = 0; j < 4; j++) lds_load16(aq[j] + sb * 256, st + 1024 * j);
-                if (lane < 32) lds_load16(ab + sb * 16, st + ABS_OFF);
-                if (lane < 16) lds_load4(ad + sb, st + AD_OFF);
-            }
+            for (int q = 0; q < 2; q++) ra[q] = xr_arow<false>(I, pids, N, K, c, F::arow_lane(lane, q));
+            for (int sb = wave; sb < nsb; sb += XT_WAVES) F::load_act(act, H, sb, rq, ra, &s_act[sb][c * F::ASTEP], lane);
         }
     }
     EXPERT_WAIT_VM(0);
@@ -232,10 +298,10 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
             for (int i = 0; i < 4; i++) acc[c][r][i] = 0.0f;
     // (each tile folded once for both blocks, compute_folded2, measured
     // slower: 252 VGPRs against 220, 1.41 against 1.33 ms at 2048 tokens)
-    auto step = [&](const Q4KTile (&t)[2], int s) __attribute__((always_inline)) {
+    auto step = [&](const typename F::Tile (&t)[2], int s) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < XR_NC; c++)
-            if (c < I.nblk) compute_sb<2>(t, &s_act[s][c * ASTEP_BYTES], r16, g, acc[c]);
+            if (c < I.nblk) F::compute2(t, &s_act[s][c * F::ASTEP], r16, g, acc[c]);
     };
     for (int s = 0; s < steps; s += 2) {
         load(o[1]);
@@ -286,9 +352,10 @@ constexpr int XR_DN_IT = 2;
 constexpr int XR_DN_ROWS = XR_DN_PASS * XR_DN_IT;       // 512
 constexpr int XR_DN_MAX_SB = 4;                         // moe_ff <= 1024
 
+template <class F>
 __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
 {
-    __shared__ __align__(16) uint8_t s_act[2][XR_DN_MAX_SB][XR_NC * ASTEP_BYTES];
+    __shared__ __align__(16) uint8_t s_act[2][XR_DN_MAX_SB][XR_NC * F::ASTEP];
     // pair lists of items i, i + 1 (its activations load during item i) and
     // i + 2 (loaded from perm during item i, written at its end)
     __shared__ int32_t s_pids[3][XR_CHUNK];
@@ -319,41 +386,29 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
         const ActI8 &act = X.shared ? job.ahs : job.ah;
         const int c = wave >> 2, sb = wave & 3;
         if (c >= X.nblk || sb >= nsb) return;
-        uint8_t *st = &s_act[b][sb][c * ASTEP_BYTES];
+        int rq[4], ra[2];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int row = 4 * j + (lane >> 4);
-            lds_load16(act.q + (size_t)xr_arow<true>(X, pids, N, K, c, row) * FF + sb * 256 +
-                           (((lane & 15) ^ (row & 11)) * 16),
-                       st + 1024 * j);
-        }
-        if (lane < 32)
-            lds_load16(act.bs + (size_t)xr_arow<true>(X, pids, N, K, c, (lane >> 1) & 15) * (FF / 16) + sb * 16 +
-                           (lane & 1) * 8,
-                       st + ABS_OFF);
-        if (lane < 16) lds_load4(act.d + (size_t)xr_arow<true>(X, pids, N, K, c, lane & 15) * nsb + sb, st + AD_OFF);
+        for (int j = 0; j < 4; j++) rq[j] = xr_arow<true>(X, pids, N, K, c, 4 * j + (lane >> 4));
+#pragma unroll
+        for (int q = 0; q < 2; q++) ra[q] = xr_arow<true>(X, pids, N, K, c, F::arow_lane(lane, q));
+        F::load_act(act, FF, sb, rq, ra, &s_act[b][sb][c * F::ASTEP], lane);
     };
     static_assert(XT_WAVES == 2 * XR_DN_MAX_SB && XR_NC == 2, "one (block, super-block) per wavefront");
 
     // this wavefront's tiles of pass p of item X: rows rg 512 + 256 p + 32 wave + 16 r
     auto tile0 = [&](const XrItem &X) -> const uint8_t * {
         const WTensor &W = X.shared ? job.sd : job.ed;
-        return W.data + (size_t)X.e * W.nb2 + (size_t)((X.rg * XR_DN_ROWS + 32 * wave) / 16) * nsb * TILE_BYTES;
+        return W.data + (size_t)X.e * W.nb2 + (size_t)((X.rg * XR_DN_ROWS + 32 * wave) / 16) * nsb * F::TILE;
     };
-    const size_t pass_step = (size_t)(XR_DN_PASS / 16) * nsb * TILE_BYTES;
+    const size_t pass_step = (size_t)(XR_DN_PASS / 16) * nsb * F::TILE;
     const uint8_t *lt = tile0(I);
     int l_st = 0;                          // the load cursor's step in its item
     bool l_last = false;
-    auto load = [&](Q4KTile (&o)[2]) __attribute__((always_inline)) {
+    auto load = [&](typename F::Tile (&o)[2]) __attribute__((always_inline)) {
         const int it = l_st >= nsb ? 1 : 0, sb = l_st - it * nsb;
-        const uint8_t *b = lt + (size_t)it * pass_step + (size_t)sb * TILE_BYTES;
+        const uint8_t *b = lt + (size_t)it * pass_step + (size_t)sb * F::TILE;
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(b + (size_t)r * nsb * TILE_BYTES);
-            o[r].h = xt_ld_nt16(p + r16);
-            o[r].q0 = xt_ld_nt16(p + (1 + 2 * g) * 16 + r16);
-            o[r].q1 = xt_ld_nt16(p + (2 + 2 * g) * 16 + r16);
-        }
+        for (int r = 0; r < 2; r++) F::load(o[r], b + (size_t)r * nsb * F::TILE, r16, g);
         if (l_st + 1 < steps) {
             l_st++;
         } else if (!l_last) {
@@ -367,7 +422,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
     };
     static_assert(XR_DN_IT == 2, "two passes");
 
-    Q4KTile o[2][2];
+    typename F::Tile o[2][2];
     load(o[0]);
     load_act(I, s_pids[0], 0);
     EXPERT_WAIT_VM(0);
@@ -395,10 +450,10 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
     float *out = I.shared ? job.ys : job.ye;
     const int32_t *pids = s_pids[pb];
     int c_sb = 0, c_it = 0;
-    auto step = [&](const Q4KTile (&t)[2]) __attribute__((always_inline)) {
+    auto step = [&](const typename F::Tile (&t)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < XR_NC; c++)
-            if (c < I.nblk) compute_sb<2>(t, &s_act[buf][c_sb][c * ASTEP_BYTES], r16, g, acc[c]);
+            if (c < I.nblk) F::compute2(t, &s_act[buf][c_sb][c * F::ASTEP], r16, g, acc[c]);
         if (++c_sb == nsb) {
             // the pass's results (the two digits of a shared token summed)
             const int row0 = I.rg * XR_DN_ROWS + c_it * XR_DN_PASS + 32 * wave + r16;
@@ -479,10 +534,19 @@ hipError_t launch_expert_tile(int phase, const MoeJob &job, hipStream_t s)
     const hipError_t e = device_cu_count(&n_cu);
     if (e != hipSuccess) return e;
     const int grid = ((n_cu + 7) / 8) * 8;
-    if (phase == 0)
-        hipLaunchKernelGGL(k_gu_rr, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
-    else
-        hipLaunchKernelGGL(k_dn_rr, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+    const bool q80 = job.eg.type == DMOE_TYPE_Q8_0;
+    if (!q80 && job.eg.type != DMOE_TYPE_Q4_K) return hipErrorInvalidValue;
+    if (phase == 0) {
+        if (q80)
+            hipLaunchKernelGGL(k_gu_rr<FmtQ80>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+        else
+            hipLaunchKernelGGL(k_gu_rr<FmtQ4K>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+    } else {
+        if (q80)
+            hipLaunchKernelGGL(k_dn_rr<FmtQ80>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+        else
+            hipLaunchKernelGGL(k_dn_rr<FmtQ4K>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+    }
     return hipGetLastError();
 }
 

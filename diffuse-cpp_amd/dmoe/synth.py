@@ -87,6 +87,11 @@ CONFIGS = {
     # LLaDA2-flash shape, Q8_0 experts, one 32-token block
     "flash_q8_0": LayerConfig("flash_q8_0", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q8_0,
                               TYPE_Q8_0, 32, -0.1, 0.1),
+    # Q8_0 experts over 8 blocks and over the sampler's 2048-token window
+    "flash_q8_0_n256": LayerConfig("flash_q8_0_n256", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q8_0,
+                                   TYPE_Q8_0, 256, -0.1, 0.1),
+    "flash_q8_0_n2048": LayerConfig("flash_q8_0_n2048", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q8_0,
+                                    TYPE_Q8_0, 2048, -0.1, 0.1),
     # the headline workload: Q4_K experts, one 32-token block
     "flash_q4k": LayerConfig("flash_q4k", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_Q4_K, TYPE_Q4_K,
                              32, -0.1, 0.1),

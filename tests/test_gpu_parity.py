@@ -111,14 +111,16 @@ def test_small_layer_many_items(ctx, O, wtype):
 
 
 @pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "flash_q4k_n512",
-                                  "flash_q4k_n768", "flash_q4k_n1024", "flash_q4k_n2048", "prefill_f16"])
+                                  "flash_q4k_n768", "flash_q4k_n1024", "flash_q4k_n2048", "flash_q8_0_n256",
+                                  "flash_q8_0_n2048", "prefill_f16"])
 def test_flash_layer(ctx, O, name):
     """Flash-shaped layers: one 32-token block (Q4_K, Q8_0), eight blocks
     (Q4_K, 256 tokens, each block its own allowed set), the sampler's 512-
     and 768-token windows (one column block with more pairs than the
     register-ring kernel's LDS routing tables hold), its 1024- and 2048-token
-    windows and the 2048-token F16 prefill.  From 256 tokens the Q4_K layers
-    run on the tile kernels (many tokens per expert)."""
+    windows, Q8_0 over 256 and 2048 tokens and the 2048-token F16 prefill.
+    From 256 tokens the Q4_K and Q8_0 layers run on the tile kernels (many
+    tokens per expert)."""
     import torch
     import dmoe
     from dmoe import synth
@@ -230,27 +232,33 @@ def test_gateup_register_ring_bit_exact(ctx, name, monkeypatch):
 
 
 @pytest.mark.parametrize("name", ["flash_q4k_n256", "flash_q4k_n2048", "small_q4k_n40", "small_q4k_n96",
-                                  "small_q4k_n2048", "small_q4k_n1000"])
+                                  "small_q4k_n2048", "small_q4k_n1000", "flash_q8_0_n256", "small_q80_n96",
+                                  "small_q80_n1000"])
 def test_tile_path_bit_exact(ctx, name, monkeypatch):
-    """Q4_K products of many tokens per expert on the tile kernels (units of
-    up to 128 pairs of an expert, h through HBM and one conversion) against
-    items of four column blocks: the same products in the same order, so the
-    layer outputs are identical bit for bit.  Each tile call follows one on
-    other inputs of the same size (the work counters and h left by that call
-    must not leak into this one); 40 and 1000 tokens run without block
-    routing, and the small layer's shared expert spans partial units."""
+    """Products of many tokens per expert on the tile kernels (units of up to
+    32 pairs of an expert with their activations held in LDS, h through HBM
+    and one conversion) against the item kernels (Q4_K: four column blocks;
+    Q8_0: k_expert_q80): the same products in the same order, so the layer
+    outputs are identical bit for bit.  Each tile call follows one on other
+    inputs of the same size (h and pair lists left by that call must not leak
+    into this one); 40 and 1000 tokens run without block routing, and the
+    small layer's shared expert spans partial units."""
     import dmoe
     from dmoe import synth
     if name.startswith("small"):
-        cfg = _small(dmoe, synth, 12, int(name.rsplit("_n", 1)[1]))
+        wt = 8 if "q80" in name else 12
+        cfg = _small(dmoe, synth, wt, int(name.rsplit("_n", 1)[1]))
     else:
         cfg = synth.CONFIGS[name]
-    _say(f"case: tile kernels vs four column blocks, {name}")
+    _say(f"case: tile kernels vs item kernels, {name}")
     wd = synth.device_layer(cfg, 33, ctx)
     layer = ctx.wrap_device(wd)
     x = synth.make_x(cfg, 33, cfg.n_tokens)
     xo = synth.make_x(cfg, 34, cfg.n_tokens)
-    c = _ctx_with(monkeypatch, {"DMOE_Q4K_COLUMN_BLOCKS": "4", "DMOE_Q4K_TILE": "0"})
+    ref_env = {"DMOE_Q4K_TILE": "0"}
+    if cfg.wtype == 12:
+        ref_env["DMOE_Q4K_COLUMN_BLOCKS"] = "4"
+    c = _ctx_with(monkeypatch, ref_env)
     ref = [c.forward(layer, a) for a in (x, xo)]
     c.close()
     c = _ctx_with(monkeypatch, {"DMOE_Q4K_TILE": "1"})
