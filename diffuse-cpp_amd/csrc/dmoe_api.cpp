@@ -343,23 +343,27 @@ int q4k_column_blocks(const KernelSwitches &sw, const dmoe_hparams &hp, int N)
 }
 
 bool use_q80_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared);
+bool use_gemm_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared);
 
-// Many tokens per expert (pairs per expert averaged over all experts, N k / E,
-// of 8 or more: the flash layer from 256 tokens on): the Q4_K and Q8_0
-// products run on the tile kernels of k_expert_tile.hip (units of up to 32
-// pairs of an expert whose activations stay in LDS for the whole reduction,
-// h through HBM as f32 and one conversion).  DMOE_Q4K_TILE = 0 / 1 turns the
-// choice off / on for every N (with the shapes the tile kernels take).
+// The tile kernels of k_expert_tile.hip (units of up to 32 pairs of an expert,
+// 16 for F16, whose activations stay in LDS for the whole reduction; h
+// through HBM as f32 and one conversion), by the forward's pairs per expert
+// averaged over all experts (N k / E): Q4_K and Q8_0 from 8 on (the flash
+// layer from 256 tokens; fewer take the item kernels, whose finer work
+// division fills the chip), F16 below 8 (more take the grouped GEMM of
+// 256-pair items).  DMOE_EXPERT_TILE = 0 / 1 turns the choice off / on for
+// every N (with the shapes the tile kernels take).
 bool use_tile_path(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
                    int N)
 {
-    if (!(use_mfma_path(hp, wtype, stype, shared) || use_q80_path(hp, wtype, stype, shared)) ||
+    const bool f16 = use_gemm_path(hp, wtype, stype, shared);
+    if (!(use_mfma_path(hp, wtype, stype, shared) || use_q80_path(hp, wtype, stype, shared) || f16) ||
         !expert_tile_ok(hp.n_embd, hp.moe_ff, hp.shared_ff, shared))
         return false;
-    if (sw.q4k_tile >= 0) return sw.q4k_tile == 1;
+    if (sw.expert_tile >= 0) return sw.expert_tile == 1;
     if (sw.q4k_column_blocks && wtype == DMOE_TYPE_Q4_K) return false;
     const long avg = (long)N * hp.top_k / (hp.n_experts > 0 ? hp.n_experts : 1);
-    return avg >= 8;
+    return f16 ? avg < 8 : avg >= 8;
 }
 
 // Few tokens of Q4_K experts: the down products and the combine run as one
@@ -460,8 +464,8 @@ size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t 
     const bool gemv = !gemm && !use_mfma_path(hp, wtype, stype, shared) &&
                       !use_q80_path(hp, wtype, stype, shared);
     const bool tile = use_tile_path(sw, hp, wtype, stype, shared, N);
-    t.wl.chunk = gemm ? GM
-                 : tile ? expert_tile_chunk()
+    t.wl.chunk = tile ? expert_tile_chunk(wtype)
+                 : gemm ? GM
                         : EXPERT_CHUNK * (use_mfma_path(hp, wtype, stype, shared) ? q4k_column_blocks(sw, hp, N) : 1);
     t.wl.n_ec = (int32_t *)take(4);
     t.wl.ec_expert = (int32_t *)take((size_t)(E + P / EXPERT_CHUNK + 1) * 4);
@@ -503,6 +507,10 @@ size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t 
             t.x16 = (uint16_t *)take((size_t)N * H * 2);
         }
         t.h16 = (uint16_t *)take((size_t)P * FF * 2);
+        if (tile) {
+            t.h = (float *)take((size_t)P * FF * 4);
+            if (shared) t.hs = (float *)take((size_t)N * SF * 4);
+        }
     }
     if (gemv) {
         // activations of the GEMV kernels (k_gemv.hip) and their f32 h
@@ -718,6 +726,47 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
             return DMOE_OK;
         }
         STAGE(ST_DOWN, expert(1, job));
+        STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
+                                         K, H, y, s));
+        return DMOE_OK;
+    }
+    if (gemm && use_tile_path(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+        // F16 experts, few tokens per expert: the tile kernels on f16 x and h
+        MoeJob job{};
+        job.eg = L->eg;
+        job.eu = L->eu;
+        job.ed = L->ed;
+        job.sg = L->sg;
+        job.su = L->su;
+        job.sd = L->sd;
+        job.has_shared = L->has_shared;
+        job.H = H;
+        job.FF = FF;
+        job.SF = hp.shared_ff;
+        job.n_tokens = N;
+        job.top_k = K;
+        job.perm = w.rb.perm;
+        job.offsets = w.rb.offsets;
+        job.counts = w.rb.counts;
+        job.E = E;
+        job.ec_cap = E + N * K / EXPERT_CHUNK + 1;
+        job.wl = w.wl;
+        job.h = w.h;
+        job.hs = w.hs;
+        job.ye = w.ye;
+        job.ys = w.ys;
+        job.x16 = w.x16;
+        job.xs16 = w.xs16;
+        job.h16 = w.h16;
+        job.hs16 = w.hs16;
+        if (L->has_shared)
+            STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 1, w.xs16, s));
+        else
+            STAGE(ST_ACTQ_X, launch_cvt_f16(x, N, H, 0, w.x16, s));
+        STAGE(ST_GATEUP, launch_expert_tile(0, job, s));
+        STAGE(ST_ACTQ_H, launch_cvt_f16(w.h, N * K, FF, 0, w.h16, s));
+        if (L->has_shared) STAGE(ST_ACTQ_H, launch_cvt_f16(w.hs, N, hp.shared_ff, 1, w.hs16, s));
+        STAGE(ST_DOWN, launch_expert_tile(1, job, s));
         STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
                                          K, H, y, s));
         return DMOE_OK;
@@ -1625,9 +1674,9 @@ KernelSwitches read_kernel_switches()
     }
     sw.down_fused = flag("DMOE_DOWN_FUSED");
     sw.gateup_lds = flag("DMOE_GATEUP_LDS");
-    if (const char *v = getenv("DMOE_Q4K_TILE")) {
+    if (const char *v = getenv("DMOE_EXPERT_TILE")) {
         const int n = atoi(v);
-        if (n == 0 || n == 1) sw.q4k_tile = n;
+        if (n == 0 || n == 1) sw.expert_tile = n;
     }
     return sw;
 }

@@ -111,6 +111,10 @@ struct MoeJob {
     float *h, *hs;           // gate/up results [N*K][FF], [N][SF]
     ActI8 ah, ahs;         // h and hs converted for the down products
     float *ye, *ys;          // down results [N*K][H], [N][H]
+    // F16 experts (k_expert_tile.hip): x and h as f16 rows, the shared
+    // expert's as hi / lo pairs (lo rows after the hi rows)
+    const uint16_t *x16, *xs16;
+    uint16_t *h16, *hs16;
 };
 
 // Alternative kernels kept selectable for measurement, read from the
@@ -118,10 +122,10 @@ struct MoeJob {
 //   DMOE_Q4K_COLUMN_BLOCKS = 1, 2, 4  column blocks of the Q4_K items (0: by tokens per expert)
 //   DMOE_DOWN_FUSED = 1               few-token Q4_K down products as the single fused launch
 //   DMOE_GATEUP_LDS = 1               the LDS-ring gate/up kernel instead of the register ring
-//   DMOE_Q4K_TILE = 0 / 1             the many-token Q4_K tile kernels off / on for every N
+//   DMOE_EXPERT_TILE = 0 / 1          the tile kernels (k_expert_tile.hip) off / on for every N
 struct KernelSwitches {
     int q4k_column_blocks = 0;
-    int q4k_tile = -1;                   // -1: by tokens per expert
+    int expert_tile = -1;                // -1: by tokens per expert
     bool down_fused = false;
     bool gateup_lds = false;
 };
@@ -275,13 +279,14 @@ constexpr int SHARED_CHUNK = 8;     // tokens per shared-expert work item
 // nc: activation column blocks of 16 pairs per routed item (1, 2 or 4; the
 // work list's chunk is 16 nc): each weight tile read serves 16 nc pairs.
 hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc = 1, bool gateup_lds = false);
-// The same products when many tokens reach each expert (k_expert_tile.hip):
-// units of up to expert_tile_chunk() = 128 pairs (the work list's chunk) or 64
-// shared tokens; phase 0 writes f32 h / hs ([N K][FF], [N][SF]) for one
-// conversion launch (launch_prep, ACT_Q8K / ACT_SPLIT) into ah / ahs, phase 1
-// writes ye / ys for the combine.
+// Expert products with each item's activations held in LDS (k_expert_tile.hip):
+// Q4_K and Q8_0 experts with many tokens per expert, F16 experts with few.
+// Units of up to expert_tile_chunk(type) pairs (the work list's chunk) or
+// half as many shared tokens; phase 0 writes f32 h / hs ([N K][FF],
+// [N][SF]) for a conversion launch into ah / ahs (Q4_K, Q8_0) or h16 / hs16
+// (F16), phase 1 writes ye / ys for the combine.
 bool expert_tile_ok(int H, int FF, int SF, bool shared);
-int expert_tile_chunk();
+int expert_tile_chunk(int32_t type);
 hipError_t launch_expert_tile(int phase, const MoeJob &job, hipStream_t s);
 // Down products of the Q4_K experts and the weighted combine in one launch
 // for few tokens (k_down_rows.hip): one workgroup per 16 output rows, every

@@ -63,20 +63,22 @@ __device__ __forceinline__ T xt_ldc(const T *p, int i)
 }
 
 // Item k is row group k % rg_n of unit k / rg_n; a unit is work-list entry
-// u < n_ec, else shared chunk u - n_ec.  Every field is wave-uniform.
-constexpr int XR_NC = 2;
-constexpr int XR_CHUNK = EXPERT_CHUNK * XR_NC;    // 32
-constexpr int XR_SCHUNK = SHARED_CHUNK * XR_NC;   // 16
-constexpr int XR_ROWS = XT_WAVES * 16;            // h rows of an item (128)
-constexpr int XR_MAX_SB = 16;                     // n_embd <= 4096
+// u < n_ec (up to 16 NC pairs), else shared chunk u - n_ec (8 NC tokens).
+// Every field is wave-uniform.
+constexpr int XR_MAX_NC = 2;
+constexpr int XR_MAX_CHUNK = EXPERT_CHUNK * XR_MAX_NC;   // 32
+constexpr int XR_ROWS = XT_WAVES * 16;                   // h rows of an item (128)
+constexpr int XR_MAX_K = 4096;                           // n_embd the gate/up LDS holds
 
 struct XrItem {
     int rg, e, t_first, nt, nblk;
     bool shared, valid;
 };
 
+template <int NC>
 __device__ __forceinline__ XrItem xr_decode(const MoeJob &job, int k, int rg_n, int n_ec, int nch)
 {
+    constexpr int XR_CHUNK = EXPERT_CHUNK * NC, XR_SCHUNK = SHARED_CHUNK * NC;
     XrItem I{};
     const int unit = k / rg_n;
     I.rg = k - unit * rg_n;
@@ -111,19 +113,28 @@ __device__ __forceinline__ int xr_arow(const XrItem &I, const int32_t *s_pids, i
 }
 
 // ---------------------------------------------------------------------------
-// Weight formats.  Each gives the bytes of one 16-row tile step (TILE) and of
-// one 16-row block's activation step in LDS (ASTEP), a lane's share of a
-// tile step (Tile, load), the products of two tiles against one activation
-// block (compute2) and the loads of one activation step (load_act: the
-// lane's source rows rq (rows 4j + lane / 16 of the block, for the quants)
-// and ra (its row for the scale and sum loads)).
-
-// Q4_K (ggml's vec_dot_q4_K_q8_K; activations Q8_K, or two int8 digits for
-// the shared expert).
+// Weight formats.  Each gives:
+//   NC, STEP      column blocks of 16 rows per unit; values of the reduction
+//                 per step
+//   TILE          bytes of one 16-row tile and step (its stride in HBM for
+//                 the tiled int8 layouts)
+//   ASTEP         LDS bytes of one block's activation step
+//   tile, step    the first step of 16-row tile t16 of a matrix (Kin values
+//                 per row) and the byte offset of step s from it
+//   Tile, load    a lane's share of a tile step
+//   compute2      the products of two tiles against one activation block
+//   NR, row       the block rows whose activations a lane loads (NR lookups)
+//   Src, src      the activation arrays (x or h; routed or shared)
+//   load_act      the loads of one block's activation step into LDS
 struct FmtQ4K {
-    static constexpr int TILE = TILE_BYTES;
-    static constexpr int ASTEP = ASTEP_BYTES;
+    static constexpr int NC = 2, STEP = 256, TILE = TILE_BYTES, ASTEP = ASTEP_BYTES, NR = 6;
     typedef Q4KTile Tile;
+    typedef ActI8 Src;
+    __device__ static const uint8_t *tile(const uint8_t *m, int t16, int Kin)
+    {
+        return m + (size_t)t16 * (Kin / STEP) * TILE;
+    }
+    __device__ static size_t step(int s) { return (size_t)s * TILE; }
     __device__ static void load(Tile &t, const uint8_t *run, int r16, int g)
     {
         const uint4 *p = reinterpret_cast<const uint4 *>(run);
@@ -135,30 +146,38 @@ struct FmtQ4K {
     {
         compute_sb<2>(t, ast, r16, g, acc);
     }
-    // the scale / sum loads: bs by lanes 0..31 (row lane / 2, half lane % 2),
-    // d by lanes 0..15 (row lane)
-    __device__ static int arow_lane(int lane, int which) { return which == 0 ? (lane >> 1) & 15 : lane & 15; }
-    __device__ static void load_act(const ActI8 &act, int Kin, int sb, const int (&rq)[4], const int (&ra)[2],
-                                    uint8_t *st, int lane)
+    // quants: rows 4j + lane / 16; bs: lanes 0..31, row lane / 2; d: lanes 0..15
+    __device__ static int row(int lane, int i)
+    {
+        return i < 4 ? 4 * i + (lane >> 4) : i == 4 ? (lane >> 1) & 15 : lane & 15;
+    }
+    __device__ static const Src &src(const MoeJob &j, bool down, bool shared)
+    {
+        return down ? (shared ? j.ahs : j.ah) : (shared ? j.axs : j.ax);
+    }
+    __device__ static void load_act(const Src &act, int Kin, int sb, const int (&rows)[NR], uint8_t *st, int lane)
     {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int row = 4 * j + (lane >> 4);
-            lds_load16(act.q + (size_t)rq[j] * Kin + sb * 256 + (((lane & 15) ^ (row & 11)) * 16), st + 1024 * j);
+            const int r = 4 * j + (lane >> 4);
+            lds_load16(act.q + (size_t)rows[j] * Kin + sb * 256 + (((lane & 15) ^ (r & 11)) * 16), st + 1024 * j);
         }
-        if (lane < 32) lds_load16(act.bs + (size_t)ra[0] * (Kin / 16) + sb * 16 + (lane & 1) * 8, st + ABS_OFF);
-        if (lane < 16) lds_load4(act.d + (size_t)ra[1] * (Kin / 256) + sb, st + AD_OFF);
+        if (lane < 32) lds_load16(act.bs + (size_t)rows[4] * (Kin / 16) + sb * 16 + (lane & 1) * 8, st + ABS_OFF);
+        if (lane < 16) lds_load4(act.d + (size_t)rows[5] * (Kin / 256) + sb, st + AD_OFF);
     }
 };
 
-// Q8_0 (ggml's vec_dot_q8_0_q8_0; activations Q8_0, or two int8 digits per
-// 32 values for the shared expert).
 struct FmtQ80 {
-    static constexpr int TILE = Q80_TILE;
-    static constexpr int ASTEP = Q80_ASTEP;
+    static constexpr int NC = 2, STEP = 256, TILE = Q80_TILE, ASTEP = Q80_ASTEP, NR = 5;
     struct Tile {
         uint4 d, q[4];          // piece 0 of row r16; lane group g's quant pieces
     };
+    typedef ActI8 Src;
+    __device__ static const uint8_t *tile(const uint8_t *m, int t16, int Kin)
+    {
+        return m + (size_t)t16 * (Kin / STEP) * TILE;
+    }
+    __device__ static size_t step(int s) { return (size_t)s * TILE; }
     __device__ static void load(Tile &t, const uint8_t *run, int r16, int g)
     {
         const uint4 *p = reinterpret_cast<const uint4 *>(run);
@@ -177,19 +196,84 @@ struct FmtQ80 {
             q80_products(a, w, t[r].d, ast, g, acc[r]);
         }
     }
-    // the scales: two loads of 64 lanes, lane -> (block 4 h + lane / 16, row lane % 16)
-    __device__ static int arow_lane(int lane, int which) { return lane & 15; }
-    __device__ static void load_act(const ActI8 &act, int Kin, int sb, const int (&rq)[4], const int (&ra)[2],
-                                    uint8_t *st, int lane)
+    // quants: rows 4j + lane / 16; scales: two loads of 64 lanes, lane ->
+    // (block 4 h + lane / 16, row lane % 16)
+    __device__ static int row(int lane, int i) { return i < 4 ? 4 * i + (lane >> 4) : lane & 15; }
+    __device__ static const Src &src(const MoeJob &j, bool down, bool shared)
+    {
+        return down ? (shared ? j.ahs : j.ah) : (shared ? j.axs : j.ax);
+    }
+    __device__ static void load_act(const Src &act, int Kin, int sb, const int (&rows)[NR], uint8_t *st, int lane)
     {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int row = 4 * j + (lane >> 4);
-            lds_load16(act.q + (size_t)rq[j] * Kin + sb * 256 + (((lane & 15) ^ (row & 11)) * 16), st + 1024 * j);
+            const int r = 4 * j + (lane >> 4);
+            lds_load16(act.q + (size_t)rows[j] * Kin + sb * 256 + (((lane & 15) ^ (r & 11)) * 16), st + 1024 * j);
         }
 #pragma unroll
         for (int h = 0; h < 2; h++)
-            lds_load4(act.d + (size_t)ra[h] * (Kin / 32) + sb * 8 + 4 * h + (lane >> 4), st + Q80_AD_OFF + 256 * h);
+            lds_load4(act.d + (size_t)rows[4] * (Kin / 32) + sb * 8 + 4 * h + (lane >> 4), st + Q80_AD_OFF + 256 * h);
+    }
+};
+
+// F16 (ggml's F16 products: activations rounded to f16, products accumulated
+// in f32; the shared expert's f32 activations as an f16 hi and lo row): the
+// tiled layout of k_gemm.hip (128-row blocks, k-step-major: the 128 rows x 32
+// values of k step ks of block b are the 8 KB at (b Kin / 32 + ks) 8192, row
+// r at r 64 with its 16-byte chunk q at slot q ^ swz(r), swz(r) = (r >> 1) &
+// 3), steps of 128 values = four k steps, one column block per unit (an
+// item's activations, 16 rows x 4096 f16, fill 128 KB of LDS).  Activation
+// steps in LDS: four 1 KB k steps, row r at r 64, chunk q at slot q ^ swz(r)
+// (the operand reads conflict-free, as in k_gemm.hip).
+typedef _Float16 xt_h8 __attribute__((ext_vector_type(8)));
+typedef float xt_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int xt_swz(int r) { return (r >> 1) & 3; }
+
+struct FmtF16 {
+    static constexpr int NC = 1, STEP = 128, TILE = 4 * 1024, ASTEP = 4 * 1024, NR = 1;
+    struct Tile {
+        uint4 w[4];             // row r16, k chunk g of the step's four k steps
+    };
+    typedef const uint16_t *Src;
+    __device__ static const uint8_t *tile(const uint8_t *m, int t16, int Kin)
+    {
+        return m + (size_t)(t16 >> 3) * (Kin / 32) * 8192 + (size_t)(t16 & 7) * 1024;
+    }
+    __device__ static size_t step(int s) { return (size_t)s * 4 * 8192; }
+    __device__ static void load(Tile &t, const uint8_t *run, int r16, int g)
+    {
+        const uint8_t *p = run + r16 * 64 + ((g ^ xt_swz(r16)) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) t.w[j] = xt_ld_nt16(p + j * 8192);
+    }
+    __device__ static void compute2(const Tile (&t)[2], const uint8_t *ast, int r16, int g, float (&acc)[2][4])
+    {
+        const uint8_t *ap = ast + r16 * 64 + ((g ^ xt_swz(r16)) * 16);
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            xt_f4 c = {acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const xt_h8 a = *reinterpret_cast<const xt_h8 *>(ap + j * 1024);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(xt_h8, t[r].w[j]), c, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[r][i] = c[i];
+        }
+    }
+    // a k step of 16 rows x 64 bytes is one 64-lane load: lane -> row lane / 4,
+    // slot lane % 4 (holding chunk (lane % 4) ^ swz(row))
+    __device__ static int row(int lane, int) { return lane >> 2; }
+    __device__ static Src src(const MoeJob &j, bool down, bool shared)
+    {
+        return down ? (shared ? j.hs16 : j.h16) : (shared ? j.xs16 : j.x16);
+    }
+    __device__ static void load_act(Src act, int Kin, int sb, const int (&rows)[NR], uint8_t *st, int lane)
+    {
+        const int q = (lane & 3) ^ xt_swz(lane >> 2);
+        const uint8_t *p = reinterpret_cast<const uint8_t *>(act + (size_t)rows[0] * Kin) + q * 16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) lds_load16(p + (size_t)(4 * sb + j) * 64, st + 1024 * j);
     }
 };
 
@@ -209,7 +293,8 @@ struct FmtQ80 {
 template <class F>
 __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
 {
-    __shared__ __align__(16) uint8_t s_act[XR_MAX_SB][XR_NC * F::ASTEP];
+    constexpr int XR_NC = F::NC, XR_CHUNK = EXPERT_CHUNK * F::NC, XR_SCHUNK = SHARED_CHUNK * F::NC;
+    __shared__ __align__(16) uint8_t s_act[XR_MAX_K / F::STEP][XR_NC * F::ASTEP];
     __shared__ int32_t s_pids[2][XR_CHUNK];          // routed items: their pair ids
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -219,12 +304,12 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     const int n_ec = xt_ldc(job.wl.n_ec, 0);
     const int nch = job.has_shared ? (N + XR_SCHUNK - 1) / XR_SCHUNK : 0;
     const int rg_n = job.FF / XR_ROWS;
-    const int nsb = H / 256;
+    const int nsb = H / F::STEP;
     const int steps = nsb;                 // even (n_embd a multiple of 512)
     const int G = gridDim.x;
 
     int k = blockIdx.x;
-    XrItem I = xr_decode(job, k, rg_n, n_ec, nch);
+    XrItem I = xr_decode<F::NC>(job, k, rg_n, n_ec, nch);
     if (!I.valid) return;
     if (tid < XR_CHUNK && !I.shared) s_pids[0][tid] = job.perm[I.t_first + min(tid, I.nt - 1)];
     int buf = 0;
@@ -234,9 +319,9 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     auto tiles = [&](const XrItem &X, const uint8_t *&tg, const uint8_t *&tu) {
         const WTensor &a = X.shared ? job.sg : job.eg;
         const WTensor &b = X.shared ? job.su : job.eu;
-        const size_t t16 = (size_t)((X.rg * XR_ROWS + 16 * wave) / 16) * nsb * F::TILE;
-        tg = a.data + (size_t)X.e * a.nb2 + t16;
-        tu = b.data + (size_t)X.e * b.nb2 + t16;
+        const int t16 = (X.rg * XR_ROWS + 16 * wave) / 16;
+        tg = F::tile(a.data + (size_t)X.e * a.nb2, t16, H);
+        tu = F::tile(b.data + (size_t)X.e * b.nb2, t16, H);
     };
     // weight loads run one step ahead over the concatenation of the items:
     // (lg, lu) the cursor's tiles, l_sb its super-block; past the last item
@@ -247,8 +332,8 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     bool l_last = false;                   // the cursor is on the schedule's last step
     XrItem NI{};
     auto load = [&](typename F::Tile (&o)[2]) __attribute__((always_inline)) {
-        F::load(o[0], lg + (size_t)l_sb * F::TILE, r16, g);
-        F::load(o[1], lu + (size_t)l_sb * F::TILE, r16, g);
+        F::load(o[0], lg + F::step(l_sb), r16, g);
+        F::load(o[1], lu + F::step(l_sb), r16, g);
         if (l_sb + 1 < steps) {
             l_sb++;
         } else if (!l_last) {
@@ -262,7 +347,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
         }
     };
     typename F::Tile o[2][2];
-    NI = xr_decode(job, k + G, rg_n, n_ec, nch);
+    NI = xr_decode<F::NC>(job, k + G, rg_n, n_ec, nch);
     load(o[0]);
     __syncthreads();                       // the first item's pair list
 
@@ -270,17 +355,15 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     // the item's activations: wavefront w loads super-blocks w, w + 8, ...
     // of both blocks
     {
-        const ActI8 &act = I.shared ? job.axs : job.ax;
+        const auto &act = F::src(job, false, I.shared);
         const int32_t *pids = s_pids[buf];
 #pragma unroll
         for (int c = 0; c < XR_NC; c++) {
             if (c >= I.nblk) continue;
-            int rq[4], ra[2];
+            int rows[F::NR];
 #pragma unroll
-            for (int j = 0; j < 4; j++) rq[j] = xr_arow<false>(I, pids, N, K, c, 4 * j + (lane >> 4));
-#pragma unroll
-            for (int q = 0; q < 2; q++) ra[q] = xr_arow<false>(I, pids, N, K, c, F::arow_lane(lane, q));
-            for (int sb = wave; sb < nsb; sb += XT_WAVES) F::load_act(act, H, sb, rq, ra, &s_act[sb][c * F::ASTEP], lane);
+            for (int i = 0; i < F::NR; i++) rows[i] = xr_arow<false>(I, pids, N, K, c, F::row(lane, i));
+            for (int sb = wave; sb < nsb; sb += XT_WAVES) F::load_act(act, H, sb, rows, &s_act[sb][c * F::ASTEP], lane);
         }
     }
     EXPERT_WAIT_VM(0);
@@ -339,7 +422,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     I = NI;
     k += G;
     buf ^= 1;
-    NI = xr_decode(job, k + G, rg_n, n_ec, nch);
+    NI = xr_decode<F::NC>(job, k + G, rg_n, n_ec, nch);
     }
 }
 
@@ -350,12 +433,14 @@ constexpr int XR_DN_TILES = 2;                          // tiles per wavefront a
 constexpr int XR_DN_PASS = XT_WAVES * 16 * XR_DN_TILES; // 256
 constexpr int XR_DN_IT = 2;
 constexpr int XR_DN_ROWS = XR_DN_PASS * XR_DN_IT;       // 512
-constexpr int XR_DN_MAX_SB = 4;                         // moe_ff <= 1024
+constexpr int XR_DN_MAX_K = 1024;                       // moe_ff the down LDS holds
 
 template <class F>
 __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
 {
-    __shared__ __align__(16) uint8_t s_act[2][XR_DN_MAX_SB][XR_NC * F::ASTEP];
+    constexpr int XR_NC = F::NC, XR_CHUNK = EXPERT_CHUNK * F::NC, XR_SCHUNK = SHARED_CHUNK * F::NC;
+    constexpr int MAX_SB = XR_DN_MAX_K / F::STEP;
+    __shared__ __align__(16) uint8_t s_act[2][MAX_SB][XR_NC * F::ASTEP];
     // pair lists of items i, i + 1 (its activations load during item i) and
     // i + 2 (loaded from perm during item i, written at its end)
     __shared__ int32_t s_pids[3][XR_CHUNK];
@@ -367,53 +452,54 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
     const int n_ec = xt_ldc(job.wl.n_ec, 0);
     const int nch = job.has_shared ? (N + XR_SCHUNK - 1) / XR_SCHUNK : 0;
     const int rg_n = H / XR_DN_ROWS;
-    const int nsb = FF / 256;
+    const int nsb = FF / F::STEP;
     const int steps = XR_DN_IT * nsb;      // even
     const int G = gridDim.x;
 
     int k = blockIdx.x;
-    XrItem I = xr_decode(job, k, rg_n, n_ec, nch);
+    XrItem I = xr_decode<F::NC>(job, k, rg_n, n_ec, nch);
     if (!I.valid) return;
-    XrItem NI = xr_decode(job, k + G, rg_n, n_ec, nch);
+    XrItem NI = xr_decode<F::NC>(job, k + G, rg_n, n_ec, nch);
     if (tid < XR_CHUNK && !I.shared) s_pids[0][tid] = job.perm[I.t_first + min(tid, I.nt - 1)];
     if (tid < XR_CHUNK && NI.valid && !NI.shared) s_pids[1][tid] = job.perm[NI.t_first + min(tid, NI.nt - 1)];
     __syncthreads();
 
     // activations of item X (its pair list in pids) into buffer b: wavefront
-    // w loads block w / 4's super-block w % 4 (more super-blocks than four
-    // never occur: moe_ff <= 1024)
+    // w loads the (block, step) pairs w, w + 8, ... of the NC x nsb
     auto load_act = [&](const XrItem &X, const int32_t *pids, int b) {
-        const ActI8 &act = X.shared ? job.ahs : job.ah;
-        const int c = wave >> 2, sb = wave & 3;
-        if (c >= X.nblk || sb >= nsb) return;
-        int rq[4], ra[2];
+        const auto &act = F::src(job, true, X.shared);
+        for (int i = wave; i < XR_NC * nsb; i += XT_WAVES) {
+            const int c = i / nsb, sb = i - c * nsb;
+            if (c >= X.nblk) break;
+            int rows[F::NR];
 #pragma unroll
-        for (int j = 0; j < 4; j++) rq[j] = xr_arow<true>(X, pids, N, K, c, 4 * j + (lane >> 4));
-#pragma unroll
-        for (int q = 0; q < 2; q++) ra[q] = xr_arow<true>(X, pids, N, K, c, F::arow_lane(lane, q));
-        F::load_act(act, FF, sb, rq, ra, &s_act[b][sb][c * F::ASTEP], lane);
+            for (int q = 0; q < F::NR; q++) rows[q] = xr_arow<true>(X, pids, N, K, c, F::row(lane, q));
+            F::load_act(act, FF, sb, rows, &s_act[b][sb][c * F::ASTEP], lane);
+        }
     };
-    static_assert(XT_WAVES == 2 * XR_DN_MAX_SB && XR_NC == 2, "one (block, super-block) per wavefront");
 
     // this wavefront's tiles of pass p of item X: rows rg 512 + 256 p + 32 wave + 16 r
-    auto tile0 = [&](const XrItem &X) -> const uint8_t * {
+    // (tiles t16 and t16 + 1; pass p's 16 tiles further)
+    auto tile0 = [&](const XrItem &X) -> int { return (X.rg * XR_DN_ROWS + 32 * wave) / 16; };
+    auto matrix = [&](const XrItem &X) -> const uint8_t * {
         const WTensor &W = X.shared ? job.sd : job.ed;
-        return W.data + (size_t)X.e * W.nb2 + (size_t)((X.rg * XR_DN_ROWS + 32 * wave) / 16) * nsb * F::TILE;
+        return W.data + (size_t)X.e * W.nb2;
     };
-    const size_t pass_step = (size_t)(XR_DN_PASS / 16) * nsb * F::TILE;
-    const uint8_t *lt = tile0(I);
+    int lt = tile0(I);
+    const uint8_t *lm = matrix(I);
     int l_st = 0;                          // the load cursor's step in its item
     bool l_last = false;
     auto load = [&](typename F::Tile (&o)[2]) __attribute__((always_inline)) {
         const int it = l_st >= nsb ? 1 : 0, sb = l_st - it * nsb;
-        const uint8_t *b = lt + (size_t)it * pass_step + (size_t)sb * F::TILE;
+        const int t = lt + it * (XR_DN_PASS / 16);
 #pragma unroll
-        for (int r = 0; r < 2; r++) F::load(o[r], b + (size_t)r * nsb * F::TILE, r16, g);
+        for (int r = 0; r < 2; r++) F::load(o[r], F::tile(lm, t + r, FF) + F::step(sb), r16, g);
         if (l_st + 1 < steps) {
             l_st++;
         } else if (!l_last) {
             if (NI.valid) {
                 lt = tile0(NI);
+                lm = matrix(NI);
                 l_st = 0;
             } else {
                 l_last = true;
@@ -435,7 +521,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
     // item i + 2's pair list (written at the end of this item), then item
     // i + 1's activations into the other buffer (issued here, ahead of this
     // item's weight loads)
-    const XrItem NNI = xr_decode(job, k + 2 * G, rg_n, n_ec, nch);
+    const XrItem NNI = xr_decode<F::NC>(job, k + 2 * G, rg_n, n_ec, nch);
     if (tid < XR_CHUNK && NNI.valid && !NNI.shared) npid = job.perm[NNI.t_first + min(tid, NNI.nt - 1)];
     const int pb1 = pb == 2 ? 0 : pb + 1, pb2 = pb1 == 2 ? 0 : pb1 + 1;
     if (NI.valid) load_act(NI, s_pids[pb1], buf ^ 1);
@@ -514,19 +600,24 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
 bool expert_tile_ok(int H, int FF, int SF, bool shared)
 {
     if (H % 512 || FF % 256 || H % XR_DN_ROWS || FF % XR_ROWS) return false;
-    if (H / 256 > XR_MAX_SB || FF / 256 > XR_DN_MAX_SB) return false;
+    if (H > XR_MAX_K || FF > XR_DN_MAX_K) return false;
     if (shared && SF != FF) return false;
     return true;
 }
 
-int expert_tile_chunk() { return XR_CHUNK; }
+int expert_tile_chunk(int32_t type) { return EXPERT_CHUNK * (type == DMOE_TYPE_F16 ? FmtF16::NC : FmtQ4K::NC); }
 
 // One workgroup per CU (the gate/up LDS holds one), a multiple of 8 (one row
 // group per XCD); each runs its items until the schedule's units end.
 hipError_t launch_expert_tile(int phase, const MoeJob &job, hipStream_t s)
 {
-    if (!expert_tile_ok(job.H, job.FF, job.SF, job.has_shared) || job.ax.K != job.H || job.ah.K != job.FF ||
-        job.wl.chunk != XR_CHUNK || !job.wl.n_ec)
+    const int32_t t = job.eg.type;
+    if (t != DMOE_TYPE_Q4_K && t != DMOE_TYPE_Q8_0 && t != DMOE_TYPE_F16) return hipErrorInvalidValue;
+    if (!expert_tile_ok(job.H, job.FF, job.SF, job.has_shared) || job.wl.chunk != expert_tile_chunk(t) ||
+        !job.wl.n_ec)
+        return hipErrorInvalidValue;
+    if (t == DMOE_TYPE_F16 ? (!job.x16 || !job.h16 || (job.has_shared && (!job.xs16 || !job.hs16)))
+                           : (job.ax.K != job.H || job.ah.K != job.FF))
         return hipErrorInvalidValue;
     if (phase == 0 ? (!job.h || (job.has_shared && !job.hs)) : (!job.ye || (job.has_shared && !job.ys)))
         return hipErrorInvalidValue;
@@ -534,18 +625,21 @@ hipError_t launch_expert_tile(int phase, const MoeJob &job, hipStream_t s)
     const hipError_t e = device_cu_count(&n_cu);
     if (e != hipSuccess) return e;
     const int grid = ((n_cu + 7) / 8) * 8;
-    const bool q80 = job.eg.type == DMOE_TYPE_Q8_0;
-    if (!q80 && job.eg.type != DMOE_TYPE_Q4_K) return hipErrorInvalidValue;
+    const dim3 gd(grid), bd(XT_WAVES * 64);
     if (phase == 0) {
-        if (q80)
-            hipLaunchKernelGGL(k_gu_rr<FmtQ80>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+        if (t == DMOE_TYPE_Q8_0)
+            hipLaunchKernelGGL(k_gu_rr<FmtQ80>, gd, bd, 0, s, job);
+        else if (t == DMOE_TYPE_F16)
+            hipLaunchKernelGGL(k_gu_rr<FmtF16>, gd, bd, 0, s, job);
         else
-            hipLaunchKernelGGL(k_gu_rr<FmtQ4K>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+            hipLaunchKernelGGL(k_gu_rr<FmtQ4K>, gd, bd, 0, s, job);
     } else {
-        if (q80)
-            hipLaunchKernelGGL(k_dn_rr<FmtQ80>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+        if (t == DMOE_TYPE_Q8_0)
+            hipLaunchKernelGGL(k_dn_rr<FmtQ80>, gd, bd, 0, s, job);
+        else if (t == DMOE_TYPE_F16)
+            hipLaunchKernelGGL(k_dn_rr<FmtF16>, gd, bd, 0, s, job);
         else
-            hipLaunchKernelGGL(k_dn_rr<FmtQ4K>, dim3(grid), dim3(XT_WAVES * 64), 0, s, job);
+            hipLaunchKernelGGL(k_dn_rr<FmtQ4K>, gd, bd, 0, s, job);
     }
     return hipGetLastError();
 }

@@ -110,6 +110,8 @@ CONFIGS = {
     # F16 experts on one 32-token block (few tokens per expert on the GEMM path)
     "flash_f16": LayerConfig("flash_f16", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_F16, TYPE_F16, 32,
                              -0.1, 0.1),
+    "flash_f16_n256": LayerConfig("flash_f16_n256", 4096, 256, 1024, 48, 8, 32, 1024, TYPE_F16, TYPE_F16,
+                                  256, -0.1, 0.1),
     # prompt prefill: F16 experts, 64 blocks; bias ~U(-0.05, 0.05) plus 0.05 on
     # a hot quarter of the experts, so that about 60% of each block's routed
     # pairs go to the layer's 48 most-used experts (routing_stats'

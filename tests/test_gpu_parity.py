@@ -112,15 +112,16 @@ def test_small_layer_many_items(ctx, O, wtype):
 
 @pytest.mark.parametrize("name", ["flash_q4k", "flash_q8_0", "flash_q4k_n256", "flash_q4k_n512",
                                   "flash_q4k_n768", "flash_q4k_n1024", "flash_q4k_n2048", "flash_q8_0_n256",
-                                  "flash_q8_0_n2048", "prefill_f16"])
+                                  "flash_q8_0_n2048", "flash_f16", "prefill_f16"])
 def test_flash_layer(ctx, O, name):
     """Flash-shaped layers: one 32-token block (Q4_K, Q8_0), eight blocks
     (Q4_K, 256 tokens, each block its own allowed set), the sampler's 512-
     and 768-token windows (one column block with more pairs than the
     register-ring kernel's LDS routing tables hold), its 1024- and 2048-token
-    windows, Q8_0 over 256 and 2048 tokens and the 2048-token F16 prefill.
-    From 256 tokens the Q4_K and Q8_0 layers run on the tile kernels (many
-    tokens per expert)."""
+    windows, Q8_0 over 256 and 2048 tokens, F16 over one block and the
+    2048-token F16 prefill.  From 256 tokens the Q4_K and Q8_0 layers run on
+    the tile kernels (many tokens per expert); the one-block F16 layer runs
+    on them too (few tokens per expert), the prefill on the grouped GEMM."""
     import torch
     import dmoe
     from dmoe import synth
@@ -189,10 +190,10 @@ def test_down_span_bit_exact(ctx, name, monkeypatch):
     n2 = cfg.n_tokens // 2 + 3
     # (the few-token kernels at every size: 96 and 128 tokens of the small
     # layer would otherwise take the tile kernels)
-    c = _ctx_with(monkeypatch, {"DMOE_DOWN_FUSED": "1", "DMOE_Q4K_TILE": "0"})
+    c = _ctx_with(monkeypatch, {"DMOE_DOWN_FUSED": "1", "DMOE_EXPERT_TILE": "0"})
     ref = [c.forward(layer, a) for a in (x, xo, x[:n2], xo[:n2])]
     c.close()
-    c = _ctx_with(monkeypatch, {"DMOE_Q4K_TILE": "0"})
+    c = _ctx_with(monkeypatch, {"DMOE_EXPERT_TILE": "0"})
     got = [c.forward(layer, a) for a in (xo, x, xo[:n2], x[:n2])]
     c.close()
     for r, g in zip(ref, (got[1], got[0], got[3], got[2])):
@@ -221,10 +222,10 @@ def test_gateup_register_ring_bit_exact(ctx, name, monkeypatch):
     xo = synth.make_x(cfg, 30, cfg.n_tokens)
     # (the one-column-block kernels at every size: from 256 tokens the flash
     # layer would otherwise take the tile kernels)
-    c = _ctx_with(monkeypatch, {"DMOE_GATEUP_LDS": "1", "DMOE_Q4K_TILE": "0"})
+    c = _ctx_with(monkeypatch, {"DMOE_GATEUP_LDS": "1", "DMOE_EXPERT_TILE": "0"})
     ref = [c.forward(layer, a) for a in (x, xo)]
     c.close()
-    c = _ctx_with(monkeypatch, {"DMOE_Q4K_TILE": "0"})
+    c = _ctx_with(monkeypatch, {"DMOE_EXPERT_TILE": "0"})
     got = [c.forward(layer, a) for a in (xo, x)]
     c.close()
     assert np.array_equal(got[1].view(np.uint32), ref[0].view(np.uint32))
@@ -255,18 +256,43 @@ def test_tile_path_bit_exact(ctx, name, monkeypatch):
     layer = ctx.wrap_device(wd)
     x = synth.make_x(cfg, 33, cfg.n_tokens)
     xo = synth.make_x(cfg, 34, cfg.n_tokens)
-    ref_env = {"DMOE_Q4K_TILE": "0"}
+    ref_env = {"DMOE_EXPERT_TILE": "0"}
     if cfg.wtype == 12:
         ref_env["DMOE_Q4K_COLUMN_BLOCKS"] = "4"
     c = _ctx_with(monkeypatch, ref_env)
     ref = [c.forward(layer, a) for a in (x, xo)]
     c.close()
-    c = _ctx_with(monkeypatch, {"DMOE_Q4K_TILE": "1"})
+    c = _ctx_with(monkeypatch, {"DMOE_EXPERT_TILE": "1"})
     got = [c.forward(layer, a) for a in (xo, x)]
     c.close()
     assert np.isfinite(ref[0]).all()
     assert np.array_equal(got[1].view(np.uint32), ref[0].view(np.uint32))
     assert np.array_equal(got[0].view(np.uint32), ref[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("n_tokens,tile", [(32, 0), (40, 0), (128, 1), (2048, 1), (1000, 1)],
+                         ids=["N32_gemm", "N40_gemm", "N128_tile", "N2048_tile", "N1000_tile"])
+def test_f16_paths(ctx, O, n_tokens, tile, monkeypatch):
+    """F16 experts through the path the automatic choice does not take at
+    that size: the grouped GEMM at few tokens per expert, the tile kernels
+    (16-pair units, f16 x and h held in LDS per item) at many, each against
+    the oracle within the F16 bar (1000 tokens: no block routing)."""
+    import dmoe
+    from dmoe import synth
+    _say(f"case: small F16 layer N={n_tokens}, DMOE_EXPERT_TILE={tile}")
+    cfg = _small(dmoe, synth, 1, n_tokens)
+    w = synth.host_layer(cfg, 41, O.quantize_rows)
+    x = synth.make_x(cfg, 41, n_tokens)
+    c = _ctx_with(monkeypatch, {"DMOE_EXPERT_TILE": str(tile)})
+    layer = c.upload(w)
+    y, dg = c.forward(layer, x, debug=True)
+    yr, dr = O.layer_forward(w, x, debug=True)
+    _check_routing(dg, dr)
+    err = max_rel_err(y, yr)
+    _say(f"  max rel err {err:.3e}")
+    assert err <= TOL[1]
+    layer.free()
+    c.close()
 
 
 def test_route_logits_flash_shape(ctx, O):
