@@ -109,6 +109,25 @@ def cpu_info():
             "isa": isa}
 
 
+def uses_tile_kernels(cfg):
+    """Whether the library runs cfg's expert products on its tile kernels
+    (k_expert_tile.hip): the rule of use_tile_path in dmoe_api.cpp for the
+    flash shapes (Q8_0 always; Q4_K from 8 pairs per expert averaged over
+    all experts, N k / E; F16 below 8), DMOE_EXPERT_TILE overriding it."""
+    import dmoe
+    env = os.environ.get("DMOE_EXPERT_TILE")
+    if env in ("0", "1"):
+        return env == "1"
+    avg = cfg.n_tokens * cfg.top_k // cfg.n_experts
+    if cfg.wtype == dmoe.TYPE_Q8_0:
+        return True
+    if cfg.wtype == dmoe.TYPE_Q4_K:
+        return avg >= 8
+    if cfg.wtype == dmoe.TYPE_F16:
+        return avg < 8
+    return False
+
+
 def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
     """One MoE layer of config cfg: tokens/s, per-stage times, the dominant
     kernel's roofline, realised routing and (cpu_seconds > 0) the oracle's
@@ -167,21 +186,25 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
     stages = {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.items()}   # us per launch
 
     # The dominant kernel is the gate/up launch (routed experts and the shared
-    # expert in one launch).  Q4_K / Q8_0 (HBM-bound): its algorithmic bytes
-    # are the touched experts' and the shared expert's gate and up matrices,
-    # the activations in their operand layout (int8 values with, for Q4_K, f16
-    # sums of 16 and an f32 scale per 256, for Q8_0 an f32 scale per 32; the
-    # shared expert's as two int8 digit rows) and h written in the down
-    # products' operand layout.  F16 (the prefill, MFMA-bound): its algorithmic
-    # FLOPs, 2 per multiply-add of the routed pairs' and the tokens' shared
-    # gate and up products (the shared expert's two f16 passes count once).
+    # expert in one launch).  Streaming launches (Q4_K, Q8_0, and F16 at few
+    # tokens per expert: HBM-bound): its algorithmic bytes are the touched
+    # experts' and the shared expert's gate and up matrices, the activations
+    # in their operand layout (int8 values with, for Q4_K, f16 sums of 16 and
+    # an f32 scale per 256, for Q8_0 an f32 scale per 32; the shared expert's
+    # as two int8 digit rows; F16: f16 hi / lo rows) and h written (the
+    # few-token Q4_K kernel: in the down products' operand layout; the tile
+    # kernels: f32).  The F16 grouped GEMM (the prefill, MFMA-bound): its
+    # algorithmic FLOPs, 2 per multiply-add of the routed pairs' and the
+    # tokens' shared gate and up products (the shared expert's two f16 passes
+    # count once).
     rs_h = dmoe.row_size(cfg.wtype, H)
     SF = cfg.shared_ff
     P = N * K
     dom_stage = "gateup_routed"
     dom_us = stages.get(dom_stage)
     flops = 2.0 * N * (K * 3 * H * FF + 3 * H * SF + H * E)
-    if cfg.wtype == dmoe.TYPE_F16:
+    tile = uses_tile_kernels(cfg)
+    if cfg.wtype == dmoe.TYPE_F16 and not tile:
         dom_kernel = "dmoe::k_gemm_f16<0>"
         dom_flops = 2.0 * (P * 2 * H * FF + N * 2 * H * SF)
         achieved = dom_flops / (dom_us * 1e-6) / 1e12 if dom_us else None
@@ -202,24 +225,28 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
                     **traffic_from_profile(dom_stage, cfg.name),
                     "algorithmic_flops": dom_flops, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
     else:
-        if cfg.wtype in (dmoe.TYPE_Q4_K, dmoe.TYPE_Q8_0):
-            if cfg.wtype == dmoe.TYPE_Q4_K:
-                def act_row(n):
-                    return n + (n // 16) * 2 + (n // 256) * 4
-                # items of one column block (fewer than 32 pairs per expert on
-                # average) run on the register-ring kernel
-                dom_kernel = "dmoe::k_gateup_rr<true>" if N * K // E < 32 else "dmoe::k_expert_q4k<0>"
-            else:
-                def act_row(n):
-                    return n + (n // 32) * 4
-                dom_kernel = "dmoe::k_expert_q80<0>"
-            # x rows in (routed, shared digit rows), h rows out in the down
-            # products' layout (routed pairs, shared digit rows)
-            dom_bytes = (touched * 2 * FF * rs_h + 2 * SF * rs_h + 3 * N * act_row(H)
-                         + P * act_row(FF) + 2 * N * act_row(SF))
+        fmt = {dmoe.TYPE_Q4_K: "FmtQ4K", dmoe.TYPE_Q8_0: "FmtQ80", dmoe.TYPE_F16: "FmtF16"}.get(cfg.wtype)
+        if cfg.wtype == dmoe.TYPE_Q4_K:
+            def act_row(n):
+                return n + (n // 16) * 2 + (n // 256) * 4
+        elif cfg.wtype == dmoe.TYPE_Q8_0:
+            def act_row(n):
+                return n + (n // 32) * 4
+        else:
+            def act_row(n):
+                return 2 * n
+        if fmt and tile:
+            dom_kernel = f"dmoe::k_gu_rr<dmoe::{fmt}>"
+            h_bytes = P * FF * 4 + N * SF * 4
+        elif cfg.wtype == dmoe.TYPE_Q4_K:
+            # items of one column block on the register-ring kernel
+            dom_kernel = "dmoe::k_gateup_rr<true>"
+            h_bytes = P * act_row(FF) + 2 * N * act_row(SF)
         else:
             dom_kernel = "dmoe::k_gateup_routed"
-            dom_bytes = touched * 2 * FF * rs_h + N * H * 2 + P * FF * 4
+            h_bytes = P * FF * 4
+        # x rows in (routed, shared digit rows), h out
+        dom_bytes = touched * 2 * FF * rs_h + 2 * SF * rs_h + 3 * N * act_row(H) + h_bytes
         achieved = dom_bytes / (dom_us * 1e-6) / 1e9 if dom_us else None
         roofline = {"bound": "hbm", "kernel": dom_stage,
                     "achieved": round(achieved, 1) if achieved else None,

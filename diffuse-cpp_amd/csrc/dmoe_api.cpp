@@ -348,11 +348,12 @@ bool use_gemm_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
 // The tile kernels of k_expert_tile.hip (units of up to 32 pairs of an expert,
 // 16 for F16, whose activations stay in LDS for the whole reduction; h
 // through HBM as f32 and one conversion), by the forward's pairs per expert
-// averaged over all experts (N k / E): Q4_K and Q8_0 from 8 on (the flash
-// layer from 256 tokens; fewer take the item kernels, whose finer work
-// division fills the chip), F16 below 8 (more take the grouped GEMM of
-// 256-pair items).  DMOE_EXPERT_TILE = 0 / 1 turns the choice off / on for
-// every N (with the shapes the tile kernels take).
+// averaged over all experts (N k / E): Q8_0 at every N (at one 32-token
+// block of the flash layer 146 against 160 us for the item kernels); Q4_K
+// from 8 on (the flash layer from 256 tokens; fewer take the few-token
+// kernels: 91 against 110 us at 32 tokens); F16 below 8 (more take the
+// grouped GEMM of 256-pair items).  DMOE_EXPERT_TILE = 0 / 1 turns the
+// choice off / on for every N (with the shapes the tile kernels take).
 bool use_tile_path(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
                    int N)
 {
@@ -362,6 +363,7 @@ bool use_tile_path(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wty
         return false;
     if (sw.expert_tile >= 0) return sw.expert_tile == 1;
     if (sw.q4k_column_blocks && wtype == DMOE_TYPE_Q4_K) return false;
+    if (wtype == DMOE_TYPE_Q8_0) return true;
     const long avg = (long)N * hp.top_k / (hp.n_experts > 0 ? hp.n_experts : 1);
     return f16 ? avg < 8 : avg >= 8;
 }
