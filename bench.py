@@ -128,10 +128,11 @@ def uses_tile_kernels(cfg):
     return False
 
 
-def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
+def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds, cpu_tokens=None):
     """One MoE layer of config cfg: tokens/s, per-stage times, the dominant
     kernel's roofline, realised routing and (cpu_seconds > 0) the oracle's
-    rate on this host."""
+    rate on this host, over the first cpu_tokens tokens of the input (all of
+    them by default)."""
     import numpy as np
     import torch
     import dmoe
@@ -295,26 +296,31 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
         import oracle as O
         wh = synth.to_host(weights[0])
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        # the quantised dots through AVX-512 VNNI where the host has it (the
-        # same results bit for bit as the scalar dots)
+        ns = min(N, cpu_tokens or N)
+        xs = np.ascontiguousarray(x_host[:ns])
+        # the dots through AVX-512 where the host has it (quantised: VNNI,
+        # the same results bit for bit as the scalar dots; F32 / F16: binary32
+        # sums in ggml's SIMD order)
         simd = O.set_simd(True)
-        yr = O.layer_forward(wh, x_host, n_threads=threads)     # warm-up
+        yr = O.layer_forward(wh, xs, n_threads=threads)     # warm-up
         reps, t_start = 0, time.time()
         while True:
-            O.layer_forward(wh, x_host, n_threads=threads)
+            O.layer_forward(wh, xs, n_threads=threads)
             reps += 1
             el = time.time() - t_start
             if el >= cpu_seconds or reps >= 1000:
                 break
         info = cpu_info()
+        part = (f"the same {N}-token layer" if ns == N else
+                f"the first {ns} of the {N} tokens ({ns // cfg.block_size} blocks, each routed alone as in the "
+                f"full input)")
         rec["cpu_baseline"] = {
-            "value": round(N * reps / el, 2),
+            "value": round(ns * reps / el, 2),
             "unit": "tokens/s",
             "cores": threads,
             "kind": "port",
-            "sample": f"{reps} forwards of the same {N}-token layer ({el:.1f} s), oracle (C, gcc -O2, "
-                      f"OpenMP over rows; quantised dots "
-                      f"{'AVX-512 VNNI' if simd else 'scalar'}, F32 dots scalar binary64) "
+            "sample": f"{reps} forwards of {part} ({el:.1f} s), oracle (C, gcc -O2, OpenMP over rows; "
+                      f"dots {'AVX-512 (VNNI for the quantised types; binary32 F32 / F16 sums)' if simd else 'scalar'}) "
                       f"with {threads} threads",
             "cpu_model": info["model"],
             "physical_cores": info["physical_cores"],
@@ -323,10 +329,14 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds):
             "isa": info["isa"],
         }
         O.set_simd(False)
-        ctx.forward_device(layers[0], x, N, y, sp)
+        # the GPU forward of the same sample, checked against the oracle
+        xd = torch.from_numpy(xs).to(dev)
+        yd = torch.empty_like(xd)
+        ctx.forward_device(layers[0], xd, ns, yd, sp)
         torch.cuda.synchronize(dev)
-        err = float(np.abs(y.cpu().numpy() - yr).max() / np.abs(yr).max())
+        err = float(np.abs(yd.cpu().numpy() - yr).max() / np.abs(yr).max())
         rec["check_max_rel_err_vs_oracle"] = err
+        del wh, xd, yd
 
     del layers, weights, x, y
     ctx.close()
@@ -475,7 +485,10 @@ def main():
     # MFMA-bound), measured in the same run
     if a.prefill_steps > 0 and cfg.n_tokens <= 256:
         pcfg = synth.CONFIGS["prefill_f16"]
-        pre = bench_layer(a, pcfg, a.prefill_steps, max(1, a.prefill_steps // 4), 1, 0)
+        # its CPU baseline over the first 256 tokens (a bounded sample: the
+        # oracle's F16 dots over all 2048 would take minutes)
+        pre = bench_layer(a, pcfg, a.prefill_steps, max(1, a.prefill_steps // 4), 1,
+                          0 if a.no_cpu else a.cpu_seconds, cpu_tokens=256)
         pre["unit"] = "tokens/s"
         out["prefill"] = pre
 

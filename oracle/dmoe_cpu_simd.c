@@ -1,6 +1,6 @@
 /* dmoe_cpu_simd.c -- AVX-512 VNNI versions of the oracle's quantised dots,
- * for the CPU baseline that bench.py times (test infrastructure: the
- * checker's fast twin, never the product).
+ * and AVX-512 fp32 / f16 dots, for the CPU baseline that bench.py times
+ * (test infrastructure: the checker's fast twin, never the product).
  *
  * ggml's vec_dot_q4_K_q8_K and vec_dot_q8_0_q8_0 have SIMD kernels of their
  * own in the ggml submodule, which is absent from the reference checkout;
@@ -10,6 +10,12 @@
  * instruction; int8 x int8 block sums by vpmaddwd), and the float steps run
  * in the scalar functions' order, so every result equals the scalar
  * oracle's bit for bit (tests/test_oracle_simd.py).
+ *
+ * The F32 and F16 dots follow ggml's SIMD ggml_vec_dot_f32 / _f16 on
+ * AVX-512 (products and sums in binary32: four 16-lane fused multiply-add
+ * accumulators, added and reduced at the end); they round differently from
+ * the scalar oracle's binary64 sums, within the tolerance the tests state
+ * (tests/test_oracle_simd.py).
  *
  * Functions carry their target attributes and run only when the CPU reports
  * AVX-512 F / BW and VNNI (dmo_simd_available); the library itself stays
@@ -143,4 +149,39 @@ SIMD_TARGET void dmo_rows_q4K_simd(int64_t n, const dmo_block_q4_K *w, const uin
         }
         out[(size_t)i * out_stride] = s;
     }
+}
+
+/* F32 x F32: four accumulators of 16 lanes over steps of 64 values, fused
+ * multiply-adds, then the accumulators added and the lanes reduced; the
+ * tail (n % 64) one lane at a time. */
+SIMD_TARGET float dmo_dot_f32_simd(int64_t n, const float *w, const float *x)
+{
+    __m512 a0 = _mm512_setzero_ps(), a1 = _mm512_setzero_ps(), a2 = _mm512_setzero_ps(),
+           a3 = _mm512_setzero_ps();
+    int64_t i = 0;
+    for (; i + 64 <= n; i += 64) {
+        a0 = _mm512_fmadd_ps(_mm512_loadu_ps(w + i), _mm512_loadu_ps(x + i), a0);
+        a1 = _mm512_fmadd_ps(_mm512_loadu_ps(w + i + 16), _mm512_loadu_ps(x + i + 16), a1);
+        a2 = _mm512_fmadd_ps(_mm512_loadu_ps(w + i + 32), _mm512_loadu_ps(x + i + 32), a2);
+        a3 = _mm512_fmadd_ps(_mm512_loadu_ps(w + i + 48), _mm512_loadu_ps(x + i + 48), a3);
+    }
+    float s = _mm512_reduce_add_ps(_mm512_add_ps(_mm512_add_ps(a0, a1), _mm512_add_ps(a2, a3)));
+    for (; i < n; i++) s += w[i] * x[i];
+    return s;
+}
+
+/* F16 x F16: the same on values converted to binary32 (exactly). */
+SIMD_TARGET float dmo_dot_f16_simd(int64_t n, const uint16_t *w, const uint16_t *x)
+{
+    __m512 acc[4] = {_mm512_setzero_ps(), _mm512_setzero_ps(), _mm512_setzero_ps(), _mm512_setzero_ps()};
+    int64_t i = 0;
+    for (; i + 64 <= n; i += 64)
+        for (int k = 0; k < 4; k++) {
+            const __m512 wv = _mm512_cvtph_ps(_mm256_loadu_si256((const __m256i *)(w + i + 16 * k)));
+            const __m512 xv = _mm512_cvtph_ps(_mm256_loadu_si256((const __m256i *)(x + i + 16 * k)));
+            acc[k] = _mm512_fmadd_ps(wv, xv, acc[k]);
+        }
+    float s = _mm512_reduce_add_ps(_mm512_add_ps(_mm512_add_ps(acc[0], acc[1]), _mm512_add_ps(acc[2], acc[3])));
+    for (; i < n; i++) s += dmo_f16_to_f32(w[i]) * dmo_f16_to_f32(x[i]);
+    return s;
 }

@@ -559,8 +559,10 @@ static float dot_q6K(int64_t n, const dmo_block_q6_K *w, const dmo_block_q8_K *x
     return s;
 }
 
-/* The AVX-512 VNNI dots of dmoe_cpu_simd.c (bit-identical results), used
- * for the quantised types once dmo_set_simd(1) has found them supported. */
+/* The AVX-512 dots of dmoe_cpu_simd.c, used once dmo_set_simd(1) has found
+ * them supported (the CPU baseline): bit-identical results for the
+ * quantised types; binary32 sums for F32 / F16 (ggml's SIMD order, within
+ * tolerance of the binary64 sums here). */
 static int g_simd = 0;
 
 int dmo_set_simd(int on)
@@ -576,6 +578,10 @@ float dmo_vec_dot(int32_t wtype, int64_t n, const void *wrow, const void *xrow)
             return dmo_dot_q4K_simd(n, (const dmo_block_q4_K *)wrow, (const dmo_block_q8_K *)xrow);
         if (wtype == DMOE_TYPE_Q8_0)
             return dmo_dot_q8_0_simd(n, (const dmo_block_q8_0 *)wrow, (const dmo_block_q8_0 *)xrow);
+        if (wtype == DMOE_TYPE_F16)
+            return dmo_dot_f16_simd(n, (const uint16_t *)wrow, (const uint16_t *)xrow);
+        if (wtype == DMOE_TYPE_F32)
+            return dmo_dot_f32_simd(n, (const float *)wrow, (const float *)xrow);
     }
     switch (wtype) {
     case DMOE_TYPE_F32:  return dot_f32(n, (const float *)wrow, (const float *)xrow);
@@ -813,6 +819,8 @@ static void swiglu_f32(int H, int FF, const dmoe_tensor *gate, const dmoe_tensor
 {
     float *sg = (float *)malloc((size_t)N * FF * 4);
     float *su = (float *)malloc((size_t)N * FF * 4);
+    /* the CPU baseline's dots (dmo_set_simd) or the binary64 sums */
+    float (*dotf)(int64_t, const float *, const float *) = g_simd ? dmo_dot_f32_simd : dot_f32;
 #ifdef _OPENMP
 #pragma omp parallel for schedule(dynamic)
 #endif
@@ -822,8 +830,8 @@ static void swiglu_f32(int H, int FF, const dmoe_tensor *gate, const dmoe_tensor
         dmo_dequant_row(gate->type, tensor_row(gate, r, 0), wg, H);
         dmo_dequant_row(up->type, tensor_row(up, r, 0), wu, H);
         for (int t = 0; t < N; t++) {
-            float gv = dot_f32(H, wg, x + (size_t)t * H);
-            float uv = dot_f32(H, wu, x + (size_t)t * H);
+            float gv = dotf(H, wg, x + (size_t)t * H);
+            float uv = dotf(H, wu, x + (size_t)t * H);
             sg[(size_t)t * FF + r] = silu_f32(gv);        /* ggml_silu(g) */
             su[(size_t)t * FF + r] = uv;
         }
@@ -838,7 +846,7 @@ static void swiglu_f32(int H, int FF, const dmoe_tensor *gate, const dmoe_tensor
         float *wd = (float *)malloc((size_t)FF * 4);
         dmo_dequant_row(down->type, tensor_row(down, r, 0), wd, FF);
         for (int t = 0; t < N; t++)
-            y[(size_t)t * H + r] = dot_f32(FF, wd, sg + (size_t)t * FF);
+            y[(size_t)t * H + r] = dotf(FF, wd, sg + (size_t)t * FF);
         free(wd);
     }
     free(sg);

@@ -87,6 +87,8 @@ int      dmo_simd_available(void);
 int      dmo_set_simd(int on);
 float    dmo_dot_q4K_simd(int64_t n, const dmo_block_q4_K *w, const dmo_block_q8_K *x);
 float    dmo_dot_q8_0_simd(int64_t n, const dmo_block_q8_0 *w, const dmo_block_q8_0 *x);
+float    dmo_dot_f32_simd(int64_t n, const float *w, const float *x);
+float    dmo_dot_f16_simd(int64_t n, const uint16_t *w, const uint16_t *x);
 void     dmo_rows_q4K_simd(int64_t n, const dmo_block_q4_K *w, const uint8_t *act, size_t act_stride,
                            const int32_t *rows_in, int n_in, float *out, size_t out_stride);
 

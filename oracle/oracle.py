@@ -87,6 +87,10 @@ def load() -> C.CDLL:
     lib.dmo_dot_q4K_simd.restype = C.c_float
     lib.dmo_dot_q8_0_simd.argtypes = [C.c_int64, P, P]
     lib.dmo_dot_q8_0_simd.restype = C.c_float
+    lib.dmo_dot_f32_simd.argtypes = [C.c_int64, P, P]
+    lib.dmo_dot_f32_simd.restype = C.c_float
+    lib.dmo_dot_f16_simd.argtypes = [C.c_int64, P, P]
+    lib.dmo_dot_f16_simd.restype = C.c_float
     lib.dmo_rope_neox.argtypes = [P, C.c_int, C.c_int, C.c_int, C.c_float]
     lib.dmo_rope_neox.restype = None
     lib.dmo_attn_forward.argtypes = [C.POINTER(AttnHParams), C.POINTER(AttnDesc), P, C.c_int, P, P, C.c_int]
@@ -294,13 +298,16 @@ def simd_available() -> bool:
 
 
 def set_simd(on: bool) -> bool:
-    """Route the quantised dots through the AVX-512 VNNI versions (bit-identical
-    results; the CPU baseline's fast path).  Returns whether they are in use."""
+    """Route the dots through the AVX-512 versions (the CPU baseline's fast
+    path: bit-identical results for the quantised types, binary32 sums for
+    F32 / F16).  Returns whether they are in use."""
     return bool(load().dmo_set_simd(1 if on else 0))
 
 
 def vec_dot_simd(wt: int, n: int, wrow: np.ndarray, xrow: np.ndarray) -> float:
-    f = load().dmo_dot_q4K_simd if wt == 12 else load().dmo_dot_q8_0_simd
+    lib = load()
+    f = {12: lib.dmo_dot_q4K_simd, 8: lib.dmo_dot_q8_0_simd, 0: lib.dmo_dot_f32_simd,
+         1: lib.dmo_dot_f16_simd}[wt]
     return float(f(n, _p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(xrow))))
 
 
