@@ -142,10 +142,10 @@ struct RouteParams {
 // ---------------------------------------------------------------------------
 // Kernel launchers (each returns the hipGetLastError of its launch).
 // F16 expert products on MFMA, the prefill path (k_gemm.hip).
-constexpr int GM = 256;             // (token, slot) pairs per work item
+constexpr int GM = 128;             // (token, slot) pairs per work item
 constexpr int GK = 32;              // k per pipeline step
-constexpr int GN_GU = 128;          // moe_ff rows of a gate/up item (gate and up)
-constexpr int GN_DN = 256;          // n_embd rows of a down item
+constexpr int GN_GU = 256;          // moe_ff rows of a gate/up item (gate and up)
+constexpr int GN_DN = 512;          // n_embd rows of a down item
 constexpr int GEMM_BLOCKS = 1024;   // persistent grid
 struct GemmJob {
     WTensor eg, eu, ed;      // routed gate, up, down (F16, ggml row layout)

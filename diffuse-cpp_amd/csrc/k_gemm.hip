@@ -9,18 +9,22 @@
 //            phase 1 (routed) or as their hi / lo pair (shared)
 //   phase 1: y = W_down h
 //
-// Work item: one expert, a block of up to 256 of its (token, slot) pairs (or
-// 256 tokens of the shared expert) and a group of output rows (128 moe_ff rows
-// of gate and of up, or 256 n_embd rows of down).  Items of one expert and
+// Work item: one expert, a block of up to 128 of its (token, slot) pairs (or
+// 128 tokens of the shared expert) and a group of output rows (256 moe_ff rows
+// of gate and of up, or 512 n_embd rows of down).  Items of one expert and
 // row group but different pair blocks are a row-group count apart, so they run
 // together and share the weight rows through the caches.  Each 32-wide k
-// step stages the 256 activation rows and the 256 weight rows in LDS with the
-// LDS-direct global loads (global_load_lds_dwordx4: no registers held, so a
-// 5-stage ring keeps four steps of loads in flight to cover HBM latency);
-// each of the 8 wavefronts computes a 128 x 64 output
-// tile as 8 x 4 v_mfma_f32_16x16x32_f16 (operand layout as in k_expert.hip: srcA lane l =
+// step stages the 128 activation rows (8 KB) and the 512 weight rows (32 KB)
+// in LDS with the LDS-direct global loads (global_load_lds_dwordx4: no
+// registers held, so a 4-stage ring keeps three steps of loads in flight to
+// cover HBM latency); each of the 8 wavefronts computes a 128 x 64 output
+// tile (all 128 activation rows, its own 64 weight rows) as 8 x 4
+// v_mfma_f32_16x16x32_f16 (operand layout as in k_expert.hip: srcA lane l =
 // activation row l%16, k = 8*(l/16)+e; srcB = weight row, same k; D lane l =
-// weight row l%16, activation rows 4*(l/16)+i).
+// weight row l%16, activation rows 4*(l/16)+i).  (Items of 256 pairs x 256
+// weight rows, half of every stage the activation tile: the touched experts'
+// pairs, ~100 on average at the prefill's routing, padded 2.9x, and the
+// weights streamed at ~3.5 TB/s.)
 #include "dmoe_internal.h"
 
 #include <type_traits>
@@ -32,10 +36,14 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int GWAVES = 8;
 constexpr int GT = GWAVES * 64;      // threads per workgroup
-constexpr int GNW = 256;             // weight rows per item (gate/up: 128 moe_ff rows of each)
-constexpr int GS = 5;                // LDS pipeline stages (5 x 32 KB: all of the CU's LDS)
-constexpr int GTILE = GM * GK * 2;   // bytes of one operand tile of a stage (64-byte rows)
-constexpr int GP = GM * GK / 8 / GT; // 16-byte pieces per thread per tile and stage
+constexpr int GNW = 512;             // weight rows per item (gate/up: 256 moe_ff rows of each)
+constexpr int GS = 4;                // LDS pipeline stages (4 x 40 KB: all of the CU's LDS)
+constexpr int GTA = GM * GK * 2;     // bytes of a stage's activation tile (64-byte rows)
+constexpr int GTW = GNW * GK * 2;    // bytes of a stage's weight tile
+constexpr int GSTAGE = GTA + GTW;
+constexpr int GPA = GTA / 16 / GT;   // 16-byte pieces per thread and stage: activations
+constexpr int GPW = GTW / 16 / GT;   // weights
+constexpr int GLOADS = GPA + GPW;    // LDS-direct loads per thread and stage
 
 __device__ __forceinline__ float gsilu(float g) { return g / (1.0f + __expf(-g)); }
 
@@ -63,6 +71,19 @@ __device__ __forceinline__ void lds_load16(const void *src, uint32_t lds)
                  : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
+// The same with a wave-uniform 64-bit base (held in SGPRs) and a 32-bit
+// per-lane byte offset: one VGPR per stream instead of a 64-bit address.
+// (No non-temporal hint: the chunks of an expert read its rows through L2.)
+__device__ __forceinline__ void lds_load16_base(const void *base, uint32_t voff, uint32_t lds)
+{
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    const uint64_t sb = (uint64_t)lo | ((uint64_t)hi << 32);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 : : "v"(voff), "s"(sb), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+
 // LDS byte address of a shared-memory object
 __device__ __forceinline__ uint32_t lds_addr(const void *p)
 {
@@ -74,12 +95,12 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
 {
     constexpr bool DOWN = PHASE == 1;
     constexpr int GN = DOWN ? GN_DN : GN_GU;         // output rows per item
-    static_assert(GP * GT * 8 == GM * GK && GNW == GM && GP == 2 && GN_GU == 128 && GK == 32,
-                  "tile shapes: a stage's weight tile is two 128-row blocks of the tiled layout");
-    // stage s: activation tile at S[s][0], weight tile at S[s][1]; row r of a
-    // tile is 64 bytes at r * 64, its k-chunks swizzled by swz(r)
-    __shared__ __align__(16) uint8_t S[GS][2][GTILE];
-    const uint32_t s_base = __builtin_amdgcn_readfirstlane(lds_addr(&S[0][0][0]));
+    static_assert(GPA == 1 && GPW == 4 && GNW == 2 * GN_GU && GNW == GN_DN && GN_GU == 256 && GK == 32,
+                  "tile shapes: a stage's weight tile is four 128-row blocks of the tiled layout");
+    // stage s: activation tile at S[s][0 .. GTA), weight tile at S[s][GTA ..);
+    // row r of a tile is 64 bytes at r * 64, its k-chunks swizzled by swz(r)
+    __shared__ __align__(16) uint8_t S[GS][GSTAGE];
+    const uint32_t s_base = __builtin_amdgcn_readfirstlane(lds_addr(&S[0][0]));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -111,14 +132,14 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
     const int nr = max(0, min(u1, n_ec) - u0);                             // routed units
     const int s0 = max(u0, n_ec) - n_ec, ns = max(0, u1 - max(u0, n_ec)); // shared chunks
     const int seg_items = nr * rg + ns * rg_sh;
-    // wave grid 2 (activation rows) x 4 (weight rows): 128 x 64 per wave
-    const int tok0 = 128 * (wave >> 2);
-    const int wq = wave & 3;
+    // wave grid 1 (activation rows) x 8 (weight rows): 128 x 64 per wave
+    const int tok0 = 0;
+    const int wq = wave;
     // byte offsets of this lane's operand chunk g in a tile (swz depends on
     // row bits 1..2 only: the same for every 16-row tile): activation rows
-    // tok0 + 16 ti + r16 at aoff + 1024 ti; the wave's four 16-row weight
-    // tiles at boff + bstep(tw): down: rows 64 wq + 16 tw; gate/up: 32 moe_ff
-    // rows of gate (tiles 0, 1) and the same rows of up (tiles 2, 3)
+    // 16 ti + r16 at aoff + 1024 ti; the wave's four 16-row weight tiles at
+    // boff + bstep(tw): down: rows 64 wq + 16 tw; gate/up: 32 moe_ff rows of
+    // gate (tiles 0, 1) and the same rows of up (tiles 2, 3)
     const int aoff = (tok0 + r16) * 64 + ((g ^ swz(r16)) << 4);
     const int boff = ((DOWN ? 64 : 32) * wq + r16) * 64 + ((g ^ swz(r16)) << 4);
     auto bstep = [](int tw) -> int { return DOWN ? 1024 * tw : (tw < 2 ? 1024 * tw : GN * 64 + 1024 * (tw - 2)); };
@@ -146,22 +167,24 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         const size_t lo_off = (size_t)N * Kin;           // split arrays only
 
         // weight rows of the item (tiled layout, 128-row blocks of 8 KB per k
-        // step): gate rows 0..127 and up rows 128..255 of the same moe_ff rows
-        // (block rb of each), or 256 down rows (blocks 2 rb, 2 rb + 1).  (The
-        // fields are selected here, not in a lambda: a lambda that captured
-        // the argument struct would copy it to private memory.)
+        // step): gate rows 0..255 and up rows 256..511 of the same moe_ff rows
+        // (blocks 2 rb, 2 rb + 1 of each), or 512 down rows (blocks 4 rb ..
+        // 4 rb + 3).  (The fields are selected here, not in a lambda: a lambda
+        // that captured the argument struct would copy it to private memory.)
         const WTensor &w0 = DOWN ? (shared ? job.sd : job.ed) : (shared ? job.sg : job.eg);
         const WTensor &w1 = DOWN ? (shared ? job.sd : job.ed) : (shared ? job.su : job.eu);
         const size_t kblk = (size_t)nsteps * 8192;       // one 128-row block
-        const uint8_t *wb0 = w0.data + (size_t)e * w0.nb2 + (size_t)(DOWN ? 2 * rb : rb) * kblk;
-        const uint8_t *wb1 = DOWN ? wb0 + kblk : w1.data + (size_t)e * w1.nb2 + (size_t)rb * kblk;
+        const uint8_t *wb0 = w0.data + (size_t)e * w0.nb2 + (size_t)(DOWN ? 4 * rb : 2 * rb) * kblk;
+        const uint8_t *wb1 = DOWN ? wb0 + 2 * kblk : w1.data + (size_t)e * w1.nb2 + (size_t)(2 * rb) * kblk;
         // piece c = i * GT + tid of a tile (16 bytes at c * 16): row c >> 2,
         // slot c & 3, holding k-chunk (c & 3) ^ swz(row).  A wavefront's pieces
         // of one load are 1 KB of consecutive LDS, as the LDS-direct load
-        // writes, and of the tiled weights in HBM.
-        const uint8_t *ap[GP], *bp[GP];
+        // writes, and of the tiled weights in HBM: weight piece i * GT + tid
+        // is piece tid of 128-row block i of the item (block i & 1 of wb0 for
+        // i < 2, of wb1 after), its k step ks at ks * 8192.
+        const uint8_t *ap[GPA], *bp[GPW];
 #pragma unroll
-        for (int i = 0; i < GP; i++) {
+        for (int i = 0; i < GPA; i++) {
             const int c = i * GT + tid, row = c >> 2;
             const int q = (c & 3) ^ swz(row);
             int arow;
@@ -172,32 +195,39 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
                 arow = DOWN ? p : p / K;
             }
             ap[i] = reinterpret_cast<const uint8_t *>(A + (size_t)arow * Kin) + q * 16;
-            bp[i] = (c < 512 ? wb0 : wb1) + (size_t)(c & 511) * 16;
         }
-        // stage st of the k loop into LDS buffer st % GS: 2 GP loads per thread
-        // (none past the last stage, so nothing is in flight when the item ends)
+#pragma unroll
+        for (int i = 0; i < GPW; i++) {
+            const uint64_t b = (uint64_t)(uintptr_t)((i < 2 ? wb0 : wb1) + (size_t)(i & 1) * kblk);
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+            bp[i] = reinterpret_cast<const uint8_t *>((uintptr_t)((uint64_t)lo | ((uint64_t)hi << 32)));
+        }
+        const uint32_t bv = (uint32_t)tid * 16;
+        // stage st of the k loop into LDS buffer st % GS: GLOADS loads per
+        // thread (none past the last stage, so nothing is in flight when the
+        // item ends)
         auto issue = [&](int st) {
             if (st >= total_steps) return;
             const int pass = st >= nsteps ? 1 : 0;
             const int ks = st - pass * nsteps;
             const size_t ab = (size_t)ks * GK * 2 + (pass ? lo_off * 2 : 0);
             const size_t wbk = (size_t)ks * 8192;
-            const uint32_t sb = s_base + (uint32_t)((st % GS) * 2 * GTILE + wave * 1024);
+            const uint32_t sb = s_base + (uint32_t)((st % GS) * GSTAGE + wave * 1024);
 #pragma unroll
-            for (int i = 0; i < GP; i++) {
-                lds_load16(ap[i] + ab, sb + i * GT * 16);
-                lds_load16(bp[i] + wbk, sb + GTILE + i * GT * 16);
-            }
+            for (int i = 0; i < GPA; i++) lds_load16(ap[i] + ab, sb + i * GT * 16);
+#pragma unroll
+            for (int i = 0; i < GPW; i++) lds_load16_base(bp[i], bv + (uint32_t)wbk, sb + GTA + i * GT * 16);
         };
         // Operand reads of a stage (buffer buf, at the LDS byte offset of the
         // buffer in S): the lane offsets go through an empty asm so that the
         // compiler keeps one register each and adds the buffer offset per
         // step, instead of holding a precomputed address per buffer.
         auto read_w = [&](uint32_t boffs, int t) -> h8 {
-            return *reinterpret_cast<const h8 *>(&S[0][0][0] + boffs + bstep(t));
+            return *reinterpret_cast<const h8 *>(&S[0][0] + boffs + bstep(t));
         };
         auto read_a = [&](uint32_t aoffs, int ti) -> h8 {
-            return *reinterpret_cast<const h8 *>(&S[0][0][0] + aoffs + 1024 * ti);
+            return *reinterpret_cast<const h8 *>(&S[0][0] + aoffs + 1024 * ti);
         };
 
         f4 acc[8][4];
@@ -222,11 +252,11 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         // before the next step's first MFMA.
         // NTI (8, 4 or 0): the wavefront's 16-row activation blocks that hold
         // pairs of the item; the MFMAs and operand reads of the others are
-        // skipped (an item of fewer than 256 pairs repeats its last row)
+        // skipped (an item of fewer than 128 pairs repeats its last row)
         auto step = [&](auto nti_c, int st, int c, bool tail, bool next) {
             constexpr int NTI = decltype(nti_c)::value;
             if (!tail)
-                GEMM_WAIT_VM(2 * GP * (GS - 2));
+                GEMM_WAIT_VM(GLOADS * (GS - 2));
             else
                 GEMM_WAIT_VM(0);
             __builtin_amdgcn_s_barrier();
@@ -234,8 +264,8 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
             if (!tail) issue(st + GS);
             uint32_t al = aoff, bl = boff;
             asm volatile("" : "+v"(al), "+v"(bl));
-            const uint32_t nb = (uint32_t)(((st + 1) % GS) * 2 * GTILE);
-            const uint32_t aoffs = al + nb, boffs = bl + nb + GTILE;
+            const uint32_t nb = (uint32_t)(((st + 1) % GS) * GSTAGE);
+            const uint32_t aoffs = al + nb, boffs = bl + nb + GTA;
 #pragma unroll
             for (int ti = 0; ti < NTI; ti++) {
                 if (next) {
@@ -264,13 +294,13 @@ __global__ __launch_bounds__(GT) void k_gemm_f16(GemmJob job)
         for (int st = 0; st < GS; st++) issue(st);
         // stage 0 in LDS, its operands in set 0
         if (GS - 1 < total_steps)
-            GEMM_WAIT_VM(2 * GP * (GS - 1));
+            GEMM_WAIT_VM(GLOADS * (GS - 1));
         else
             GEMM_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
 #pragma unroll
-        for (int t = 0; t < 4; t++) rw[0][t] = read_w(boff + GTILE, t);
+        for (int t = 0; t < 4; t++) rw[0][t] = read_w(boff + GTA, t);
 #pragma unroll
         for (int ti = 0; ti < 8; ti++) ra[0][ti] = read_a(aoff, ti);
         // total_steps is even (Kin % 64 == 0): two steps per iteration, one
