@@ -9,6 +9,15 @@
 
 namespace dmoe {
 
+// A load of element i of a wave-uniform array through the scalar cache
+// (s_load: counted by lgkmcnt, never by the vmcnt of the vector loads, and
+// not queued behind them).  For data the kernel does not write.
+template <class T>
+__device__ __forceinline__ T ldc(const T *p, int i)
+{
+    return ((const __attribute__((address_space(4))) T *)(uintptr_t)p)[i];
+}
+
 // The f32 epilogue of one Q4_K super-block product: acc + dx (d S - dmin M),
 // rounded the same way in every kernel whatever its file's contraction
 // setting: d S rounded, then two fused multiply-adds.  (Left to

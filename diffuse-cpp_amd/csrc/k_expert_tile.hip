@@ -53,15 +53,6 @@ __device__ __forceinline__ uint4 xt_ld_nt16(const void *p)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// A load from memory no thread of the launch writes, at a wave-uniform
-// address: through the scalar cache (s_load), so that it is counted by
-// lgkmcnt and never by the vmcnt of the vector loads.
-template <class T>
-__device__ __forceinline__ T xt_ldc(const T *p, int i)
-{
-    return ((const __attribute__((address_space(4))) T *)(uintptr_t)p)[i];
-}
-
 // Item k is row group k % rg_n of unit k / rg_n; a unit is work-list entry
 // u < n_ec (up to 16 NC pairs), else shared chunk u - n_ec (8 NC tokens).
 // Every field is wave-uniform.
@@ -86,10 +77,10 @@ __device__ __forceinline__ XrItem xr_decode(const MoeJob &job, int k, int rg_n, 
     if (!I.valid) return I;
     I.shared = unit >= n_ec;
     if (!I.shared) {
-        I.e = xt_ldc(job.wl.ec_expert, unit);
-        const int c0 = xt_ldc(job.wl.ec_chunk, unit) * XR_CHUNK;
-        I.t_first = xt_ldc(job.offsets, I.e) + c0;
-        I.nt = min(XR_CHUNK, xt_ldc(job.counts, I.e) - c0);
+        I.e = ldc(job.wl.ec_expert, unit);
+        const int c0 = ldc(job.wl.ec_chunk, unit) * XR_CHUNK;
+        I.t_first = ldc(job.offsets, I.e) + c0;
+        I.nt = min(XR_CHUNK, ldc(job.counts, I.e) - c0);
         I.nblk = (I.nt + EXPERT_CHUNK - 1) / EXPERT_CHUNK;
     } else {
         I.e = 0;
@@ -301,7 +292,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_gu_rr(MoeJob job)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r16 = lane & 15;
     const int H = job.H, N = job.n_tokens, K = job.top_k;
-    const int n_ec = xt_ldc(job.wl.n_ec, 0);
+    const int n_ec = ldc(job.wl.n_ec, 0);
     const int nch = job.has_shared ? (N + XR_SCHUNK - 1) / XR_SCHUNK : 0;
     const int rg_n = job.FF / XR_ROWS;
     const int nsb = H / F::STEP;
@@ -449,7 +440,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void k_dn_rr(MoeJob job)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r16 = lane & 15;
     const int H = job.H, FF = job.FF, N = job.n_tokens, K = job.top_k;
-    const int n_ec = xt_ldc(job.wl.n_ec, 0);
+    const int n_ec = ldc(job.wl.n_ec, 0);
     const int nch = job.has_shared ? (N + XR_SCHUNK - 1) / XR_SCHUNK : 0;
     const int rg_n = H / XR_DN_ROWS;
     const int nsb = FF / F::STEP;
