@@ -290,8 +290,8 @@ int  dmoe_layer_forward_device(dmoe_ctx *ctx, const dmoe_layer *layer,
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * it).  Its workspace is a fixed array of DMOE_NOALLOC_SCRATCH_BYTES in
  * device memory, one per GPU, held until the process ends; a forward whose
- * workspace would exceed it (the LLaDA2-flash Q4_K layer takes up to 380
- * tokens, eleven 32-token blocks) is rejected with DMOE_ERR_INVALID_ARG
+ * workspace would exceed it (the LLaDA2-flash Q4_K layer takes up to 314
+ * tokens, nine whole 32-token blocks) is rejected with DMOE_ERR_INVALID_ARG
  * before anything is queued.  Every call on one GPU shares that GPU's array: calls that overlap
  * on one GPU (other streams, other contexts, other threads) race, so the
  * caller serialises them.  Results are identical to
