@@ -1083,13 +1083,31 @@ int dense_chunk(int path, int N) { return path == DP_Q6K ? std::min(N, PROJ_MAX_
 // any token count 1 .. nmax (a smaller last chunk may split its reduction
 // into more slices than a full one); with split_only, counting only launches
 // whose reduction is split (KS > 1), 0 when none is.
+// The scan costs a few thousand plan evaluations and every forward of a
+// projection plans its workspace twice, so results are kept per thread for
+// the last few shapes (the host enqueue of a 32-token dense MLP otherwise
+// took longer than its kernels).
 size_t proj_partial_max(int R, int K, int M, int nmax, bool split_only)
 {
+    struct Entry {
+        int R, K, M, nmax, split;
+        size_t v;
+    };
+    constexpr int kEntries = 16;
+    thread_local Entry cache[kEntries];
+    thread_local int used = 0, next = 0;
+    for (int i = 0; i < used; i++) {
+        const Entry &c = cache[i];
+        if (c.R == R && c.K == K && c.M == M && c.nmax == nmax && c.split == (int)split_only) return c.v;
+    }
     size_t best = 0;
     for (int n = 1; n <= nmax; n++) {
         if (split_only && proj_plan(R, K, M, n).KS <= 1) continue;
         best = std::max(best, proj_partial_floats(R, K, M, n));
     }
+    cache[next] = Entry{R, K, M, nmax, (int)split_only, best};
+    next = (next + 1) % kEntries;
+    used = std::min(used + 1, kEntries);
     return best;
 }
 
