@@ -29,6 +29,7 @@ sys.path.insert(0, str(ROOT / "diffuse-cpp_amd"))
 METRIC = "MoE-layer tokens/s + % HBM-BW roofline (32-tok block, Q4_K); prefill % MFMA"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+MFMA_INT8_PEAK_TOPS = 5000.0   # MI355X dense int8
 
 
 def parse():
@@ -255,6 +256,14 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds, cpu_tokens=None):
                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
                     **traffic_from_profile(dom_stage, cfg.name),
                     "algorithmic_bytes": dom_bytes, "hip_kernel": dom_kernel, "us_per_launch": dom_us}
+        if cfg.wtype in (dmoe.TYPE_Q4_K, dmoe.TYPE_Q8_0) and dom_us:
+            # the same launch against dense int8 MFMA: its integer dot
+            # products, 2 per multiply-add of the routed pairs' and the
+            # tokens' shared gate and up rows (the shared expert's two
+            # digit rows count once)
+            ops = 2.0 * (P * 2 * H * FF + N * 2 * H * SF)
+            roofline["int8_ops"] = ops
+            roofline["int8_frac"] = round(ops / (dom_us * 1e-6) / (MFMA_INT8_PEAK_TOPS * 1e12), 4)
 
     # layer-level: every weight byte the layer must read
     layer_bytes = touched * eb + sb + E * H * 4 + E * 4 + 2 * N * H * 4
