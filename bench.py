@@ -386,6 +386,17 @@ def bench_rows(a):
         torch.cuda.synchronize(dev)
         return e0.elapsed_time(e1) / a.rows_steps * 1e3          # us per call
 
+    def stage_times(fn, copies, names):
+        """us per launch of each stage over 10 profiled calls (HIP events
+        around every stage on the launch stream), under the row's names"""
+        ctx.profile(True)
+        for i in range(10):
+            fn(i % copies)
+        torch.cuda.synchronize(dev)
+        prof = ctx.profile_read()
+        ctx.profile(False)
+        return {names.get(k, k): round(v[0] / v[1] * 1e3, 2) for k, v in prof.items()}
+
     def rec(workload, us, nbytes, what):
         gbs = nbytes / (us * 1e-6) / 1e9
         return {"workload": workload, "us_per_call": round(us, 2), "algorithmic_bytes": int(nbytes),
@@ -414,6 +425,11 @@ def bench_rows(a):
         recs[f"n{N}"] = rec(f"attention half, flash shape (32 / 4 heads of 128, RoPE 64, Q4_K projections), "
                             f"{N} tokens", us, wbytes + act, "wqkv + wo weights, h in, h_out and moe_in out, "
                             "qkv and attention rows written and read")
+        recs[f"n{N}"]["stage_us"] = stage_times(
+            lambda i: ctx.attn_forward_device(layers[i], h, N, ho, mi, stream=sp), copies,
+            {"front": "input_norm", "gateup_shared": "qkv_proj", "act_quant_x": "qkv_x_quant",
+             "route": "qk_norm_rope", "scores": "attention", "act_quant_h": "attn_out_quant",
+             "down_shared": "out_proj", "combine": "residual_post_norm"})
     out["attention"] = recs
     del layers, keep
     torch.cuda.empty_cache()
@@ -433,6 +449,10 @@ def bench_rows(a):
     wb = 2 * FF * dmoe.row_size(dmoe.TYPE_Q4_K, Hd) + Hd * dmoe.row_size(dmoe.TYPE_Q4_K, FF)
     out["dense_mlp"] = rec(f"dense layer-0 MLP {Hd} x {FF}, Q4_K (F32 weight semantics), {N} tokens", us,
                            wb + 2 * N * Hd * 4, "gate, up and down weights, x in, y out")
+    out["dense_mlp"]["stage_us"] = stage_times(
+        lambda i: ctx.forward_device(dl[i], x, N, y, sp), copies,
+        {"act_quant_x": "x_quant", "gateup_shared": "gate_up_proj", "act_quant_h": "swiglu_h_quant",
+         "down_shared": "down_proj", "combine": "slice_reduce"})
     del dl, keep
     torch.cuda.empty_cache()
 
@@ -451,6 +471,9 @@ def bench_rows(a):
     wb = V * dmoe.row_size(dmoe.TYPE_Q4_K, Hh)
     out["step_tail"] = rec(f"step tail: RMSNorm, LM head {Hh} x {V} Q4_K, argmax + confidence, {N} tokens", us,
                            wb + 2 * N * V * 4 + N * Hh * 4, "output weights, logits written and read once, h in")
+    out["step_tail"]["stage_us"] = stage_times(
+        lambda i: ctx.head_forward_device(hl[i], h, N, 1e-6, tok, prob, None, sp), copies,
+        {"front": "output_norm", "act_quant_h": "h_quant", "down_shared": "lm_head", "combine": "argmax_confidence"})
     del hl, keep
     ctx.close()
     torch.cuda.empty_cache()
