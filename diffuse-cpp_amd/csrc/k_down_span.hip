@@ -135,9 +135,14 @@ __global__ __launch_bounds__(DS_WAVES * 64) void k_down_span(DownRowsJob job)
     }
     __syncthreads();
 
-    // this wavefront's tile-units i0 .. i1 - 1, nsb steps each
+    // this wavefront's tile-units i0 .. i1 - 1, nsb steps each: eighth
+    // 2 (w % 4) + w / 4, so that the two wavefronts of one SIMD (w and
+    // w + 4) take adjacent eighths, which together hold a quarter of the
+    // range to within one tile (eighths alternate between the floor and the
+    // ceiling of a fractional size)
     const long L = hi - lo;
-    const long i0 = lo + L * wave / DS_WAVES, i1 = lo + L * (wave + 1) / DS_WAVES;
+    const int e8 = 2 * (wave & 3) + (wave >> 2);
+    const long i0 = lo + L * e8 / DS_WAVES, i1 = lo + L * (e8 + 1) / DS_WAVES;
     const int Q = (int)(i1 - i0) * nsb;
     // a step's place: unit slot, tile, super-block
     struct Cur {
