@@ -95,3 +95,54 @@ def test_noalloc_rejects_oversize(ctx, O):
     layer.free()
     del w
     torch.cuda.empty_cache()
+
+
+def test_noalloc_forward_replayed_from_a_hip_graph(ctx):
+    """The allocation-free forward captured into a HIP graph (torch's graph
+    capture on a side stream of default priority) and replayed on three new
+    inputs copied into the captured input buffer: every replay equals the
+    allocating forward's eager result on the same input bit for bit, with an
+    eager forward and a synchronisation between the replays.  (The forward
+    clears its flags and counters with fill kernels, not memset nodes.)"""
+    import torch
+    from dmoe import synth
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS["flash_q4k"]
+    w = synth.device_layer(cfg, 7, ctx)
+    layer = ctx.wrap_device(w)
+    xs = [torch.from_numpy(synth.make_x(cfg, 70 + i, 32)).to(dev) for i in range(3)]
+    main = torch.cuda.current_stream(dev)
+    refs = []
+    for x in xs:
+        y = torch.empty_like(x)
+        ctx.forward_device(layer, x, 32, y, main.cuda_stream)
+        refs.append(y)
+    torch.cuda.synchronize(dev)
+    x_in = torch.zeros_like(xs[0])
+    y_out = torch.full_like(xs[0], float("nan"))
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        # one eager call on the capture stream first
+        ctx.forward_device_noalloc(layer, x_in, 32, y_out, side.cuda_stream)
+    side.synchronize()
+    g = torch.cuda.CUDAGraph()
+    _say("case: allocation-free forward captured in a HIP graph, flash Q4_K, N=32")
+    with torch.cuda.graph(g, stream=side):
+        ctx.forward_device_noalloc(layer, x_in, 32, y_out, side.cuda_stream)
+    torch.cuda.synchronize(dev)
+    for i, x in enumerate(xs):
+        x_in.copy_(x)
+        y_out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y_out.view(torch.int32), refs[i].view(torch.int32)), f"replay {i}"
+        # eager work between the replays
+        y = torch.empty_like(x)
+        ctx.forward_device(layer, xs[(i + 1) % 3], 32, y, main.cuda_stream)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y.view(torch.int32), refs[(i + 1) % 3].view(torch.int32))
+    del g
+    layer.free()
+    del w
+    torch.cuda.empty_cache()
