@@ -129,6 +129,23 @@ def uses_tile_kernels(cfg):
     return False
 
 
+def uses_q4k_gemm(cfg):
+    """Whether the library runs cfg's Q4_K expert products on its grouped
+    GEMM (k_expert_gemm.hip): the rule of use_q4k_gemm in dmoe_api.cpp for
+    the flash shapes (64 or more pairs per expert averaged over all experts,
+    N k / E), DMOE_EXPERT_GEMM overriding it and DMOE_EXPERT_TILE turning it
+    off."""
+    import dmoe
+    if cfg.wtype != dmoe.TYPE_Q4_K:
+        return False
+    env = os.environ.get("DMOE_EXPERT_GEMM")
+    if env in ("0", "1"):
+        return env == "1"
+    if os.environ.get("DMOE_EXPERT_TILE") in ("0", "1") or os.environ.get("DMOE_Q4K_COLUMN_BLOCKS"):
+        return False
+    return cfg.n_tokens * cfg.top_k // cfg.n_experts >= 64
+
+
 def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds, cpu_tokens=None):
     """One MoE layer of config cfg: tokens/s, per-stage times, the dominant
     kernel's roofline, realised routing and (cpu_seconds > 0) the oracle's
@@ -237,7 +254,10 @@ def bench_layer(a, cfg, steps, warmup, copies, cpu_seconds, cpu_tokens=None):
         else:
             def act_row(n):
                 return 2 * n
-        if fmt and tile:
+        if uses_q4k_gemm(cfg):
+            dom_kernel = "dmoe::k_gemm_q4k<false>"
+            h_bytes = P * FF * 4 + N * SF * 4
+        elif fmt and tile:
             dom_kernel = f"dmoe::k_gu_rr<dmoe::{fmt}>"
             h_bytes = P * FF * 4 + N * SF * 4
         elif cfg.wtype == dmoe.TYPE_Q4_K:

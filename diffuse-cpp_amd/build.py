@@ -36,7 +36,7 @@ CFLAGS = [
     f"-I{ROOT / 'include'}",
 ]
 
-SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "k_expert_tile.hip", "k_down_span.hip", "k_expert_q80.hip",
+SOURCES = ["k_router.hip", "k_quant.hip", "k_gemv.hip", "k_prep.hip", "k_expert.hip", "k_expert_tile.hip", "k_expert_gemm.hip", "k_down_span.hip", "k_expert_q80.hip",
            "k_gemm.hip", "k_norm.hip", "k_down_rows.hip", "k_head.hip", "k_attn.hip", "k_proj.hip",
            "dmoe_api.cpp", "dmoe_gguf.cpp"]
 HEADERS = ["dmoe_internal.h", "dmoe_device.h", "dmoe_prep.h", "dmoe_q4k.h"]

@@ -354,9 +354,30 @@ bool use_gemm_path(const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool sh
 // kernels: 91 against 110 us at 32 tokens); F16 below 8 (more take the
 // grouped GEMM of 256-pair items).  DMOE_EXPERT_TILE = 0 / 1 turns the
 // choice off / on for every N (with the shapes the tile kernels take).
+// The Q4_K grouped GEMM of k_expert_gemm.hip (units of up to 128 pairs, each
+// step's weight tiles applied to all of a unit's pairs): by the forward's
+// pairs per expert averaged over all experts, N k / E of at least
+// GEMM_Q4K_MIN_AVG.  DMOE_EXPERT_GEMM = 0 / 1 turns it off / on for every N;
+// DMOE_EXPERT_TILE or DMOE_Q4K_COLUMN_BLOCKS set selects their kernels.
+constexpr long GEMM_Q4K_MIN_AVG = 64;
+
+bool use_q4k_gemm(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
+                  int N)
+{
+    if (!use_mfma_path(hp, wtype, stype, shared) || !expert_gemm_q4k_ok(hp.n_embd, hp.moe_ff, hp.shared_ff, shared))
+        return false;
+    // 32-bit byte offsets into the activation arrays
+    if ((long)N * hp.top_k * hp.moe_ff >= (1L << 31) || 2L * N * hp.n_embd >= (1L << 31)) return false;
+    if (sw.expert_gemm >= 0) return sw.expert_gemm == 1;
+    if (sw.expert_tile >= 0 || sw.q4k_column_blocks) return false;
+    const long avg = (long)N * hp.top_k / (hp.n_experts > 0 ? hp.n_experts : 1);
+    return avg >= GEMM_Q4K_MIN_AVG;
+}
+
 bool use_tile_path(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wtype, int32_t stype, bool shared,
                    int N)
 {
+    if (use_q4k_gemm(sw, hp, wtype, stype, shared, N)) return false;
     const bool f16 = use_gemm_path(hp, wtype, stype, shared);
     if (!(use_mfma_path(hp, wtype, stype, shared) || use_q80_path(hp, wtype, stype, shared) || f16) ||
         !expert_tile_ok(hp.n_embd, hp.moe_ff, hp.shared_ff, shared))
@@ -375,6 +396,7 @@ bool use_down_rows(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t wty
                    int N)
 {
     return use_mfma_path(hp, wtype, stype, shared) && !use_tile_path(sw, hp, wtype, stype, shared, N) &&
+           !use_q4k_gemm(sw, hp, wtype, stype, shared, N) &&
            down_rows_ok(N, hp.top_k, hp.n_experts, hp.n_embd, hp.moe_ff) && q4k_column_blocks(sw, hp, N) == 1;
 }
 
@@ -466,7 +488,8 @@ size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t 
     const bool gemv = !gemm && !use_mfma_path(hp, wtype, stype, shared) &&
                       !use_q80_path(hp, wtype, stype, shared);
     const bool tile = use_tile_path(sw, hp, wtype, stype, shared, N);
-    t.wl.chunk = tile ? expert_tile_chunk(wtype)
+    t.wl.chunk = use_q4k_gemm(sw, hp, wtype, stype, shared, N) ? EXPERT_GEMM_CHUNK
+                 : tile                                         ? expert_tile_chunk(wtype)
                  : gemm ? GM
                         : EXPERT_CHUNK * (use_mfma_path(hp, wtype, stype, shared) ? q4k_column_blocks(sw, hp, N) : 1);
     t.wl.n_ec = (int32_t *)take(4);
@@ -480,8 +503,8 @@ size_t plan_workspace(const KernelSwitches &sw, const dmoe_hparams &hp, int32_t 
             t.axs = take_act(take, N, H, true);
             t.ahs = take_act(take, N, SF, true);
         }
-        if (tile) {
-            // the tile kernels' f32 h, converted by one launch
+        if (tile || use_q4k_gemm(sw, hp, wtype, stype, shared, N)) {
+            // the tile kernels' and the grouped GEMM's f32 h, converted by one launch
             t.h = (float *)take((size_t)P * FF * 4);
             if (shared) t.hs = (float *)take((size_t)N * SF * 4);
         }
@@ -680,15 +703,17 @@ int enqueue_forward(dmoe_ctx *ctx, const dmoe_layer *L, const Workspace &w, cons
         job.ahs = w.ahs;
         job.ye = w.ye;
         job.ys = w.ys;
-        if (use_tile_path(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N)) {
-            // many tokens per expert: the tile kernels, h converted between them
-            STAGE(ST_GATEUP, launch_expert_tile(0, job, s));
+        const bool xgemm = use_q4k_gemm(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N);
+        if (xgemm || use_tile_path(ctx->sw, hp, L->eg.type, L->sg.type, L->has_shared, N)) {
+            // many tokens per expert: the grouped GEMM or the tile kernels, h
+            // converted between the two launches
+            STAGE(ST_GATEUP, xgemm ? launch_expert_gemm_q4k(0, job, s) : launch_expert_tile(0, job, s));
             PrepJob hj[2];
             int nhj = 0;
             hj[nhj++] = PrepJob{w.h, N * K, FF, q8 ? ACT_Q80 : ACT_Q8K, w.ah};
             if (L->has_shared) hj[nhj++] = PrepJob{w.hs, N, hp.shared_ff, q8 ? ACT_SPLIT32 : ACT_SPLIT, w.ahs};
             STAGE(ST_ACTQ_H, launch_prep(hj, nhj, s));
-            STAGE(ST_DOWN, launch_expert_tile(1, job, s));
+            STAGE(ST_DOWN, xgemm ? launch_expert_gemm_q4k(1, job, s) : launch_expert_tile(1, job, s));
             STAGE(ST_COMBINE, launch_combine(w.ye, w.rb.weights, L->has_shared ? w.ys : nullptr, N,
                                              K, H, y, s));
             return DMOE_OK;
@@ -1697,6 +1722,10 @@ KernelSwitches read_kernel_switches()
     if (const char *v = getenv("DMOE_EXPERT_TILE")) {
         const int n = atoi(v);
         if (n == 0 || n == 1) sw.expert_tile = n;
+    }
+    if (const char *v = getenv("DMOE_EXPERT_GEMM")) {
+        const int n = atoi(v);
+        if (n == 0 || n == 1) sw.expert_gemm = n;
     }
     return sw;
 }

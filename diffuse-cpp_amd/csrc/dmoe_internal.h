@@ -123,9 +123,11 @@ struct MoeJob {
 //   DMOE_DOWN_FUSED = 1               few-token Q4_K down products as the single fused launch
 //   DMOE_GATEUP_LDS = 1               the LDS-ring gate/up kernel instead of the register ring
 //   DMOE_EXPERT_TILE = 0 / 1          the tile kernels (k_expert_tile.hip) off / on for every N
+//   DMOE_EXPERT_GEMM = 0 / 1          the Q4_K grouped GEMM (k_expert_gemm.hip) off / on for every N
 struct KernelSwitches {
     int q4k_column_blocks = 0;
     int expert_tile = -1;                // -1: by tokens per expert
+    int expert_gemm = -1;                // -1: by tokens per expert
     bool down_fused = false;
     bool gateup_lds = false;
 };
@@ -288,6 +290,13 @@ hipError_t launch_expert_q4k(int phase, const MoeJob &job, hipStream_t s, int nc
 bool expert_tile_ok(int H, int FF, int SF, bool shared);
 int expert_tile_chunk(int32_t type);
 hipError_t launch_expert_tile(int phase, const MoeJob &job, hipStream_t s);
+// Q4_K expert products as a grouped int8-MFMA GEMM for many pairs per expert
+// (k_expert_gemm.hip): units of up to 128 pairs (the work list's chunk) or
+// 64 shared tokens, a step's weights and activations streamed through LDS
+// together; h / hs and ye / ys as with the tile kernels.
+constexpr int EXPERT_GEMM_CHUNK = 128;
+bool expert_gemm_q4k_ok(int H, int FF, int SF, bool shared);
+hipError_t launch_expert_gemm_q4k(int phase, const MoeJob &job, hipStream_t s);
 // Down products of the Q4_K experts and the weighted combine in one launch
 // for few tokens (k_down_rows.hip): one workgroup per 16 output rows, every
 // touched expert's 16-row tile, results folded in slot order in LDS.

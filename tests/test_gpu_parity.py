@@ -270,6 +270,40 @@ def test_tile_path_bit_exact(ctx, name, monkeypatch):
     assert np.array_equal(got[0].view(np.uint32), ref[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("name", ["flash_q4k_n2048", "flash_q4k_n1024", "flash_q4k_n256", "mid_q4k_n1000",
+                                  "mid_q4k_n200"])
+def test_q4k_gemm_bit_exact(ctx, name, monkeypatch):
+    """Q4_K products on the grouped GEMM (units of up to 128 pairs of an
+    expert, eight column blocks per weight-tile step, weights and activations
+    streamed through LDS together) against the tile kernels: the same integer
+    sums per super-block and the same epilogue in the same order, so the layer
+    outputs are identical bit for bit.  Each GEMM call follows one on other
+    inputs of the same size; 256 and 200 tokens force the GEMM onto units of
+    one or two blocks, and the mid-sized layers (1000 and 200 tokens, no block
+    routing) end their shared expert on a partial unit."""
+    import dmoe
+    from dmoe import synth
+    if name.startswith("mid"):
+        n = int(name.rsplit("_n", 1)[1])
+        cfg = synth.LayerConfig(name, 512, 32, 512, 8, 4, 32, 512, 12, 12, n, -0.05, 0.05)
+    else:
+        cfg = synth.CONFIGS[name]
+    _say(f"case: grouped Q4_K GEMM vs tile kernels, {name}")
+    wd = synth.device_layer(cfg, 35, ctx)
+    layer = ctx.wrap_device(wd)
+    x = synth.make_x(cfg, 35, cfg.n_tokens)
+    xo = synth.make_x(cfg, 36, cfg.n_tokens)
+    c = _ctx_with(monkeypatch, {"DMOE_EXPERT_TILE": "1", "DMOE_EXPERT_GEMM": "0"})
+    ref = [c.forward(layer, a) for a in (x, xo)]
+    c.close()
+    c = _ctx_with(monkeypatch, {"DMOE_EXPERT_GEMM": "1"})
+    got = [c.forward(layer, a) for a in (xo, x)]
+    c.close()
+    assert np.isfinite(ref[0]).all()
+    assert np.array_equal(got[1].view(np.uint32), ref[0].view(np.uint32))
+    assert np.array_equal(got[0].view(np.uint32), ref[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("n_tokens,tile", [(32, 0), (40, 0), (128, 1), (2048, 1), (1000, 1)],
                          ids=["N32_gemm", "N40_gemm", "N128_tile", "N2048_tile", "N1000_tile"])
 def test_f16_paths(ctx, O, n_tokens, tile, monkeypatch):
