@@ -1335,8 +1335,30 @@ struct ProjWs {
 // in chunks of up to PROJ_MAX_TOKENS tokens.
 int proj_chunk(int path, int N) { return path == DP_Q6K ? std::min(N, PROJ_MAX_TOKENS) : N; }
 
+// Q4_K projections of PROJ_GEMM_MIN_TOKENS or more tokens run on the grouped
+// GEMM's down launch (k_expert_gemm.hip) with shared units only: 64 tokens
+// (128 digit rows) per unit, 256 output rows per item, the reduction split
+// into the fewest slices (2 or more super-blocks each) that give every CU an
+// item.  Returns the slice count, 0 where the GEMM does not take the shape.
+constexpr int PROJ_GEMM_MIN_TOKENS = 64;
+
+int proj_gemm_slices(const KernelSwitches &sw, int path, int rows, int K, int N)
+{
+    if (path != DP_Q4K || sw.proj_gemm == 0 || (sw.proj_gemm < 0 && N < PROJ_GEMM_MIN_TOKENS) ||
+        !expert_gemm_q4k_ok(rows, K, K, true) || 2L * N * K >= (1L << 31))
+        return 0;
+    int n_cu = 0;
+    if (device_cu_count(&n_cu) != hipSuccess || n_cu <= 0) n_cu = 256;
+    const long items = (long)((N + 63) / 64) * (rows / 256);
+    const int nsb = K / 256;
+    int best = 1;
+    for (int ks = 2; ks <= 16 && items * best < n_cu; ks *= 2)
+        if (nsb % ks == 0 && nsb / ks >= 2) best = ks;
+    return best;
+}
+
 template <class Take>
-ProjWs plan_proj(int path, int N, int K, int rows, Take &&take)
+ProjWs plan_proj(const KernelSwitches &sw, int path, int N, int K, int rows, Take &&take)
 {
     ProjWs p{};
     p.n_ec = (int32_t *)take(4);
@@ -1345,8 +1367,11 @@ ProjWs plan_proj(int path, int N, int K, int rows, Take &&take)
     case DP_Q6K: {
         const int n = proj_chunk(path, N);
         p.act = take_act(take, n, K, true);
-        if (proj_ok(rows, K, n))
+        if (proj_ok(rows, K, n)) {
             if (const size_t pf = proj_partial_max(rows, K, 1, n, true)) p.part = (float *)take(pf * 4);
+        } else if (const int ks = proj_gemm_slices(sw, path, rows, K, N); ks > 1) {
+            p.part = (float *)take((size_t)ks * N * rows * 4);
+        }
         break;
     }
     case DP_Q80: p.act = take_act(take, N, K, true, true); break;
@@ -1417,6 +1442,28 @@ int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTens
     LAUNCH_TRY(ctx, launch_fill_i32(p.n_ec, 0, 1, s));
     WorkList wl{};
     wl.n_ec = p.n_ec;
+    if (const int ks = proj_gemm_slices(ctx->sw, path, rows, K, N)) {
+        // many tokens of Q4_K: the grouped GEMM's down launch over shared
+        // units, its reduction slices added in order
+        wl.chunk = EXPERT_GEMM_CHUNK;
+        MoeJob job{};
+        job.sd = W;
+        job.has_shared = 1;
+        job.H = rows;
+        job.FF = K;
+        job.SF = K;
+        job.n_tokens = N;
+        job.top_k = 1;
+        job.wl = wl;
+        job.ahs = p.act;
+        job.ys = ks > 1 ? p.part : y;
+        job.ks = ks;
+        PrepJob pj{x, N, K, ACT_SPLIT, p.act};
+        STAGE(st_conv, launch_prep(&pj, 1, s));
+        STAGE(st_prod, launch_expert_gemm_q4k(1, job, s));
+        if (ks > 1) STAGE(ST_COMBINE, launch_proj_reduce(p.part, ks, N, rows, y, rows, s));
+        return DMOE_OK;
+    }
     if (path == DP_F16) {
         wl.chunk = GM;
         GemmJob job{};
@@ -1521,7 +1568,8 @@ struct HeadWs {
     ProjWs proj;
 };
 
-size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint8_t *base, HeadWs *w)
+size_t plan_head(const KernelSwitches &sw, const dmoe_layer *L, int N, bool host_io, bool own_logits, uint8_t *base,
+                 HeadWs *w)
 {
     const int H = L->hp.n_embd, V = L->n_vocab;
     size_t off = 0;
@@ -1539,7 +1587,7 @@ size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint
     t.xn = (float *)take((size_t)N * H * 4);
     if (own_logits) t.logits = (float *)take((size_t)N * V * 4);
     t.part = (ArgmaxPart *)take(argmax_partials_bytes(N, V));
-    t.proj = plan_proj(head_path(L->sd.type, V, H), N, H, V, take);
+    t.proj = plan_proj(sw, head_path(L->sd.type, V, H), N, H, V, take);
     if (w) *w = t;
     return off;
 }
@@ -1547,9 +1595,9 @@ size_t plan_head(const dmoe_layer *L, int N, bool host_io, bool own_logits, uint
 int ensure_head_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, bool own_logits,
                           HeadWs *w)
 {
-    int rc = grow_workspace(ctx, plan_head(L, N, host_io, own_logits, nullptr, nullptr));
+    int rc = grow_workspace(ctx, plan_head(ctx->sw, L, N, host_io, own_logits, nullptr, nullptr));
     if (rc) return rc;
-    plan_head(L, N, host_io, own_logits, (uint8_t *)ctx->ws, w);
+    plan_head(ctx->sw, L, N, host_io, own_logits, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
 }
 
@@ -1596,7 +1644,7 @@ struct AttnWs {
     ProjWs pq, po;
 };
 
-size_t plan_attn(const dmoe_layer *L, int N, bool host_io, uint8_t *base, AttnWs *w)
+size_t plan_attn(const KernelSwitches &sw, const dmoe_layer *L, int N, bool host_io, uint8_t *base, AttnWs *w)
 {
     const dmoe_attn_hparams &a = L->ahp;
     const int H = a.n_embd, QD = a.n_head * a.head_dim, KD = a.n_head_kv * a.head_dim, QKV = QD + 2 * KD;
@@ -1620,8 +1668,8 @@ size_t plan_attn(const dmoe_layer *L, int N, bool host_io, uint8_t *base, AttnWs
     t.att = (float *)take((size_t)N * QD * 4);
     t.proj = (float *)take((size_t)N * H * 4);
     t.scratch = (float *)take((size_t)N * H * 4);
-    t.pq = plan_proj(head_path(L->aqkv.type, QKV, H), N, H, QKV, take);
-    t.po = plan_proj(head_path(L->awo.type, H, QD), N, QD, H, take);
+    t.pq = plan_proj(sw, head_path(L->aqkv.type, QKV, H), N, H, QKV, take);
+    t.po = plan_proj(sw, head_path(L->awo.type, H, QD), N, QD, H, take);
     if (w) *w = t;
     return off;
 }
@@ -1726,6 +1774,10 @@ KernelSwitches read_kernel_switches()
     if (const char *v = getenv("DMOE_EXPERT_GEMM")) {
         const int n = atoi(v);
         if (n == 0 || n == 1) sw.expert_gemm = n;
+    }
+    if (const char *v = getenv("DMOE_PROJ_GEMM")) {
+        const int n = atoi(v);
+        if (n == 0 || n == 1) sw.proj_gemm = n;
     }
     return sw;
 }
@@ -2091,10 +2143,10 @@ int dmoe_attn_forward(dmoe_ctx *ctx, const dmoe_layer *L, const float *h, int32_
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "h/h_out NULL or n_tokens = %d", n_tokens);
     const int H = L->ahp.n_embd;
     HIP_TRY(ctx, hipSetDevice(ctx->device));
-    int rc = grow_workspace(ctx, plan_attn(L, n_tokens, true, nullptr, nullptr));
+    int rc = grow_workspace(ctx, plan_attn(ctx->sw, L, n_tokens, true, nullptr, nullptr));
     if (rc) return rc;
     AttnWs w;
-    plan_attn(L, n_tokens, true, (uint8_t *)ctx->ws, &w);
+    plan_attn(ctx->sw, L, n_tokens, true, (uint8_t *)ctx->ws, &w);
     hipStream_t s = ctx->stream;
     HIP_TRY(ctx, hipMemcpyAsync(w.h, h, (size_t)n_tokens * H * 4, hipMemcpyHostToDevice, s));
     if ((rc = enqueue_attn(ctx, L, w, w.h, n_tokens, w.h_out, moe_in ? w.moe_in : nullptr, s))) return rc;
@@ -2115,10 +2167,10 @@ int dmoe_attn_forward_device(dmoe_ctx *ctx, const dmoe_layer *L, const float *h_
     if (!al16(h_dev) || !al16(h_out_dev) || (moe_in_dev && !al16(moe_in_dev)))
         return set_err(ctx, DMOE_ERR_INVALID_ARG, "device buffers must be 16-byte aligned");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
-    int rc = grow_workspace(ctx, plan_attn(L, n_tokens, false, nullptr, nullptr));
+    int rc = grow_workspace(ctx, plan_attn(ctx->sw, L, n_tokens, false, nullptr, nullptr));
     if (rc) return rc;
     AttnWs w;
-    plan_attn(L, n_tokens, false, (uint8_t *)ctx->ws, &w);
+    plan_attn(ctx->sw, L, n_tokens, false, (uint8_t *)ctx->ws, &w);
     return enqueue_attn(ctx, L, w, h_dev, n_tokens, h_out_dev, moe_in_dev, (hipStream_t)stream);
 }
 

@@ -111,6 +111,10 @@ struct MoeJob {
     float *h, *hs;           // gate/up results [N*K][FF], [N][SF]
     ActI8 ah, ahs;         // h and hs converted for the down products
     float *ye, *ys;          // down results [N*K][H], [N][H]
+    // Grouped Q4_K GEMM down launches with only shared units (a projection of
+    // many tokens, k_expert_gemm.hip): the reduction in ks slices, slice s's
+    // results at ys + s N H (0 or 1: one slice, ys itself)
+    int32_t ks;
     // F16 experts (k_expert_tile.hip): x and h as f16 rows, the shared
     // expert's as hi / lo pairs (lo rows after the hi rows)
     const uint16_t *x16, *xs16;
@@ -124,10 +128,13 @@ struct MoeJob {
 //   DMOE_GATEUP_LDS = 1               the LDS-ring gate/up kernel instead of the register ring
 //   DMOE_EXPERT_TILE = 0 / 1          the tile kernels (k_expert_tile.hip) off / on for every N
 //   DMOE_EXPERT_GEMM = 0 / 1          the Q4_K grouped GEMM (k_expert_gemm.hip) off / on for every N
+//   DMOE_PROJ_GEMM = 0 / 1            Q4_K projections (attention, LM head) past the few-token
+//                                     kernel on that GEMM off / on for every N
 struct KernelSwitches {
     int q4k_column_blocks = 0;
     int expert_tile = -1;                // -1: by tokens per expert
     int expert_gemm = -1;                // -1: by tokens per expert
+    int proj_gemm = -1;                  // -1: by tokens
     bool down_fused = false;
     bool gateup_lds = false;
 };

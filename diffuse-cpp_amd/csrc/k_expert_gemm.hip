@@ -160,13 +160,18 @@ __global__ __launch_bounds__(XG_WAVES * 64) void k_gemm_q4k(MoeJob job)
     const int nch = job.has_shared ? (N + XG_SCHUNK - 1) / XG_SCHUNK : 0;
     const int rg_n = DOWN ? H / XG_DN_ROWS : FF / XG_GU_ROWS;
     const int Kin = DOWN ? FF : H;
-    const int steps = Kin / 256;                     // >= 2
+    // down launches of a projection split the reduction into KS slices of
+    // `steps` super-blocks (item k: slice k % KS of item k / KS)
+    const int KS = DOWN && job.ks > 1 ? job.ks : 1;
+    const int steps = Kin / 256 / KS;                // >= 2
     const int G = gridDim.x;
 
     int k = blockIdx.x;
-    XgItem I = xg_decode(job, k, rg_n, n_ec, nch);
+    XgItem I = xg_decode(job, k / KS, rg_n, n_ec, nch);
     if (!I.valid) return;
-    XgItem NI = xg_decode(job, k + G, rg_n, n_ec, nch);
+    int slice = k % KS;
+    XgItem NI = xg_decode(job, (k + G) / KS, rg_n, n_ec, nch);
+    int nslice = (k + G) % KS;
     if (tid < XG_CHUNK && !I.shared) s_pids[0][tid] = job.perm[I.t_first + min(tid, I.nt - 1)];
     __syncthreads();
 
@@ -179,25 +184,27 @@ __global__ __launch_bounds__(XG_WAVES * 64) void k_gemm_q4k(MoeJob job)
     const uint8_t *aqb = nullptr, *absb = nullptr, *adb = nullptr;
     uint32_t aqo[4] = {0, 0, 0, 0}, abso = 0, ado = 0;
     bool act_on = false;
-    auto set_cursor = [&](const XgItem &C, const int32_t *pids) {
+    // (the cursor's slice cs starts at super-block cs * steps of every row)
+    auto set_cursor = [&](const XgItem &C, int cs, const int32_t *pids) {
+        const int nsb = Kin / 256, sb0 = cs * steps;
         if (!DOWN) {
             const WTensor &a = C.shared ? job.sg : job.eg;
             const WTensor &b = C.shared ? job.su : job.eu;
             const int t16 = C.rg * (XG_GU_ROWS / 16) + wave;
-            wb0 = a.data + (size_t)C.e * a.nb2 + (size_t)t16 * steps * TILE_BYTES;
-            wb1 = b.data + (size_t)C.e * b.nb2 + (size_t)t16 * steps * TILE_BYTES;
+            wb0 = a.data + (size_t)C.e * a.nb2 + (size_t)t16 * nsb * TILE_BYTES;
+            wb1 = b.data + (size_t)C.e * b.nb2 + (size_t)t16 * nsb * TILE_BYTES;
         } else {
             const WTensor &W = C.shared ? job.sd : job.ed;
             const int t16 = C.rg * (XG_DN_ROWS / 16) + 2 * wave;
-            wb0 = W.data + (size_t)C.e * W.nb2 + (size_t)t16 * steps * TILE_BYTES;
-            wb1 = wb0 + (size_t)steps * TILE_BYTES;
+            wb0 = W.data + (size_t)C.e * W.nb2 + ((size_t)t16 * nsb + sb0) * TILE_BYTES;
+            wb1 = wb0 + (size_t)nsb * TILE_BYTES;
         }
         act_on = wave < C.nblk;
         if (act_on) {
             const ActI8 &A = DOWN ? (C.shared ? job.ahs : job.ah) : (C.shared ? job.axs : job.ax);
-            aqb = reinterpret_cast<const uint8_t *>(A.q);
-            absb = reinterpret_cast<const uint8_t *>(A.bs);
-            adb = reinterpret_cast<const uint8_t *>(A.d);
+            aqb = reinterpret_cast<const uint8_t *>(A.q) + (size_t)sb0 * 256;
+            absb = reinterpret_cast<const uint8_t *>(A.bs) + (size_t)sb0 * 32;
+            adb = reinterpret_cast<const uint8_t *>(A.d) + (size_t)sb0 * 4;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int r = 4 * j + (lane >> 4);
@@ -232,7 +239,7 @@ __global__ __launch_bounds__(XG_WAVES * 64) void k_gemm_q4k(MoeJob job)
         }
     };
 
-    set_cursor(I, s_pids[0]);
+    set_cursor(I, slice, s_pids[0]);
     issue(0, 0);
     int stg = 0;                                      // the stage the products read
     int buf = 0;                                      // the pair list of item I
@@ -258,7 +265,7 @@ __global__ __launch_bounds__(XG_WAVES * 64) void k_gemm_q4k(MoeJob job)
             if (s + 1 < steps) {
                 issue(stg ^ 1, s + 1);
             } else if (NI.valid) {
-                set_cursor(NI, s_pids[buf ^ 1]);
+                set_cursor(NI, nslice, s_pids[buf ^ 1]);
                 issue(stg ^ 1, 0);
             }
             if (s == 0 && tid < XG_CHUNK && NI.valid && !NI.shared)
@@ -303,7 +310,7 @@ __global__ __launch_bounds__(XG_WAVES * 64) void k_gemm_q4k(MoeJob job)
             }
         } else {
             const int row0 = I.rg * XG_DN_ROWS + 32 * wave + r16;
-            float *out = I.shared ? job.ys : job.ye;
+            float *out = I.shared ? job.ys + (size_t)slice * N * H : job.ye;
 #pragma unroll
             for (int c = 0; c < XG_NC; c++) {
                 if (c >= I.nblk) continue;
@@ -332,9 +339,11 @@ __global__ __launch_bounds__(XG_WAVES * 64) void k_gemm_q4k(MoeJob job)
         }
         if (!NI.valid) break;
         I = NI;
+        slice = nslice;
         k += G;
         buf ^= 1;
-        NI = xg_decode(job, k + G, rg_n, n_ec, nch);
+        NI = xg_decode(job, (k + G) / KS, rg_n, n_ec, nch);
+        nslice = (k + G) % KS;
     }
     // every wavefront leaves with no loads in flight
     EXPERT_WAIT_VM(0);
@@ -352,17 +361,31 @@ bool expert_gemm_q4k_ok(int H, int FF, int SF, bool shared)
 // row group per XCD); each runs its items until the schedule's units end.
 hipError_t launch_expert_gemm_q4k(int phase, const MoeJob &job, hipStream_t s)
 {
-    if (job.eg.type != DMOE_TYPE_Q4_K || (job.has_shared && job.sg.type != DMOE_TYPE_Q4_K))
+    // routed experts (eg / eu / ed), the shared one (sg / su / sd) or both;
+    // a projection is a down launch of shared units only (no routed weights,
+    // the work list empty), optionally in ks reduction slices
+    const bool routed = job.eg.data || job.ed.data;
+    const WTensor &wr = phase == 0 ? job.eg : job.ed, &ws = phase == 0 ? job.sg : job.sd;
+    if ((routed && wr.type != DMOE_TYPE_Q4_K) || (job.has_shared && ws.type != DMOE_TYPE_Q4_K) ||
+        (!routed && !job.has_shared))
         return hipErrorInvalidValue;
     if (!expert_gemm_q4k_ok(job.H, job.FF, job.SF, job.has_shared) || job.wl.chunk != XG_CHUNK || !job.wl.n_ec)
         return hipErrorInvalidValue;
-    if (job.ax.K != job.H || job.ah.K != job.FF || (job.has_shared && (job.axs.K != job.H || job.ahs.K != job.SF)))
+    if (phase == 0 ? (job.ax.K != job.H || (job.has_shared && job.axs.K != job.H))
+                   : ((routed && job.ah.K != job.FF) || (job.has_shared && job.ahs.K != job.SF)))
         return hipErrorInvalidValue;
-    // the activation arrays' byte offsets are 32-bit (the largest: the
-    // routed h rows, N k x moe_ff bytes)
-    if ((long)job.n_tokens * job.top_k * job.FF >= (1L << 31) || 2L * job.n_tokens * job.H >= (1L << 31))
+    // slices: down launches of shared units only, each slice two or more
+    // super-blocks
+    if (job.ks > 1 && (phase == 0 || routed || (job.FF / 256) % job.ks || job.FF / 256 / job.ks < 2))
         return hipErrorInvalidValue;
-    if (phase == 0 ? (!job.h || (job.has_shared && !job.hs)) : (!job.ye || (job.has_shared && !job.ys)))
+    // the activation arrays' byte offsets are 32-bit: x (N rows, two digit
+    // rows per token for the shared expert) and h (N k and 2 N rows)
+    const long N = job.n_tokens;
+    if (phase == 0 ? 2L * N * job.H >= (1L << 31)
+                   : N * job.top_k * job.FF >= (1L << 31) || 2L * N * job.SF >= (1L << 31))
+        return hipErrorInvalidValue;
+    if (phase == 0 ? ((routed && !job.h) || (job.has_shared && !job.hs))
+                   : ((routed && !job.ye) || (job.has_shared && !job.ys)))
         return hipErrorInvalidValue;
     int n_cu = 0;
     const hipError_t e = device_cu_count(&n_cu);
