@@ -1340,7 +1340,7 @@ int proj_chunk(int path, int N) { return path == DP_Q6K ? std::min(N, PROJ_MAX_T
 // (128 digit rows) per unit, 256 output rows per item, the reduction split
 // into the fewest slices (2 or more super-blocks each) that give every CU an
 // item.  Returns the slice count, 0 where the GEMM does not take the shape.
-constexpr int PROJ_GEMM_MIN_TOKENS = 64;
+constexpr int PROJ_GEMM_MIN_TOKENS = 33;
 
 int proj_gemm_slices(const KernelSwitches &sw, int path, int rows, int K, int N)
 {

@@ -15,7 +15,8 @@
 // k_attn: flash attention with the block-causal mask of :19-55 (query i sees
 //   key j iff j / B <= i / B; every key when B <= 0), scale 1/sqrt(hd), GQA
 //   query head h on kv head h / (n_head / n_head_kv) (:158-167).  One
-//   workgroup per (64 queries, head), four wavefronts of 16 queries each;
+//   workgroup per (head, 64 queries), the last query blocks (the most keys)
+//   dispatched first, four wavefronts of 16 queries each;
 //   64-key tiles of K and V staged in LDS; S = Q K^T and O += P V on
 //   v_mfma_f32_16x16x4f32 (fp32 operands and accumulation), online softmax
 //   per query row in registers.  Keys past the last block a query tile can
@@ -102,6 +103,7 @@ hipError_t launch_qk_rope(const float *qkv, int ks, size_t kstride, const float 
 
 constexpr int AT_Q = 64;              // queries per workgroup (16 per wavefront)
 constexpr int AT_K = 64;              // keys per tile
+constexpr int AT_KB = AT_K / 16;      // 16-key blocks of a tile
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, const float *__restrict__ Kh,
@@ -120,14 +122,20 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     __shared__ float sP[4][16 * LDP];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int N = a.n, h = blockIdx.y, kvh = h / (a.nh / a.nkv);
-    const int q_wg = blockIdx.x * AT_Q;
+    // the grid's x is the head and y the query block, last block first: the
+    // dispatch order then starts the workgroups with the most key tiles
+    // (a block-causal tile row grows with its query block) and the short ones
+    // fill in behind them
+    const int N = a.n, h = blockIdx.x, kvh = h / (a.nh / a.nkv);
+    const int q_wg = (gridDim.y - 1 - blockIdx.y) * AT_Q;
     const float *Q = Qh + (size_t)h * N * HD, *K = Kh + (size_t)kvh * N * HD, *V = Vh + (size_t)kvh * N * HD;
-    // 16-byte pieces of a 64-row tile of HD floats: every thread's pieces are
-    // loaded before any is stored, so the loads overlap
-    constexpr int PPT = AT_K * HD / 4 / 256;          // pieces per thread (8 or 4)
-    static_assert(PPT * 256 * 4 == AT_K * HD, "whole pieces per thread");
-    auto stage_tile = [&](const float *src, int row0, float *dst, int ld) {
+    // 16-byte pieces of a tile of ROWS rows of HD floats (the queries' 64,
+    // a key tile's AT_K): every thread's pieces are loaded before any is
+    // stored, so the loads overlap
+    auto stage_tile = [&](auto rows_c, const float *src, int row0, float *dst, int ld) {
+        constexpr int ROWS = decltype(rows_c)::value;
+        constexpr int PPT = ROWS * HD / 4 / 256;          // pieces per thread
+        static_assert(PPT * 256 * 4 == ROWS * HD, "whole pieces per thread");
         float4 v[PPT];
 #pragma unroll
         for (int j = 0; j < PPT; j++) {
@@ -142,7 +150,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         }
     };
     // queries of the workgroup (rows past N: zero)
-    stage_tile(Q, q_wg, sQ, LD);
+    stage_tile(std::integral_constant<int, AT_Q>{}, Q, q_wg, sQ, LD);
     // keys the workgroup's last query can see
     const int q_last = min(N, q_wg + AT_Q) - 1;
     const int k_end = a.block > 0 ? min(N, (q_last / a.block + 1) * a.block) : N;
@@ -159,19 +167,19 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     for (int b = 0; b < HD / 16; b++) o[b] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = 0; k0 < k_end; k0 += AT_K) {
         __syncthreads();
-        stage_tile(K, k0, sK, LD);
-        stage_tile(V, k0, sV, LDV);
+        stage_tile(std::integral_constant<int, AT_K>{}, K, k0, sK, LD);
+        stage_tile(std::integral_constant<int, AT_K>{}, V, k0, sV, LDV);
         __syncthreads();
         // a wavefront whose queries are all past N, and key blocks / steps
         // wholly past the last visible key, have nothing to add (their
         // probabilities are 0): skipped
         if (q0 >= N) continue;
-        const int nkb = min(4, (k_end - k0 + 15) / 16);
+        const int nkb = min(AT_KB, (k_end - k0 + 15) / 16);
         const int nps = min(AT_K / 4, (k_end - k0 + 3) / 4);
-        // S[16 q][64 k]: lane holds rows 4g + i of key block kb, key kb*16 + r16
-        f4v sacc[4];
+        // S[16 q][AT_K k]: lane holds rows 4g + i of key block kb, key kb*16 + r16
+        f4v sacc[AT_KB];
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++) sacc[kb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kb = 0; kb < AT_KB; kb++) sacc[kb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
         const float *qrow = sQ + (16 * w + r16) * LD;
         auto qk = [&](auto nkb_c) {
             constexpr int NKB = decltype(nkb_c)::value;
@@ -185,6 +193,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
                 }
             }
         };
+        static_assert(AT_KB == 4, "a tile of four 16-key blocks");
         switch (nkb) {
         case 1: qk(std::integral_constant<int, 1>{}); break;
         case 2: qk(std::integral_constant<int, 2>{}); break;
@@ -198,7 +207,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
             const int q = q0 + 4 * g + i;
             float mx = -__builtin_inff();
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
+            for (int kb = 0; kb < AT_KB; kb++) {
                 const int k = k0 + kb * 16 + r16;
                 const bool ok = k < N && (a.block <= 0 || k / a.block <= q / a.block);
                 const float v = ok ? sacc[kb][i] * scale : -__builtin_inff();
@@ -217,7 +226,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
             corr[i] = mn == -__builtin_inff() ? 1.0f : expf(m[i] - mn);
             float rs = 0.0f;
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
+            for (int kb = 0; kb < AT_KB; kb++) {
                 const float p = mn == -__builtin_inff() ? 0.0f : expf(sacc[kb][i] - mn);
                 sacc[kb][i] = p;
                 rs += p;
@@ -234,12 +243,12 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         // P to LDS in the layout of the next product's A operand
         float *pw = sP[w];
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++)
+        for (int kb = 0; kb < AT_KB; kb++)
 #pragma unroll
             for (int i = 0; i < 4; i++) pw[(4 * g + i) * LDP + kb * 16 + r16] = sacc[kb][i];
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // O[16 q][HD] += P[16 q][64 k] V[64 k][HD]
+        // O[16 q][HD] += P[16 q][AT_K k] V[AT_K k][HD]
         auto pv = [&](int ns) {
 #pragma unroll 4
             for (int s = 0; s < ns; s++) {
@@ -273,7 +282,7 @@ hipError_t launch_attn(const float *Qh, const float *Kh, const float *Vh, const 
                        hipStream_t s)
 {
     if (a.nkv <= 0 || a.nh % a.nkv) return hipErrorInvalidValue;
-    const dim3 grid((a.n + AT_Q - 1) / AT_Q, a.nh);
+    const dim3 grid(a.nh, (a.n + AT_Q - 1) / AT_Q);
     switch (a.hd) {
     case 64: hipLaunchKernelGGL(k_attn<64>, grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
     case 128: hipLaunchKernelGGL(k_attn<128>, grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
