@@ -1136,7 +1136,9 @@ size_t proj_partial_max(int R, int K, int M, int nmax, bool split_only)
     return best;
 }
 
-size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, DenseWs *w)
+int dense_gemm_slices(const KernelSwitches &sw, int path, int H, int FF, int N);
+
+size_t plan_dense(const KernelSwitches &sw, const dmoe_layer *L, int N, bool host_io, uint8_t *base, DenseWs *w)
 {
     const int H = L->hp.n_embd, FF = L->hp.shared_ff;
     size_t off = 0;
@@ -1162,6 +1164,10 @@ size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, Dense
         if (dense_few(path, H, FF, n)) {
             t.part_gu = (float *)take(proj_partial_max(FF, H, 2, n, false) * 4);
             if (const size_t pd = proj_partial_max(H, FF, 1, n, true)) t.part_d = (float *)take(pd * 4);
+        } else if (const int ks = dense_gemm_slices(sw, path, H, FF, N)) {
+            // the grouped GEMM: f32 h, the down launch's slices
+            t.hs = (float *)take((size_t)N * FF * 4);
+            if (ks > 1) t.part_d = (float *)take((size_t)ks * N * H * 4);
         }
         break;
     }
@@ -1183,7 +1189,7 @@ size_t plan_dense(const dmoe_layer *L, int N, bool host_io, uint8_t *base, Dense
 
 int ensure_dense_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_io, DenseWs *w)
 {
-    const size_t need = plan_dense(L, N, host_io, nullptr, nullptr);
+    const size_t need = plan_dense(ctx->sw, L, N, host_io, nullptr, nullptr);
     if (need > ctx->ws_bytes) {
         if (ctx->ws) {
             HIP_TRY(ctx, hipDeviceSynchronize());
@@ -1196,7 +1202,7 @@ int ensure_dense_workspace(dmoe_ctx *ctx, const dmoe_layer *L, int N, bool host_
         HIP_TRY(ctx, hipMalloc(&ctx->ws, need));
         ctx->ws_bytes = need;
     }
-    plan_dense(L, N, host_io, (uint8_t *)ctx->ws, w);
+    plan_dense(ctx->sw, L, N, host_io, (uint8_t *)ctx->ws, w);
     return DMOE_OK;
 }
 
@@ -1253,6 +1259,36 @@ int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const fl
     LAUNCH_TRY(ctx, launch_fill_i32(w.n_ec, 0, 1, s));
     WorkList wl{};
     wl.n_ec = w.n_ec;
+    if (const int ks = dense_gemm_slices(ctx->sw, path, H, FF, N)) {
+        // many tokens of Q4_K: the grouped GEMM's gate/up and down launches
+        // over shared units, h converted between them, the down reduction in
+        // slices added in order
+        wl.chunk = EXPERT_GEMM_CHUNK;
+        MoeJob job{};
+        job.sg = L->sg;
+        job.su = L->su;
+        job.sd = L->sd;
+        job.has_shared = 1;
+        job.H = H;
+        job.FF = FF;
+        job.SF = FF;
+        job.n_tokens = N;
+        job.top_k = 1;
+        job.wl = wl;
+        job.axs = w.axs;
+        job.hs = w.hs;
+        job.ahs = w.ahs;
+        job.ys = ks > 1 ? w.part_d : y;
+        job.ks = ks;
+        PrepJob pj{x, N, H, ACT_SPLIT, w.axs};
+        STAGE(ST_ACTQ_X, launch_prep(&pj, 1, s));
+        STAGE(ST_SH_GATEUP, launch_expert_gemm_q4k(0, job, s));
+        PrepJob hj{w.hs, N, FF, ACT_SPLIT, w.ahs};
+        STAGE(ST_ACTQ_H, launch_prep(&hj, 1, s));
+        STAGE(ST_SH_DOWN, launch_expert_gemm_q4k(1, job, s));
+        if (ks > 1) STAGE(ST_COMBINE, launch_proj_reduce(w.part_d, ks, N, H, y, H, s));
+        return DMOE_OK;
+    }
     if (path == DP_F16) {
         wl.chunk = GM;
         GemmJob job{};
@@ -1355,6 +1391,14 @@ int proj_gemm_slices(const KernelSwitches &sw, int path, int rows, int K, int N)
     for (int ks = 2; ks <= 16 && items * best < n_cu; ks *= 2)
         if (nsb % ks == 0 && nsb / ks >= 2) best = ks;
     return best;
+}
+
+// The dense MLP past the few-token kernels on the same GEMM (gate/up, then
+// down in proj_gemm_slices slices): 0 where it does not take the shape.
+int dense_gemm_slices(const KernelSwitches &sw, int path, int H, int FF, int N)
+{
+    if (2L * N * H >= (1L << 31)) return 0;
+    return proj_gemm_slices(sw, path, H, FF, N);
 }
 
 template <class Take>
@@ -2288,7 +2332,7 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
                        L->device, ctx->device);
     if (!ctx->scratch)
         return set_err(ctx, DMOE_ERR_HIP, "scratch address of device %d not resolved", ctx->device);
-    const size_t need = L->dense ? plan_dense(L, n_tokens, false, nullptr, nullptr)
+    const size_t need = L->dense ? plan_dense(ctx->sw, L, n_tokens, false, nullptr, nullptr)
                                  : plan_workspace(ctx->sw, L->hp, L->eg.type, L->sg.type, L->has_shared, n_tokens,
                                                   false, nullptr, nullptr);
     if (need > DMOE_NOALLOC_SCRATCH_BYTES)
@@ -2301,7 +2345,7 @@ int dmoe_layer_forward_device_noalloc(dmoe_ctx *ctx, const dmoe_layer *L, const 
     // what a previous call left in the scratch needs no clearing.
     if (L->dense) {
         DenseWs dw;
-        plan_dense(L, n_tokens, false, ctx->scratch, &dw);
+        plan_dense(ctx->sw, L, n_tokens, false, ctx->scratch, &dw);
         return enqueue_dense(ctx, L, dw, x_dev, n_tokens, y_dev, (hipStream_t)stream, false);
     }
     Workspace w;

@@ -371,12 +371,12 @@ hipError_t launch_expert_gemm_q4k(int phase, const MoeJob &job, hipStream_t s)
         return hipErrorInvalidValue;
     if (!expert_gemm_q4k_ok(job.H, job.FF, job.SF, job.has_shared) || job.wl.chunk != XG_CHUNK || !job.wl.n_ec)
         return hipErrorInvalidValue;
-    if (phase == 0 ? (job.ax.K != job.H || (job.has_shared && job.axs.K != job.H))
+    if (phase == 0 ? ((routed && job.ax.K != job.H) || (job.has_shared && job.axs.K != job.H))
                    : ((routed && job.ah.K != job.FF) || (job.has_shared && job.ahs.K != job.SF)))
         return hipErrorInvalidValue;
-    // slices: down launches of shared units only, each slice two or more
-    // super-blocks
-    if (job.ks > 1 && (phase == 0 || routed || (job.FF / 256) % job.ks || job.FF / 256 / job.ks < 2))
+    // slices (read by the down launch only): shared units only, each slice
+    // two or more super-blocks
+    if (phase == 1 && job.ks > 1 && (routed || (job.FF / 256) % job.ks || job.FF / 256 / job.ks < 2))
         return hipErrorInvalidValue;
     // the activation arrays' byte offsets are 32-bit: x (N rows, two digit
     // rows per token for the shared expert) and h (N k and 2 N rows)
