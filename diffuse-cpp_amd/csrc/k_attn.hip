@@ -165,6 +165,15 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     }
 #pragma unroll
     for (int b = 0; b < HD / 16; b++) o[b] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    // the mask of query row i as a key limit: k / B <= q / B exactly when
+    // k < (q / B + 1) B, so a key is visible iff k < kvis[i] (no division per
+    // score)
+    int kvis[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = q0 + 4 * g + i;
+        kvis[i] = a.block > 0 ? min(N, (q / a.block + 1) * a.block) : N;
+    }
     for (int k0 = 0; k0 < k_end; k0 += AT_K) {
         __syncthreads();
         stage_tile(std::integral_constant<int, AT_K>{}, K, k0, sK, LD);
@@ -204,12 +213,11 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         float mt[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int q = q0 + 4 * g + i;
             float mx = -__builtin_inff();
 #pragma unroll
             for (int kb = 0; kb < AT_KB; kb++) {
                 const int k = k0 + kb * 16 + r16;
-                const bool ok = k < N && (a.block <= 0 || k / a.block <= q / a.block);
+                const bool ok = k < kvis[i];
                 const float v = ok ? sacc[kb][i] * scale : -__builtin_inff();
                 sacc[kb][i] = v;
                 mx = fmaxf(mx, v);
