@@ -154,7 +154,9 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     // keys the workgroup's last query can see
     const int q_last = min(N, q_wg + AT_Q) - 1;
     const int k_end = a.block > 0 ? min(N, (q_last / a.block + 1) * a.block) : N;
-    const float scale = a.scale;
+    // scores in the base-2 domain: s' = s scale log2(e), p = 2^(s' - m') (the
+    // hardware exp2; the same probabilities as exp(s scale - m) to ~1e-7)
+    const float scale = a.scale * 1.44269504088896341f;
     const int q0 = q_wg + 16 * w;                      // this wavefront's first query
     float m[4], l[4];
     f4v o[HD / 16];
@@ -231,11 +233,11 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         for (int i = 0; i < 4; i++) {
             const float mn = fmaxf(m[i], mt[i]);
             // a row with no visible key yet keeps m = -inf and contributes 0
-            corr[i] = mn == -__builtin_inff() ? 1.0f : expf(m[i] - mn);
+            corr[i] = mn == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mn);
             float rs = 0.0f;
 #pragma unroll
             for (int kb = 0; kb < AT_KB; kb++) {
-                const float p = mn == -__builtin_inff() ? 0.0f : expf(sacc[kb][i] - mn);
+                const float p = mn == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sacc[kb][i] - mn);
                 sacc[kb][i] = p;
                 rs += p;
             }
