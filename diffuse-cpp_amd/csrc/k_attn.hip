@@ -176,11 +176,37 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         const int q = q0 + 4 * g + i;
         kvis[i] = a.block > 0 ? min(N, (q / a.block + 1) * a.block) : N;
     }
+    // K and V tiles: the next tile's loads go to registers while the current
+    // one is in use, and to LDS once every wavefront is done with it
+    constexpr int KPT = AT_K * HD / 4 / 256;           // pieces per thread and tile
+    float4 kv[2][KPT];
+    auto load_kv = [&](int row0) {
+#pragma unroll
+        for (int j = 0; j < KPT; j++) {
+            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
+            const bool in = row0 + r < N;
+            const size_t off = (size_t)(row0 + r) * HD + 4 * c;
+            kv[0][j] = in ? *reinterpret_cast<const float4 *>(K + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            kv[1][j] = in ? *reinterpret_cast<const float4 *>(V + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto store_kv = [&]() {
+#pragma unroll
+        for (int j = 0; j < KPT; j++) {
+            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
+            *reinterpret_cast<float4 *>(sK + r * LD + 4 * c) = kv[0][j];
+            *reinterpret_cast<float4 *>(sV + r * LDV + 4 * c) = kv[1][j];
+        }
+    };
+    if (k_end > 0) load_kv(0);
     for (int k0 = 0; k0 < k_end; k0 += AT_K) {
+        // every wavefront is done with the previous tile; this one (loaded
+        // during the previous tile's products) to LDS; then the next one's
+        // loads, in flight during this tile's products
         __syncthreads();
-        stage_tile(std::integral_constant<int, AT_K>{}, K, k0, sK, LD);
-        stage_tile(std::integral_constant<int, AT_K>{}, V, k0, sV, LDV);
+        store_kv();
         __syncthreads();
+        if (k0 + AT_K < k_end) load_kv(k0 + AT_K);
         // a wavefront whose queries are all past N, and key blocks / steps
         // wholly past the last visible key, have nothing to add (their
         // probabilities are 0): skipped
