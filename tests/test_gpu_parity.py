@@ -271,7 +271,7 @@ def test_tile_path_bit_exact(ctx, name, monkeypatch):
 
 
 @pytest.mark.parametrize("name", ["flash_q4k_n2048", "flash_q4k_n1024", "flash_q4k_n256", "mid_q4k_n1000",
-                                  "mid_q4k_n200"])
+                                  "mid_q4k_n200", "mid_noshared_q4k_n1000"])
 def test_q4k_gemm_bit_exact(ctx, name, monkeypatch):
     """Q4_K products on the grouped GEMM (units of up to 128 pairs of an
     expert, eight column blocks per weight-tile step, weights and activations
@@ -280,12 +280,14 @@ def test_q4k_gemm_bit_exact(ctx, name, monkeypatch):
     outputs are identical bit for bit.  Each GEMM call follows one on other
     inputs of the same size; 256 and 200 tokens force the GEMM onto units of
     one or two blocks, and the mid-sized layers (1000 and 200 tokens, no block
-    routing) end their shared expert on a partial unit."""
+    routing) end their shared expert on a partial unit; one has no shared
+    expert at all."""
     import dmoe
     from dmoe import synth
     if name.startswith("mid"):
         n = int(name.rsplit("_n", 1)[1])
-        cfg = synth.LayerConfig(name, 512, 32, 512, 8, 4, 32, 512, 12, 12, n, -0.05, 0.05)
+        sf = 0 if "noshared" in name else 512
+        cfg = synth.LayerConfig(name, 512, 32, 512, 8, 4, 32, sf, 12, 12, n, -0.05, 0.05)
     else:
         cfg = synth.CONFIGS[name]
     _say(f"case: grouped Q4_K GEMM vs tile kernels, {name}")
