@@ -1255,14 +1255,11 @@ int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const fl
         }
         return DMOE_OK;
     }
-    // the expert kernels read an empty routed work list
-    LAUNCH_TRY(ctx, launch_fill_i32(w.n_ec, 0, 1, s));
-    WorkList wl{};
-    wl.n_ec = w.n_ec;
     if (const int ks = dense_gemm_slices(ctx->sw, path, H, FF, N)) {
         // many tokens of Q4_K: the grouped GEMM's gate/up and down launches
-        // over shared units, h converted between them, the down reduction in
-        // slices added in order
+        // over shared units (no routed work list), h converted between them,
+        // the down reduction in slices added in order
+        WorkList wl{};
         wl.chunk = EXPERT_GEMM_CHUNK;
         MoeJob job{};
         job.sg = L->sg;
@@ -1289,6 +1286,10 @@ int enqueue_dense(dmoe_ctx *ctx, const dmoe_layer *L, const DenseWs &w, const fl
         if (ks > 1) STAGE(ST_COMBINE, launch_proj_reduce(w.part_d, ks, N, H, y, H, s));
         return DMOE_OK;
     }
+    // the expert kernels read an empty routed work list
+    LAUNCH_TRY(ctx, launch_fill_i32(w.n_ec, 0, 1, s));
+    WorkList wl{};
+    wl.n_ec = w.n_ec;
     if (path == DP_F16) {
         wl.chunk = GM;
         GemmJob job{};
@@ -1462,6 +1463,54 @@ int enqueue_proj_few(dmoe_ctx *ctx, bool prof, int st_prod, const WTensor &W, in
     return DMOE_OK;
 }
 
+// y [N][rows] = W x from p.act on the grouped GEMM's down launch over
+// shared units (no routed work list), in ks reduction slices; with ks_out the
+// slices are left to the consumer as in enqueue_proj_few, else added into y.
+int enqueue_proj_gemm(dmoe_ctx *ctx, bool prof, int st_prod, const WTensor &W, int rows, int K, int N, int ks,
+                      const ProjWs &p, float *y, int *ks_out, const float **src_out, hipStream_t s)
+{
+#define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
+    MoeJob job{};
+    job.sd = W;
+    job.has_shared = 1;
+    job.H = rows;
+    job.FF = K;
+    job.SF = K;
+    job.n_tokens = N;
+    job.top_k = 1;
+    job.wl.chunk = EXPERT_GEMM_CHUNK;
+    job.ahs = p.act;
+    job.ys = ks > 1 ? p.part : y;
+    job.ks = ks;
+    STAGE(st_prod, launch_expert_gemm_q4k(1, job, s));
+    if (ks_out) {
+        *ks_out = ks;
+        *src_out = job.ys;
+    } else if (ks > 1) {
+        STAGE(ST_COMBINE, launch_proj_reduce(p.part, ks, N, rows, y, rows, s));
+    }
+#undef STAGE
+    return DMOE_OK;
+}
+
+// Projections that take p.act's digits from the caller (k_norm_fused writes
+// them beside its RMSNorm): the few-token kernel or, for many tokens of Q4_K,
+// the GEMM (*gemm_ks its slice count, else 0).
+bool proj_takes_digits(const KernelSwitches &sw, int path, int rows, int K, int N, int *gemm_ks)
+{
+    *gemm_ks = 0;
+    if (proj_few(path, rows, K, N)) return true;
+    *gemm_ks = proj_gemm_slices(sw, path, rows, K, N);
+    return *gemm_ks > 0;
+}
+
+int enqueue_proj_digits(dmoe_ctx *ctx, bool prof, int st_prod, const WTensor &W, int rows, int K, int N, int gemm_ks,
+                        const ProjWs &p, float *y, int *ks_out, const float **src_out, hipStream_t s)
+{
+    return gemm_ks ? enqueue_proj_gemm(ctx, prof, st_prod, W, rows, K, N, gemm_ks, p, y, ks_out, src_out, s)
+                   : enqueue_proj_few(ctx, prof, st_prod, W, rows, K, N, p, y, ks_out, src_out, s);
+}
+
 int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTensor &W, int rows, int K,
                  const float *x, int N, float *y, const ProjWs &p, hipStream_t s)
 {
@@ -1483,31 +1532,16 @@ int enqueue_proj(dmoe_ctx *ctx, bool prof, int st_conv, int st_prod, const WTens
         }
         return DMOE_OK;
     }
-    LAUNCH_TRY(ctx, launch_fill_i32(p.n_ec, 0, 1, s));
-    WorkList wl{};
-    wl.n_ec = p.n_ec;
     if (const int ks = proj_gemm_slices(ctx->sw, path, rows, K, N)) {
         // many tokens of Q4_K: the grouped GEMM's down launch over shared
         // units, its reduction slices added in order
-        wl.chunk = EXPERT_GEMM_CHUNK;
-        MoeJob job{};
-        job.sd = W;
-        job.has_shared = 1;
-        job.H = rows;
-        job.FF = K;
-        job.SF = K;
-        job.n_tokens = N;
-        job.top_k = 1;
-        job.wl = wl;
-        job.ahs = p.act;
-        job.ys = ks > 1 ? p.part : y;
-        job.ks = ks;
         PrepJob pj{x, N, K, ACT_SPLIT, p.act};
         STAGE(st_conv, launch_prep(&pj, 1, s));
-        STAGE(st_prod, launch_expert_gemm_q4k(1, job, s));
-        if (ks > 1) STAGE(ST_COMBINE, launch_proj_reduce(p.part, ks, N, rows, y, rows, s));
-        return DMOE_OK;
+        return enqueue_proj_gemm(ctx, prof, st_prod, W, rows, K, N, ks, p, y, nullptr, nullptr, s);
     }
+    LAUNCH_TRY(ctx, launch_fill_i32(p.n_ec, 0, 1, s));
+    WorkList wl{};
+    wl.n_ec = p.n_ec;
     if (path == DP_F16) {
         wl.chunk = GM;
         GemmJob job{};
@@ -1652,10 +1686,10 @@ int enqueue_head(dmoe_ctx *ctx, const dmoe_layer *L, const HeadWs &w, const floa
     const bool prof = ctx->prof;
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
     // :296-297 rms_norm(cur) * output_norm (h is only read: no residual add);
-    // :299 the LM head.  Few tokens of Q4_K: the norm hands the head its
-    // int8 digits directly.
-    int rc;
-    if (proj_few(head_path(L->sd.type, V, H), V, H, N) && H <= 8192) {
+    // :299 the LM head.  On the few-token kernel or the GEMM the norm hands
+    // the head its int8 digits directly.
+    int rc, gh = 0;
+    if (proj_takes_digits(ctx->sw, head_path(L->sd.type, V, H), V, H, N, &gh) && H <= 8192) {
         NormArgs na{};
         na.h_in = h;
         na.gain = L->gate_w;
@@ -1664,7 +1698,7 @@ int enqueue_head(dmoe_ctx *ctx, const dmoe_layer *L, const HeadWs &w, const floa
         na.H = H;
         na.eps = eps;
         STAGE(ST_FRONT, launch_norm_fused(na, s));
-        rc = enqueue_proj_few(ctx, prof, ST_SH_DOWN, L->sd, V, H, N, w.proj, logits, nullptr, nullptr, s);
+        rc = enqueue_proj_digits(ctx, prof, ST_SH_DOWN, L->sd, V, H, N, gh, w.proj, logits, nullptr, nullptr, s);
     } else {
         STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->gate_w, w.xn, N, H, eps, s));
         rc = enqueue_proj(ctx, prof, ST_ACTQ_H, ST_SH_DOWN, L->sd, V, H, w.xn, N, logits, w.proj, s);
@@ -1724,10 +1758,12 @@ int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const floa
     const dmoe_attn_hparams &a = L->ahp;
     const int H = a.n_embd, QD = a.n_head * a.head_dim, KD = a.n_head_kv * a.head_dim, QKV = QD + 2 * KD;
     const bool prof = ctx->prof;
-    // few tokens of Q4_K projections: the norms hand them int8 digits and take
-    // their reduction slices directly (k_norm_fused, k_qk_rope)
-    const bool fq = proj_few(head_path(L->aqkv.type, QKV, H), QKV, H, N) && H <= 8192;
-    const bool fo = proj_few(head_path(L->awo.type, H, QD), H, QD, N) && H <= 8192;
+    // Q4_K / Q6_K projections on the few-token kernel or the GEMM: the norms
+    // hand them int8 digits and take their reduction slices directly
+    // (k_norm_fused, k_qk_rope)
+    int gq = 0, go = 0;
+    const bool fq = proj_takes_digits(ctx->sw, head_path(L->aqkv.type, QKV, H), QKV, H, N, &gq) && H <= 8192;
+    const bool fo = proj_takes_digits(ctx->sw, head_path(L->awo.type, H, QD), H, QD, N, &go) && H <= 8192;
 #define STAGE(id, call) LAUNCH_TRY(ctx, stage(ctx, prof, id, s, [&] { return call; }))
     // :120-121 input layernorm; :124 fused QKV
     const float *qkv = w.qkv;
@@ -1742,7 +1778,7 @@ int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const floa
         na.H = H;
         na.eps = a.rms_eps;
         STAGE(ST_FRONT, launch_norm_fused(na, s));
-        if ((rc = enqueue_proj_few(ctx, prof, ST_SH_GATEUP, L->aqkv, QKV, H, N, w.pq, w.qkv, &qks, &qkv, s)))
+        if ((rc = enqueue_proj_digits(ctx, prof, ST_SH_GATEUP, L->aqkv, QKV, H, N, gq, w.pq, w.qkv, &qks, &qkv, s)))
             return rc;
     } else {
         STAGE(ST_FRONT, launch_residual_rmsnorm(const_cast<float *>(h), nullptr, L->attn_norm, w.xn, N, H,
@@ -1771,7 +1807,7 @@ int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const floa
         STAGE(ST_ACTQ_H, launch_prep(&pj, 1, s));
         const float *o = w.proj;
         int oks = 1;
-        if ((rc = enqueue_proj_few(ctx, prof, ST_SH_DOWN, L->awo, H, QD, N, w.po, w.proj, &oks, &o, s)))
+        if ((rc = enqueue_proj_digits(ctx, prof, ST_SH_DOWN, L->awo, H, QD, N, go, w.po, w.proj, &oks, &o, s)))
             return rc;
         NormArgs na{};
         na.h_in = h;

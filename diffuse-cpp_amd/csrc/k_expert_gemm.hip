@@ -156,7 +156,7 @@ __global__ __launch_bounds__(XG_WAVES * 64) void k_gemm_q4k(MoeJob job)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r16 = lane & 15;
     const int H = job.H, FF = job.FF, N = job.n_tokens, K = job.top_k;
-    const int n_ec = ldc(job.wl.n_ec, 0);
+    const int n_ec = job.wl.n_ec ? ldc(job.wl.n_ec, 0) : 0;   // none: shared units only
     const int nch = job.has_shared ? (N + XG_SCHUNK - 1) / XG_SCHUNK : 0;
     const int rg_n = DOWN ? H / XG_DN_ROWS : FF / XG_GU_ROWS;
     const int Kin = DOWN ? FF : H;
@@ -362,14 +362,16 @@ bool expert_gemm_q4k_ok(int H, int FF, int SF, bool shared)
 hipError_t launch_expert_gemm_q4k(int phase, const MoeJob &job, hipStream_t s)
 {
     // routed experts (eg / eu / ed), the shared one (sg / su / sd) or both;
-    // a projection is a down launch of shared units only (no routed weights,
-    // the work list empty), optionally in ks reduction slices
+    // a projection is a down launch of shared units only (no routed weights;
+    // the work list's count may be null there), optionally in ks reduction
+    // slices
     const bool routed = job.eg.data || job.ed.data;
     const WTensor &wr = phase == 0 ? job.eg : job.ed, &ws = phase == 0 ? job.sg : job.sd;
     if ((routed && wr.type != DMOE_TYPE_Q4_K) || (job.has_shared && ws.type != DMOE_TYPE_Q4_K) ||
         (!routed && !job.has_shared))
         return hipErrorInvalidValue;
-    if (!expert_gemm_q4k_ok(job.H, job.FF, job.SF, job.has_shared) || job.wl.chunk != XG_CHUNK || !job.wl.n_ec)
+    if (!expert_gemm_q4k_ok(job.H, job.FF, job.SF, job.has_shared) || job.wl.chunk != XG_CHUNK ||
+        (routed && !job.wl.n_ec))
         return hipErrorInvalidValue;
     if (phase == 0 ? ((routed && job.ax.K != job.H) || (job.has_shared && job.axs.K != job.H))
                    : ((routed && job.ah.K != job.FF) || (job.has_shared && job.ahs.K != job.SF)))
