@@ -18,9 +18,11 @@
 //   workgroup per (head, 64 queries), the last query blocks (the most keys)
 //   dispatched first, four wavefronts of 16 queries each;
 //   64-key tiles of K and V staged in LDS; S = Q K^T and O += P V on
-//   v_mfma_f32_16x16x4f32 (fp32 operands and accumulation), online softmax
-//   per query row in registers.  Keys past the last block a query tile can
-//   see are not visited.
+//   v_mfma_f32_16x16x32_f16 with every f32 operand split into f16 hi + lo
+//   halves (hi lo' + lo hi' + hi hi', f32 accumulation: ~2^-22 relative per
+//   product, the fp32 result to within its own rounding; |values| below
+//   65504, the f16 range), online softmax per query row in registers.  Keys
+//   past the last block a query tile can see are not visited.
 #include <type_traits>
 
 #include "dmoe_internal.h"
@@ -104,22 +106,31 @@ hipError_t launch_qk_rope(const float *qkv, int ks, size_t kstride, const float 
 constexpr int AT_Q = 64;              // queries per workgroup (16 per wavefront)
 constexpr int AT_K = 64;              // keys per tile
 constexpr int AT_KB = AT_K / 16;      // 16-key blocks of a tile
+constexpr int AT_LVT = AT_K + 8;      // f16 row stride of the transposed V tile and of P
+
+typedef _Float16 at_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 at_h4 __attribute__((ext_vector_type(4)));
+
+// x = hi + lo with hi = f16(x) and lo = f16(x - hi) (x - hi is exact in f32):
+// 22 significant bits, and hi lo' + hi' lo + hi hi' is x x' to ~2^-22
+// relative (the products are exact in f32)
+__device__ __forceinline__ void at_split(float x, _Float16 &hi, _Float16 &lo)
+{
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, const float *__restrict__ Kh,
                                               const float *__restrict__ Vh, AttnDims a, float *__restrict__ out)
 {
-    // padded LDS rows, so that the 64 lanes of an operand read hit 64
-    // different banks: Q and K are read at row r16, column 4 s + g (a row
-    // stride of 4 mod 64 words spreads them), V at row 4 s + g, column
-    // 16 b + r16 (16 mod 64), P like Q
-    constexpr int LD = HD + 4;
-    constexpr int LDV = HD + 16;
-    constexpr int LDP = AT_K + 4;
-    __shared__ __align__(16) float sQ[AT_Q * LD];
-    __shared__ __align__(16) float sK[AT_K * LD];
-    __shared__ __align__(16) float sV[AT_K * LDV];
-    __shared__ float sP[4][16 * LDP];
+    // f16 hi / lo planes in LDS, rows padded so that the 16-byte operand
+    // reads of a wavefront's 16 rows hit different banks: K [key][d] (row
+    // stride HD + 8), V transposed [d][key] and P [query][key] (AT_K + 8)
+    constexpr int LK = HD + 8;
+    __shared__ __align__(16) _Float16 sK[2][AT_K * LK];
+    __shared__ __align__(16) _Float16 sV[2][HD * AT_LVT];
+    __shared__ __align__(16) _Float16 sP[4][2][16 * AT_LVT];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     // the grid's x is the head and y the query block, last block first: the
@@ -129,28 +140,6 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     const int N = a.n, h = blockIdx.x, kvh = h / (a.nh / a.nkv);
     const int q_wg = (gridDim.y - 1 - blockIdx.y) * AT_Q;
     const float *Q = Qh + (size_t)h * N * HD, *K = Kh + (size_t)kvh * N * HD, *V = Vh + (size_t)kvh * N * HD;
-    // 16-byte pieces of a tile of ROWS rows of HD floats (the queries' 64,
-    // a key tile's AT_K): every thread's pieces are loaded before any is
-    // stored, so the loads overlap
-    auto stage_tile = [&](auto rows_c, const float *src, int row0, float *dst, int ld) {
-        constexpr int ROWS = decltype(rows_c)::value;
-        constexpr int PPT = ROWS * HD / 4 / 256;          // pieces per thread
-        static_assert(PPT * 256 * 4 == ROWS * HD, "whole pieces per thread");
-        float4 v[PPT];
-#pragma unroll
-        for (int j = 0; j < PPT; j++) {
-            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
-            v[j] = row0 + r < N ? *reinterpret_cast<const float4 *>(src + (size_t)(row0 + r) * HD + 4 * c)
-                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-#pragma unroll
-        for (int j = 0; j < PPT; j++) {
-            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
-            *reinterpret_cast<float4 *>(dst + r * ld + 4 * c) = v[j];
-        }
-    };
-    // queries of the workgroup (rows past N: zero)
-    stage_tile(std::integral_constant<int, AT_Q>{}, Q, q_wg, sQ, LD);
     // keys the workgroup's last query can see
     const int q_last = min(N, q_wg + AT_Q) - 1;
     const int k_end = a.block > 0 ? min(N, (q_last / a.block + 1) * a.block) : N;
@@ -158,6 +147,26 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     // hardware exp2; the same probabilities as exp(s scale - m) to ~1e-7)
     const float scale = a.scale * 1.44269504088896341f;
     const int q0 = q_wg + 16 * w;                      // this wavefront's first query
+    // this wavefront's Q operands in registers: row q0 + r16 (zero past N),
+    // dims 32 c + 8 g .. + 7 of chunk c, as hi / lo halves
+    at_h8 qa[HD / 32][2];
+    {
+        const bool in = q0 + r16 < N;
+        const float *qr = Q + (size_t)(q0 + r16) * HD + 8 * g;
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++) {
+            const float4 x0 = in ? *reinterpret_cast<const float4 *>(qr + 32 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 x1 = in ? *reinterpret_cast<const float4 *>(qr + 32 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                _Float16 hi, lo;
+                at_split(xs[e], hi, lo);
+                qa[c][0][e] = hi;
+                qa[c][1][e] = lo;
+            }
+        }
+    }
     float m[4], l[4];
     f4v o[HD / 16];
 #pragma unroll
@@ -177,25 +186,62 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         kvis[i] = a.block > 0 ? min(N, (q / a.block + 1) * a.block) : N;
     }
     // K and V tiles: the next tile's loads go to registers while the current
-    // one is in use, and to LDS once every wavefront is done with it
+    // one is in use, and to LDS (split, V transposed) once every wavefront is
+    // done with it.  K piece j of a thread: row i / (HD / 4), dims 4 (i %
+    // (HD / 4)) .. + 3 (i = tid + 256 j); V piece pair j: rows 2 p and 2 p + 1
+    // (p = i % (AT_K / 2)), the same four dims 4 (i / (AT_K / 2)) .. + 3, so
+    // that the transposed stores write two keys per 32-bit word
     constexpr int KPT = AT_K * HD / 4 / 256;           // pieces per thread and tile
-    float4 kv[2][KPT];
+    static_assert(KPT % 2 == 0 && KPT * 256 * 4 == AT_K * HD, "whole piece pairs per thread");
+    float4 kr[KPT], vr[KPT];
     auto load_kv = [&](int row0) {
 #pragma unroll
         for (int j = 0; j < KPT; j++) {
             const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
-            const bool in = row0 + r < N;
-            const size_t off = (size_t)(row0 + r) * HD + 4 * c;
-            kv[0][j] = in ? *reinterpret_cast<const float4 *>(K + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            kv[1][j] = in ? *reinterpret_cast<const float4 *>(V + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            kr[j] = row0 + r < N ? *reinterpret_cast<const float4 *>(K + (size_t)(row0 + r) * HD + 4 * c)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int j = 0; j < KPT / 2; j++) {
+            const int i = tid + 256 * j, p = i % (AT_K / 2), c = i / (AT_K / 2);
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int r = 2 * p + u;
+                vr[2 * j + u] = row0 + r < N ? *reinterpret_cast<const float4 *>(V + (size_t)(row0 + r) * HD + 4 * c)
+                                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
         }
     };
     auto store_kv = [&]() {
 #pragma unroll
         for (int j = 0; j < KPT; j++) {
             const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
-            *reinterpret_cast<float4 *>(sK + r * LD + 4 * c) = kv[0][j];
-            *reinterpret_cast<float4 *>(sV + r * LDV + 4 * c) = kv[1][j];
+            const float x[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+            at_h4 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                _Float16 a0, a1;
+                at_split(x[e], a0, a1);
+                hi[e] = a0;
+                lo[e] = a1;
+            }
+            *reinterpret_cast<at_h4 *>(&sK[0][r * LK + 4 * c]) = hi;
+            *reinterpret_cast<at_h4 *>(&sK[1][r * LK + 4 * c]) = lo;
+        }
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int j = 0; j < KPT / 2; j++) {
+            const int i = tid + 256 * j, p = i % (AT_K / 2), c = i / (AT_K / 2);
+            const float x0[4] = {vr[2 * j].x, vr[2 * j].y, vr[2 * j].z, vr[2 * j].w};
+            const float x1[4] = {vr[2 * j + 1].x, vr[2 * j + 1].y, vr[2 * j + 1].z, vr[2 * j + 1].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                _Float16 h0, l0, h1, l1;
+                at_split(x0[e], h0, l0);
+                at_split(x1[e], h1, l1);
+                *reinterpret_cast<h2 *>(&sV[0][(4 * c + e) * AT_LVT + 2 * p]) = h2{h0, h1};
+                *reinterpret_cast<h2 *>(&sV[1][(4 * c + e) * AT_LVT + 2 * p]) = h2{l0, l1};
+            }
         }
     };
     if (k_end > 0) load_kv(0);
@@ -207,28 +253,29 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         store_kv();
         __syncthreads();
         if (k0 + AT_K < k_end) load_kv(k0 + AT_K);
-        // a wavefront whose queries are all past N, and key blocks / steps
+        // a wavefront whose queries are all past N, and key blocks / chunks
         // wholly past the last visible key, have nothing to add (their
         // probabilities are 0): skipped
         if (q0 >= N) continue;
         const int nkb = min(AT_KB, (k_end - k0 + 15) / 16);
-        const int nps = min(AT_K / 4, (k_end - k0 + 3) / 4);
+        const int npc = min(AT_K / 32, (k_end - k0 + 31) / 32);
         // S[16 q][AT_K k]: lane holds rows 4g + i of key block kb, key kb*16 + r16
         f4v sacc[AT_KB];
 #pragma unroll
         for (int kb = 0; kb < AT_KB; kb++) sacc[kb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-        const float *qrow = sQ + (16 * w + r16) * LD;
         auto qk = [&](auto nkb_c) {
             constexpr int NKB = decltype(nkb_c)::value;
-#pragma unroll 4
-            for (int s = 0; s < HD / 4; s++) {
-                const float av = qrow[4 * s + g];
+#pragma unroll
+            for (int c = 0; c < HD / 32; c++)
 #pragma unroll
                 for (int kb = 0; kb < NKB; kb++) {
-                    const float bv = sK[(kb * 16 + r16) * LD + 4 * s + g];
-                    sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, sacc[kb], 0, 0, 0);
+                    const int off = (kb * 16 + r16) * LK + 32 * c + 8 * g;
+                    const at_h8 kh = *reinterpret_cast<const at_h8 *>(&sK[0][off]);
+                    const at_h8 kl = *reinterpret_cast<const at_h8 *>(&sK[1][off]);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c][1], kh, sacc[kb], 0, 0, 0);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c][0], kl, sacc[kb], 0, 0, 0);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c][0], kh, sacc[kb], 0, 0, 0);
                 }
-            }
         };
         static_assert(AT_KB == 4, "a tile of four 16-key blocks");
         switch (nkb) {
@@ -276,29 +323,44 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         for (int b = 0; b < HD / 16; b++)
 #pragma unroll
             for (int i = 0; i < 4; i++) o[b][i] *= corr[i];
-        // P to LDS in the layout of the next product's A operand
-        float *pw = sP[w];
+        // P to LDS as hi / lo halves in the layout of the next product's A
+        // operand (row = query, 16-byte pieces of 8 keys)
+        _Float16 *ph = sP[w][0], *pl = sP[w][1];
 #pragma unroll
         for (int kb = 0; kb < AT_KB; kb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) pw[(4 * g + i) * LDP + kb * 16 + r16] = sacc[kb][i];
+            for (int i = 0; i < 4; i++) {
+                _Float16 hi, lo;
+                at_split(sacc[kb][i], hi, lo);
+                ph[(4 * g + i) * AT_LVT + kb * 16 + r16] = hi;
+                pl[(4 * g + i) * AT_LVT + kb * 16 + r16] = lo;
+            }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // O[16 q][HD] += P[16 q][AT_K k] V[AT_K k][HD]
-        auto pv = [&](int ns) {
-#pragma unroll 4
-            for (int s = 0; s < ns; s++) {
-                const float av = pw[r16 * LDP + 4 * s + g];
-                const float *vrow = sV + (4 * s + g) * LDV;
+        // O[16 q][HD] += P[16 q][AT_K k] V[AT_K k][HD], 32 keys per chunk
+        auto pv = [&](auto npc_c) {
+            constexpr int NPC = decltype(npc_c)::value;
 #pragma unroll
-                for (int b = 0; b < HD / 16; b++)
-                    o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, vrow[b * 16 + r16], o[b], 0, 0, 0);
+            for (int c = 0; c < NPC; c++) {
+                const int po = r16 * AT_LVT + 32 * c + 8 * g;
+                const at_h8 pah = *reinterpret_cast<const at_h8 *>(ph + po);
+                const at_h8 pal = *reinterpret_cast<const at_h8 *>(pl + po);
+#pragma unroll
+                for (int b = 0; b < HD / 16; b++) {
+                    const int vo = (b * 16 + r16) * AT_LVT + 32 * c + 8 * g;
+                    const at_h8 vh = *reinterpret_cast<const at_h8 *>(&sV[0][vo]);
+                    const at_h8 vl = *reinterpret_cast<const at_h8 *>(&sV[1][vo]);
+                    o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pal, vh, o[b], 0, 0, 0);
+                    o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, vl, o[b], 0, 0, 0);
+                    o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, vh, o[b], 0, 0, 0);
+                }
             }
         };
-        if (nps == AT_K / 4)
-            pv(AT_K / 4);
+        static_assert(AT_K == 64, "a tile of two 32-key chunks");
+        if (npc == 2)
+            pv(std::integral_constant<int, 2>{});
         else
-            pv(nps);
+            pv(std::integral_constant<int, 1>{});
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
