@@ -1798,6 +1798,7 @@ int enqueue_attn(dmoe_ctx *ctx, const dmoe_layer *L, const AttnWs &w, const floa
     // the rope cache's angle step, as ggml computes it on the host
     d.theta_scale = a.rotary_dim > 0 ? powf(a.rope_base, -2.0f / (float)a.rotary_dim) : 1.0f;
     d.scale = 1.0f / sqrtf((float)a.head_dim);
+    d.waves = ctx->sw.attn_waves;
     STAGE(ST_ROUTE, launch_qk_rope(qkv, qks, (size_t)N * QKV, L->qn, L->kn, d, w.Qh, w.Kh, w.Vh, s));
     STAGE(ST_SCORES, launch_attn(w.Qh, w.Kh, w.Vh, d, w.att, s));
     // :172 output projection; :175-178 residual, then the post-attention
@@ -1858,6 +1859,10 @@ KernelSwitches read_kernel_switches()
     if (const char *v = getenv("DMOE_PROJ_GEMM")) {
         const int n = atoi(v);
         if (n == 0 || n == 1) sw.proj_gemm = n;
+    }
+    if (const char *v = getenv("DMOE_ATTN_WAVES")) {
+        const int n = atoi(v);
+        if (n == 4 || n == 8) sw.attn_waves = n;
     }
     return sw;
 }

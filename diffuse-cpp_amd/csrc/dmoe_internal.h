@@ -135,6 +135,7 @@ struct KernelSwitches {
     int expert_tile = -1;                // -1: by tokens per expert
     int expert_gemm = -1;                // -1: by tokens per expert
     int proj_gemm = -1;                  // -1: by tokens
+    int attn_waves = 0;                  // 0: by grid size, else 4 or 8 per workgroup
     bool down_fused = false;
     bool gateup_lds = false;
 };
@@ -235,6 +236,7 @@ struct AttnDims {
     int32_t n, nh, nkv, hd, rd;          // tokens, heads, kv heads, head_dim, rotary_dim
     int32_t qk_norm, block;              // use_qk_norm, block_length (0: bidirectional)
     float eps, theta_scale, scale;       // rms eps, powf(base, -2/rd), 1/sqrt(hd)
+    int32_t waves;                       // attention wavefronts per workgroup: 4, 8, 0 by grid size
 };
 // fused QKV rows [N][(nh + 2 nkv) hd] (the sum of ks slices kstride floats
 // apart) -> QK RMSNorm, partial NEOX RoPE -> head-major Q [nh][N][hd], K, V

@@ -15,8 +15,8 @@
 // k_attn: flash attention with the block-causal mask of :19-55 (query i sees
 //   key j iff j / B <= i / B; every key when B <= 0), scale 1/sqrt(hd), GQA
 //   query head h on kv head h / (n_head / n_head_kv) (:158-167).  One
-//   workgroup per (head, 64 queries), the last query blocks (the most keys)
-//   dispatched first, four wavefronts of 16 queries each;
+//   workgroup per (head, 64 or 128 queries), the last query blocks (the most
+//   keys) dispatched first, four or eight wavefronts of 16 queries each;
 //   64-key tiles of K and V staged in LDS; S = Q K^T and O += P V on
 //   v_mfma_f32_16x16x32_f16 with every f32 operand split into f16 hi + lo
 //   halves (hi lo' + lo hi' + hi hi', f32 accumulation: ~2^-22 relative per
@@ -103,7 +103,6 @@ hipError_t launch_qk_rope(const float *qkv, int ks, size_t kstride, const float 
     return hipGetLastError();
 }
 
-constexpr int AT_Q = 64;              // queries per workgroup (16 per wavefront)
 constexpr int AT_K = 64;              // keys per tile
 constexpr int AT_KB = AT_K / 16;      // 16-key blocks of a tile
 constexpr int AT_LVT = AT_K + 8;      // f16 row stride of the transposed V tile and of P
@@ -120,17 +119,19 @@ __device__ __forceinline__ void at_split(float x, _Float16 &hi, _Float16 &lo)
     lo = (_Float16)(x - (float)hi);
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, const float *__restrict__ Kh,
+template <int HD, int QW>
+__global__ __launch_bounds__(QW * 64) void k_attn(const float *__restrict__ Qh, const float *__restrict__ Kh,
                                               const float *__restrict__ Vh, AttnDims a, float *__restrict__ out)
 {
+    constexpr int AT_Q = 16 * QW;     // queries per workgroup (16 per wavefront)
+    constexpr int AT_T = 64 * QW;     // threads per workgroup
     // f16 hi / lo planes in LDS, rows padded so that the 16-byte operand
     // reads of a wavefront's 16 rows hit different banks: K [key][d] (row
     // stride HD + 8), V transposed [d][key] and P [query][key] (AT_K + 8)
     constexpr int LK = HD + 8;
     __shared__ __align__(16) _Float16 sK[2][AT_K * LK];
     __shared__ __align__(16) _Float16 sV[2][HD * AT_LVT];
-    __shared__ __align__(16) _Float16 sP[4][2][16 * AT_LVT];
+    __shared__ __align__(16) _Float16 sP[AT_Q / 16][2][16 * AT_LVT];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     // the grid's x is the head and y the query block, last block first: the
@@ -185,25 +186,28 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         const int q = q0 + 4 * g + i;
         kvis[i] = a.block > 0 ? min(N, (q / a.block + 1) * a.block) : N;
     }
+    // keys the wavefront's last query can see
+    const int qw_last = min(N, q0 + 16) - 1;
+    const int kw_end = a.block > 0 ? min(N, (qw_last / a.block + 1) * a.block) : N;
     // K and V tiles: the next tile's loads go to registers while the current
     // one is in use, and to LDS (split, V transposed) once every wavefront is
     // done with it.  K piece j of a thread: row i / (HD / 4), dims 4 (i %
-    // (HD / 4)) .. + 3 (i = tid + 256 j); V piece pair j: rows 2 p and 2 p + 1
+    // (HD / 4)) .. + 3 (i = tid + AT_T j); V piece pair j: rows 2 p and 2 p + 1
     // (p = i % (AT_K / 2)), the same four dims 4 (i / (AT_K / 2)) .. + 3, so
     // that the transposed stores write two keys per 32-bit word
-    constexpr int KPT = AT_K * HD / 4 / 256;           // pieces per thread and tile
-    static_assert(KPT % 2 == 0 && KPT * 256 * 4 == AT_K * HD, "whole piece pairs per thread");
+    constexpr int KPT = AT_K * HD / 4 / AT_T;          // pieces per thread and tile
+    static_assert(KPT % 2 == 0 && KPT * AT_T * 4 == AT_K * HD, "whole piece pairs per thread");
     float4 kr[KPT], vr[KPT];
     auto load_kv = [&](int row0) {
 #pragma unroll
         for (int j = 0; j < KPT; j++) {
-            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
+            const int i = tid + AT_T * j, r = i / (HD / 4), c = i % (HD / 4);
             kr[j] = row0 + r < N ? *reinterpret_cast<const float4 *>(K + (size_t)(row0 + r) * HD + 4 * c)
                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
 #pragma unroll
         for (int j = 0; j < KPT / 2; j++) {
-            const int i = tid + 256 * j, p = i % (AT_K / 2), c = i / (AT_K / 2);
+            const int i = tid + AT_T * j, p = i % (AT_K / 2), c = i / (AT_K / 2);
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 const int r = 2 * p + u;
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
     auto store_kv = [&]() {
 #pragma unroll
         for (int j = 0; j < KPT; j++) {
-            const int i = tid + 256 * j, r = i / (HD / 4), c = i % (HD / 4);
+            const int i = tid + AT_T * j, r = i / (HD / 4), c = i % (HD / 4);
             const float x[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
             at_h4 hi, lo;
 #pragma unroll
@@ -231,7 +235,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #pragma unroll
         for (int j = 0; j < KPT / 2; j++) {
-            const int i = tid + 256 * j, p = i % (AT_K / 2), c = i / (AT_K / 2);
+            const int i = tid + AT_T * j, p = i % (AT_K / 2), c = i / (AT_K / 2);
             const float x0[4] = {vr[2 * j].x, vr[2 * j].y, vr[2 * j].z, vr[2 * j].w};
             const float x1[4] = {vr[2 * j + 1].x, vr[2 * j + 1].y, vr[2 * j + 1].z, vr[2 * j + 1].w};
 #pragma unroll
@@ -253,12 +257,12 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
         store_kv();
         __syncthreads();
         if (k0 + AT_K < k_end) load_kv(k0 + AT_K);
-        // a wavefront whose queries are all past N, and key blocks / chunks
-        // wholly past the last visible key, have nothing to add (their
-        // probabilities are 0): skipped
-        if (q0 >= N) continue;
-        const int nkb = min(AT_KB, (k_end - k0 + 15) / 16);
-        const int npc = min(AT_K / 32, (k_end - k0 + 31) / 32);
+        // a wavefront whose queries are all past N, and key tiles, blocks and
+        // chunks wholly past its last query's last visible key, have nothing
+        // to add (their probabilities are 0): skipped
+        if (q0 >= N || k0 >= kw_end) continue;
+        const int nkb = min(AT_KB, (kw_end - k0 + 15) / 16);
+        const int npc = min(AT_K / 32, (kw_end - k0 + 31) / 32);
         // S[16 q][AT_K k]: lane holds rows 4g + i of key block kb, key kb*16 + r16
         f4v sacc[AT_KB];
 #pragma unroll
@@ -379,11 +383,20 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ Qh, cons
 hipError_t launch_attn(const float *Qh, const float *Kh, const float *Vh, const AttnDims &a, float *out,
                        hipStream_t s)
 {
-    if (a.nkv <= 0 || a.nh % a.nkv) return hipErrorInvalidValue;
-    const dim3 grid(a.nh, (a.n + AT_Q - 1) / AT_Q);
-    switch (a.hd) {
-    case 64: hipLaunchKernelGGL(k_attn<64>, grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
-    case 128: hipLaunchKernelGGL(k_attn<128>, grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
+    if (a.nkv <= 0 || a.nh % a.nkv || (a.waves != 0 && a.waves != 4 && a.waves != 8)) return hipErrorInvalidValue;
+    // eight wavefronts (128 queries) per workgroup once that still gives two
+    // workgroups per CU (each K / V tile staged once for twice the queries),
+    // else four (more workgroups for the few-query grids)
+    int n_cu = 0;
+    const hipError_t e = device_cu_count(&n_cu);
+    if (e != hipSuccess) return e;
+    const bool wide = a.waves ? a.waves == 8 : (long)a.nh * ((a.n + 127) / 128) >= 2L * n_cu;
+    const dim3 grid(a.nh, (a.n + (wide ? 127 : 63)) / (wide ? 128 : 64));
+    switch (a.hd * (wide ? -1 : 1)) {
+    case 64: hipLaunchKernelGGL((k_attn<64, 4>), grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
+    case 128: hipLaunchKernelGGL((k_attn<128, 4>), grid, dim3(256), 0, s, Qh, Kh, Vh, a, out); break;
+    case -64: hipLaunchKernelGGL((k_attn<64, 8>), grid, dim3(512), 0, s, Qh, Kh, Vh, a, out); break;
+    case -128: hipLaunchKernelGGL((k_attn<128, 8>), grid, dim3(512), 0, s, Qh, Kh, Vh, a, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -81,6 +81,28 @@ def test_attn_flash(ctx, O, flash_attn, N):
     layer.free()
 
 
+@pytest.mark.parametrize("waves", ["4", "8"])
+def test_attn_waves(ctx, O, flash_attn, monkeypatch, waves):
+    """The attention kernel with four or eight wavefronts per workgroup (64 or
+    128 queries; the grid size picks one, the switch pins it): the flash shape
+    at 256 tokens and a ragged small shape against the oracle."""
+    import dmoe
+    from dmoe import synth
+    monkeypatch.setenv("DMOE_ATTN_WAVES", waves)
+    c = dmoe.Context(0)
+    monkeypatch.delenv("DMOE_ATTN_WAVES")
+    try:
+        _say(f"case: attn flash shape Q4_K N=256, {waves} wavefronts")
+        layer, *_ = _run(c, O, flash_attn, 256, 200, TOL[12])
+        layer.free()
+        _say(f"case: attn H512 8/2 heads d64 B16 N=200 F32, {waves} wavefronts")
+        w = synth.host_attn(0, 201, O.quantize_rows, 512, 8, 2, 64, 64, block_length=16)
+        layer, *_ = _run(c, O, w, 200, 202, TOL[0])
+        layer.free()
+    finally:
+        c.close()
+
+
 def test_attn_device_entry(ctx, O, flash_attn):
     """dmoe_attn_wrap_device + dmoe_attn_forward_device on torch buffers: the
     same bits as the host-io entry; without moe_in only h_out is written."""
