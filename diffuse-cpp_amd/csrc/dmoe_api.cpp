@@ -1375,8 +1375,9 @@ int proj_chunk(int path, int N) { return path == DP_Q6K ? std::min(N, PROJ_MAX_T
 // Q4_K projections of PROJ_GEMM_MIN_TOKENS or more tokens run on the grouped
 // GEMM's down launch (k_expert_gemm.hip) with shared units only: 64 tokens
 // (128 digit rows) per unit, 256 output rows per item, the reduction split
-// into the fewest slices (2 or more super-blocks each) that give every CU an
-// item.  Returns the slice count, 0 where the GEMM does not take the shape.
+// into slices of 2 or more super-blocks, as many as minimise the static
+// schedule's rounds x steps plus the slices' own traffic.  Returns the slice
+// count, 0 where the GEMM does not take the shape.
 constexpr int PROJ_GEMM_MIN_TOKENS = 33;
 
 int proj_gemm_slices(const KernelSwitches &sw, int path, int rows, int K, int N)
@@ -1388,9 +1389,21 @@ int proj_gemm_slices(const KernelSwitches &sw, int path, int rows, int K, int N)
     if (device_cu_count(&n_cu) != hipSuccess || n_cu <= 0) n_cu = 256;
     const long items = (long)((N + 63) / 64) * (rows / 256);
     const int nsb = K / 256;
+    const long grid = (n_cu + 7) / 8 * 8;
+    // rounds of the static schedule x super-blocks per item at ~4.5 us per
+    // step, plus the slices written and read again at ~4 TB/s
     int best = 1;
-    for (int ks = 2; ks <= 16 && items * best < n_cu; ks *= 2)
-        if (nsb % ks == 0 && nsb / ks >= 2) best = ks;
+    double best_us = 0.0;
+    for (int ks = 1; ks <= 16; ks *= 2) {
+        if (nsb % ks || (ks > 1 && nsb / ks < 2)) continue;
+        const long rounds = (items * ks + grid - 1) / grid;
+        double us = 4.5 * (double)(rounds * (nsb / ks));
+        if (ks > 1) us += (double)ks * N * rows * 8 / 4e6;
+        if (ks == 1 || us < best_us) {
+            best = ks;
+            best_us = us;
+        }
+    }
     return best;
 }
 
