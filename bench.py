@@ -377,9 +377,9 @@ def bench_rows(a):
     """The rows next to the MoE segment at their flash shapes, each timed over
     a.rows_steps calls with HIP events on the launch stream, weights resident
     in HBM (copies rotated past the 256 MB memory-side cache): the attention
-    half of a layer (32 and 256 tokens), the dense layer-0 MLP (32 tokens) and
-    the step tail (final norm, 157,184-row LM head, argmax and confidence;
-    32 tokens).  All three stream weights: the roofline is HBM, the
+    half of a layer (32, 256 and 2048 tokens), the dense layer-0 MLP (32
+    tokens) and the step tail (final norm, 157,184-row LM head, argmax and
+    confidence; 32 tokens).  All three stream weights: the roofline is HBM, the
     algorithmic bytes are stated per record."""
     import torch
     import dmoe
@@ -434,7 +434,7 @@ def bench_rows(a):
     QD = A["n_head"] * A["head_dim"]
     wbytes = (QKV + H) * rs                                       # wqkv and wo, Q4_K
     recs = {}
-    for N in (32, 256):
+    for N in (32, 256, 2048):
         h = torch.randn((N, H), device=dev)
         ho = torch.empty_like(h)
         mi = torch.empty_like(h)
