@@ -74,7 +74,7 @@ def flash_attn(O):
     return synth.host_attn(12, 5, O.quantize_rows, **synth.ATTN_FLASH)
 
 
-@pytest.mark.parametrize("N", [32, 256])
+@pytest.mark.parametrize("N", [32, 256, 1024])
 def test_attn_flash(ctx, O, flash_attn, N):
     _say(f"case: attn flash shape Q4_K N={N}")
     layer, *_ = _run(ctx, O, flash_attn, N, 100 + N, TOL[12])
