@@ -1,6 +1,6 @@
 // k_attn.hip — the attention half of the LLaDA2 layer on gfx950
 // (src/diffuse-moe-graph.cpp:116-178), between the fused QKV projection and
-// the output projection (both run on the expert kernels' shared-down path).
+// the output projection.
 //
 // k_qk_rope: per (token, head) one wavefront: the head's slice of the fused
 //   QKV row (Q heads, then K heads, then V heads, :132-134), the QK RMSNorm
