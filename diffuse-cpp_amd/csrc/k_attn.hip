@@ -119,6 +119,34 @@ __device__ __forceinline__ void at_split(float x, _Float16 &hi, _Float16 &lo)
     lo = (_Float16)(x - (float)hi);
 }
 
+// The partner of each lane in a 16-lane row by DPP (no LDS round trip):
+// quad_perm [1,0,3,2] and [2,3,0,1] (lane ^ 1, lane ^ 2), then the half-row
+// and row mirrors, which pair quad q with quad q ^ 1 and half h with half
+// h ^ 1 as lane ^ 4 and lane ^ 8 do: after the four steps of
+// v = op(v, partner) every lane holds the same tree over its row as the
+// __shfl_xor butterfly over 1, 2, 4, 8 (op commutative), so the same bits.
+template <int CTRL>
+__device__ __forceinline__ float at_dpp(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float at_row_max(float v)
+{
+    v = fmaxf(v, at_dpp<0xb1>(v));
+    v = fmaxf(v, at_dpp<0x4e>(v));
+    v = fmaxf(v, at_dpp<0x141>(v));
+    return fmaxf(v, at_dpp<0x140>(v));
+}
+
+__device__ __forceinline__ float at_row_sum(float v)
+{
+    v = v + at_dpp<0xb1>(v);
+    v = v + at_dpp<0x4e>(v);
+    v = v + at_dpp<0x141>(v);
+    return v + at_dpp<0x140>(v);
+}
+
 template <int HD, int QW>
 __global__ __launch_bounds__(QW * 64) void k_attn(const float *__restrict__ Qh, const float *__restrict__ Kh,
                                               const float *__restrict__ Vh, AttnDims a, float *__restrict__ out)
@@ -301,9 +329,7 @@ __global__ __launch_bounds__(QW * 64) void k_attn(const float *__restrict__ Qh, 
                 sacc[kb][i] = v;
                 mx = fmaxf(mx, v);
             }
-#pragma unroll
-            for (int sh = 1; sh < 16; sh <<= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, 16));
-            mt[i] = mx;
+            mt[i] = at_row_max(mx);
         }
         float corr[4];
 #pragma unroll
@@ -318,8 +344,7 @@ __global__ __launch_bounds__(QW * 64) void k_attn(const float *__restrict__ Qh, 
                 sacc[kb][i] = p;
                 rs += p;
             }
-#pragma unroll
-            for (int sh = 1; sh < 16; sh <<= 1) rs += __shfl_xor(rs, sh, 16);
+            rs = at_row_sum(rs);
             l[i] = l[i] * corr[i] + rs;
             m[i] = mn;
         }
