@@ -29,6 +29,7 @@ sys.path.insert(0, str(ROOT / "diffuse-cpp_amd"))
 METRIC = "MoE-layer tokens/s + % HBM-BW roofline (32-tok block, Q4_K); prefill % MFMA"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32
 MFMA_INT8_PEAK_TOPS = 5000.0   # MI355X dense int8
 
 
@@ -450,6 +451,20 @@ def bench_rows(a):
             {"front": "input_norm", "gateup_shared": "qkv_proj", "act_quant_x": "qkv_x_quant",
              "route": "qk_norm_rope", "scores": "attention", "act_quant_h": "attn_out_quant",
              "down_shared": "out_proj", "combine": "residual_post_norm"})
+        # the attention kernel against the compute roofline: Q K^T and P V
+        # over each query's visible keys (block-causal, block_length B), two
+        # flops per multiply-add; fp32 semantics, run as three f16 MFMA
+        # products per multiply-add (hi / lo halves)
+        B = A.get("block_length", 32)
+        vis = sum(min(N, (q // B + 1) * B) if B > 0 else N for q in range(N))
+        flops = 4.0 * A["head_dim"] * A["n_head"] * vis
+        at_us = recs[f"n{N}"]["stage_us"].get("attention")
+        if at_us:
+            tf = flops / (at_us * 1e-6) / 1e12
+            recs[f"n{N}"]["attention_kernel"] = {
+                "us": at_us, "gflop": round(flops / 1e9, 3), "tflops": round(tf, 1),
+                "of_fp32_mfma_peak": round(tf / MFMA_F32_PEAK_TFLOPS, 3),
+                "split_f16_mfma_frac": round(3 * tf / MFMA_F16_PEAK_TFLOPS, 3)}
     out["attention"] = recs
     del layers, keep
     torch.cuda.empty_cache()
