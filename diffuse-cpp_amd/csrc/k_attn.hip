@@ -105,7 +105,8 @@ hipError_t launch_qk_rope(const float *qkv, int ks, size_t kstride, const float 
 
 constexpr int AT_K = 64;              // keys per tile
 constexpr int AT_KB = AT_K / 16;      // 16-key blocks of a tile
-constexpr int AT_LVT = AT_K + 8;      // f16 row stride of the transposed V tile and of P
+constexpr int AT_LVT = AT_K + 16;     // f16 row stride of the transposed V tile
+constexpr int AT_LP = AT_K + 8;       // f16 row stride of P
 
 typedef _Float16 at_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 at_h4 __attribute__((ext_vector_type(4)));
@@ -154,12 +155,15 @@ __global__ __launch_bounds__(QW * 64) void k_attn(const float *__restrict__ Qh, 
     constexpr int AT_Q = 16 * QW;     // queries per workgroup (16 per wavefront)
     constexpr int AT_T = 64 * QW;     // threads per workgroup
     // f16 hi / lo planes in LDS, rows padded so that the 16-byte operand
-    // reads of a wavefront's 16 rows hit different banks: K [key][d] (row
-    // stride HD + 8), V transposed [d][key] and P [query][key] (AT_K + 8)
-    constexpr int LK = HD + 8;
+    // reads of a wavefront's 16 rows do not conflict: a row stride of 8 dwords
+    // mod 32 (measured: 4, 12, 16 and 20 conflict) for K [key][d] (HD + 16
+    // halves) and V transposed [d][key] (AT_K + 16); P [query][key] keeps
+    // AT_K + 8, where its 2-byte writes by rows 4 g + i do not conflict
+    // either (with AT_K + 16 they do)
+    constexpr int LK = HD + 16;
     __shared__ __align__(16) _Float16 sK[2][AT_K * LK];
     __shared__ __align__(16) _Float16 sV[2][HD * AT_LVT];
-    __shared__ __align__(16) _Float16 sP[AT_Q / 16][2][16 * AT_LVT];
+    __shared__ __align__(16) _Float16 sP[AT_Q / 16][2][16 * AT_LP];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     // the grid's x is the head and y the query block, last block first: the
@@ -361,8 +365,8 @@ __global__ __launch_bounds__(QW * 64) void k_attn(const float *__restrict__ Qh, 
             for (int i = 0; i < 4; i++) {
                 _Float16 hi, lo;
                 at_split(sacc[kb][i], hi, lo);
-                ph[(4 * g + i) * AT_LVT + kb * 16 + r16] = hi;
-                pl[(4 * g + i) * AT_LVT + kb * 16 + r16] = lo;
+                ph[(4 * g + i) * AT_LP + kb * 16 + r16] = hi;
+                pl[(4 * g + i) * AT_LP + kb * 16 + r16] = lo;
             }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -371,7 +375,7 @@ __global__ __launch_bounds__(QW * 64) void k_attn(const float *__restrict__ Qh, 
             constexpr int NPC = decltype(npc_c)::value;
 #pragma unroll
             for (int c = 0; c < NPC; c++) {
-                const int po = r16 * AT_LVT + 32 * c + 8 * g;
+                const int po = r16 * AT_LP + 32 * c + 8 * g;
                 const at_h8 pah = *reinterpret_cast<const at_h8 *>(ph + po);
                 const at_h8 pal = *reinterpret_cast<const at_h8 *>(pl + po);
 #pragma unroll
